@@ -1,0 +1,308 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X int4 decode hot path (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
+
+Workload (one "step"): config 1 of the benchmark definition — one decoder layer's decode projections at batch 1,
+int4 g128, x fp16 ~N(0,1): fused QKV (2048 -> 3072), O (2048 -> 2048), fused gate+up (2048 -> 2*11008) followed by
+SiLU(gate)*up, down (11008 -> 2048). Each step uses the weights of the next of 16 distinct synthetic layers (665 MB
+in all), so no step is served from the 256 MB Infinity Cache. A step is one hipGraph replay; weights and inputs are
+resident in HBM before timing.
+
+value = algorithmic bytes per step (sum over the four projections of N*K/2 + 4*N*K/128 + 2K + 2N) / wall time.
+roofline: the dominant kernel (the gate+up GEMV, 24,001,536 B per launch), its average launch duration measured
+with HIP events on its stream over back-to-back launches with rotated weights.
+cpu_baseline: the CPU oracle's dequantize-then-matmul of the same step (numpy fp32), on this host's cores.
+Extra fields: the per-projection kernel times, the int8 audio head (config 2) and the int4 prefill (config 3).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "rumik-fast_amd" / "kernels", ROOT / "rumik-fast_amd" / "engine"):
+    sys.path.insert(0, str(p))
+
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
+PEAK_FP16_TFLOPS = 2500.0    # MI355X dense fp16 MFMA, published
+H, INTER, NQKV = 2048, 11008, 2048 + 512 + 512
+SHAPES = {"qkv": (NQKV, H), "o": (H, H), "gate_up": (2 * INTER, H), "down": (H, INTER)}
+N_COPIES = 16
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def int4_bytes(N, K):
+    return N * K // 2 + 4 * N * (K // 128) + 2 * K + 2 * N
+
+
+def int8_bytes(N, K):
+    return N * K + 2 * N + 2 * K + 4 * N
+
+
+def graph_of(fns):
+    import torch
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph_us(g, launches_per_replay, reps=20, trials=5):
+    """best-of-trials average per launch (HIP events on the replay stream)"""
+    import torch
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = math.inf
+    for _ in range(trials):
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / reps / launches_per_replay)
+    return best
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, if present."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return d.get("gemv_int4_gate_up_22016x2048", {}).get("traffic_bytes")
+    except Exception:
+        return None
+
+
+def cpu_baseline(budget_s):
+    """numpy oracle: dequantize-then-matmul of one config-1 step, repeated for about budget_s seconds."""
+    import numpy as np
+    import torch
+    import synth
+    from oracle import int4 as O
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        cores = 1
+    g = synth.generator(1)
+    mats = {k: tuple(t.numpy() for t in synth.int4_weights(N, K, g)) for k, (N, K) in SHAPES.items()}
+    x = synth.activations(H, g).numpy()
+    ob = synth.activations(H, g).numpy()
+
+    def step():
+        O.gemv_int4(x, *mats["qkv"])
+        O.gemv_int4(ob, *mats["o"])
+        gu = O.gemv_int4(x, *mats["gate_up"])
+        gate, up = gu[:INTER], gu[INTER:]
+        act = (gate / (1 + np.exp(-gate)) * up).astype(np.float16)
+        O.gemv_int4(act, *mats["down"])
+
+    step()  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    nbytes = sum(int4_bytes(N, K) for N, K in SHAPES.values())
+    return {"value": round(nbytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": int(cores), "kind": "port",
+            "sample": f"{n} config-1 steps (one weight copy), numpy fp32 dequantize-then-matmul, {dt:.1f} s"}
+
+
+def run_decode(dev, steps):
+    """Config 4: tok/s of the captured 36-layer step (random-init int4 weights, int8 head, fp16 KV cache ~N(0,1)
+    filled to ctx - 1 slots; each step writes slot ctx - 1 and attends over ctx slots). pos is reset before every
+    replay (one tiny fill kernel per step, inside the timed loop)."""
+    import torch
+    import decode
+    cfg = decode.Config()
+    w = decode.random_weights(cfg, 4, device=dev)
+    eng = decode.DecodeStep(cfg, w, device=dev)
+    out = {"weights_bytes_per_token": cfg.weight_bytes(), "layers": cfg.L}
+    eng.fill_cache(cfg.S, seed=5)
+    eng.set_state(7, 0)
+    eng.capture()
+    for ctx in (256, 1024, 2048):
+        for _ in range(5):
+            eng.pos.fill_(ctx - 1)
+            eng.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eng.pos.fill_(ctx - 1)
+            eng.replay()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        nbytes = cfg.weight_bytes() + cfg.kv_bytes(ctx)
+        out[f"ctx{ctx}"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1),
+                            "GB_s": round(nbytes * steps / dt / 1e9, 1), "bytes_per_token": nbytes}
+        log(f"[bench] decode ctx {ctx}: {out[f'ctx{ctx}']}")
+    del eng, w
+    torch.cuda.empty_cache()
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=100, help="timed decode steps per context length (0: skip)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: --gpus {args.gpus} requested, but this build measures one GPU only: the int4 decode path "
+              "is a single-GPU batch-1 workload here (no collectives are built); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import cuda_gemv
+    import mm_int4
+    import synth
+    import _hiplib as HL
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"[bench] {torch.cuda.get_device_name(dev)}, {torch.cuda.get_device_properties(dev).multi_processor_count} CUs")
+
+    # ---- weights: 16 distinct layers (GPU-side RNG: values are irrelevant to timing)
+    gen = synth.generator(1, "cuda")
+    layers = [{k: synth.int4_weights(N, K, gen, device=dev) for k, (N, K) in SHAPES.items()} for _ in range(N_COPIES)]
+    x = torch.randn(H, device=dev, generator=gen).half()
+    ob = torch.randn(H, device=dev, generator=gen).half()
+    y_qkv = torch.empty(NQKV, device=dev, dtype=torch.float16)
+    y_o = torch.empty(H, device=dev, dtype=torch.float16)
+    y_gu = torch.empty(2 * INTER, device=dev, dtype=torch.float16)
+    act = torch.empty(INTER, device=dev, dtype=torch.float16)
+    y_d = torch.empty(H, device=dev, dtype=torch.float16)
+
+    def silu_mul():
+        HL.check(HL.lib().rk_silu_mul(HL.ptr(y_gu), HL.ptr(act), HL.F16, INTER, HL.stream(dev)))
+
+    def step_fns(L):
+        return [lambda: cuda_gemv.gemv_int4_cuda(x, *L["qkv"], out=y_qkv),
+                lambda: cuda_gemv.gemv_int4_cuda(ob, *L["o"], out=y_o),
+                lambda: cuda_gemv.gemv_int4_cuda(x, *L["gate_up"], out=y_gu),
+                silu_mul,
+                lambda: cuda_gemv.gemv_int4_cuda(act, *L["down"], out=y_d)]
+
+    graphs = [graph_of(step_fns(L)) for L in layers]
+    step_bytes = sum(int4_bytes(N, K) for N, K in SHAPES.values())
+
+    # ---- timed region: exactly K steps, synchronized on both sides
+    for i in range(args.warmup):
+        graphs[i % N_COPIES].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        graphs[i % N_COPIES].replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = step_bytes * args.steps / elapsed / 1e9
+    log(f"[bench] config 1: {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s")
+
+    # ---- per-projection kernel times (back-to-back launches over the 16 copies)
+    proj = {}
+    for k, (N, K) in SHAPES.items():
+        out = {"qkv": y_qkv, "o": y_o, "gate_up": y_gu, "down": y_d}[k]
+        inp = {"o": ob, "down": act}.get(k, x)
+        g = graph_of([lambda L=L: cuda_gemv.gemv_int4_cuda(inp, *L[k], out=out) for L in layers])
+        us = time_graph_us(g, N_COPIES)
+        proj[k] = {"N": N, "K": K, "us": round(us, 2), "GB_s": round(int4_bytes(N, K) / us / 1e3, 1)}
+        del g
+    log(f"[bench] projections: {proj}")
+    gu_us = proj["gate_up"]["us"]
+    achieved = int4_bytes(*SHAPES["gate_up"]) / gu_us / 1e3
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": load_traffic(),
+                "kernel": "gemv int4 g128, gate+up N=22016 K=2048", "us_per_launch": gu_us}
+    del graphs
+    del layers
+    torch.cuda.empty_cache()
+
+    # ---- config 2: int8 audio head (16385 x 2048, fp16 row scale, fp32 logits), 20 rotated copies
+    heads = [synth.int8_weights(16385, H, gen, device=dev) for _ in range(20)]
+    hx = torch.randn(H, device=dev, generator=gen).half()
+    logits = torch.empty(16385, device=dev, dtype=torch.float32)
+    g = graph_of([lambda w=w: cuda_gemv.gemv_int8_cuda(hx, w[0], w[1], out=logits) for w in heads])
+    us = time_graph_us(g, len(heads))
+    head = {"N": 16385, "K": H, "us": round(us, 2), "GB_s": round(int8_bytes(16385, H) / us / 1e3, 1)}
+    log(f"[bench] int8 head: {head}")
+    del g, heads
+    torch.cuda.empty_cache()
+
+    # ---- config 3: int4 prefill matmul (M in {34, 128, 512}), 8 rotated copies per shape
+    prefill = {}
+    for (N, K) in ((NQKV, H), (2 * INTER, H), (H, INTER)):
+        mats = [synth.int4_weights(N, K, gen, device=dev) for _ in range(8)]
+        for M in (34, 128, 512):
+            X = torch.randn(M, K, device=dev, generator=gen).half()
+            Y = torch.empty(M, N, device=dev, dtype=torch.float16)
+            try:
+                g = graph_of([lambda w=w: mm_int4.mm_int4(X, *w, out=Y) for w in mats])
+            except Exception as e:  # prefill kernel not available in this build
+                prefill = {"error": str(e)[:200]}
+                break
+            us = time_graph_us(g, len(mats), reps=10, trials=3)
+            fl = 2.0 * M * N * K
+            prefill[f"M{M}_{N}x{K}"] = {"us": round(us, 2), "TFLOP_s": round(fl / us / 1e6, 1),
+                                        "mfma_frac": round(fl / us / 1e6 / PEAK_FP16_TFLOPS, 4)}
+            del g
+        if "error" in prefill:
+            break
+        del mats
+        torch.cuda.empty_cache()
+    log(f"[bench] prefill: {prefill}")
+
+    # ---- config 4: the full 36-layer decode step, hipGraph replays at ctx 256 / 1024 / 2048
+    decode_res = run_decode(dev, args.decode_steps) if args.decode_steps > 0 else None
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    if cpu:
+        log(f"[bench] cpu baseline: {cpu}")
+
+    rec = {
+        "metric": "int4 GEMV HBM GB/s (% of peak); batch-1 decode tok/s, 36-layer 3B synthetic",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights x fp16 activations, fp32 accumulate",
+        "data": "synthetic (seeded int4 g128 codes / fp16 scale+min, x ~ N(0,1)); 16 distinct weight copies",
+        "config": {"workload": "config 1: one decoder layer's decode projections (qkv 3072x2048, o 2048x2048, "
+                               "gate+up 22016x2048 + SiLU*up, down 2048x11008), batch 1",
+                   "bytes_per_step": step_bytes, "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "projections": proj,
+        "int8_head": head,
+        "prefill": prefill,
+        "decode": decode_res,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,136 @@
+/* rumik_hip.h — C ABI of the MI355X (gfx950) int4 decode hot path.
+ *
+ * Every entry point takes raw device pointers, sizes, dtype codes and a HIP stream (passed as void*), launches
+ * asynchronously on that stream, allocates nothing and never synchronizes, so every call can be captured in a
+ * hipGraph. The return value is RK_OK or a negative status (rk_status_string gives the text); invalid arguments
+ * are rejected on the host before any launch.
+ *
+ * Tensor layouts (row-major, contiguous):
+ *   int4 weights  q uint8 [N, K/2] (low nibble = even column), scale fp16 [N, K/128], min fp16 [N, K/128];
+ *                 w[n,k] = code[n,k] * scale[n,k/128] + min[n,k/128]
+ *   int8 weights  q int8 [N, K] (RK_Q_S8) or uint8 = int8 + 128 (RK_Q_U8); one scale per row (fp16 or fp32)
+ *   activations   fp16 / bf16 vectors; outputs fp16 / bf16 / fp32
+ */
+#ifndef RUMIK_HIP_H
+#define RUMIK_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define RK_F16 0
+#define RK_BF16 1
+#define RK_F32 2
+
+/* int8 code layouts */
+#define RK_Q_S8 0 /* signed int8 codes in [-127, 127] */
+#define RK_Q_U8 1 /* uint8 = int8 + 128 (kernels/cuda_gemv.py:234-242 of the reference) */
+
+/* status codes */
+#define RK_OK 0
+#define RK_ERR_SHAPE (-1)  /* unsupported or inconsistent sizes ("shape") */
+#define RK_ERR_BLOCK (-2)  /* unsupported block shape (waves / rows knobs) */
+#define RK_ERR_DTYPE (-3)  /* unsupported dtype code */
+#define RK_ERR_NULL (-4)   /* a required pointer is NULL */
+#define RK_ERR_ALIGN (-5)  /* a pointer is not aligned as the kernel's vector loads need */
+#define RK_ERR_LAUNCH (-6) /* the HIP launch itself failed */
+
+typedef void* rk_stream_t; /* a hipStream_t; NULL = the default stream */
+
+/* Version of this ABI (bumped when a signature changes). */
+int rk_abi_version(void);
+
+/* Text of a status code (static storage). */
+const char* rk_status_string(int status);
+
+/* Batch-1 int4 group-128 GEMV: y[n] = sum_k (code[n,k]*scale[n,k/128] + min[n,k/128]) * x[k], fp32 accumulate.
+ * Replaces gemv_int4_cuda(x, q, s, m, out, warps, rows) -> gemv_int4 -> launch_int4
+ *   (reference kernels/cuda_gemv.py:226-231, :130-136, :117-128) and the Triton fallback gemv_int4
+ *   (kernels/int4_gemv.py:84-96).
+ * x: [K] fp16/bf16, 16-byte aligned; q: 16-byte aligned; y: [N] of y_dtype.
+ * K % 128 == 0 (reference: TORCH_CHECK(... K % GROUP == 0, "shape")) and K <= ~80000 (x is staged in LDS);
+ * any N >= 1 (no multiple-of-block rule). The kernel is picked per shape: the matrix-core kernel
+ * (rk_gemv_int4_g128_mfma) for N >= 8192 with K <= 4096, the VALU kernel (rk_gemv_int4_g128_valu) otherwise.
+ * waves: waves per block (the reference's `warps` knob), in {1,2,4,8,16}; rows: rows per wave (the reference's
+ * `rows`), in {1,2,4,8}; 0 = tuned default. Anything else returns RK_ERR_BLOCK ("unsupported block shape"). */
+int rk_gemv_int4_g128(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale, const uint16_t* min,
+                      void* y, int y_dtype, int N, int K, int waves, int rows, rk_stream_t stream);
+
+/* The matrix-core kernel for any shape: a wave owns a 16-row tile; each v_mfma_f32_16x16x32_f16 takes the
+ * exactly dequantized codes as B and x as A. waves above 4 are clamped to 4 per block; rows is validated, unused.
+ * Same contract as rk_gemv_int4_g128 (no separate reference counterpart). */
+int rk_gemv_int4_g128_mfma(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                           const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                           rk_stream_t stream);
+
+/* The VALU kernel for any shape (v_dot2_f32_f16): `rows` rows per wave, `waves` per block, exactly the
+ * reference's (warps, rows) knobs. Same contract as rk_gemv_int4_g128 (no separate reference counterpart). */
+int rk_gemv_int4_g128_valu(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                           const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                           rk_stream_t stream);
+
+/* Batch-1 int8 per-row GEMV: y[n] = scale[n] * sum_k code[n,k] * x[k], fp32 accumulate.
+ * Replaces gemv_int8_cuda(x, q, s, out) -> gemv_int8 (reference kernels/cuda_gemv.py:245-249, :188-195).
+ * q_kind: RK_Q_S8 or RK_Q_U8; scale dtype RK_F16 or RK_F32; y dtype RK_F32 / RK_BF16 / RK_F16.
+ * K % 16 == 0, x and q 16-byte aligned; any N >= 1 (the reference needs N % 16 == 0 and K % 512 == 0). */
+int rk_gemv_int8_rows(const void* x, int x_dtype, const void* q, int q_kind, const void* scale, int s_dtype,
+                      void* y, int y_dtype, int N, int K, rk_stream_t stream);
+
+/* int4 group-128 matrix product for the prefill: Y[m,n] = sum_k X[m,k] * w[n,k], fp32 accumulate, MFMA.
+ * Replaces mm_int4(x, q, s, m) -> _mm_int4 (reference kernels/mm_int4.py:59-73, :24-46).
+ * X: [M, K] fp16/bf16 with row stride ldx elements (ldx % 8 == 0, 16-byte aligned rows);
+ * Y: [M, N] of y_dtype with row stride ldy. K % 128 == 0; any M >= 1, N >= 1. */
+int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
+                    const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, rk_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Decode-step glue (reference engine/fused.py). Activations of one decode step are vectors of `act_dtype`
+ * (fp16 or bf16); the KV cache is [NKV, S, HD] per layer in act_dtype; `pos` is an int64 on the device, read by
+ * the kernels, so one captured graph serves every sequence length.
+ * ------------------------------------------------------------------------------------------------------------ */
+
+/* x = bf16/fp16(emb_q[tok] * emb_s[tok]) (int8 row, fp16 scale); h = LayerNorm(x) * w.
+ * Replaces fused.embed_ln (reference engine/fused.py:16-27). tok: int64 on the device. */
+int rk_embed_ln(const int64_t* tok, const int8_t* emb_q, const uint16_t* emb_s, const void* ln_w, void* x, void* h,
+                int act_dtype, int H, float eps, rk_stream_t stream);
+
+/* x = x + a + b (fp32 sum, one rounding); h = LayerNorm(x) * w (centre, rsqrt(var + eps), no bias).
+ * Replaces fused.add_ln (reference engine/fused.py:30-41). b may be NULL (then x = x + a). */
+int rk_add_ln(void* x, const void* a, const void* b, const void* ln_w, void* h, int act_dtype, int H, float eps,
+              rk_stream_t stream);
+
+/* Everything between the fused projection and attention: interleaved RoPE on the NH query heads (-> q_out) and
+ * NKV key heads (-> k cache at slot pos), value heads copied to the v cache, act = silu(gate) * up.
+ * y layout [q NH*HD | k NKV*HD | v NKV*HD | gate inter | up inter]; cos/sin tables [S, HD] in act_dtype.
+ * rope = 0 skips the rotation (NoPE layers). Replaces fused.post (reference engine/fused.py:44-84). */
+int rk_post(const void* y, const int64_t* pos, const void* cos_t, const void* sin_t, void* k_cache, void* v_cache,
+            void* q_out, void* act, int act_dtype, int NH, int NKV, int HD, int S, int inter, int rope,
+            rk_stream_t stream);
+
+/* Flash-decoding partials over cache slots 0..pos: grid (NKV, nsplit); partial (m, l, acc) per query head and
+ * split into pm/pl [NH, nsplit] and po [NH, nsplit, HD] (fp32). Replaces fused.attn_split (engine/fused.py:120-169).
+ * HD must be 128. */
+int rk_attn_split(const void* q, const void* k_cache, const void* v_cache, const int64_t* pos, float* po, float* pm,
+                  float* pl, int act_dtype, int NH, int NKV, int HD, int S, int nsplit, float scale,
+                  rk_stream_t stream);
+
+/* Merge the nsplit partials of every head: out = sum_i w_i acc_i / sum_i w_i l_i, w_i = exp(m_i - max m).
+ * Replaces fused.attn_combine (reference engine/fused.py:172-187). */
+int rk_attn_combine(const float* po, const float* pm, const float* pl, const int64_t* pos, void* out, int act_dtype,
+                    int NH, int HD, int nsplit, rk_stream_t stream);
+
+/* act[i] = silu(gate[i]) * up[i] for gate_up = [gate inter | up inter], fp32 math, one rounding: the MLP job of
+ * fused.post (reference engine/fused.py:76-84), used between the gate/up and down projections. */
+int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_stream_t stream);
+
+/* pos[0] += 1 on the device (the `self.pos += 1` of the captured step, reference engine/rumik_fused.py:120). */
+int rk_pos_advance(int64_t* pos, rk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RUMIK_HIP_H */

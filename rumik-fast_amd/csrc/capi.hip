@@ -1,0 +1,80 @@
+// Exported C ABI (include/rumik_hip.h): host-side validation and dispatch. Kernels live in the other files.
+#include "common.h"
+
+extern "C" int rk_gemv_int4_g128_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                                      const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                                      int subn, rk_stream_t stream);
+extern "C" int rk_gemv_int4_mfma_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                                      const uint16_t* min, void* y, int y_dtype, int N, int K, int waves,
+                                      rk_stream_t stream);
+extern "C" int rk_gemv_int8_rows_impl(const void* x, int x_dtype, const void* q, int q_kind, const void* scale,
+                                      int s_dtype, void* y, int y_dtype, int N, int K, int waves, int rows,
+                                      rk_stream_t stream);
+
+extern "C" {
+
+int rk_abi_version(void) { return 1; }
+
+const char* rk_status_string(int status) {
+    switch (status) {
+        case RK_OK: return "ok";
+        case RK_ERR_SHAPE: return "shape";
+        case RK_ERR_BLOCK: return "unsupported block shape";
+        case RK_ERR_DTYPE: return "unsupported dtype";
+        case RK_ERR_NULL: return "null pointer";
+        case RK_ERR_ALIGN: return "misaligned pointer (16-byte alignment required)";
+        case RK_ERR_LAUNCH: return "kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+int rk_gemv_int4_g128(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale, const uint16_t* min,
+                      void* y, int y_dtype, int N, int K, int waves, int rows, rk_stream_t stream) {
+    // Path per shape, from measurements on MI355X (hipGraph-timed, weights rotated past the 256 MB MALL):
+    // many short rows (N >= 8192, K <= 4096: the fused q/k/v/gate/up projection) run faster on the matrix
+    // cores; long rows (K = 11008) and small N run faster on the VALU kernel.
+    if (N >= 8192 && K <= 4096) {
+        if (rows && !(rows == 1 || rows == 2 || rows == 4 || rows == 8)) return RK_ERR_BLOCK;
+        return rk_gemv_int4_mfma_impl(x, x_dtype, q, scale, min, y, y_dtype, N, K, waves, stream);
+    }
+    return rk_gemv_int4_g128_impl(x, x_dtype, q, scale, min, y, y_dtype, N, K, waves, rows, 0, stream);
+}
+
+// The MFMA kernel for every shape (16-row tile per wave; `rows` validated, unused).
+int rk_gemv_int4_g128_mfma(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                           const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                           rk_stream_t stream) {
+    if (rows && !(rows == 1 || rows == 2 || rows == 4 || rows == 8)) return RK_ERR_BLOCK;
+    return rk_gemv_int4_mfma_impl(x, x_dtype, q, scale, min, y, y_dtype, N, K, waves, stream);
+}
+
+// The same GEMV with the multiply-adds on the VALU (v_dot2_f32_f16, exact 1024-magic dequant, transposed DPP
+// row reduction): R rows per wave, the reference's (warps, rows) knobs map to (waves per block, rows per wave).
+int rk_gemv_int4_g128_valu(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                           const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                           rk_stream_t stream) {
+    return rk_gemv_int4_g128_impl(x, x_dtype, q, scale, min, y, y_dtype, N, K, waves, rows, 0, stream);
+}
+
+// VALU GEMV with the codes encoded as fp16 subnormals (c * 2^-24, no de-bias op: 9 instead of 13 VALU ops per
+// 8 weights). Measured on gfx950, v_dot2_f32_f16 products of subnormal inputs lose precision (error up to
+// ~3.6 u * sum|w x| against ~0.3 for the 1024-magic path), which breaks the per-output 1e-2 bar on near-zero
+// outputs, so it is not used by default; kept for comparison only.
+int rk_gemv_int4_g128_subn(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                           const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                           rk_stream_t stream) {
+    return rk_gemv_int4_g128_impl(x, x_dtype, q, scale, min, y, y_dtype, N, K, waves, rows, 1, stream);
+}
+
+int rk_gemv_int8_rows(const void* x, int x_dtype, const void* q, int q_kind, const void* scale, int s_dtype,
+                      void* y, int y_dtype, int N, int K, rk_stream_t stream) {
+    return rk_gemv_int8_rows_impl(x, x_dtype, q, q_kind, scale, s_dtype, y, y_dtype, N, K, 0, 0, stream);
+}
+
+// Block-shape-explicit int8 GEMV (waves per block, rows per wave; 0 = default), for tuning sweeps.
+int rk_gemv_int8_rows_ex(const void* x, int x_dtype, const void* q, int q_kind, const void* scale, int s_dtype,
+                         void* y, int y_dtype, int N, int K, int waves, int rows, rk_stream_t stream) {
+    return rk_gemv_int8_rows_impl(x, x_dtype, q, q_kind, scale, s_dtype, y, y_dtype, N, K, waves, rows, stream);
+}
+
+}  // extern "C"

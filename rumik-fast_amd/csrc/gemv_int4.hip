@@ -1,0 +1,289 @@
+// Batch-1 int4 group-128 GEMV for gfx950: y[n] = sum_g scale[n,g] * sum_{k in g} code[n,k] x[k] + min[n,g] * sum_{k in g} x[k]
+// (the affine identity of the reference, kernels/int4_gemv.py:1-4; CUDA version kernels/cuda_gemv.py:38-115).
+//
+// Design (bandwidth-bound; one pass over the weights):
+//   * A "team" of KS waves owns R rows. Thread t of the team (t < 64*KS) owns the 32-column chunks
+//     c = t + j*64*KS (j < NJ). Each chunk of one row is one 16-byte load (global_load_dwordx4, non-temporal), so
+//     a wave instruction streams 1 KiB of codes of one row: fully coalesced 128-byte lines.
+//   * x is staged once per wave, in registers: the 32 values of each owned chunk as 16 fp16 pairs in the order
+//     (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8 columns, plus their fp32 sum. It is reused for all R rows.
+//   * Dequant in registers, exact: (w & 0x000F000F) | 0x64006400 is the fp16 pair (1024 + c0, 1024 + c4) (fp16
+//     1024.0 = 0x6400 has a mantissa LSB worth 1); a packed fp16 add of -1024 leaves (c0, c4) exactly. The high
+//     nibbles give 1024 + 16c, brought back to c by one exact packed fma (x 1/16, -64); the same for w >> 8.
+//     v_dot2_f32_f16 multiplies each code pair with the matching x pair and accumulates in fp32, so every product
+//     is exact and only the fp32 sums round (13 VALU ops per 8 weights).
+//     SUBN = true encodes the codes as fp16 subnormals instead ((w & 0x000F000F) = (c0 * 2^-24, c4 * 2^-24),
+//     no de-bias op, 9 ops per 8 weights, powers of two folded into the scale). On gfx950 the dot2 products of
+//     subnormal inputs lose precision (measured error ~10x the default path's), so it is only a variant.
+//   * Per (row, chunk): acc += (scale * 2^24) * dot + min * xsum, in fp32.
+//   * Rows are reduced over the wave with a transposed butterfly (R + 6 exchanges for R rows, DPP inside 16-lane
+//     rows), then over the KS waves of a team through LDS.
+#include "common.h"
+
+namespace {
+
+constexpr int kMaxThreads = 1024;
+
+// Load the 32 x values of chunk c as 16 fp16 pairs in dequant order, and their fp32 sum.
+RK_DEV void load_x_chunk(const void* __restrict__ x, int xdt, int c, uint32_t (&xp)[16], float& xs) {
+    const u4_t* xv = reinterpret_cast<const u4_t*>(x) + (size_t)c * 4;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u4_t d = xv[i];  // 8 consecutive 16-bit values: d.x = (x0,x1), d.y = (x2,x3), d.z = (x4,x5), d.w = (x6,x7)
+        if (xdt == RK_BF16) {
+            // bf16 -> fp32 (exact, summed) -> fp16 (round to nearest even) pairs
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t v = d[e];
+                f[2 * e] = __builtin_bit_cast(float, v << 16);
+                f[2 * e + 1] = __builtin_bit_cast(float, v & 0xffff0000u);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += f[e];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h2_t p;
+                p.x = (_Float16)f[e];
+                p.y = (_Float16)f[e + 4];
+                xp[4 * i + e] = as_u32(p);
+            }
+        } else {
+            xp[4 * i + 0] = perm(d.z, d.x, 0x05040100u);  // (x0, x4)
+            xp[4 * i + 1] = perm(d.z, d.x, 0x07060302u);  // (x1, x5)
+            xp[4 * i + 2] = perm(d.w, d.y, 0x05040100u);  // (x2, x6)
+            xp[4 * i + 3] = perm(d.w, d.y, 0x07060302u);  // (x3, x7)
+            const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s = dot2(as_h2(d[e]), one, s);
+        }
+    }
+    xs = s;
+}
+
+// Dot of one 16-byte code chunk (32 codes) with its x pairs. SUBN: returns sum(code * x) * 2^-24.
+template <bool SUBN>
+RK_DEV float chunk_dot(u4_t w, const uint32_t (&xp)[16]) {
+    if constexpr (SUBN) {
+        float lo = 0.f, hi = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = w[i], b = a >> 8;
+            lo = dot2(as_h2(a & 0x000F000Fu), as_h2(xp[4 * i + 0]), lo);
+            hi = dot2(as_h2(a & 0x00F000F0u), as_h2(xp[4 * i + 1]), hi);
+            lo = dot2(as_h2(b & 0x000F000Fu), as_h2(xp[4 * i + 2]), lo);
+            hi = dot2(as_h2(b & 0x00F000F0u), as_h2(xp[4 * i + 3]), hi);
+        }
+        return __builtin_fmaf(hi, 0.0625f, lo);  // hi holds 16 * code * 2^-24 * x
+    } else {
+        const h2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+        const h2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const h2_t m64 = {(_Float16)-64.f, (_Float16)-64.f};
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = w[i], b = a >> 8;
+            h2_t c04 = as_h2((a & 0x000F000Fu) | 0x64006400u) + m1024;
+            h2_t c15 = as_h2((a & 0x00F000F0u) | 0x64006400u) * s16 + m64;
+            h2_t c26 = as_h2((b & 0x000F000Fu) | 0x64006400u) + m1024;
+            h2_t c37 = as_h2((b & 0x00F000F0u) | 0x64006400u) * s16 + m64;
+            acc0 = dot2(c04, as_h2(xp[4 * i + 0]), acc0);
+            acc1 = dot2(c15, as_h2(xp[4 * i + 1]), acc1);
+            acc0 = dot2(c26, as_h2(xp[4 * i + 2]), acc0);
+            acc1 = dot2(c37, as_h2(xp[4 * i + 3]), acc1);
+        }
+        return acc0 + acc1;
+    }
+}
+
+template <int R, int KS, int NJ, bool SUBN>
+__global__ __launch_bounds__(kMaxThreads) void gemv_int4_kernel(const void* __restrict__ x, int xdt,
+                                                                const uint8_t* __restrict__ q,
+                                                                const uint16_t* __restrict__ sc,
+                                                                const uint16_t* __restrict__ mn,
+                                                                void* __restrict__ y, int ydt, int N, int K) {
+    __shared__ float red[kMaxThreads / 64][R];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int team = wave / KS;
+    const int kw = wave - team * KS;
+    const int teams = blockDim.x / (64 * KS);
+    const int t = kw * 64 + lane;
+    const int nch = K >> 5;
+    const int ng = K >> 7;
+    const int row0 = (blockIdx.x * teams + team) * R;  // teams past N (last block only) clamp and store nothing
+
+    const float sfold = SUBN ? 16777216.0f : 1.0f;  // 2^24 undoes the subnormal encoding of the codes
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+    // K is walked in passes of 64*KS*NJ chunks (one pass whenever the plan allows it)
+    for (int c0 = 0; c0 < nch; c0 += 64 * KS * NJ) {
+        // ---- loads first: R rows x NJ chunks of codes, then their scales / mins (all independent, all in flight)
+        u4_t w[R][NJ];
+        uint16_t s16[R][NJ], m16[R][NJ];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, N - 1);  // rows past N re-read the last row; their result is dropped
+            const u4_t* qr = reinterpret_cast<const u4_t*>(q + (size_t)row * (size_t)(K >> 1));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int c = c0 + t + j * 64 * KS;
+                if (c < nch) w[r][j] = __builtin_nontemporal_load(qr + c);
+                else w[r][j] = u4_t{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, N - 1);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int c = c0 + t + j * 64 * KS;
+                const size_t gi = (size_t)row * ng + (c >> 2);
+                if (c < nch) { s16[r][j] = sc[gi]; m16[r][j] = mn[gi]; }
+                else { s16[r][j] = 0; m16[r][j] = 0; }
+            }
+        }
+
+        // ---- x chunks (from L2: the same small vector for every wave)
+        uint32_t xp[NJ][16];
+        float xs[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int c = c0 + t + j * 64 * KS;
+            if (c < nch) {
+                load_x_chunk(x, xdt, c, xp[j], xs[j]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) xp[j][e] = 0u;
+                xs[j] = 0.f;
+            }
+        }
+
+        // ---- dequant + dot + group affine
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float a = acc[r];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const float d = chunk_dot<SUBN>(w[r][j], xp[j]);
+                const float sv = f16_bits_to_f32(s16[r][j]) * sfold;
+                const float mv = f16_bits_to_f32(m16[r][j]);
+                a = __builtin_fmaf(d, sv, __builtin_fmaf(mv, xs[j], a));
+            }
+            acc[r] = a;
+        }
+    }
+
+    // ---- reduce over the wave, then over the KS waves of the team
+    wave_reduce_rows<R>(acc);
+    const bool writer = (lane & (64 / R - 1)) == 0;
+    const int rr = row_of_lane<R>(lane);
+    if constexpr (KS == 1) {
+        if (writer && row0 + rr < N) store_act(y, ydt, (size_t)(row0 + rr), acc[0]);
+    } else {
+        if (writer) red[wave][rr] = acc[0];
+        __syncthreads();
+        if (kw == 0 && lane < R && row0 + lane < N) {
+            float v = 0.f;
+#pragma unroll
+            for (int k = 0; k < KS; ++k) v += red[team * KS + k][lane];
+            store_act(y, ydt, (size_t)(row0 + lane), v);
+        }
+    }
+}
+
+template <int R, int KS, int NJ, bool SUBN>
+hipError_t launch(const void* x, int xdt, const uint8_t* q, const uint16_t* s, const uint16_t* m, void* y, int ydt,
+                  int N, int K, int waves, hipStream_t st) {
+    const int teams = waves / KS;
+    const int rows_per_block = teams * R;
+    const int blocks = (N + rows_per_block - 1) / rows_per_block;
+    hipLaunchKernelGGL((gemv_int4_kernel<R, KS, NJ, SUBN>), dim3(blocks), dim3(waves * 64), 0, st, x, xdt, q, s, m,
+                       y, ydt, N, K);
+    return hipGetLastError();
+}
+
+template <int R, int KS, bool SUBN>
+hipError_t by_nj(int nj, const void* x, int xdt, const uint8_t* q, const uint16_t* s, const uint16_t* m, void* y,
+                 int ydt, int N, int K, int waves, hipStream_t st) {
+    switch (nj) {
+        case 1: return launch<R, KS, 1, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 2: return launch<R, KS, 2, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 3: return launch<R, KS, 3, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 4: return launch<R, KS, 4, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int R, bool SUBN>
+hipError_t by_ks(int ks, int nj, const void* x, int xdt, const uint8_t* q, const uint16_t* s, const uint16_t* m,
+                 void* y, int ydt, int N, int K, int waves, hipStream_t st) {
+    switch (ks) {
+        case 1: return by_nj<R, 1, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 2: return by_nj<R, 2, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 4: return by_nj<R, 4, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 8: return by_nj<R, 8, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+// Launch plan for one call (host side). Returns RK_OK or RK_ERR_BLOCK / RK_ERR_SHAPE.
+struct Int4Plan {
+    int waves, rows, ks, nj;
+};
+
+static int plan_int4(int N, int K, int waves, int rows, Int4Plan* p) {
+    const int nch = K / 32;
+    // tuned defaults: short rows (K <= 4096) are handled by one wave per row set; long rows are split over 4 waves
+    int w = waves ? waves : 4;
+    int r = rows ? rows : (nch <= 128 ? 4 : 2);
+    if (!(w == 1 || w == 2 || w == 4 || w == 8 || w == 16)) return RK_ERR_BLOCK;
+    if (!(r == 1 || r == 2 || r == 4 || r == 8)) return RK_ERR_BLOCK;
+    int ks = nch <= 128 ? 1 : 4;
+    while (ks < 8 && (nch + 64 * ks - 1) / (64 * ks) > 4) ks *= 2;
+    if (ks > w) ks = w;  // a small explicit block splits K over all of its waves
+    int nj = (nch + 64 * ks - 1) / (64 * ks);
+    if (nj > 4) nj = 4;  // longer rows take several passes over K
+    p->waves = w;
+    p->rows = r;
+    p->ks = ks;
+    p->nj = nj;
+    (void)N;
+    return RK_OK;
+}
+
+extern "C" int rk_gemv_int4_g128_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                                      const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                                      int subn, rk_stream_t stream) {
+    if (!x || !q || !scale || !min || !y) return RK_ERR_NULL;
+    if (N <= 0 || K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
+    if (x_dtype != RK_F16 && x_dtype != RK_BF16) return RK_ERR_DTYPE;
+    if (y_dtype != RK_F16 && y_dtype != RK_BF16 && y_dtype != RK_F32) return RK_ERR_DTYPE;
+    if (((uintptr_t)x & 15) || ((uintptr_t)q & 15)) return RK_ERR_ALIGN;
+    Int4Plan p;
+    int st = plan_int4(N, K, waves, rows, &p);
+    if (st != RK_OK) return st;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (subn) {
+        switch (p.rows) {
+            case 1: e = by_ks<1, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+            case 2: e = by_ks<2, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+            case 4: e = by_ks<4, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+            default: e = by_ks<8, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+        }
+    } else {
+        switch (p.rows) {
+            case 1: e = by_ks<1, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+            case 2: e = by_ks<2, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+            case 4: e = by_ks<4, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+            default: e = by_ks<8, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+        }
+    }
+    return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}

@@ -1,0 +1,88 @@
+"""ctypes binding of librumik_hip.so (the C ABI in include/rumik_hip.h).
+
+torch is imported first on purpose: its bundled HIP runtime carries the SONAME libamdhip64.so.7, so the dynamic
+linker binds the library to that same runtime and torch's streams and device pointers are valid inside it.
+There is no fallback: if the library is missing, every call raises.
+"""
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "librumik_hip.so"
+
+F16, BF16, F32 = 0, 1, 2
+Q_S8, Q_U8 = 0, 1
+DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+
+_p, _i, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+_SIGS = {
+    "rk_abi_version": ([], _i),
+    "rk_status_string": ([_i], ctypes.c_char_p),
+    "rk_gemv_int4_g128": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_gemv_int4_g128_mfma": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_gemv_int4_g128_valu": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_gemv_int4_g128_subn": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_gemv_int8_rows": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _p], _i),
+    "rk_gemv_int8_rows_ex": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_mm_int4_g128": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_embed_ln": ([_p, _p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
+    "rk_add_ln": ([_p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
+    "rk_post": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
+    "rk_attn_split": ([_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p], _i),
+    "rk_attn_combine": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _p], _i),
+    "rk_pos_advance": ([_p, _p], _i),
+    "rk_silu_mul": ([_p, _p, _i, _i, _p], _i),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (loaded once; raises RuntimeError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python rumik-fast_amd/build.py` (or "
+                               "__graft_entry__.build()) first; there is no non-HIP fallback")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, ret) in _SIGS.items():
+            fn = getattr(L, name, None)
+            if fn is None:
+                continue
+            fn.argtypes, fn.restype = args, ret
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    """Names the C ABI declares, for the load/export check."""
+    return list(_SIGS)
+
+
+def check(status: int, what: str = ""):
+    if status != 0:
+        msg = lib().rk_status_string(status).decode()
+        raise RuntimeError(f"{what}: {msg}" if what else msg)
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def dt(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {t.dtype}") from None
+
+
+def stream(device: torch.device | None = None):
+    """The current torch stream of `device` as a raw hipStream_t (so calls are graph-capturable)."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu(*ts: torch.Tensor):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("rumik HIP kernels need GPU tensors (there is no CPU path)")

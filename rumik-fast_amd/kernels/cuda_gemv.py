@@ -1,0 +1,87 @@
+"""Batch-1 GEMVs of the decode step on MI355X: drop-in for the reference's kernels/cuda_gemv.py.
+
+Same names and arguments as the reference module (kernels/cuda_gemv.py:222-249): gemv_int4_cuda, gemv_int8_cuda,
+quantize_int8_rows and the SHAPE table, so engine/rumik_fused.py:9 can import them unchanged. The work is done by
+hand-written gfx950 kernels in librumik_hip.so (csrc/gemv_int4.hip, csrc/gemv_int8.hip), launched on the current
+torch stream with no allocation when `out` is given, so the calls can be captured in a hipGraph.
+
+Differences from the reference, all widening what is accepted:
+  * x may be fp16 or bf16 (the reference reads bf16 only); y is x's dtype unless `out` says otherwise
+    (for the reference's bf16 x that is bf16, as before); out may also be fp32;
+  * any N (the reference needs N % (warps*rows) == 0) and, for int8, any K % 16 == 0 (reference: K % 512 == 0);
+  * int8 codes may be the reference's uint8 = int8 + 128 or plain int8; the row scale fp32 or fp16.
+Errors keep the reference's messages: RuntimeError("shape"), RuntimeError("unsupported block shape").
+"""
+import torch
+
+try:
+    from . import _hiplib as H
+except ImportError:  # imported with this directory on sys.path, as the reference engine does
+    import _hiplib as H
+
+G = 128
+
+# block shape (waves per block, rows per wave) per (N, K); an empty table means the library's tuned defaults.
+# Same role as the reference's SHAPE (kernels/cuda_gemv.py:222-223).
+SHAPE = {}
+
+
+def _check_int4(x, q, s, m, y):
+    H.require_gpu(x, q, s, m, y)
+    if q.dim() != 2 or q.dtype != torch.uint8:
+        raise RuntimeError("shape")
+    N, K = q.shape[0], q.shape[1] * 2
+    if K % G or x.numel() != K or y.numel() < N:
+        raise RuntimeError("shape")
+    if s.dtype != torch.float16 or m.dtype != torch.float16 or s.numel() != N * (K // G) or m.numel() != N * (K // G):
+        raise RuntimeError("shape")
+    for t in (x, q, s, m, y):
+        if not t.is_contiguous():
+            raise RuntimeError("shape")
+    return N, K
+
+
+def gemv_int4_cuda(x, q, s, m, out=None, warps=None, rows=None):
+    """int4 g128 GEMV: x [K] (fp16/bf16) -> y [N] = dequant(q, s, m) @ x, fp32 accumulation.
+    Reference contract: kernels/cuda_gemv.py:226-231 (x bf16 [K] -> y bf16 [N])."""
+    y = out if out is not None else torch.empty(q.shape[0], device=x.device, dtype=x.dtype)
+    N, K = _check_int4(x, q, s, m, y)
+    w, r = SHAPE.get((N, K), (0, 0))
+    st = H.lib().rk_gemv_int4_g128(H.ptr(x), H.dt(x), H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(y), H.dt(y), N, K,
+                                   int(warps or w), int(rows or r), H.stream(x.device))
+    H.check(st)
+    return y
+
+
+def quantize_int8_rows(w, pad_to=16):
+    """[N, K] -> (uint8 [N', K] = int8 + 128, fp32 scale [N']), rows zero-padded to a multiple of pad_to.
+    Symmetric per row: w ~ (q - 128) * scale, scale = max|w| / 127 (reference kernels/cuda_gemv.py:234-242)."""
+    n, k = w.shape
+    n_pad = -(-n // pad_to) * pad_to
+    wf = torch.zeros(n_pad, k, device=w.device, dtype=torch.float32)
+    wf[:n] = w.float()
+    scale = torch.clamp(wf.abs().amax(dim=1) / 127.0, min=1e-8)
+    codes = torch.clamp(torch.round(wf / scale[:, None]), -127, 127)
+    return (codes + 128).to(torch.uint8).contiguous(), scale.contiguous()
+
+
+def gemv_int8_cuda(x, q, s, out=None):
+    """int8 per-row GEMV: x [K] -> y [N] = s * (codes @ x). codes are uint8 = int8 + 128 (reference layout) or
+    int8. y defaults to bf16 as in the reference (kernels/cuda_gemv.py:245-249); pass an fp32 `out` for logits."""
+    y = out if out is not None else torch.empty(q.shape[0], device=x.device, dtype=torch.bfloat16)
+    H.require_gpu(x, q, s, y)
+    if q.dim() != 2 or q.dtype not in (torch.uint8, torch.int8):
+        raise RuntimeError("shape")
+    N, K = q.shape
+    if x.numel() != K or s.numel() != N or y.numel() < N or K % 16:
+        raise RuntimeError("shape")
+    if s.dtype not in (torch.float32, torch.float16):
+        raise RuntimeError("unsupported dtype")
+    for t in (x, q, s, y):
+        if not t.is_contiguous():
+            raise RuntimeError("shape")
+    kind = H.Q_U8 if q.dtype == torch.uint8 else H.Q_S8
+    st = H.lib().rk_gemv_int8_rows(H.ptr(x), H.dt(x), H.ptr(q), kind, H.ptr(s), H.dt(s), H.ptr(y), H.dt(y), N, K,
+                                   H.stream(x.device))
+    H.check(st)
+    return y

@@ -1,0 +1,90 @@
+"""The whole decode step (config 4) on the GPU vs the CPU oracle's decode_step (oracle/glue.py), from identical
+seeded weights, KV cache and token, over several consecutive steps (pos advances on the device), eagerly and as a
+replayed hipGraph. State is compared after every step (the reference's state-cloning check pattern,
+engine/check_fused.py:20-34).
+
+Tolerances: every activation is stored in fp16 and the step chains ~8 kernels per layer, so results are compared by
+norm-relative error / cosine: hidden state and logits within 1e-2 / 0.9999 per step on the small model and on the
+full-width model (4 layers of the 36-layer shape; each layer is the same computation).
+"""
+import numpy as np
+import pytest
+import torch
+
+import decode
+from oracle import glue as OG
+from oracle import int4 as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _oracle_model(cfg, w):
+    n = lambda t: t.cpu().numpy()  # noqa: E731
+    cos, sin = OG.rope_tables(cfg.S, cfg.HD, cfg.rope_theta)
+    return OG.DecodeModel(
+        L=cfg.L, H=cfg.H, NH=cfg.NH, NKV=cfg.NKV, HD=cfg.HD, inter=cfg.inter, eps=cfg.eps,
+        w_in=[tuple(map(n, t)) for t in w["w_in"]], w_o=[tuple(map(n, t)) for t in w["w_o"]],
+        w_down=[tuple(map(n, t)) for t in w["w_down"]], ln=[n(t) for t in w["ln"]], norm=n(w["norm"]),
+        emb=(n(w["emb"][0]), n(w["emb"][1])), head=(n(w["head"][0]), n(w["head"][1])),
+        rope=(cos.astype(np.float16).astype(np.float32), sin.astype(np.float16).astype(np.float32)),
+        sliding=cfg.sliding)
+
+
+def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2):
+    w = decode.random_weights(cfg, seed, device="cpu", gen_device="cpu")
+    wd = {k: ([tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for v in vv]
+              if isinstance(vv, list) else (tuple(t.to(dev) for t in vv) if isinstance(vv, tuple) else vv.to(dev)))
+          for k, vv in w.items()}
+    eng = decode.DecodeStep(cfg, wd, device=dev)
+    g = torch.Generator().manual_seed(seed + 1)
+    kc = torch.zeros(cfg.L, cfg.NKV, cfg.S, cfg.HD, dtype=torch.float16)
+    kc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).half()
+    vc = torch.zeros_like(kc)
+    vc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).half()
+    eng.kc.copy_(kc.to(dev))
+    eng.vc.copy_(vc.to(dev))
+    tok = 7
+    eng.set_state(tok, ctx)
+    if use_graph:
+        eng.capture()
+    md = _oracle_model(cfg, w)
+    okc, ovc = kc.numpy().copy(), vc.numpy().copy()
+    reps = []
+    for s in range(steps):
+        pos = ctx + s
+        eng.replay() if use_graph else eng.step()
+        torch.cuda.synchronize()
+        logits, h, x = OG.decode_step(md, tok, pos, okc, ovc)
+        assert int(eng.pos.item()) == pos + 1
+        rx = O.parity_report(_np(eng.x), x)
+        rl = O.parity_report(_np(eng.logits), logits)
+        reps.append((rx, rl))
+        assert rx["norm_rel"] < tol and rx["cosine"] > 0.9999, (s, rx)
+        assert rl["norm_rel"] < tol and rl["cosine"] > 0.9999, (s, rl)
+        # this step's K/V were written at slot pos of every layer
+        np.testing.assert_allclose(_np(eng.vc[:, :, pos]), ovc[:, :, pos].astype(np.float32), rtol=1e-2, atol=1e-2)
+        # continue from the oracle's own state for the next step, so errors do not compound across steps
+        eng.x.copy_(torch.tensor(x).half().to(dev))
+        eng.kc[:, :, pos].copy_(torch.tensor(okc[:, :, pos]).to(dev))
+        eng.vc[:, :, pos].copy_(torch.tensor(ovc[:, :, pos]).to(dev))
+    return reps
+
+
+SMALL = dict(L=3, H=256, NH=4, NKV=2, HD=128, inter=384, S=64, n_audio=100, vocab=50, nsplit=8)
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_small_model_steps(use_graph, dev):
+    cfg = decode.Config(**SMALL)
+    reps = _run(cfg, dev, ctx=5, steps=4, use_graph=use_graph)
+    print(reps[-1])
+
+
+def test_full_width_four_layers(dev):
+    cfg = decode.Config(L=4, vocab=64)
+    reps = _run(cfg, dev, ctx=300, steps=2, use_graph=True)
+    print(reps[-1])

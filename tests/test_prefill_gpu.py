@@ -1,0 +1,125 @@
+"""int4 prefill matmul (config 3) on the GPU vs the CPU oracle X @ dequantize(W)^T in fp32
+(reference kernels/mm_int4.py:92-106 checks the same product with a norm-relative error).
+Bar: max relative error <= 1e-2 with the per-output floor max(2^-14, 256 u32 sum_k |X_mk w_nk|), cosine >= 0.9999."""
+import numpy as np
+import pytest
+import torch
+
+import cuda_gemv
+import mm_int4
+import synth
+import _hiplib as H
+from oracle import int4 as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _ref(X, q, s, m):
+    a = (_np(X), q.cpu().numpy(), s.cpu().numpy(), m.cpu().numpy())
+    return O.mm_int4(*a), O.cond_floor(O.mm_int4_abs(*a))
+
+
+def _check(Y, ref, label=""):
+    rep = O.parity_report(_np(Y), *ref)
+    assert rep["max_rel"] <= 1e-2 and rep["cosine"] >= 0.9999, f"{label} {rep}"
+    return rep
+
+
+@pytest.mark.parametrize("N,K", [(3072, 2048), (22016, 2048), (2048, 11008)])
+@pytest.mark.parametrize("M", [34, 128])
+def test_config3_shapes(M, N, K, dev):
+    X, q, s, m = synth.prefill_case(M, N, K, 3)
+    Y = mm_int4.mm_int4(X.to(dev), q.to(dev), s.to(dev), m.to(dev))
+    assert Y.shape == (M, N) and Y.dtype == torch.float16
+    rep = _check(Y, _ref(X, q, s, m), f"M={M} N={N} K={K}")
+    print(f"M={M} N={N} K={K}: {rep}")
+
+
+def test_config3_m512(dev):
+    X, q, s, m = synth.prefill_case(512, 3072, 2048, 3)
+    Y = mm_int4.mm_int4(X.to(dev), q.to(dev), s.to(dev), m.to(dev))
+    _check(Y, _ref(X, q, s, m), "M=512")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (3, 17, 256), (17, 100, 384), (33, 48, 2048), (65, 129, 1152),
+                                   (200, 33, 11008)])
+def test_ragged(M, N, K, dev):
+    X, q, s, m = synth.prefill_case(M, N, K, 4)
+    Y = mm_int4.mm_int4(X.to(dev), q.to(dev), s.to(dev), m.to(dev))
+    _check(Y, _ref(X, q, s, m), f"M={M} N={N} K={K}")
+
+
+def test_bf16_and_fp32_out(dev):
+    X, q, s, m = synth.prefill_case(40, 256, 2048, 5)
+    Xb = X.bfloat16()
+    Y = mm_int4.mm_int4(Xb.to(dev), q.to(dev), s.to(dev), m.to(dev))
+    assert Y.dtype == torch.bfloat16
+    _check(Y, _ref(Xb, q, s, m), "bf16")
+    Y32 = torch.empty(40, 256, device=dev, dtype=torch.float32)
+    mm_int4.mm_int4(Xb.to(dev), q.to(dev), s.to(dev), m.to(dev), out=Y32)
+    _check(Y32, _ref(Xb, q, s, m), "fp32 out")
+
+
+def test_rows_match_gemv(dev):
+    # row m of the prefill product is the batch-1 GEMV of X[m] (both within the bar of the same oracle)
+    X, q, s, m = (t.to(dev) for t in synth.prefill_case(9, 3072, 2048, 6))
+    Y = mm_int4.mm_int4(X, q, s, m, out=torch.empty(9, 3072, device=dev, dtype=torch.float32))
+    for i in range(9):
+        y = torch.empty(3072, device=dev, dtype=torch.float32)
+        cuda_gemv.gemv_int4_cuda(X[i].contiguous(), q, s, m, out=y)
+        np.testing.assert_allclose(_np(Y[i]), _np(y), rtol=1e-4, atol=2e-5)
+
+
+def test_strided_rows_through_c_abi(dev):
+    # X rows with a stride larger than K (a view into a wider buffer), Y with a padded row stride
+    M, N, K = 20, 96, 512
+    X, q, s, m = synth.prefill_case(M, N, K, 7)
+    Xw = torch.zeros(M, K + 64, dtype=torch.float16)
+    Xw[:, :K] = X
+    Xd, qd, sd, md = Xw.to(dev), q.to(dev), s.to(dev), m.to(dev)
+    Yw = torch.full((M, N + 16), 7.0, device=dev, dtype=torch.float32)
+    H.check(H.lib().rk_mm_int4_g128(H.ptr(Xd), H.F16, K + 64, H.ptr(qd), H.ptr(sd), H.ptr(md), H.ptr(Yw), H.F32,
+                                    N + 16, M, N, K, H.stream(dev)))
+    torch.cuda.synchronize()
+    _check(Yw[:, :N], _ref(X, q, s, m), "strided")
+    assert torch.all(Yw[:, N:] == 7.0)  # nothing written outside the [M, N] window
+
+
+def test_min_term_known_answer(dev):
+    M, N, K = 37, 80, 2048
+    X = torch.ones(M, K, dtype=torch.float16, device=dev)
+    q = torch.zeros(N, K // 2, dtype=torch.uint8, device=dev)
+    s = (torch.rand(N, K // 128, device=dev) * 0.02 + 0.001).half()
+    m = torch.ones(N, K // 128, dtype=torch.float16, device=dev)
+    Y = mm_int4.mm_int4(X, q, s, m, out=torch.empty(M, N, device=dev, dtype=torch.float32))
+    assert torch.equal(Y.cpu(), torch.full((M, N), float(K)))
+
+
+def test_errors_and_knobs(dev):
+    X, q, s, m = (t.to(dev) for t in synth.prefill_case(4, 32, 256, 8))
+    mm_int4.mm_int4(X, q, s, m, BM=16, BN=128, num_warps=8, num_stages=2)  # Triton knobs accepted
+    with pytest.raises(AssertionError):
+        mm_int4.mm_int4(X[:, :128], q, s, m)
+    with pytest.raises(AssertionError):
+        mm_int4.mm_int4(X, q, s, m, BN=0)
+
+
+def test_warmup_and_graph(dev):
+    mm_int4.warmup([(64, 256)])
+    X, q, s, m = (t.to(dev) for t in synth.prefill_case(34, 512, 2048, 9))
+    Y = torch.empty(34, 512, device=dev, dtype=torch.float16)
+    mm_int4.mm_int4(X, q, s, m, out=Y)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        mm_int4.mm_int4(X, q, s, m, out=Y)
+    for i in range(3):
+        X.copy_(synth.prefill_case(34, 512, 2048, 20 + i)[0].to(dev))
+        Y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        _check(Y, _ref(X.cpu(), q.cpu(), s.cpu(), m.cpu()), f"replay {i}")

@@ -126,6 +126,60 @@ int rk_attn_combine(const float* po, const float* pm, const float* pl, const int
  * fused.post (reference engine/fused.py:76-84), used between the gate/up and down projections. */
 int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------------------------
+ * The whole decode step in one persistent launch (no reference counterpart as a single kernel: it replaces the
+ * ~260 launches of RumikFused._step, engine/rumik_fused.py:97-121, plus the audio head of _logits, :84-89).
+ * Hidden size 2048 and head dim 128 are fixed; NH * 128 == 2048; NH / NKV in {1, 2, 4, 8}; inter % 128 == 0 and
+ * inter <= 11008. Weights are stacked over layers; w_in rows are [q | k | v | then per 8 channels: 8 gate rows,
+ * 8 up rows] (the reference's q/k/v/gate/up concatenation, gate and up interleaved by 8 at load time).
+ * nblocks = NKV * nsp, one block per CU (256 on MI355X), each owning ceil(2048 / nblocks) <= 8 rows of w_o / w_down.
+ * Workspace: flags [nblocks * 32] (one 128-byte line per block), status and grp_ctr [NKV] must start at zero.
+ * status bit 1 = a grid barrier waited longer than 200 ms (the step then finishes early with garbage; reset status);
+ * bit 2 = pos outside [0, S) (nothing is computed or written, pos is not advanced).
+ * ------------------------------------------------------------------------------------------------------------ */
+typedef struct rk_decode_params {
+    int L, NH, NKV, inter, S, n_audio, nsp;
+    float eps, scale;
+    unsigned long long sliding; /* bit l set: RoPE on layer l */
+    const int64_t* tok;
+    int64_t* pos;
+    const int8_t* emb_q;    /* [vocab, 2048] */
+    const uint16_t* emb_s;  /* [vocab] fp16 */
+    const uint8_t* win_q;   /* [L, n_in, 1024] */
+    const uint16_t* win_s;  /* [L, n_in, 16] */
+    const uint16_t* win_m;
+    const uint8_t* wo_q;    /* [L, 2048, NH*64] */
+    const uint16_t* wo_s;
+    const uint16_t* wo_m;
+    const uint8_t* wd_q;    /* [L, 2048, inter/2] */
+    const uint16_t* wd_s;
+    const uint16_t* wd_m;
+    const uint16_t* ln_w;   /* [L, 2048] fp16 */
+    const uint16_t* norm_w; /* [2048] */
+    const uint16_t* cos_t;  /* [S, 128] fp16 */
+    const uint16_t* sin_t;
+    uint16_t* kc;           /* [L, NKV, S, 128] fp16 */
+    uint16_t* vc;
+    const int8_t* head_q;   /* [n_audio, 2048] */
+    const uint16_t* head_s; /* [n_audio] fp16 */
+    float* logits;          /* [n_audio] */
+    uint16_t* x;            /* [2048] residual stream (workspace) */
+    uint16_t* qbuf;         /* [NH*128] */
+    uint16_t* act;          /* [inter] */
+    uint16_t* ob;           /* [NH*128] */
+    float* po;              /* [NH, nsp, 128] */
+    float* pm;              /* [NH, nsp] */
+    float* pl;
+    unsigned* grp_ctr;      /* [NKV] */
+    unsigned* flags;        /* [nblocks * 32] */
+    unsigned* status;
+} rk_decode_params;
+
+int rk_decode_step_persistent(const rk_decode_params* params, int nblocks, rk_stream_t stream);
+
+/* sizeof(rk_decode_params) as compiled (for bindings that build the struct by hand) */
+int rk_decode_params_size(void);
+
 /* pos[0] += 1 on the device (the `self.pos += 1` of the captured step, reference engine/rumik_fused.py:120). */
 int rk_pos_advance(int64_t* pos, rk_stream_t stream);
 

@@ -1,0 +1,86 @@
+// Exact int4 / int8 dequantization and small dot-product building blocks shared by the GEMV kernels, the prefill
+// and the persistent decode kernel.
+#pragma once
+
+#include "common.h"
+
+// A constant the optimizer cannot see through, materialized once in a VGPR. gfx9 VOP3 encodings take no literal
+// operands, so (a & mask) | bits with literal masks becomes v_and + v_or; with the masks in VGPRs the compiler
+// emits a single v_and_or_b32.
+RK_DEV uint32_t opaque_vgpr(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+struct Int4Masks {
+    uint32_t lo, hi, magic;
+};
+
+RK_DEV Int4Masks int4_masks() { return {opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)}; }
+
+// One dword of int4 codes (8 columns c0..c7, nibble i = column i) -> exact fp16 codes in the order
+// (c0,c4),(c1,c5),(c2,c6),(c3,c7): (w & 0x000F000F) | 0x64006400 is the fp16 pair (1024 + c0, 1024 + c4) (1024.0
+// has a mantissa LSB worth 1); a packed fp16 add of -1024 leaves the codes. The high nibbles give 1024 + 16c,
+// brought back by one exact packed fma (x 1/16, -64).
+RK_DEV void dequant_pairs(uint32_t w, const Int4Masks& k, h2_t (&p)[4]) {
+    const h2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    const h2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const h2_t m64 = {(_Float16)-64.f, (_Float16)-64.f};
+    const uint32_t b = w >> 8;
+    p[0] = as_h2((w & k.lo) | k.magic) + m1024;
+    p[1] = as_h2((w & k.hi) | k.magic) * s16 + m64;
+    p[2] = as_h2((b & k.lo) | k.magic) + m1024;
+    p[3] = as_h2((b & k.hi) | k.magic) * s16 + m64;
+}
+
+// the same as an MFMA B fragment (8 fp16)
+RK_DEV h8_t dequant_frag(uint32_t w, const Int4Masks& k) {
+    h2_t p[4];
+    dequant_pairs(w, k, p);
+    h8_t r;
+    r[0] = p[0].x; r[1] = p[0].y; r[2] = p[1].x; r[3] = p[1].y;
+    r[4] = p[2].x; r[5] = p[2].y; r[6] = p[3].x; r[7] = p[3].y;
+    return r;
+}
+
+// 8 consecutive fp16 activations (x0..x7) -> pairs (x0,x4),(x1,x5),(x2,x6),(x3,x7), matching dequant_pairs
+RK_DEV void pair_permute(u4_t d, uint32_t (&h)[4]) {
+    h[0] = perm(d.z, d.x, 0x05040100u);
+    h[1] = perm(d.z, d.x, 0x07060302u);
+    h[2] = perm(d.w, d.y, 0x05040100u);
+    h[3] = perm(d.w, d.y, 0x07060302u);
+}
+
+// sum(code * x) over one 16-byte chunk (32 codes) against its 16 permuted x pairs, fp32 accumulate (v_dot2)
+RK_DEV float chunk_dot_int4(u4_t w, const uint32_t* xp, const Int4Masks& k) {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h2_t p[4];
+        dequant_pairs(w[i], k, p);
+        a0 = dot2(p[0], as_h2(xp[4 * i + 0]), a0);
+        a1 = dot2(p[1], as_h2(xp[4 * i + 1]), a1);
+        a0 = dot2(p[2], as_h2(xp[4 * i + 2]), a0);
+        a1 = dot2(p[3], as_h2(xp[4 * i + 3]), a1);
+    }
+    return a0 + a1;
+}
+
+// sum(code * x) over one 16-byte chunk of int8 codes (16 columns) against natural fp16 pairs (x0,x1),(x2,x3)...
+// Each byte u is placed under 0x64 (fp16 1024 + u) by v_perm_b32; -1152 gives u - 128 exactly. SIGNED codes are
+// first mapped to u = b ^ 0x80.
+template <bool SIGNED>
+RK_DEV float chunk_dot_int8(u4_t w, const uint32_t* xp) {
+    const h2_t m1152 = {(_Float16)-1152.f, (_Float16)-1152.f};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t v = w[i];
+        if constexpr (SIGNED) v ^= 0x80808080u;
+        const h2_t c01 = as_h2(perm(0x64646464u, v, 0x04010400u)) + m1152;
+        const h2_t c23 = as_h2(perm(0x64646464u, v, 0x04030402u)) + m1152;
+        a0 = dot2(c01, as_h2(xp[2 * i]), a0);
+        a1 = dot2(c23, as_h2(xp[2 * i + 1]), a1);
+    }
+    return a0 + a1;
+}

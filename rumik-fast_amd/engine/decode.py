@@ -12,7 +12,7 @@ is int8 with a per-row scale; the token embedding is int8 with a per-row fp16 sc
 `pos` / `tok` live on the GPU, so one captured hipGraph replays the step at every position
 (reference engine/rumik_int4.py:225-248). The sampler after the head is outside this path.
 """
-import math
+import ctypes
 import sys
 from pathlib import Path
 
@@ -21,6 +21,7 @@ import torch
 sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "kernels"))
 import cuda_gemv  # noqa: E402
 import synth  # noqa: E402
+import _hiplib as HL  # noqa: E402
 import fused  # noqa: E402
 
 
@@ -144,3 +145,119 @@ class DecodeStep:
 
     def replay(self):
         self.graph.replay()
+
+
+# ---------------------------------------------------------------------------------------------- one-launch step
+class RkDecodeParams(ctypes.Structure):
+    """ctypes mirror of rk_decode_params (include/rumik_hip.h); its size is checked against the library."""
+    _fields_ = [(n, ctypes.c_int) for n in ("L", "NH", "NKV", "inter", "S", "n_audio", "nsp")] + [
+        ("eps", ctypes.c_float), ("scale", ctypes.c_float), ("sliding", ctypes.c_ulonglong)] + [
+        (n, ctypes.c_void_p) for n in (
+            "tok", "pos", "emb_q", "emb_s", "win_q", "win_s", "win_m", "wo_q", "wo_s", "wo_m", "wd_q", "wd_s", "wd_m",
+            "ln_w", "norm_w", "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "x", "qbuf", "act", "ob",
+            "po", "pm", "pl", "grp_ctr", "flags", "status")]
+
+
+def interleave_gate_up(t, cfg):
+    """Reorder w_in rows (or their scale / min rows) [q | k | v | gate | up] -> [q | k | v | (gate 8, up 8) ...]:
+    the persistent kernel computes silu(gate) * up in the epilogue of a 16-row tile holding both."""
+    a = (cfg.NH + 2 * cfg.NKV) * cfg.HD
+    g, u = t[a:a + cfg.inter], t[a + cfg.inter:]
+    gu = torch.stack([g.reshape(cfg.inter // 8, 8, -1), u.reshape(cfg.inter // 8, 8, -1)], 1)
+    return torch.cat([t[:a], gu.reshape(2 * cfg.inter, -1)]).contiguous()
+
+
+class PersistentDecode:
+    """The decode step as one persistent kernel launch (csrc/decode_persistent.hip). Same weights, state and
+    outputs as DecodeStep; needs hidden 2048 and head dim 128. `weights` as from random_weights; they are
+    re-laid out (stacked over layers, gate / up interleaved) and the per-layer copies can then be dropped."""
+
+    def __init__(self, cfg: Config, weights, device="cuda", nblocks=None, keep_layer_weights=False):
+        if cfg.H != 2048 or cfg.HD != 128 or cfg.NH * cfg.HD != 2048:
+            raise ValueError("the persistent step is built for hidden 2048 / head dim 128")
+        self.cfg, self.dev = cfg, torch.device(device)
+        d = self.dev
+        if nblocks is None:
+            nblocks = torch.cuda.get_device_properties(d).multi_processor_count
+        nblocks -= nblocks % cfg.NKV
+        self.nblocks, self.nsp = nblocks, nblocks // cfg.NKV
+        lib = HL.lib()
+        if lib.rk_decode_params_size() != ctypes.sizeof(RkDecodeParams):
+            raise RuntimeError("rk_decode_params layout mismatch between the library and decode.py")
+        w = weights
+        self.win = [torch.stack([interleave_gate_up(t[k], cfg) for t in w["w_in"]]) for k in range(3)]
+        self.wo = [torch.stack([t[k] for t in w["w_o"]]) for k in range(3)]
+        self.wd = [torch.stack([t[k] for t in w["w_down"]]) for k in range(3)]
+        self.ln = torch.stack(w["ln"]).contiguous()
+        self.norm, self.emb, self.head = w["norm"], w["emb"], w["head"]
+        if not keep_layer_weights:
+            for k in ("w_in", "w_o", "w_down"):
+                w[k].clear()
+        f16, f32, i32 = torch.float16, torch.float32, torch.int32
+        c = cfg
+        self.x = torch.zeros(2048, dtype=f16, device=d)
+        self.qbuf = torch.zeros(c.NH * c.HD, dtype=f16, device=d)
+        self.act = torch.zeros(c.inter, dtype=f16, device=d)
+        self.ob = torch.zeros(c.NH * c.HD, dtype=f16, device=d)
+        self.po = torch.zeros(c.NH, self.nsp, c.HD, dtype=f32, device=d)
+        self.pm = torch.zeros(c.NH, self.nsp, dtype=f32, device=d)
+        self.pl = torch.zeros(c.NH, self.nsp, dtype=f32, device=d)
+        self.grp_ctr = torch.zeros(c.NKV, dtype=i32, device=d)
+        self.flags = torch.zeros(nblocks * 32, dtype=i32, device=d)  # one 128-byte line per block
+        self.status = torch.zeros(1, dtype=i32, device=d)
+        self.logits = torch.zeros(c.n_audio, dtype=f32, device=d)
+        self.kc = torch.zeros(c.L, c.NKV, c.S, c.HD, dtype=f16, device=d)
+        self.vc = torch.zeros_like(self.kc)
+        self.tok = torch.zeros(1, dtype=torch.int64, device=d)
+        self.pos = torch.zeros(1, dtype=torch.int64, device=d)
+        self.cos, self.sin = rope_tables(c.S, c.HD, c.rope_theta, f16, d)
+        sliding = sum(1 << i for i, on in enumerate(c.sliding) if on)
+        P = RkDecodeParams(L=c.L, NH=c.NH, NKV=c.NKV, inter=c.inter, S=c.S, n_audio=c.n_audio, nsp=self.nsp,
+                           eps=c.eps, scale=c.HD ** -0.5, sliding=sliding)
+        for name, t in (("tok", self.tok), ("pos", self.pos), ("emb_q", self.emb[0]), ("emb_s", self.emb[1]),
+                        ("win_q", self.win[0]), ("win_s", self.win[1]), ("win_m", self.win[2]),
+                        ("wo_q", self.wo[0]), ("wo_s", self.wo[1]), ("wo_m", self.wo[2]),
+                        ("wd_q", self.wd[0]), ("wd_s", self.wd[1]), ("wd_m", self.wd[2]),
+                        ("ln_w", self.ln), ("norm_w", self.norm), ("cos_t", self.cos), ("sin_t", self.sin),
+                        ("kc", self.kc), ("vc", self.vc), ("head_q", self.head[0]), ("head_s", self.head[1]),
+                        ("logits", self.logits), ("x", self.x), ("qbuf", self.qbuf), ("act", self.act),
+                        ("ob", self.ob), ("po", self.po), ("pm", self.pm), ("pl", self.pl),
+                        ("grp_ctr", self.grp_ctr), ("flags", self.flags), ("status", self.status)):
+            if not t.is_contiguous() or t.device != d:
+                raise RuntimeError(f"{name} must be a contiguous tensor on {d}")
+            setattr(P, name, t.data_ptr())
+        self.params = P
+        self.graph = None
+
+    def set_state(self, tok: int, pos: int):
+        self.tok.fill_(tok)
+        self.pos.fill_(pos)
+
+    def fill_cache(self, ctx: int, seed: int = 0):
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        self.kc[:, :, :ctx].normal_(generator=g)
+        self.vc[:, :, :ctx].normal_(generator=g)
+
+    def step(self):
+        HL.check(HL.lib().rk_decode_step_persistent(ctypes.byref(self.params), self.nblocks, HL.stream(self.dev)),
+                 "decode_step_persistent")
+
+    def capture(self):
+        saved = (self.x.clone(), self.kc.clone(), self.vc.clone(), self.pos.clone())
+        self.step()
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        torch.cuda.synchronize(self.dev)
+        self.x.copy_(saved[0]); self.kc.copy_(saved[1]); self.vc.copy_(saved[2]); self.pos.copy_(saved[3])
+        torch.cuda.synchronize(self.dev)
+        self.graph = g
+        return g
+
+    def replay(self):
+        self.graph.replay()
+
+    def status_word(self) -> int:
+        """0 when every grid barrier of every step so far completed in time."""
+        return int(self.status.item())

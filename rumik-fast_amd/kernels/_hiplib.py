@@ -33,6 +33,8 @@ _SIGS = {
     "rk_attn_combine": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _p], _i),
     "rk_pos_advance": ([_p, _p], _i),
     "rk_silu_mul": ([_p, _p, _i, _i, _p], _i),
+    "rk_decode_step_persistent": ([_p, _i, _p], _i),
+    "rk_decode_params_size": ([], _i),
 }
 
 _lib = None

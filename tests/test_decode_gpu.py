@@ -34,12 +34,12 @@ def _oracle_model(cfg, w):
         sliding=cfg.sliding)
 
 
-def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2):
+def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph"):
     w = decode.random_weights(cfg, seed, device="cpu", gen_device="cpu")
     wd = {k: ([tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for v in vv]
               if isinstance(vv, list) else (tuple(t.to(dev) for t in vv) if isinstance(vv, tuple) else vv.to(dev)))
           for k, vv in w.items()}
-    eng = decode.DecodeStep(cfg, wd, device=dev)
+    eng = decode.DecodeStep(cfg, wd, device=dev) if engine == "graph" else decode.PersistentDecode(cfg, wd, device=dev)
     g = torch.Generator().manual_seed(seed + 1)
     kc = torch.zeros(cfg.L, cfg.NKV, cfg.S, cfg.HD, dtype=torch.float16)
     kc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).half()
@@ -60,6 +60,8 @@ def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2):
         torch.cuda.synchronize()
         logits, h, x = OG.decode_step(md, tok, pos, okc, ovc)
         assert int(eng.pos.item()) == pos + 1
+        if engine == "persistent":
+            assert eng.status_word() == 0, "a grid barrier timed out"
         rx = O.parity_report(_np(eng.x), x)
         rl = O.parity_report(_np(eng.logits), logits)
         reps.append((rx, rl))
@@ -88,3 +90,18 @@ def test_full_width_four_layers(dev):
     cfg = decode.Config(L=4, vocab=64)
     reps = _run(cfg, dev, ctx=300, steps=2, use_graph=True)
     print(reps[-1])
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_persistent_full_width(use_graph, dev):
+    # the one-launch step: hidden 2048, 16 / 4 heads, MLP 11008, 3 layers (one of them NoPE), ctx 300
+    cfg = decode.Config(L=3, vocab=64, sliding=[True, False, True])
+    reps = _run(cfg, dev, ctx=300, steps=3, use_graph=use_graph, engine="persistent")
+    print(reps[-1])
+
+
+def test_persistent_small_mlp_and_ctx_edges(dev):
+    # inter 2048, contexts at the edges: first slot and the last slot of the cache
+    cfg = decode.Config(L=2, inter=2048, S=256, vocab=32, n_audio=1000)
+    _run(cfg, dev, ctx=0, steps=2, use_graph=True, engine="persistent")
+    _run(cfg, dev, ctx=254, steps=2, use_graph=False, engine="persistent")

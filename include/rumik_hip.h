@@ -133,7 +133,8 @@ int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_str
  * inter <= 11008. Weights are stacked over layers; w_in rows are [q | k | v | then per 8 channels: 8 gate rows,
  * 8 up rows] (the reference's q/k/v/gate/up concatenation, gate and up interleaved by 8 at load time).
  * nblocks = NKV * nsp, one block per CU (256 on MI355X), each owning ceil(2048 / nblocks) <= 8 rows of w_o / w_down.
- * Workspace: flags [nblocks * 32] (one 128-byte line per block), status and grp_ctr [NKV] must start at zero.
+ * Workspace: flags [nblocks * 32] words (arrival words, then a release word), status and grp_ctr [NKV] start at
+ * zero and are left consistent for the next call. The grid must be co-resident (checked: RK_ERR_BLOCK otherwise).
  * status bit 1 = a grid barrier waited longer than 200 ms (the step then finishes early with garbage; reset status);
  * bit 2 = pos outside [0, S) (nothing is computed or written, pos is not advanced).
  * ------------------------------------------------------------------------------------------------------------ */

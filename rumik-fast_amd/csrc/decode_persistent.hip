@@ -21,7 +21,9 @@
 // Cross-block data: everything one block writes for another within the step (q, K/V at pos, act, attention
 // partials and output, x) is stored with agent-scope atomic stores and read with agent-scope atomic loads, which
 // bypass the per-XCD (non-coherent) L2. A barrier is then only: wait for the block's stores to complete, publish an
-// epoch in the block's own flag word, and poll all flags — no L2 write-back / invalidate (measured ~9 us each).
+// epoch in the block's own arrival word; block 0 gathers the arrivals and publishes a release word the others poll
+// — no L2 write-back / invalidate (measured ~9 us each). The weights of each phase are issued before the barrier
+// in front of it, so they stream in while the block waits.
 // Every wait is bounded by wall-clock time: on timeout the kernel sets an abort bit in `status` and every later
 // barrier returns at once, so the grid always drains.
 #include "dequant.h"
@@ -36,7 +38,6 @@ constexpr int kNG = kH / 128;        // groups of a 2048-long row
 constexpr int kMaxRep = 8;
 constexpr uint64_t kBarrierTicks = 20000000ull;  // 200 ms at the 100 MHz wall clock
 constexpr unsigned kAbort = 1u, kTimeout = 2u, kBadPos = 4u;
-constexpr int kFlagStride = 32;  // one 128-byte line per block flag: polls spread over memory channels
 
 typedef rk_decode_params Params;
 
@@ -53,6 +54,13 @@ RK_DEV uint32_t ld_coh(const uint32_t* p) {
 RK_DEV float ld_coh_f(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+RK_DEV uint64_t ld_coh64(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+RK_DEV void st_coh64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+RK_DEV uint64_t pack_f2(float a, float b) {
+    return (uint64_t)__builtin_bit_cast(uint32_t, a) | ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
+}
 RK_DEV uint32_t pack_h2(float a, float b) {
     h2_t v;
     v.x = (_Float16)a;
@@ -61,41 +69,56 @@ RK_DEV uint32_t pack_h2(float a, float b) {
 }
 
 // ---------------------------------------------------------------------------------------------- grid barrier
-RK_DEV void grid_sync(const Params& p, unsigned epoch) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's coherent stores have completed
+// flags[b] holds the last barrier epoch block b arrived at; the release word after them (own 128-byte line) holds
+// the last epoch every block has reached. Block 0's first wave gathers the arrivals and publishes the release; the
+// other blocks poll only the release word (one line polled by all, measured faster than all-poll-all).
+RK_DEV int release_index(int nblocks) { return (nblocks + 31) & ~31; }
+
+RK_DEV bool wait_epoch(const uint32_t* w, unsigned epoch, const Params& p, uint64_t t0) {
+    while ((int)(ld_coh(w) - epoch) < 0) {
+        if (ld_coh(p.status) & kAbort) return false;
+        if (wall_clock64() - t0 > kBarrierTicks) {
+            atomicOr(p.status, kAbort | kTimeout);
+            return false;
+        }
+    }
+    return true;
+}
+
+// Arrival: every wave's coherent stores have completed (vmcnt counts loads too, so this comes before the next
+// phase's weight loads are issued), then the block publishes the epoch.
+RK_DEV void grid_arrive(const Params& p, unsigned epoch) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if (threadIdx.x == 0) st_coh(p.flags + blockIdx.x, epoch);
+}
+
+// Wait for the release of `epoch`, polled by wave 0 only: vector memory results return in issue order, so a wave
+// with weight loads in flight could not see the release before they land. Wave 0 issues its own share of the next
+// phase's loads after this returns.
+RK_DEV void grid_wait(const Params& p, unsigned epoch) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        if (lane == 0)
-            __hip_atomic_store(p.flags + blockIdx.x * kFlagStride, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint64_t t0 = wall_clock64();
-        while (true) {
-            bool ok = true;
-            for (int b = lane; b < (int)gridDim.x; b += 64)
-                ok = ok && (int)(__hip_atomic_load(p.flags + b * kFlagStride, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT) - epoch) >= 0;
-            if (__all(ok)) break;
-            if (__hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kAbort) break;
-            if (wall_clock64() - t0 > kBarrierTicks) {
-                if (lane == 0) atomicOr(p.status, kAbort | kTimeout);
-                break;
+        uint32_t* release = p.flags + release_index(gridDim.x);
+        if (blockIdx.x == 0) {
+            bool done = false;
+            while (!done) {  // every iteration has all of the lane's arrival words in flight at once
+                bool ok = true;
+                for (int b = lane; b < (int)gridDim.x; b += 64) ok &= (int)(ld_coh(p.flags + b) - epoch) >= 0;
+                done = __all(ok);
+                if (!done && (ld_coh(p.status) & kAbort)) break;
+                if (!done && wall_clock64() - t0 > kBarrierTicks) {
+                    if (lane == 0) atomicOr(p.status, kAbort | kTimeout);
+                    break;
+                }
             }
-            __builtin_amdgcn_s_sleep(1);
+            if (lane == 0 && done) st_coh(release, epoch);
+        } else if (lane == 0) {
+            wait_epoch(release, epoch, p, t0);
         }
     }
     __syncthreads();
-}
-
-// block-wide sum (every thread receives it); red: >= kWaves floats of LDS
-RK_DEV float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) t += red[i];
-    return t;
 }
 
 // ---------------------------------------------------------------------------------------------- LDS layout
@@ -104,78 +127,103 @@ struct Lds {
     float hsum[kNG];
     uint4 vecp[11008 / 8 + 8];  // permuted pairs of act (phase B) / ob (phase C) / natural pairs (head), per 8 cols
     float vsum[11008 / 32 + 8];
-    float red[16];
     float drow[kWaves];         // this block's down rows (phase B -> C)
     float xrow[kWaves];         // this block's rows of the residual stream (kept across layers)
     float s_m[kWaves][kMaxRep], s_l[kWaves][kMaxRep];
-    union {
-        float2 s_acc[kWaves][kMaxRep][64];  // the waves' partial attention outputs
-        struct {                            // then, in the combining block:
-            float cw[kMaxRep][256];         //   per-split weights exp(m_i - M)
-            float2 part[4][64];             //   per-quarter partial sums of one head
-        };
-    };
-    float cden[kMaxRep];
+    float2 s_acc[kWaves][kMaxRep][64];  // the waves' partial attention outputs; then the combine's partial sums
+    float c_m[kWaves], c_l[kWaves];     // the combine's per-wave running max / denominator
     int flag;
 };
 
-// LayerNorm of 2048 values held as 8-value blocks by threads 0..255 (v[8] each): h = round(LN(x) * w).
-RK_DEV void layernorm8(float (&v)[8], bool active, const uint16_t* w, float eps, float* red) {
-    float s = 0.f;
-    if (active)
+// x as held by wave 0 for its LayerNorm: lane holds the 8-column blocks i = lane + 64k, k < 4
+struct XWave {
+    float v[4][8];
+};
+
+RK_DEV void x_from_embedding(const Params& p, int64_t tok, XWave& xw) {
+    const int lane = threadIdx.x & 63;
+    const float es = h16(p.emb_s[tok]);
+    const uint2* er = reinterpret_cast<const uint2*>(p.emb_q + (size_t)tok * kH);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += v[e];
-    const float mean = block_sum(s, red) * (1.0f / kH);
-    float ss = 0.f;
-    if (active)
+    for (int k = 0; k < 4; ++k) {
+        const uint2 b = er[lane + 64 * k];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float d = v[e] - mean;
+            const int8_t c = (int8_t)(((e < 4 ? b.x : b.y) >> (8 * (e & 3))) & 0xFF);
+            xw.v[k][e] = rnd16((float)c * es);
+        }
+    }
+}
+
+// the residual stream written by all blocks (coherent loads)
+RK_DEV void x_load(const Params& p, XWave& xw) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t* xs = reinterpret_cast<const uint64_t*>(p.x);
+    uint64_t d[4][2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) d[k][h] = ld_coh64(xs + 2 * (lane + 64 * k) + h);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t b = (uint16_t)(d[k][e >> 2] >> (16 * (e & 3)));
+            xw.v[k][e] = h16(b);
+        }
+}
+
+// h = round(LN(x) * w) over the 2048 values of the wave (biased variance, the reference's LayerNorm)
+RK_DEV void layernorm_wave(XWave& xw, const uint16_t* w, float eps) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += xw.v[k][e];
+    const float mean = wave_sum(s) * (1.0f / kH);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float d = xw.v[k][e] - mean;
             ss += d * d;
         }
-    const float rstd = 1.0f / sqrtf(block_sum(ss, red) * (1.0f / kH) + eps);
-    if (active) {
-        const u4_t wv = reinterpret_cast<const u4_t*>(w)[threadIdx.x];
+    const float rstd = 1.0f / sqrtf(wave_sum(ss) * (1.0f / kH) + eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const u4_t wv = reinterpret_cast<const u4_t*>(w)[lane + 64 * k];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const uint16_t wb = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
-            v[e] = rnd16((v[e] - mean) * rstd * h16(wb));
+            xw.v[k][e] = rnd16((xw.v[k][e] - mean) * rstd * h16(wb));
         }
     }
 }
 
-// the residual stream written by the other blocks: 8 values per thread 0..255, coherent loads
-RK_DEV void load_x8(const Params& p, float (&v)[8]) {
-    const uint32_t* xs = reinterpret_cast<const uint32_t*>(p.x) + threadIdx.x * 4;
+// h -> MFMA A fragments + per-group sums in LDS (wave 0)
+RK_DEV void stage_h_frag(const XWave& xw, Lds& S) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const h2_t h = as_h2(ld_coh(xs + e));
-        v[2 * e] = (float)h.x;
-        v[2 * e + 1] = (float)h.y;
-    }
-}
-
-// h (8 values per thread 0..255) -> MFMA A fragments + group sums in LDS
-RK_DEV void stage_h_frag(const float (&v)[8], bool active, Lds& S) {
-    const int i = threadIdx.x;
-    float sum = 0.f;
-    if (active) {
+    for (int k = 0; k < 4; ++k) {
+        const int i = lane + 64 * k;
         u4_t d;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) d[e] = pack_h2(v[2 * e], v[2 * e + 1]);
+        for (int e = 0; e < 4; ++e) d[e] = pack_h2(xw.v[k][2 * e], xw.v[k][2 * e + 1]);
         uint32_t hp[4];
         pair_permute(d, hp);
         const int g = i >> 4, r = i & 15, s = r >> 2, t = r & 3;
         S.hfrag[g * 16 + t * 4 + s] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+        float sum = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum += v[e];
-    }
-    if (i < 256) {  // 16-thread groups = one 128-column group, inside one DPP row
+        for (int e = 0; e < 8; ++e) sum += xw.v[k][e];
+        // 16 lanes = one 128-column group, inside one DPP row
         sum += dpp<0x128>(sum);
         sum += dpp<0x124>(sum);
         sum += dpp<0x122>(sum);
         sum += dpp<0x121>(sum);
-        if ((i & 15) == 0) S.hsum[i >> 4] = sum;
+        if ((lane & 15) == 0) S.hsum[i >> 4] = sum;
     }
 }
 
@@ -325,36 +373,55 @@ RK_DEV void tile_compute(const Params& p, int l, int tile, const TileLoad& tl, i
     }
 }
 
-RK_DEV void phase_a(const Params& p, int l, float (&xv)[8], bool from_global, int64_t pos, Lds& S) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int j = lane & 15, s = lane >> 4;
-    const bool active = tid < kH / 8;
+// this wave's first w_in tile of layer l (the caller issues it before the barrier that precedes phase A)
+struct TileRange {
+    int t0, t1;
+};
+
+RK_DEV TileRange tile_range(const Params& p) {
     const int n_in = (p.NH + 2 * p.NKV) * kHD + 2 * p.inter;
     const int ntiles = n_in / 16;
-    const int t0 = (int)((long long)blockIdx.x * ntiles / gridDim.x);
-    const int t1 = (int)((long long)(blockIdx.x + 1) * ntiles / gridDim.x);
-    const uint8_t* wq = p.win_q + (size_t)l * n_in * (kH / 2);
-    const uint16_t* ws = p.win_s + (size_t)l * n_in * kNG;
-    const uint16_t* wm = p.win_m + (size_t)l * n_in * kNG;
+    return {(int)((long long)blockIdx.x * ntiles / gridDim.x), (int)((long long)(blockIdx.x + 1) * ntiles / gridDim.x)};
+}
 
-    // weights first: this wave's tile streams in while x is gathered and normalized
-    TileLoad tl;
-    const int tile = t0 + wave;
-    if (tile < t1) tile_load(tl, wq, ws, wm, tile * 16 + j, s);
+// wave w's first tile: waves 1..7 take the block's first seven tiles, wave 0 (which polls the barriers and issues
+// its loads last) an eighth if there is one
+RK_DEV int first_tile(const TileRange& tr) { return tr.t0 + ((threadIdx.x >> 6) + kWaves - 1) % kWaves; }
 
-    float v[8];
-    if (from_global && active) load_x8(p, xv);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = xv[e];
-    layernorm8(v, active, p.ln_w + (size_t)l * kH, p.eps, S.red);
-    stage_h_frag(v, active, S);
+RK_DEV void tile_issue(const Params& p, int l, TileLoad& tl) {
+    const int lane = threadIdx.x & 63;
+    const TileRange tr = tile_range(p);
+    const int tile = first_tile(tr);
+    const size_t n_in = (size_t)(p.NH + 2 * p.NKV) * kHD + 2 * p.inter;
+    if (tile < tr.t1)
+        tile_load(tl, p.win_q + (size_t)l * n_in * (kH / 2), p.win_s + (size_t)l * n_in * kNG,
+                  p.win_m + (size_t)l * n_in * kNG, tile * 16 + (lane & 15), lane >> 4);
+}
+
+RK_DEV void phase_a(const Params& p, int l, TileLoad& tl, int64_t tok, int64_t pos, Lds& S) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int j = lane & 15, s = lane >> 4;
+    const size_t n_in = (size_t)(p.NH + 2 * p.NKV) * kHD + 2 * p.inter;
+    const TileRange tr = tile_range(p);
+    const int tile = first_tile(tr);
+
+    if (tid < 64) {  // wave 0: gather x, LayerNorm, stage h (the other waves' tiles are landing meanwhile)
+        XWave xw;
+        if (l == 0)
+            x_from_embedding(p, tok, xw);
+        else
+            x_load(p, xw);
+        layernorm_wave(xw, p.ln_w + (size_t)l * kH, p.eps);
+        stage_h_frag(xw, S);
+    }
     __syncthreads();
 
     const Int4Masks km = int4_masks();
     const bool rope = (p.sliding >> l) & 1ull;
-    if (tile < t1) tile_compute(p, l, tile, tl, pos, rope, S, km);
-    for (int t2 = tile + kWaves; t2 < t1; t2 += kWaves) {  // blocks with more tiles than waves
-        tile_load(tl, wq, ws, wm, t2 * 16 + j, s);
+    if (tile < tr.t1) tile_compute(p, l, tile, tl, pos, rope, S, km);
+    for (int t2 = tile + kWaves; t2 < tr.t1; t2 += kWaves) {  // blocks with more tiles than waves
+        tile_load(tl, p.win_q + (size_t)l * n_in * (kH / 2), p.win_s + (size_t)l * n_in * kNG,
+                  p.win_m + (size_t)l * n_in * kNG, t2 * 16 + j, s);
         tile_compute(p, l, t2, tl, pos, rope, S, km);
     }
 }
@@ -440,8 +507,7 @@ RK_DEV void attention_split(const Params& p, int l, int64_t pos, Lds& S) {
             ay += wt * S.s_acc[w2][r][lane].y;
         }
         const size_t pi = (size_t)(g * REP + r) * nsp + sp;
-        st_coh_f(p.po + pi * kHD + 2 * lane, ax);
-        st_coh_f(p.po + pi * kHD + 2 * lane + 1, ay);
+        st_coh64(reinterpret_cast<uint64_t*>(p.po + pi * kHD) + lane, pack_f2(ax, ay));
         if (lane == 0) {
             st_coh_f(p.pm + pi, M);
             st_coh_f(p.pl + pi, Lt);
@@ -457,103 +523,119 @@ RK_DEV void attention_split(const Params& p, int l, int64_t pos, Lds& S) {
     }
     __syncthreads();
     if (!S.flag) return;
-    // split weights w_i = exp(m_i - M) per head, and the denominators, into LDS
-    for (int r = wave; r < REP; r += kWaves) {
-        const int hh = g * REP + r;
-        float mi[4], mx = -INFINITY;
+    // wave w merges splits part, part + kParts, ... of head r (kParts waves per head, one dim pair per lane); every
+    // load of a batch is independent of the others, so a batch costs one memory round trip
+    constexpr int kParts = kWaves / REP;
+    const int na = min(nsp, (n + ch - 1) / ch);  // splits holding at least one slot
+    const int r = wave / kParts, part = wave % kParts;
+    const size_t hb = (size_t)(g * REP + r) * nsp;
+    const uint64_t* po2 = reinterpret_cast<const uint64_t*>(p.po + hb * kHD) + lane;
+    float M = -INFINITY, den = 0.f, nx = 0.f, ny = 0.f;
+    constexpr int kCB = 8;
+    for (int i0 = part; i0 < na; i0 += kCB * kParts) {
+        float mi[kCB], li[kCB];
+        uint64_t oi[kCB];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = lane + 64 * k;
-            mi[k] = i < nsp ? ld_coh_f(p.pm + (size_t)hh * nsp + i) : -INFINITY;
-            mx = fmaxf(mx, mi[k]);
+        for (int u = 0; u < kCB; ++u) {
+            const int i = min(i0 + u * kParts, na - 1);
+            mi[u] = ld_coh_f(p.pm + hb + i);
+            li[u] = ld_coh_f(p.pl + hb + i);
+            oi[u] = ld_coh64(po2 + (size_t)i * (kHD / 2));
         }
-        mx = wave_max(mx);
-        float den = 0.f;
+        float bm = M;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = lane + 64 * k;
-            const float wt = (i < nsp && mi[k] != -INFINITY) ? __expf(mi[k] - mx) : 0.f;
-            if (i < nsp) S.cw[r][i] = wt;
-            den += i < nsp ? wt * ld_coh_f(p.pl + (size_t)hh * nsp + i) : 0.f;
+        for (int u = 0; u < kCB; ++u)
+            if (i0 + u * kParts < na) bm = fmaxf(bm, mi[u]);
+        if (bm == -INFINITY) continue;  // only empty splits so far
+        const float a = __expf(M - bm);
+        den *= a;
+        nx *= a;
+        ny *= a;
+#pragma unroll
+        for (int u = 0; u < kCB; ++u) {
+            if (i0 + u * kParts < na && mi[u] != -INFINITY) {
+                const float wt = __expf(mi[u] - bm);
+                den += wt * li[u];
+                nx += wt * __builtin_bit_cast(float, (uint32_t)oi[u]);
+                ny += wt * __builtin_bit_cast(float, (uint32_t)(oi[u] >> 32));
+            }
         }
-        den = wave_sum(den);
-        if (lane == 0) S.cden[r] = den;
+        M = bm;
+    }
+    S.s_acc[wave][0][lane] = make_float2(nx, ny);
+    if (lane == 0) {
+        S.c_m[wave] = M;
+        S.c_l[wave] = den;
     }
     __syncthreads();
-    // num[h][d] = sum_i w_i po_i[d]: thread = (dim pair, split quarter) for each head; every load of a thread
-    // is independent, so all of them are in flight at once
-    constexpr int kQ = 4;                       // split quarters
-    for (int r = 0; r < REP; ++r) {
-        const int hh = g * REP + r;
-        for (int e = tid; e < kQ * (kHD / 2); e += kThreads) {
-            const int qtr = e / (kHD / 2), d2 = 2 * (e % (kHD / 2));
-            const int i0 = qtr * ((nsp + kQ - 1) / kQ), i1 = min(nsp, i0 + (nsp + kQ - 1) / kQ);
-            const float* pr = p.po + (size_t)hh * nsp * kHD + d2;
-            float n0 = 0.f, n1 = 0.f;
-#pragma unroll 16
-            for (int i = i0; i < i1; ++i) {
-                const float wt = S.cw[r][i];
-                n0 += wt * ld_coh_f(pr + (size_t)i * kHD);
-                n1 += wt * ld_coh_f(pr + (size_t)i * kHD + 1);
-            }
-            S.part[qtr][d2 / 2] = make_float2(n0, n1);
-        }
-        __syncthreads();
-        if (tid < kHD / 2) {
-            float2 t = S.part[0][tid];
+    if (tid < REP * 64) {  // thread = (head r2, dim pair d2): merge the kParts waves of the head
+        const int r2 = tid >> 6, d2 = tid & 63;
+        float Mx = -INFINITY;
 #pragma unroll
-            for (int q = 1; q < kQ; ++q) {
-                t.x += S.part[q][tid].x;
-                t.y += S.part[q][tid].y;
-            }
-            const float inv = 1.0f / S.cden[r];
-            st_coh(reinterpret_cast<uint32_t*>(p.ob) + ((size_t)hh * kHD) / 2 + tid, pack_h2(t.x * inv, t.y * inv));
+        for (int k = 0; k < kParts; ++k) Mx = fmaxf(Mx, S.c_m[r2 * kParts + k]);
+        float dd = 0.f, ox = 0.f, oy = 0.f;
+#pragma unroll
+        for (int k = 0; k < kParts; ++k) {
+            const int w2 = r2 * kParts + k;
+            const float wt = S.c_m[w2] == -INFINITY ? 0.f : __expf(S.c_m[w2] - Mx);
+            dd += wt * S.c_l[w2];
+            ox += wt * S.s_acc[w2][0][d2].x;
+            oy += wt * S.s_acc[w2][0][d2].y;
         }
-        __syncthreads();
+        const float inv = 1.0f / dd;
+        st_coh(reinterpret_cast<uint32_t*>(p.ob) + ((size_t)(g * REP + r2) * kHD) / 2 + d2, pack_h2(ox * inv, oy * inv));
     }
 }
 
-template <int REP>
-RK_DEV void phase_b(const Params& p, int l, int64_t pos, Lds& S) {
-    const int wave = threadIdx.x >> 6;
-    const int rpb = (kH + gridDim.x - 1) / gridDim.x;
-    const int inter = p.inter;
-    // the down row's weights go out first: independent of everything this phase waits on
-    constexpr int NJ = 6;  // ceil(11008 / 32 / 64)
-    RowPrefetch<NJ> rp;
-    const int row = blockIdx.x * rpb + wave;  // at most one down row per wave (rpb <= kWaves is checked at launch)
-    const bool mine = wave < rpb && row < kH;
-    if (mine)
-        row_prefetch<NJ>(rp, p.wd_q + (size_t)l * kH * (inter / 2), p.wd_s + (size_t)l * kH * (inter / 128),
-                         p.wd_m + (size_t)l * kH * (inter / 128), row, inter);
+constexpr int kDownNJ = 6;  // ceil(11008 / 32 / 64): chunks per lane of one down row
 
+// at most one row of w_down / w_o per wave (rpb <= kWaves is checked at launch)
+RK_DEV int own_row(int& row) {
+    const int rpb = (kH + gridDim.x - 1) / gridDim.x, wave = threadIdx.x >> 6;
+    row = blockIdx.x * rpb + wave;
+    return wave < rpb && row < kH;
+}
+
+RK_DEV void down_issue(const Params& p, int l, RowPrefetch<kDownNJ>& rp) {
+    int row;
+    const int inter = p.inter;
+    if (own_row(row))
+        row_prefetch<kDownNJ>(rp, p.wd_q + (size_t)l * kH * (inter / 2), p.wd_s + (size_t)l * kH * (inter / 128),
+                              p.wd_m + (size_t)l * kH * (inter / 128), row, inter);
+}
+
+template <int REP>
+RK_DEV void phase_b(const Params& p, int l, int64_t pos, const RowPrefetch<kDownNJ>& rp, Lds& S) {
     attention_split<REP>(p, l, pos, S);
     __syncthreads();
-
-    stage_vec_pairs(p.act, inter, S);
+    stage_vec_pairs(p.act, p.inter, S);
     __syncthreads();
     const Int4Masks km = int4_masks();
-    if (mine) {
-        const float d = row_dot<NJ>(rp, inter, S, km);
-        if ((threadIdx.x & 63) == 0) S.drow[wave] = d;
+    int row;
+    if (own_row(row)) {
+        const float d = row_dot<kDownNJ>(rp, p.inter, S, km);
+        if ((threadIdx.x & 63) == 0) S.drow[threadIdx.x >> 6] = d;
     }
 }
 
 // ---------------------------------------------------------------------------------------------- phase C
-RK_DEV void phase_c(const Params& p, int l, Lds& S) {
+RK_DEV void o_issue(const Params& p, int l, RowPrefetch<1>& rp) {
+    int row;
+    const int K = p.NH * kHD;
+    if (own_row(row))
+        row_prefetch<1>(rp, p.wo_q + (size_t)l * kH * (K / 2), p.wo_s + (size_t)l * kH * (K / 128),
+                        p.wo_m + (size_t)l * kH * (K / 128), row, K);
+}
+
+RK_DEV void phase_c(const Params& p, const RowPrefetch<1>& rp, Lds& S) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int rpb = (kH + gridDim.x - 1) / gridDim.x;
     const int K = p.NH * kHD;
-    RowPrefetch<1> rp;
-    const int row = blockIdx.x * rpb + wave;
-    const bool mine = wave < rpb && row < kH;
-    if (mine)
-        row_prefetch<1>(rp, p.wo_q + (size_t)l * kH * (K / 2), p.wo_s + (size_t)l * kH * (K / 128),
-                        p.wo_m + (size_t)l * kH * (K / 128), row, K);
     stage_vec_pairs(p.ob, K, S);
     __syncthreads();
     const Int4Masks km = int4_masks();
-    if (mine) {
+    int row;
+    if (own_row(row)) {
         const float o = row_dot<1>(rp, K, S, km);
         if (lane == 0) S.xrow[wave] = rnd16(S.xrow[wave] + rnd16(o) + rnd16(S.drow[wave]));
     }
@@ -564,30 +646,68 @@ RK_DEV void phase_c(const Params& p, int l, Lds& S) {
 }
 
 // ---------------------------------------------------------------------------------------------- head
-RK_DEV void head_phase(const Params& p, const float (&hv)[8], bool active, Lds& S) {
-    if (active) S.vecp[threadIdx.x] = make_uint4(pack_h2(hv[0], hv[1]), pack_h2(hv[2], hv[3]), pack_h2(hv[4], hv[5]),
-                                                 pack_h2(hv[6], hv[7]));
+// int8 audio head: block b owns rows [b * per, (b + 1) * per), wave w rows r0 + w + 8k. The first batch of a
+// wave's rows is issued before the last barrier.
+constexpr int kHeadB = 8;  // rows per wave per batch
+
+struct HeadLoad {
+    u4_t w[kHeadB][2];
+};
+
+RK_DEV void head_rows(const Params& p, int& r0, int& r1) {
+    const int per = (p.n_audio + gridDim.x - 1) / gridDim.x;
+    r0 = min(p.n_audio, (int)blockIdx.x * per);
+    r1 = min(p.n_audio, r0 + per);
+}
+
+RK_DEV void head_load(const Params& p, int first, int r1, HeadLoad& hl) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < kHeadB; ++k) {
+        const int r = first + kWaves * k;
+        if (r < r1) {
+            const u4_t* qr = reinterpret_cast<const u4_t*>(p.head_q + (size_t)r * kH);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) hl.w[k][j] = __builtin_nontemporal_load(qr + lane + 64 * j);
+        }
+    }
+}
+
+RK_DEV void head_phase(const Params& p, HeadLoad& hl, Lds& S) {
+    if (threadIdx.x < 64) {  // wave 0: final LayerNorm, natural pairs of h in LDS
+        XWave xw;
+        x_load(p, xw);
+        layernorm_wave(xw, p.norm_w, p.eps);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float* v = xw.v[k];
+            S.vecp[threadIdx.x + 64 * k] = make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
+                                                      pack_h2(v[6], v[7]));
+        }
+    }
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int per = (p.n_audio + gridDim.x - 1) / gridDim.x;
-    const int r0 = blockIdx.x * per, r1 = min(p.n_audio, r0 + per);
-    for (int r = r0 + wave; r < r1; r += kWaves) {
-        const u4_t* qr = reinterpret_cast<const u4_t*>(p.head_q + (size_t)r * kH);
-        u4_t w[2];
+    int r0, r1;
+    head_rows(p, r0, r1);
+    for (int first = r0 + wave; first < r1; first += kWaves * kHeadB) {
+        if (first != r0 + wave) head_load(p, first, r1, hl);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) w[j] = __builtin_nontemporal_load(qr + lane + 64 * j);
-        float acc = 0.f;
+        for (int k = 0; k < kHeadB; ++k) {
+            const int r = first + kWaves * k;
+            if (r >= r1) break;
+            float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {  // 128 chunks of 16 columns
-            const int c = lane + 64 * j;
-            uint32_t xp[8];
-            const uint4 a = S.vecp[2 * c], b = S.vecp[2 * c + 1];
-            xp[0] = a.x; xp[1] = a.y; xp[2] = a.z; xp[3] = a.w;
-            xp[4] = b.x; xp[5] = b.y; xp[6] = b.z; xp[7] = b.w;
-            acc += chunk_dot_int8<true>(w[j], xp);
+            for (int j = 0; j < 2; ++j) {  // 128 chunks of 16 columns
+                const int c = lane + 64 * j;
+                uint32_t xp[8];
+                const uint4 a = S.vecp[2 * c], b = S.vecp[2 * c + 1];
+                xp[0] = a.x; xp[1] = a.y; xp[2] = a.z; xp[3] = a.w;
+                xp[4] = b.x; xp[5] = b.y; xp[6] = b.z; xp[7] = b.w;
+                acc += chunk_dot_int8<true>(hl.w[k][j], xp);
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) p.logits[r] = acc * h16(p.head_s[r]);
         }
-        acc = wave_sum(acc);
-        if (lane == 0) p.logits[r] = acc * h16(p.head_s[r]);
     }
 }
 
@@ -602,35 +722,68 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         if (blockIdx.x == 0 && tid == 0) atomicOr(p.status, kBadPos);
         return;
     }
-    unsigned epoch = __hip_atomic_load(p.flags + blockIdx.x * kFlagStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned epoch = ld_coh(p.flags + blockIdx.x);
     const int rpb = (kH + gridDim.x - 1) / gridDim.x;
+    const bool poller = tid < 64;
 
-    // embedding: x = round(emb_q[tok] * emb_s[tok]); every block keeps the whole vector for its LayerNorm and
-    // its own rows in LDS
-    const bool active = tid < kH / 8;
-    float xv[8];
-    {
-        const float es = h16(p.emb_s[tok]);
-        const int8_t* er = p.emb_q + (size_t)tok * kH;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = active ? rnd16((float)er[tid * 8 + e] * es) : 0.f;
-        if (tid < rpb) S.xrow[tid] = rnd16((float)er[blockIdx.x * rpb + tid] * es);
-    }
+    // Each phase's weights are issued between the block's arrival at the barrier in front of the phase and the
+    // wait for its release, so they stream in while the grid synchronizes: layer 0's w_in tiles right away.
+    TileLoad tl;
+    tile_issue(p, 0, tl);
+    // this block's rows of the residual stream, x = round(emb_q[tok] * emb_s[tok]), kept in LDS across layers
+    if (tid < rpb) S.xrow[tid] = rnd16((float)p.emb_q[(size_t)tok * kH + blockIdx.x * rpb + tid] * h16(p.emb_s[tok]));
 
     for (int l = 0; l < p.L; ++l) {
-        phase_a(p, l, xv, l > 0, pos, S);
-        grid_sync(p, ++epoch);
+        phase_a(p, l, tl, tok, pos, S);
+        RowPrefetch<kDownNJ> rd;
+        grid_arrive(p, ++epoch);
+        if (!poller) down_issue(p, l, rd);
+        grid_wait(p, epoch);
+        if (poller) down_issue(p, l, rd);
         if (l == 0 && blockIdx.x == 0 && tid == 0) p.pos[0] = pos + 1;  // every block has read pos by now
-        phase_b<REP>(p, l, pos, S);
-        grid_sync(p, ++epoch);
-        phase_c(p, l, S);
-        grid_sync(p, ++epoch);
+
+        phase_b<REP>(p, l, pos, rd, S);
+        RowPrefetch<1> ro;
+        grid_arrive(p, ++epoch);
+        if (!poller) o_issue(p, l, ro);
+        grid_wait(p, epoch);
+        if (poller) o_issue(p, l, ro);
+
+        phase_c(p, ro, S);
+        if (l + 1 == p.L) break;
+        grid_arrive(p, ++epoch);
+        if (!poller) tile_issue(p, l + 1, tl);
+        grid_wait(p, epoch);
+        if (poller) tile_issue(p, l + 1, tl);
     }
 
     // final LayerNorm + audio head
-    if (active) load_x8(p, xv);
-    layernorm8(xv, active, p.norm_w, p.eps, S.red);
-    head_phase(p, xv, active, S);
+    HeadLoad hl;
+    int r0, r1;
+    head_rows(p, r0, r1);
+    grid_arrive(p, ++epoch);
+    if (!poller) head_load(p, r0 + (tid >> 6), r1, hl);
+    grid_wait(p, epoch);
+    if (poller) head_load(p, r0, r1, hl);
+    head_phase(p, hl, S);
+}
+
+// can `nblocks` blocks of the kernel be resident on the current device at the same time?
+bool co_resident(int rep, int nblocks) {
+    constexpr int kMaxDev = 64;
+    static int cached[kMaxDev][4];  // resident blocks per device and rep (0: not yet asked)
+    const int ri = rep == 1 ? 0 : rep == 2 ? 1 : rep == 4 ? 2 : 3;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (dev >= 0 && dev < kMaxDev && cached[dev][ri] > 0) return nblocks <= cached[dev][ri];
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+    const void* fn = rep == 1   ? (const void*)decode_step_kernel<1>
+                     : rep == 2 ? (const void*)decode_step_kernel<2>
+                     : rep == 4 ? (const void*)decode_step_kernel<4>
+                                : (const void*)decode_step_kernel<8>;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, sizeof(Lds)) != hipSuccess) return false;
+    if (dev >= 0 && dev < kMaxDev) cached[dev][ri] = per_cu * cus;
+    return nblocks <= per_cu * cus;
 }
 
 }  // namespace
@@ -647,6 +800,7 @@ extern "C" int rk_decode_step_persistent(const rk_decode_params* params, int nbl
     if (!p.tok || !p.pos || !p.emb_q || !p.emb_s || !p.win_q || !p.wo_q || !p.wd_q || !p.kc || !p.vc ||
         !p.head_q || !p.logits || !p.x || !p.flags || !p.status || !p.grp_ctr)
         return RK_ERR_NULL;
+    if (!co_resident(rep, nblocks)) return RK_ERR_BLOCK;  // the grid barriers need every block resident at once
     hipStream_t st = (hipStream_t)stream;
     switch (rep) {
         case 1: hipLaunchKernelGGL(decode_step_kernel<1>, dim3(nblocks), dim3(kThreads), sizeof(Lds), st, p); break;

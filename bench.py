@@ -124,29 +124,35 @@ def cpu_baseline(budget_s):
 
 
 def run_decode(dev, steps):
-    """Config 4: tok/s of the captured 36-layer step (random-init int4 weights, int8 head, fp16 KV cache ~N(0,1)
-    filled to ctx - 1 slots; each step writes slot ctx - 1 and attends over ctx slots). pos is reset before every
-    replay (one tiny fill kernel per step, inside the timed loop)."""
+    """Config 4: tok/s of the 36-layer step as the one-launch persistent kernel, captured in a hipGraph
+    (random-init int4 weights, int8 head, fp16 KV cache ~N(0,1) filled to ctx - 1 slots; each step writes slot
+    ctx - 1 and attends over ctx slots). pos is reset before every replay (one tiny fill kernel per step, inside
+    the timed loop). Timed with HIP events on the engine's stream."""
     import torch
     import decode
     cfg = decode.Config()
     w = decode.random_weights(cfg, 4, device=dev)
-    eng = decode.DecodeStep(cfg, w, device=dev)
-    out = {"weights_bytes_per_token": cfg.weight_bytes(), "layers": cfg.L}
+    eng = decode.PersistentDecode(cfg, w, device=dev)
+    out = {"engine": "persistent one-launch step (hipGraph)", "weights_bytes_per_token": cfg.weight_bytes(),
+           "layers": cfg.L, "blocks": eng.nblocks}
     eng.fill_cache(cfg.S, seed=5)
     eng.set_state(7, 0)
     eng.capture()
     for ctx in (256, 1024, 2048):
-        for _ in range(5):
+        for _ in range(10):
             eng.pos.fill_(ctx - 1)
             eng.replay()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         for _ in range(steps):
             eng.pos.fill_(ctx - 1)
             eng.replay()
+        e1.record()
         torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
+        dt = e0.elapsed_time(e1) / 1e3
+        if eng.status_word() != 0:
+            raise RuntimeError(f"persistent decode step reported status {eng.status_word()}")
         nbytes = cfg.weight_bytes() + cfg.kv_bytes(ctx)
         out[f"ctx{ctx}"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1),
                             "GB_s": round(nbytes * steps / dt / 1e9, 1), "bytes_per_token": nbytes}

@@ -1,0 +1,113 @@
+#!/usr/bin/env python3
+"""HBM traffic per launch of the gate+up int4 GEMV (N=22016, K=2048), from rocprofv3 hardware counters.
+
+Two steps:
+
+    run        launches a plain elementwise copy of known size (torch.neg over 256 MiB fp16: reads and writes
+               268,435,456 B each) and then the gate+up GEMV over 16 rotated weight copies, eagerly, one dispatch
+               each. Run it under `rocprofv3 --pmc FETCH_SIZE` and again under `rocprofv3 --pmc WRITE_SIZE`.
+    summarize  reads the two counter-collection CSVs, scales each counter by what it reads for the copy kernel
+               (counter KiB * 1024 / known bytes), and writes profiles/traffic.json (read by bench.py) plus a
+               markdown summary on stdout.
+
+    cd /tmp && export TMPDIR=/tmp
+    timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE --kernel-trace -d OUT/fetch -o fetch --output-format csv \
+        -- python3 rumik-fast_amd/pmc_traffic.py run
+    timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d OUT/write -o write --output-format csv \
+        -- python3 rumik-fast_amd/pmc_traffic.py run
+    python3 rumik-fast_amd/pmc_traffic.py summarize OUT/fetch OUT/write
+"""
+import csv
+import glob
+import json
+import os
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+COPY_BYTES = 256 << 20
+N, K = 22016, 2048
+GEMV_BYTES = N * K // 2 + 4 * N * (K // 128) + 2 * K + 2 * N
+N_COPIES = 16
+
+
+def run():
+    sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "kernels"))
+    import torch
+    import cuda_gemv
+    import synth
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    gen = synth.generator(1, "cuda")
+    mats = [synth.int4_weights(N, K, gen, device=dev) for _ in range(N_COPIES)]
+    x = torch.randn(K, device=dev, generator=gen).half()
+    y = torch.empty(N, device=dev, dtype=torch.float16)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for w in mats:
+            cuda_gemv.gemv_int4_cuda(x, *w, out=y)
+    torch.cuda.synchronize()
+    print("pmc_traffic: run done", flush=True)
+
+
+def _rows(d):
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _per_dispatch(rows, counter, pred):
+    """mean over matching dispatches of the counter value (summed over the rows of one dispatch)"""
+    per = {}
+    for r in rows:
+        if r.get("Counter_Name") != counter or not pred(r.get("Kernel_Name", "")):
+            continue
+        key = r.get("Dispatch_Id") or r.get("Correlation_Id")
+        per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    if not per:
+        raise SystemExit(f"no {counter} rows for the kernel")
+    vals = list(per.values())
+    return sum(vals) / len(vals), len(vals)
+
+
+def summarize(fetch_dir, write_dir):
+    is_copy = lambda n: "neg" in n.lower()  # noqa: E731
+    is_gemv = lambda n: "gemv_int4" in n  # noqa: E731
+    fr, wr = _rows(fetch_dir), _rows(write_dir)
+    f_copy, nfc = _per_dispatch(fr, "FETCH_SIZE", is_copy)
+    w_copy, nwc = _per_dispatch(wr, "WRITE_SIZE", is_copy)
+    f_gemv, nfg = _per_dispatch(fr, "FETCH_SIZE", is_gemv)
+    w_gemv, nwg = _per_dispatch(wr, "WRITE_SIZE", is_gemv)
+    kf = f_copy * 1024 / COPY_BYTES  # counter KiB*1024 per true byte
+    kw = w_copy * 1024 / COPY_BYTES
+    fetch_b = f_gemv * 1024 / kf
+    write_b = w_gemv * 1024 / kw
+    rec = {"gemv_int4_gate_up_22016x2048": {
+        "traffic_bytes": round(fetch_b + write_b), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
+        "algorithmic_bytes": GEMV_BYTES, "fetch_scale": round(kf, 4), "write_scale": round(kw, 4),
+        "dispatches": {"copy_fetch": nfc, "copy_write": nwc, "gemv_fetch": nfg, "gemv_write": nwg}}}
+    (ROOT / "profiles" / "traffic.json").write_text(json.dumps(rec, indent=1) + "\n")
+    r = rec["gemv_int4_gate_up_22016x2048"]
+    print("| quantity | value |\n|---|---|")
+    print(f"| copy kernel (torch.neg, 256 MiB fp16) FETCH_SIZE / dispatch | {f_copy:.0f} KiB (scale {kf:.4f}) |")
+    print(f"| copy kernel WRITE_SIZE / dispatch | {w_copy:.0f} KiB (scale {kw:.4f}) |")
+    print(f"| gate+up GEMV FETCH_SIZE / dispatch | {f_gemv:.0f} KiB -> {fetch_b:,.0f} B |")
+    print(f"| gate+up GEMV WRITE_SIZE / dispatch | {w_gemv:.0f} KiB -> {write_b:,.0f} B |")
+    print(f"| traffic / launch (scaled) | {r['traffic_bytes']:,} B |")
+    print(f"| algorithmic bytes / launch | {GEMV_BYTES:,} B (traffic / algorithmic = "
+          f"{r['traffic_bytes'] / GEMV_BYTES:.3f}) |")
+
+
+if __name__ == "__main__":
+    if len(sys.argv) >= 2 and sys.argv[1] == "run":
+        run()
+    elif len(sys.argv) == 4 and sys.argv[1] == "summarize":
+        summarize(sys.argv[2], sys.argv[3])
+    else:
+        raise SystemExit(__doc__)

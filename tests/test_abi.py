@@ -1,0 +1,90 @@
+"""The C-ABI library without a GPU: it loads, exports every function include/rumik_hip.h declares, the binding
+table covers them, and argument validation answers before any device work (status codes and their texts are the
+reference's error messages, kernels/cuda_gemv.py:121,135,190)."""
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+import _hiplib as HL
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "rumik_hip.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \t\*]*?\b(rk_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_drop_in_entry_points():
+    names = declared()
+    for n in ("rk_gemv_int4_g128", "rk_gemv_int8_rows", "rk_mm_int4_g128", "rk_embed_ln", "rk_add_ln", "rk_post",
+              "rk_attn_split", "rk_attn_combine", "rk_decode_step_persistent"):
+        assert n in names, n
+
+
+def test_library_exports_every_declared_symbol():
+    lib = HL.lib()
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    out = subprocess.run(["nm", "-D", "--defined-only", str(HL.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (rk_\w+)$", out, flags=re.M))
+    assert set(declared()) <= exported, sorted(set(declared()) - exported)
+
+
+def test_binding_table_covers_the_header():
+    assert set(declared()) <= set(HL.exported_symbols())
+
+
+def test_version_and_status_strings():
+    lib = HL.lib()
+    assert lib.rk_abi_version() == 1
+    texts = {0: "ok", -1: "shape", -2: "unsupported block shape", -3: "unsupported dtype", -4: "null pointer",
+             -6: "kernel launch failed"}
+    for code, t in texts.items():
+        assert lib.rk_status_string(code).decode() == t
+    assert "misaligned" in lib.rk_status_string(-5).decode()
+
+
+def test_decode_params_struct_matches_the_binding():
+    import decode
+    assert HL.lib().rk_decode_params_size() == ctypes.sizeof(decode.RkDecodeParams)
+
+
+@pytest.mark.parametrize("N,K", [(64, 100), (64, 0), (0, 256), (-1, 256)])
+def test_gemv_int4_rejects_bad_shapes(N, K):
+    lib = HL.lib()
+    buf = ctypes.c_void_p(16)  # never dereferenced: validation comes first
+    for fn in (lib.rk_gemv_int4_g128, lib.rk_gemv_int4_g128_valu, lib.rk_gemv_int4_g128_mfma):
+        assert fn(buf, HL.F16, buf, buf, buf, buf, HL.F16, N, K, 0, 0, None) == -1
+
+
+def test_gemv_int4_rejects_bad_dtype_and_block_shape():
+    lib = HL.lib()
+    buf = ctypes.c_void_p(16)
+    assert lib.rk_gemv_int4_g128(buf, 7, buf, buf, buf, buf, HL.F16, 64, 256, 0, 0, None) == -3
+    assert lib.rk_gemv_int4_g128_mfma(buf, HL.F16, buf, buf, buf, buf, HL.F16, 64, 256, 0, 3, None) == -2
+
+
+def test_gemv_int4_rejects_null_and_misaligned():
+    lib = HL.lib()
+    buf, odd = ctypes.c_void_p(256), ctypes.c_void_p(258)
+    assert lib.rk_gemv_int4_g128(None, HL.F16, buf, buf, buf, buf, HL.F16, 64, 256, 0, 0, None) == -4
+    assert lib.rk_gemv_int4_g128(buf, HL.F16, odd, buf, buf, buf, HL.F16, 64, 256, 0, 0, None) == -5
+
+
+def test_decode_step_validates_before_launch():
+    import decode
+    p = decode.RkDecodeParams()
+    assert HL.lib().rk_decode_step_persistent(None, 256, None) == -4
+    p.L, p.NH, p.NKV, p.inter, p.S, p.nsp = 2, 16, 4, 11008, 64, 64
+    assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 256, None) == -4  # null buffers
+    p.NH = 12  # 12 * 128 != 2048
+    assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 256, None) == -1
+    p.NH, p.inter = 16, 11000  # not a multiple of 128
+    assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 256, None) == -1
+    p.inter = 11008
+    assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 200, None) == -2  # nblocks != NKV * nsp

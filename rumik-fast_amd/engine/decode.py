@@ -110,17 +110,18 @@ class DecodeStep:
         """Enqueue one decode step on the current stream (engine/rumik_fused.py:97-121)."""
         c, w = self.cfg, self.w
         scale = c.HD ** -0.5
-        fused.embed_ln(self.tok, w["emb"][0], w["emb"][1], w["ln"][0], self.x, self.h, c.eps)
+        fused.embed_ln[(1,)](self.tok, w["emb"][0], w["emb"][1], w["ln"][0], self.x, self.h, c.eps, H=c.H)
         for i in range(c.L):
             cuda_gemv.gemv_int4_cuda(self.h, *w["w_in"][i], out=self.buf_in)
-            fused.post(self.buf_in, self.pos, self.cos, self.sin, self.kc[i], self.vc[i], self.qb, self.act,
-                       c.NH, c.NKV, c.HD, c.inter, c.sliding[i])
-            fused.attn_split(self.qb, self.kc[i], self.vc[i], self.pos, self.po, self.pm, self.pl, c.NH, c.NKV, c.HD,
-                             c.nsplit, scale)
-            fused.attn_combine(self.po, self.pm, self.pl, self.pos, self.ob, c.NH, c.HD, c.nsplit)
+            fused.post[(1,)](self.buf_in, self.pos, self.cos, self.sin, self.kc[i], self.vc[i], self.qb, self.act,
+                             c.S, c.inter, NH=c.NH, NKV=c.NKV, HD=c.HD, ROPE=c.sliding[i])
+            fused.attn_split[(c.NKV, c.nsplit)](self.qb, self.kc[i], self.vc[i], self.pos, self.po, self.pm, self.pl,
+                                                c.S, scale, REP=c.NH // c.NKV, HD=c.HD, NSPLIT=c.nsplit)
+            fused.attn_combine[(c.NH,)](self.po, self.pm, self.pl, self.pos, self.ob, HD=c.HD, NSPLIT=c.nsplit)
             cuda_gemv.gemv_int4_cuda(self.ob, *w["w_o"][i], out=self.buf_o)
             cuda_gemv.gemv_int4_cuda(self.act, *w["w_down"][i], out=self.buf_d)
-            fused.add_ln(self.x, self.buf_o, self.buf_d, w["norm"] if i == c.L - 1 else w["ln"][i + 1], self.h, c.eps)
+            fused.add_ln[(1,)](self.x, self.buf_o, self.buf_d, w["norm"] if i == c.L - 1 else w["ln"][i + 1], self.h,
+                               c.eps, H=c.H)
         fused.pos_advance(self.pos)
         cuda_gemv.gemv_int8_cuda(self.h, *w["head"], out=self.logits)
 

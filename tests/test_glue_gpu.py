@@ -66,8 +66,8 @@ def _post_case(pos, rope, dev, NH=16, NKV=4, HD=128, inter=11008, S=2048):
     vc = torch.zeros_like(kc)
     qo = torch.empty(NH * HD, dtype=F16, device=dev)
     act = torch.empty(inter, dtype=F16, device=dev)
-    fused.post(y.to(dev), torch.tensor([pos], device=dev), cos.to(dev), sin.to(dev), kc, vc, qo, act, NH, NKV, HD,
-               inter, rope)
+    fused.post[(1,)](y.to(dev), torch.tensor([pos], device=dev), cos.to(dev), sin.to(dev), kc, vc, qo, act, S, inter,
+                     NH=NH, NKV=NKV, HD=HD, ROPE=rope, BLOCK=512, num_warps=4)
     return y, cos, sin, kc, vc, qo, act
 
 
@@ -102,8 +102,8 @@ def _attn(q, kc, vc, pos, dev, nsplit=64, NH=16, NKV=4, HD=128):
     pl = torch.empty(NH, nsplit, device=dev)
     out = torch.empty(NH * HD, dtype=F16, device=dev)
     p = torch.tensor([pos], device=dev)
-    fused.attn_split(q, kc, vc, p, po, pm, pl, NH, NKV, HD, nsplit, HD ** -0.5)
-    fused.attn_combine(po, pm, pl, p, out, NH, HD, nsplit)
+    fused.attn_split[(NKV, nsplit)](q, kc, vc, p, po, pm, pl, kc.shape[1], HD ** -0.5, REP=NH // NKV, HD=HD, NSPLIT=nsplit)
+    fused.attn_combine[(NH,)](po, pm, pl, p, out, HD=HD, NSPLIT=nsplit)
     torch.cuda.synchronize()
     return out, po, pm, pl
 
@@ -158,12 +158,12 @@ def test_graph_replay_reads_pos_on_device(dev):
     pm = torch.empty(NH, nsplit, device=dev)
     pl = torch.empty(NH, nsplit, device=dev)
     out = torch.empty(NH * HD, dtype=F16, device=dev)
-    fused.attn_split(q, kc, vc, pos, po, pm, pl, NH, NKV, HD, nsplit, HD ** -0.5)
+    fused.attn_split[(NKV, nsplit)](q, kc, vc, pos, po, pm, pl, kc.shape[1], HD ** -0.5, REP=NH // NKV, HD=HD, NSPLIT=nsplit)
     torch.cuda.synchronize()
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr):
-        fused.attn_split(q, kc, vc, pos, po, pm, pl, NH, NKV, HD, nsplit, HD ** -0.5)
-        fused.attn_combine(po, pm, pl, pos, out, NH, HD, nsplit)
+        fused.attn_split[(NKV, nsplit)](q, kc, vc, pos, po, pm, pl, kc.shape[1], HD ** -0.5, REP=NH // NKV, HD=HD, NSPLIT=nsplit)
+        fused.attn_combine[(NH,)](po, pm, pl, pos, out, HD=HD, NSPLIT=nsplit)
     for p in (10, 511, 2047, 64):
         pos.fill_(p)
         gr.replay()
@@ -171,3 +171,20 @@ def test_graph_replay_reads_pos_on_device(dev):
         ref = OG.attend(_np(q).reshape(NH, HD), _np(kc[:, :p + 1]), _np(vc[:, :p + 1]))
         rep = O.parity_report(_np(out), ref.ravel())
         assert rep["norm_rel"] < 2e-3, (p, rep)
+
+
+def test_unsplit_attn_matches_split(dev):
+    """fused.attn (the reference's unsplit kernel, engine/fused.py:92-125) equals the split + combine result."""
+    NH, NKV, HD, S = 16, 4, 128, 256
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(NH * HD, generator=g).half().to(dev)
+    kc = torch.randn(NKV, S, HD, generator=g).half().to(dev)
+    vc = torch.randn(NKV, S, HD, generator=g).half().to(dev)
+    pos = torch.tensor([200], device=dev)
+    o1 = torch.empty(NH * HD, dtype=F16, device=dev)
+    fused.attn[(NH,)](q, kc, vc, pos, o1, S, HD ** -0.5, REP=NH // NKV, HD=HD, BT=64, num_warps=4)
+    o2 = _attn(q, kc, vc, 200, dev, nsplit=8)[0]
+    torch.cuda.synchronize()
+    ref = OG.attend(_np(q).reshape(NH, HD), _np(kc)[:, :201], _np(vc)[:, :201])
+    np.testing.assert_allclose(_np(o1).reshape(NH, HD), ref, rtol=1e-2, atol=2e-3)
+    np.testing.assert_allclose(_np(o1), _np(o2), rtol=1e-2, atol=2e-3)

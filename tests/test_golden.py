@@ -157,7 +157,7 @@ def test_gpu_attention_fixture(dev, nsplit):
     pm = torch.empty(NH, nsplit, dtype=torch.float32, device=dev)
     pl = torch.empty_like(pm)
     out = torch.empty(NH * HD, dtype=torch.float16, device=dev)
-    fused.attn_split(q, kc, vc, pos, po, pm, pl, NH, NKV, HD, nsplit, HD ** -0.5)
-    fused.attn_combine(po, pm, pl, pos, out, NH, HD, nsplit)
+    fused.attn_split[(NKV, nsplit)](q, kc, vc, pos, po, pm, pl, kc.shape[1], HD ** -0.5, REP=NH // NKV, HD=HD, NSPLIT=nsplit)
+    fused.attn_combine[(NH,)](po, pm, pl, pos, out, HD=HD, NSPLIT=nsplit)
     torch.cuda.synchronize()
     np.testing.assert_allclose(out.float().cpu().numpy().reshape(NH, HD), d["out"], rtol=1e-2, atol=2e-3)

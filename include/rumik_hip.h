@@ -130,13 +130,20 @@ int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_str
  * The whole decode step in one persistent launch (no reference counterpart as a single kernel: it replaces the
  * ~260 launches of RumikFused._step, engine/rumik_fused.py:97-121, plus the audio head of _logits, :84-89).
  * Hidden size 2048 and head dim 128 are fixed; NH * 128 == 2048; NH / NKV in {1, 2, 4, 8}; inter % 128 == 0 and
- * inter <= 11008. Weights are stacked over layers; w_in rows are [q | k | v | then per 8 channels: 8 gate rows,
- * 8 up rows] (the reference's q/k/v/gate/up concatenation, gate and up interleaved by 8 at load time).
- * nblocks = NKV * nsp, one block per CU (256 on MI355X), each owning ceil(2048 / nblocks) <= 8 rows of w_o / w_down.
- * Workspace: flags [nblocks * 32] words (arrival words, then a release word), status and grp_ctr [NKV] start at
- * zero and are left consistent for the next call. The grid must be co-resident (checked: RK_ERR_BLOCK otherwise).
- * status bit 1 = a grid barrier waited longer than 200 ms (the step then finishes early with garbage; reset status);
- * bit 2 = pos outside [0, S) (nothing is computed or written, pos is not advanced).
+ * inter <= 11008. One block per CU (nblocks = 256 on MI355X, co-residency is checked); block b owns rows
+ * [8b, 8b + 8) of the residual stream and of w_o, the w_in tiles and w_down column slices its `work` row lists, and
+ * attention split b % nsp of KV head b / nsp (b < NKV * nsp).
+ * Weights are stacked over layers and re-laid out once at load time:
+ *   w_in rows are [q | k | v | per 8 MLP channels: 8 gate rows, 8 up rows]; tile T = rows [16T, 16T + 16);
+ *   win_t holds, per (layer, tile, 128-column group), the 16 rows x 64 bytes of codes in lane order (lane j + 16s:
+ *   row j, bytes [16s, 16s + 16) of the group); win_sm per (layer, tile, row) the 16 groups' scale | min << 16;
+ *   wd_t holds w_down by 16-column slices: per (layer, slice), 2048 rows x 8 bytes; wd_sm per (layer, group) the
+ *   2048 rows' scale | min << 16; w_o keeps the reference code layout, wo_sm its scale | min << 16.
+ * Blocks exchange fp16 values as tagged 32-bit words (value | tag << 16, tag = 1 + (step * 64 + layer) % 65535,
+ * step = the block's ctr entry) and poll the words themselves: tx, tq, tkv, tob, tdp, tpo (fp16 words) and tml
+ * (fp32 m / l | tag << 32). All exchange buffers, ctr and status start at zero; after a nonzero status, re-zero them.
+ * status bit 1 = a wait exceeded 200 ms (the step finishes early with garbage); bit 2 = pos outside [0, S)
+ * (nothing is computed or written, pos is not advanced).
  * ------------------------------------------------------------------------------------------------------------ */
 typedef struct rk_decode_params {
     int L, NH, NKV, inter, S, n_audio, nsp;
@@ -146,15 +153,12 @@ typedef struct rk_decode_params {
     int64_t* pos;
     const int8_t* emb_q;    /* [vocab, 2048] */
     const uint16_t* emb_s;  /* [vocab] fp16 */
-    const uint8_t* win_q;   /* [L, n_in, 1024] */
-    const uint16_t* win_s;  /* [L, n_in, 16] */
-    const uint16_t* win_m;
+    const uint8_t* win_t;   /* [L, n_in/16, 16, 64, 16 B] */
+    const uint32_t* win_sm; /* [L, n_in/16, 16 rows, 16 groups] */
     const uint8_t* wo_q;    /* [L, 2048, NH*64] */
-    const uint16_t* wo_s;
-    const uint16_t* wo_m;
-    const uint8_t* wd_q;    /* [L, 2048, inter/2] */
-    const uint16_t* wd_s;
-    const uint16_t* wd_m;
+    const uint32_t* wo_sm;  /* [L, 2048, NH]: scale | min << 16 */
+    const uint8_t* wd_t;    /* [L, inter/16, 2048, 8 B] */
+    const uint32_t* wd_sm;  /* [L, inter/128, 2048] */
     const uint16_t* ln_w;   /* [L, 2048] fp16 */
     const uint16_t* norm_w; /* [2048] */
     const uint16_t* cos_t;  /* [S, 128] fp16 */
@@ -164,15 +168,15 @@ typedef struct rk_decode_params {
     const int8_t* head_q;   /* [n_audio, 2048] */
     const uint16_t* head_s; /* [n_audio] fp16 */
     float* logits;          /* [n_audio] */
-    uint16_t* x;            /* [2048] residual stream (workspace) */
-    uint16_t* qbuf;         /* [NH*128] */
-    uint16_t* act;          /* [inter] */
-    uint16_t* ob;           /* [NH*128] */
-    float* po;              /* [NH, nsp, 128] */
-    float* pm;              /* [NH, nsp] */
-    float* pl;
-    unsigned* grp_ctr;      /* [NKV] */
-    unsigned* flags;        /* [nblocks * 32] */
+    const int16_t* work;    /* [nblocks, 16]: w_in tiles (8, -1 = none), slice begin, slice end, combined head (-1 = none) */
+    uint32_t* tx;           /* [2048] */
+    uint32_t* tq;           /* [NH*128] */
+    uint32_t* tkv;          /* [2, NKV*128] (k, v of the current layer at pos) */
+    uint32_t* tob;          /* [NH*128] */
+    uint32_t* tdp;          /* [nblocks, 2048] down-projection partials */
+    uint32_t* tpo;          /* [NH, nsp, 128] normalized split outputs */
+    unsigned long long* tml; /* [NH, nsp, 2] */
+    unsigned* ctr;          /* [nblocks] step counters */
     unsigned* status;
 } rk_decode_params;
 

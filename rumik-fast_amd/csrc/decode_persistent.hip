@@ -1,42 +1,58 @@
 // One batch-1 decode step of the Rumik decoder in ONE kernel launch (gfx950, MI355X).
 //
-// Why: a step is ~36 x 3 dependent GEMVs plus glue. As separate kernels each pays a launch gap and a cold
-// memory-latency ramp (measured ~3-10 us per node in a hipGraph), which alone exceeds the ~330 us a 3000 tok/s
-// step may take. Here a grid of one block per CU stays resident for the whole step; each block owns fixed slices
-// of every weight matrix and streams them, and the dependent phases of a layer are separated by device-side grid
-// barriers instead of kernel boundaries.
+// Why one launch: a step is ~36 x 3 dependent GEMVs plus glue. As separate kernels each pays a launch gap and a
+// cold memory-latency ramp (measured 2-10 us per hipGraph node), far more than the ~330 us a 3000 tok/s step may
+// take. Here a grid of one block per CU stays resident for the whole step and streams its fixed share of every
+// weight matrix.
 //
-// Per layer (the reference's step, engine/rumik_fused.py:97-121, with its parallel block x += attn(h) + mlp(h)):
-//   A  every block: h = LayerNorm(x) (redundantly, 2048 values) staged in LDS as MFMA fragments;
-//      its tiles of w_in (16 rows each, v_mfma_f32_16x16x32_f16, exact int4 dequant) with the epilogue fused:
-//      RoPE on q / k rows (pairs are adjacent rows), K/V written at slot pos, act = silu(gate) * up (gate and up
-//      rows are interleaved by 8 in the weight layout, so a tile holds both)                    [grid barrier]
-//   B  block b: one flash-decoding split (KV head b / NSP, split b % NSP) for the REP query heads of that KV head;
-//      the last block to finish a KV head merges its NSP partials into the attention output; and rows
-//      [8b, 8b+8) of w_down . act (its weight loads are issued before the attention work)      [grid barrier]
-//   C  block b: rows [8b, 8b+8) of w_o . attn; x[rows] = x + o + d (each rounded once, as the reference's
-//      add_ln)                                                                                 [grid barrier]
+// Synchronization is dataflow, not grid barriers: every value one block hands to another is stored as a tagged
+// 32-bit word (fp16 value | tag << 16; the tag names the step and the layer) with an agent-scope atomic store, and
+// the consumer polls the words themselves with agent-scope atomic loads (coherent across the XCDs' L2s). One
+// cross-block edge then costs one store-to-load hop (measured 0.75 us idle, ~1.5 us while HBM streams) instead of
+// a barrier's two plus a data load.
+//
+// Roles inside a block: wave 0 only polls, gathers and stages exchanged data in LDS. It never has weight loads in
+// flight: vector-memory results return in issue order, so a poll behind a weight burst would wait for the burst.
+// Waves 1..7 ("streamers") stream weights, issued a phase or more ahead of use, and compute. A wave has at most 63
+// vector-memory instructions outstanding, so the issue points keep each streamer's in-flight loads below that.
+//
+// Per layer l (the reference's step, engine/rumik_fused.py:97-121, with its parallel block x += attn(h) + mlp(h)):
+//   wave 0: x of layer l-1 (tagged, all 2048) -> LayerNorm -> h as MFMA fragments in LDS
+//   streamers: the block's w_in tiles (16 rows each), K-split: streamer w computes 2-3 of the 16 column groups of
+//     every tile (v_mfma_f32_16x16x32_f16, exact int4 dequant), so each wave reads its h fragments once; the
+//     partial sums meet in LDS; epilogue: RoPE on q / k rows, q / k / v published tagged (K/V also into the cache
+//     at pos), act = silu(gate) * up kept in LDS for the block's own MLP channels
+//   streamers: the w_down columns of those channels (16-column slices) times act -> a partial down output for all
+//     2048 rows, published tagged (each x-row owner sums the partials of all blocks for its rows)
+//   wave 0: q of its KV head (+ k, v at pos) -> LDS;  streamers: one flash-decoding split over the cached slots,
+//     partial (m, l, o / l) published tagged
+//   wave 0 of head h's combiner block: merges the head's split partials -> attention output, published tagged
+//   wave 0: its 8 rows of the down partials of all blocks; the attention output (all heads) -> LDS
+//   streamers: its 8 rows of w_o . attn;  wave 0: x rows = x + o + d (each rounded once, as add_ln), published
 // After the last layer: final LayerNorm and the int8 audio head (rows split over blocks); pos += 1.
 //
-// Cross-block data: everything one block writes for another within the step (q, K/V at pos, act, attention
-// partials and output, x) is stored with agent-scope atomic stores and read with agent-scope atomic loads, which
-// bypass the per-XCD (non-coherent) L2. A barrier is then only: wait for the block's stores to complete, publish an
-// epoch in the block's own arrival word; block 0 gathers the arrivals and publishes a release word the others poll
-// — no L2 write-back / invalidate (measured ~9 us each). The weights of each phase are issued before the barrier
-// in front of it, so they stream in while the block waits.
-// Every wait is bounded by wall-clock time: on timeout the kernel sets an abort bit in `status` and every later
-// barrier returns at once, so the grid always drains.
+// Every wait is bounded by wall-clock time (200 ms): on expiry the kernel sets an abort bit in `status`, every
+// later wait returns at once and the grid drains with garbage results.
 #include "dequant.h"
 
 namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kH = 2048;             // hidden size (compile-time: tiles and LDS staging are sized for it)
-constexpr int kHD = 128;             // head dim
-constexpr int kNG = kH / 128;        // groups of a 2048-long row
+constexpr int kStreamers = kWaves - 1;
+constexpr int kSLanes = 64 * kStreamers;  // 448 streamer lanes
+constexpr int kH = 2048;                   // hidden size (compile-time: tiles and staging are sized for it)
+constexpr int kHD = 128;                   // head dim
+constexpr int kNG = kH / 128;              // column groups of a w_in row
 constexpr int kMaxRep = 8;
-constexpr uint64_t kBarrierTicks = 20000000ull;  // 200 ms at the 100 MHz wall clock
+constexpr int kMaxTiles = 7;               // w_in tiles per block
+constexpr int kGPW = 3;                    // column groups per streamer (16 = 3 + 3 + 2 * 5)
+constexpr int kMaxSlices = 3;              // w_down 16-column slices per block
+constexpr int kRP = (kH / 2 + kSLanes - 1) / kSLanes;  // down row pairs per streamer lane (3)
+constexpr int kKVPre = 10;                 // cached slots per streamer whose K / V are loaded ahead
+constexpr int kHeadRows = 10;              // head rows per streamer loaded ahead
+constexpr int kWork = 16;                  // int16 entries per block in the work table
+constexpr uint64_t kWaitTicks = 20000000ull;  // 200 ms at the 100 MHz wall clock
 constexpr unsigned kAbort = 1u, kTimeout = 2u, kBadPos = 4u;
 
 typedef rk_decode_params Params;
@@ -45,22 +61,6 @@ RK_DEV float h16(uint16_t b) { return f16_bits_to_f32(b); }
 RK_DEV uint16_t f16b(float v) { return f32_to_f16_bits(v); }
 RK_DEV float rnd16(float v) { return (float)(_Float16)v; }
 
-// ---------------------------------------------------------------------------------------------- coherent access
-RK_DEV void st_coh(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-RK_DEV void st_coh_f(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-RK_DEV uint32_t ld_coh(const uint32_t* p) {
-    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-RK_DEV float ld_coh_f(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-RK_DEV uint64_t ld_coh64(const uint64_t* p) {
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-RK_DEV void st_coh64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-RK_DEV uint64_t pack_f2(float a, float b) {
-    return (uint64_t)__builtin_bit_cast(uint32_t, a) | ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
-}
 RK_DEV uint32_t pack_h2(float a, float b) {
     h2_t v;
     v.x = (_Float16)a;
@@ -68,74 +68,107 @@ RK_DEV uint32_t pack_h2(float a, float b) {
     return as_u32(v);
 }
 
-// ---------------------------------------------------------------------------------------------- grid barrier
-// flags[b] holds the last barrier epoch block b arrived at; the release word after them (own 128-byte line) holds
-// the last epoch every block has reached. Block 0's first wave gathers the arrivals and publishes the release; the
-// other blocks poll only the release word (one line polled by all, measured faster than all-poll-all).
-RK_DEV int release_index(int nblocks) { return (nblocks + 31) & ~31; }
+// ---------------------------------------------------------------------------------------------- coherent access
+RK_DEV void st_coh(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+RK_DEV uint32_t ld_coh(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+RK_DEV uint64_t ld_coh64(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+RK_DEV void st_coh64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
-RK_DEV bool wait_epoch(const uint32_t* w, unsigned epoch, const Params& p, uint64_t t0) {
-    while ((int)(ld_coh(w) - epoch) < 0) {
-        if (ld_coh(p.status) & kAbort) return false;
-        if (wall_clock64() - t0 > kBarrierTicks) {
-            atomicOr(p.status, kAbort | kTimeout);
-            return false;
-        }
+// ---------------------------------------------------------------------------------------------- tagged words
+RK_DEV uint32_t tag_of(uint32_t step, int l) { return 1u + (step * 64u + (uint32_t)l) % 65535u; }
+RK_DEV uint32_t tword(float v, uint32_t tag) { return (uint32_t)f16b(v) | (tag << 16); }
+RK_DEV uint64_t tpair(float a, float b, uint32_t tag) {
+    return (uint64_t)tword(a, tag) | ((uint64_t)tword(b, tag) << 32);
+}
+RK_DEV bool pair_ok(uint64_t q, uint32_t tag) {
+    return (uint32_t)((q >> 16) & 0xFFFFu) == tag && (uint32_t)(q >> 48) == tag;
+}
+// the two fp16 values of a tagged pair as one packed fp16x2 dword
+RK_DEV uint32_t pair_val(uint64_t q) { return (uint32_t)(q & 0xFFFFu) | ((uint32_t)(q >> 16) & 0xFFFF0000u); }
+
+// true while a wait may go on; on expiry raise the abort bit
+RK_DEV bool wait_more(const Params& p, uint64_t t0) {
+    if (ld_coh(p.status) & kAbort) return false;
+    if (wall_clock64() - t0 > kWaitTicks) {
+        if ((threadIdx.x & 63) == 0) atomicOr(p.status, kAbort | kTimeout);
+        return false;
     }
+    __builtin_amdgcn_s_sleep(1);
     return true;
 }
 
-// Arrival: every wave's coherent stores have completed (vmcnt counts loads too, so this comes before the next
-// phase's weight loads are issued), then the block publishes the epoch.
-RK_DEV void grid_arrive(const Params& p, unsigned epoch) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) st_coh(p.flags + blockIdx.x, epoch);
-}
-
-// Wait for the release of `epoch`, polled by wave 0 only: vector memory results return in issue order, so a wave
-// with weight loads in flight could not see the release before they land. Wave 0 issues its own share of the next
-// phase's loads after this returns.
-RK_DEV void grid_wait(const Params& p, unsigned epoch) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const uint64_t t0 = wall_clock64();
-        uint32_t* release = p.flags + release_index(gridDim.x);
-        if (blockIdx.x == 0) {
-            bool done = false;
-            while (!done) {  // every iteration has all of the lane's arrival words in flight at once
-                bool ok = true;
-                for (int b = lane; b < (int)gridDim.x; b += 64) ok &= (int)(ld_coh(p.flags + b) - epoch) >= 0;
-                done = __all(ok);
-                if (!done && (ld_coh(p.status) & kAbort)) break;
-                if (!done && wall_clock64() - t0 > kBarrierTicks) {
-                    if (lane == 0) atomicOr(p.status, kAbort | kTimeout);
-                    break;
-                }
+// Poll N tagged fp16 pairs per lane (qword addresses from addr(k); nullptr = not needed) until every tag matches;
+// val[k] receives the packed pair. Wave-uniform control flow; false after an abort or a timeout.
+template <int N, class Addr>
+RK_DEV bool poll_pairs(const Params& p, uint32_t tag, Addr addr, uint32_t (&val)[N]) {
+    static_assert(N <= 32, "pending mask");
+    uint32_t pending = 0;
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+        if (addr(k)) pending |= 1u << k;
+    const uint64_t t0 = wall_clock64();
+    while (true) {
+        uint64_t q[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (pending & (1u << k)) q[k] = ld_coh64(addr(k));
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if ((pending & (1u << k)) && pair_ok(q[k], tag)) {
+                val[k] = pair_val(q[k]);
+                pending &= ~(1u << k);
             }
-            if (lane == 0 && done) st_coh(release, epoch);
-        } else if (lane == 0) {
-            wait_epoch(release, epoch, p, t0);
-        }
+        if (__all(pending == 0)) return true;
+        if (!wait_more(p, t0)) return false;
     }
-    __syncthreads();
 }
 
 // ---------------------------------------------------------------------------------------------- LDS layout
 struct Lds {
-    uint4 hfrag[kH / 8];        // MFMA A fragments of h (phase A)
-    float hsum[kNG];
-    uint4 vecp[11008 / 8 + 8];  // permuted pairs of act (phase B) / ob (phase C) / natural pairs (head), per 8 cols
-    float vsum[11008 / 32 + 8];
-    float drow[kWaves];         // this block's down rows (phase B -> C)
-    float xrow[kWaves];         // this block's rows of the residual stream (kept across layers)
-    float s_m[kWaves][kMaxRep], s_l[kWaves][kMaxRep];
-    float2 s_acc[kWaves][kMaxRep][64];  // the waves' partial attention outputs; then the combine's partial sums
-    float c_m[kWaves], c_l[kWaves];     // the combine's per-wave running max / denominator
-    int flag;
+    uint4 hfrag[kH / 8];                      // MFMA A fragments of h
+    float hsum[kNG];                          // per-group sums of h
+    float tpart[kStreamers][kMaxTiles][16];   // K-split partial dots of the block's tiles
+    float ty[kMaxTiles][16];                  // the tiles' projection outputs (rounded)
+    float act[kMaxSlices * 16];               // act of the block's MLP channels
+    uint32_t qs[kMaxRep][64];                 // q pairs of the block's KV head
+    uint32_t knew[64], vnew[64];              // k, v at pos of that KV head
+    float s_m[kStreamers][kMaxRep], s_l[kStreamers][kMaxRep];
+    float2 s_acc[kStreamers][kMaxRep][64];    // per-streamer attention partials
+    uint4 vecp[kH / 8];                       // attention output (permuted pairs) / h (natural pairs, head)
+    float vsum[kH / 32];                      // per-32-column sums of the attention output
+    uint32_t cst[32][64];                     // the combine's validated split outputs (one batch)
+    float orow[8], drow[8], xrow[8];          // this block's rows of o, down and the residual stream
+    int16_t work[kWork];
 };
 
-// x as held by wave 0 for its LayerNorm: lane holds the 8-column blocks i = lane + 64k, k < 4
+// ---------------------------------------------------------------------------------------------- block work
+struct Work {
+    int nt;     // w_in tiles
+    int sb, se; // down slices [sb, se)
+    int comb;   // head this block combines (-1: none)
+};
+
+RK_DEV Work work_of(const Lds& S) {
+    Work w;
+    w.nt = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxTiles; ++t) w.nt += S.work[t] >= 0;
+    w.sb = S.work[8];
+    w.se = S.work[9];
+    w.comb = S.work[10];
+    return w;
+}
+
+// streamer sw's column groups of every tile: {0, 1, 2}, {3, 4, 5}, then pairs {2sw + 2, 2sw + 3}
+RK_DEV int group0(int sw) { return sw < 2 ? 3 * sw : 2 * sw + 2; }
+RK_DEV int n_groups(int sw) { return sw < 2 ? 3 : 2; }
+
+// ---------------------------------------------------------------------------------------------- x / h (wave 0)
+// lane holds the 8-column blocks i = lane + 64k, k < 4
 struct XWave {
     float v[4][8];
 };
@@ -155,25 +188,24 @@ RK_DEV void x_from_embedding(const Params& p, int64_t tok, XWave& xw) {
     }
 }
 
-// the residual stream written by all blocks (coherent loads)
-RK_DEV void x_load(const Params& p, XWave& xw) {
+RK_DEV bool x_poll(const Params& p, uint32_t tag, XWave& xw) {
     const int lane = threadIdx.x & 63;
-    const uint64_t* xs = reinterpret_cast<const uint64_t*>(p.x);
-    uint64_t d[4][2];
+    const uint64_t* tx = reinterpret_cast<const uint64_t*>(p.tx);
+    uint32_t v[16];
+    const bool ok = poll_pairs<16>(
+        p, tag, [&](int k) -> const uint64_t* { return tx + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v);
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) d[k][h] = ld_coh64(xs + 2 * (lane + 64 * k) + h);
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint16_t b = (uint16_t)(d[k][e >> 2] >> (16 * (e & 3)));
-            xw.v[k][e] = h16(b);
+        for (int e = 0; e < 4; ++e) {
+            const h2_t h = as_h2(v[4 * k + e]);
+            xw.v[k][2 * e] = (float)h.x;
+            xw.v[k][2 * e + 1] = (float)h.y;
         }
+    return ok;
 }
 
-// h = round(LN(x) * w) over the 2048 values of the wave (biased variance, the reference's LayerNorm)
+// h = round(LN(x) * w) (biased variance, the reference's LayerNorm, engine/rumik_int4.py:38-43)
 RK_DEV void layernorm_wave(XWave& xw, const uint16_t* w, float eps) {
     const int lane = threadIdx.x & 63;
     float s = 0.f;
@@ -202,7 +234,7 @@ RK_DEV void layernorm_wave(XWave& xw, const uint16_t* w, float eps) {
     }
 }
 
-// h -> MFMA A fragments + per-group sums in LDS (wave 0)
+// h -> MFMA A fragments (pairs permuted as the dequant orders the codes) + per-group sums
 RK_DEV void stage_h_frag(const XWave& xw, Lds& S) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -218,8 +250,7 @@ RK_DEV void stage_h_frag(const XWave& xw, Lds& S) {
         float sum = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) sum += xw.v[k][e];
-        // 16 lanes = one 128-column group, inside one DPP row
-        sum += dpp<0x128>(sum);
+        sum += dpp<0x128>(sum);  // 16 lanes = one 128-column group, inside one DPP row
         sum += dpp<0x124>(sum);
         sum += dpp<0x122>(sum);
         sum += dpp<0x121>(sum);
@@ -227,244 +258,326 @@ RK_DEV void stage_h_frag(const XWave& xw, Lds& S) {
     }
 }
 
-// an fp16 vector of n (multiple of 32) values written by other blocks -> permuted pairs per 8 columns + fp32
-// sums per 32 columns, in LDS (for the VALU row dots of phases B / C)
-RK_DEV void stage_vec_pairs(const uint16_t* src, int n, Lds& S) {
-    const int nb = n >> 3;
-    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
-    for (int base = 0; base < nb; base += kThreads) {
-        const int i = base + threadIdx.x;
-        float sum = 0.f;
-        if (i < nb) {
-            u4_t d;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) d[e] = ld_coh(s32 + 4 * i + e);
-            uint32_t hp[4];
-            pair_permute(d, hp);
-            S.vecp[i] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-            const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
-        }
-        sum += dpp<0xB1>(sum);  // 4 consecutive 8-blocks = one 32-column chunk
-        sum += dpp<0x4E>(sum);
-        if (i < nb && (i & 3) == 0) S.vsum[i >> 2] = sum;
-    }
-}
-
-// One int4 row of length K (K % 32 == 0) by one wave: the codes / scales are loaded first (RowPrefetch), the dot
-// runs once the activation vector is staged by stage_vec_pairs.
-template <int NJ>
-struct RowPrefetch {
-    u4_t w[NJ];
-    uint16_t s[NJ], m[NJ];
+// ---------------------------------------------------------------------------------------------- w_in tiles
+struct TileRegs {
+    u4_t w[kGPW][kMaxTiles];
+    uint32_t sm[kGPW][kMaxTiles];  // scale | min << 16 of (group, tile) for row lane % 16
 };
 
-template <int NJ>
-RK_DEV void row_prefetch(RowPrefetch<NJ>& rp, const uint8_t* q, const uint16_t* sc, const uint16_t* mn, int row,
-                         int K) {
-    const int lane = threadIdx.x & 63, nch = K >> 5, ng = K >> 7;
-    const u4_t* qr = reinterpret_cast<const u4_t*>(q + (size_t)row * (K >> 1));
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nch) {
-            rp.w[j] = __builtin_nontemporal_load(qr + c);
-            rp.s[j] = sc[(size_t)row * ng + (c >> 2)];
-            rp.m[j] = mn[(size_t)row * ng + (c >> 2)];
-        } else {
-            rp.w[j] = u4_t{0u, 0u, 0u, 0u};
-            rp.s[j] = 0;
-            rp.m[j] = 0;
-        }
-    }
-}
+RK_DEV size_t n_tiles(const Params& p) { return ((size_t)(p.NH + 2 * p.NKV) * kHD + 2 * p.inter) / 16; }
 
-template <int NJ>
-RK_DEV float row_dot(const RowPrefetch<NJ>& rp, int K, const Lds& S, const Int4Masks& km) {
-    const int lane = threadIdx.x & 63, nch = K >> 5;
-    float acc = 0.f;
+// win_t: per (layer, tile, group) 1 KiB of codes in lane order; win_sm: per (layer, tile, row) the 16 groups'
+// scale | min << 16, so a streamer's consecutive groups of one row come in one or two loads
+RK_DEV void tile_issue(const Params& p, int l, const Lds& S, const Work& wk, TileRegs& tr) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
+    const int g0 = group0(sw), ng = n_groups(sw);
+    const size_t base = (size_t)l * n_tiles(p);
+    // every register is written on every path (zero when unused), so no value lives across iterations
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nch) {
-            uint32_t xp[16];
+    for (int t = 0; t < kMaxTiles; ++t) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint4 v = S.vecp[c * 4 + k];
-                xp[4 * k] = v.x; xp[4 * k + 1] = v.y; xp[4 * k + 2] = v.z; xp[4 * k + 3] = v.w;
+        for (int k = 0; k < kGPW; ++k) {
+            tr.w[k][t] = u4_t{0u, 0u, 0u, 0u};
+            tr.sm[k][t] = 0u;
+        }
+        if (t < wk.nt) {
+            const size_t T = base + S.work[t];
+#pragma unroll
+            for (int k = 0; k < kGPW; ++k)
+                if (k < ng)
+                    tr.w[k][t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.win_t) +
+                                                            (T * kNG + g0 + k) * 64 + lane);
+            const uint32_t* sm = p.win_sm + (T * 16 + (lane & 15)) * kNG + g0;
+            if (sw == 1) {  // groups 3 | 4, 5
+                tr.sm[0][t] = sm[0];
+                const u2_t v = *reinterpret_cast<const u2_t*>(sm + 1);
+                tr.sm[1][t] = v.x;
+                tr.sm[2][t] = v.y;
+            } else {  // groups g0, g0 + 1 (| g0 + 2 for streamer 0)
+                const u2_t v = *reinterpret_cast<const u2_t*>(sm);
+                tr.sm[0][t] = v.x;
+                tr.sm[1][t] = v.y;
+                if (sw == 0) tr.sm[2][t] = sm[2];
             }
-            const float d = chunk_dot_int4(rp.w[j], xp, km);
-            acc = __builtin_fmaf(d, h16(rp.s[j]), __builtin_fmaf(h16(rp.m[j]), S.vsum[c], acc));
-        }
-    }
-    return wave_sum(acc);
-}
-
-RK_DEV int split_chunk(int n, int nsp) { return ((n + nsp - 1) / nsp + 7) & ~7; }
-
-// ---------------------------------------------------------------------------------------------- phase A
-// one 16-row tile of w_in: codes / scales of all 16 groups, loaded before anything else
-struct TileLoad {
-    u4_t w[kNG];
-    u4_t s8[kNG / 8], m8[kNG / 8];
-};
-
-RK_DEV void tile_load(TileLoad& tl, const uint8_t* wq, const uint16_t* ws, const uint16_t* wm, int row, int s) {
-    const uint8_t* qr = wq + (size_t)row * (kH / 2) + 16 * s;
-#pragma unroll
-    for (int g = 0; g < kNG; ++g) tl.w[g] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(qr + 64 * g));
-#pragma unroll
-    for (int b = 0; b < kNG / 8; ++b) {
-        tl.s8[b] = reinterpret_cast<const u4_t*>(ws + (size_t)row * kNG)[b];
-        tl.m8[b] = reinterpret_cast<const u4_t*>(wm + (size_t)row * kNG)[b];
-    }
-}
-
-RK_DEV void tile_compute(const Params& p, int l, int tile, const TileLoad& tl, int64_t pos, bool rope,
-                         const Lds& S, const Int4Masks& km) {
-    const int lane = threadIdx.x & 63, j = lane & 15, s = lane >> 4;
-    const int row = tile * 16 + j;
-    const int NH = p.NH, NKV = p.NKV;
-    float acc = 0.f;
-#pragma unroll
-    for (int g = 0; g < kNG; ++g) {
-        f4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const h8_t A = __builtin_bit_cast(h8_t, S.hfrag[g * 16 + t * 4 + s]);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag(tl.w[g][t], km), d, 0, 0, 0);
-        }
-        const uint16_t sb = (uint16_t)(tl.s8[g >> 3][(g & 7) >> 1] >> (16 * (g & 1)));
-        const uint16_t mb = (uint16_t)(tl.m8[g >> 3][(g & 7) >> 1] >> (16 * (g & 1)));
-        acc = __builtin_fmaf(d[0], h16(sb), __builtin_fmaf(h16(mb), S.hsum[g], acc));
-        __builtin_amdgcn_sched_barrier(0);  // keep one group's fragments live at a time
-    }
-    // ---- epilogue: the projection output is rounded to fp16 first (the reference's buf_in)
-    const float y = rnd16(acc);
-    const float partner = dpp<0xB1>(y);  // lane j ^ 1: the other element of a RoPE pair
-    const float upv = dpp<0x128>(y);     // lane (j + 8) % 16: the up row of gate row j (j < 8)
-    const int qk_rows = (NH + NKV) * kHD, v_end = (NH + 2 * NKV) * kHD;
-    float out = y;
-    if (row < qk_rows && rope) {
-        const int dd = row % kHD;
-        const float c = h16(p.cos_t[(size_t)pos * kHD + (dd & ~1)]);
-        const float sn = h16(p.sin_t[(size_t)pos * kHD + (dd & ~1)]);
-        out = (dd & 1) ? (y * c + partner * sn) : (y * c - partner * sn);
-    } else if (row >= v_end) {
-        out = y / (1.0f + __expf(-y)) * upv;  // lanes j < 8: act of channel 8 * (tile index) + j
-    }
-    out = rnd16(out);
-    const float out1 = dpp<0xB1>(out);  // the odd neighbour: even lanes store (out, out1) as one dword
-    if (lane < 16 && (j & 1) == 0) {
-        const uint32_t pr = pack_h2(out, out1);
-        if (row < NH * kHD) {
-            st_coh(reinterpret_cast<uint32_t*>(p.qbuf) + row / 2, pr);
-        } else if (row < v_end) {
-            const bool is_k = row < qk_rows;
-            const int r2 = is_k ? row - NH * kHD : row - qk_rows;
-            const int kvh = r2 / kHD, dd = r2 % kHD;
-            uint16_t* cache = is_k ? p.kc : p.vc;
-            st_coh(reinterpret_cast<uint32_t*>(cache + (((size_t)l * NKV + kvh) * p.S + pos) * kHD + dd), pr);
-        } else if (j < 8) {
-            const int ch = ((row - v_end) >> 4) * 8 + j;
-            st_coh(reinterpret_cast<uint32_t*>(p.act) + ch / 2, pr);
         }
     }
 }
 
-// this wave's first w_in tile of layer l (the caller issues it before the barrier that precedes phase A)
-struct TileRange {
-    int t0, t1;
-};
-
-RK_DEV TileRange tile_range(const Params& p) {
-    const int n_in = (p.NH + 2 * p.NKV) * kHD + 2 * p.inter;
-    const int ntiles = n_in / 16;
-    return {(int)((long long)blockIdx.x * ntiles / gridDim.x), (int)((long long)(blockIdx.x + 1) * ntiles / gridDim.x)};
+// the streamer's groups of every tile -> S.tpart[sw][t][row]
+RK_DEV void tile_compute(const TileRegs& tr, const Work& wk, Lds& S) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1, s = lane >> 4;
+    const int g0 = group0(sw), ng = n_groups(sw);
+    const Int4Masks km = int4_masks();
+    float acc[kMaxTiles];
+#pragma unroll
+    for (int t = 0; t < kMaxTiles; ++t) acc[t] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kGPW; ++k) {
+        if (k < ng) {
+            const int g = g0 + k;
+            h8_t A[4];
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) A[t4] = __builtin_bit_cast(h8_t, S.hfrag[g * 16 + t4 * 4 + s]);
+            const float hs = S.hsum[g];
+#pragma unroll
+            for (int t = 0; t < kMaxTiles; ++t) {
+                if (t < wk.nt) {
+                    f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t4 = 0; t4 < 4; ++t4)
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t4], dequant_frag(tr.w[k][t][t4], km), d, 0, 0,
+                                                                   0);
+                    const uint32_t sm = tr.sm[k][t];
+                    acc[t] = __builtin_fmaf(d[0], h16((uint16_t)sm),
+                                            __builtin_fmaf(h16((uint16_t)(sm >> 16)), hs, acc[t]));
+                    __builtin_amdgcn_sched_barrier(0);  // one (group, tile) chain's fragments live at a time
+                }
+            }
+        }
+    }
+    if (lane < 16)
+#pragma unroll
+        for (int t = 0; t < kMaxTiles; ++t)
+            if (t < wk.nt) S.tpart[sw][t][lane] = acc[t];
 }
 
-// wave w's first tile: waves 1..7 take the block's first seven tiles, wave 0 (which polls the barriers and issues
-// its loads last) an eighth if there is one
-RK_DEV int first_tile(const TileRange& tr) { return tr.t0 + ((threadIdx.x >> 6) + kWaves - 1) % kWaves; }
-
-RK_DEV void tile_issue(const Params& p, int l, TileLoad& tl) {
-    const int lane = threadIdx.x & 63;
-    const TileRange tr = tile_range(p);
-    const int tile = first_tile(tr);
-    const size_t n_in = (size_t)(p.NH + 2 * p.NKV) * kHD + 2 * p.inter;
-    if (tile < tr.t1)
-        tile_load(tl, p.win_q + (size_t)l * n_in * (kH / 2), p.win_s + (size_t)l * n_in * kNG,
-                  p.win_m + (size_t)l * n_in * kNG, tile * 16 + (lane & 15), lane >> 4);
-}
-
-RK_DEV void phase_a(const Params& p, int l, TileLoad& tl, int64_t tok, int64_t pos, Lds& S) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int j = lane & 15, s = lane >> 4;
-    const size_t n_in = (size_t)(p.NH + 2 * p.NKV) * kHD + 2 * p.inter;
-    const TileRange tr = tile_range(p);
-    const int tile = first_tile(tr);
-
-    if (tid < 64) {  // wave 0: gather x, LayerNorm, stage h (the other waves' tiles are landing meanwhile)
-        XWave xw;
-        if (l == 0)
-            x_from_embedding(p, tok, xw);
-        else
-            x_load(p, xw);
-        layernorm_wave(xw, p.ln_w + (size_t)l * kH, p.eps);
-        stage_h_frag(xw, S);
+// thread (t, j): the tile row's output, its epilogue and its publication
+RK_DEV void tile_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, const Work& wk, Lds& S) {
+    const int tid = threadIdx.x;
+    const int t = tid >> 4, j = tid & 15;
+    const bool mine = t < wk.nt;
+    if (mine) {
+        float y = 0.f;
+#pragma unroll
+        for (int w = 0; w < kStreamers; ++w) y += S.tpart[w][t][j];
+        S.ty[t][j] = rnd16(y);  // the projection output in fp16 (the reference's buf_in)
     }
     __syncthreads();
-
-    const Int4Masks km = int4_masks();
-    const bool rope = (p.sliding >> l) & 1ull;
-    if (tile < tr.t1) tile_compute(p, l, tile, tl, pos, rope, S, km);
-    for (int t2 = tile + kWaves; t2 < tr.t1; t2 += kWaves) {  // blocks with more tiles than waves
-        tile_load(tl, p.win_q + (size_t)l * n_in * (kH / 2), p.win_s + (size_t)l * n_in * kNG,
-                  p.win_m + (size_t)l * n_in * kNG, t2 * 16 + j, s);
-        tile_compute(p, l, t2, tl, pos, rope, S, km);
+    if (!mine) return;
+    const int NH = p.NH, NKV = p.NKV;
+    const int T = S.work[t];
+    const int row = T * 16 + j;
+    const int qk_rows = (NH + NKV) * kHD, v_end = (NH + 2 * NKV) * kHD;
+    const float y = S.ty[t][j];
+    if (row < qk_rows) {
+        float out = y;
+        if ((p.sliding >> l) & 1ull) {  // interleaved RoPE: pairs (2i, 2i + 1)
+            const int dd = row % kHD;
+            const float c = h16(p.cos_t[(size_t)pos * kHD + (dd & ~1)]);
+            const float sn = h16(p.sin_t[(size_t)pos * kHD + (dd & ~1)]);
+            const float partner = S.ty[t][j ^ 1];
+            out = (dd & 1) ? (y * c + partner * sn) : (y * c - partner * sn);
+        }
+        out = rnd16(out);
+        if (row < NH * kHD) {
+            st_coh(p.tq + row, tword(out, tag));
+        } else {
+            const int r2 = row - NH * kHD;
+            st_coh(p.tkv + r2, tword(out, tag));
+            p.kc[(((size_t)l * NKV + r2 / kHD) * p.S + pos) * kHD + r2 % kHD] = f16b(out);
+        }
+    } else if (row < v_end) {
+        const int r2 = row - qk_rows;
+        st_coh(p.tkv + NKV * kHD + r2, tword(y, tag));
+        p.vc[(((size_t)l * NKV + r2 / kHD) * p.S + pos) * kHD + r2 % kHD] = f16b(y);
+    } else if (j < 8) {  // gate row j, up row j + 8 of MLP channel 8 * (tile - qkv tiles) + j
+        const float up = S.ty[t][j + 8];
+        const int ch = (T - v_end / 16) * 8 + j;
+        if (ch >= wk.sb * 16 && ch < wk.se * 16) S.act[ch - wk.sb * 16] = rnd16(y / (1.0f + __expf(-y)) * up);
     }
 }
 
-// ---------------------------------------------------------------------------------------------- phase B
-template <int REP>
-RK_DEV void attention_split(const Params& p, int l, int64_t pos, Lds& S) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nsp = p.nsp, g = blockIdx.x / nsp, sp = blockIdx.x % nsp;
-    const int n = (int)min<int64_t>(pos + 1, (int64_t)p.S);
-    const int ch = split_chunk(n, nsp);
-    const int start = sp * ch, end = min(start + ch, n);
-    h2_t qv[REP];
+// ---------------------------------------------------------------------------------------------- w_down slices
+// streamer lane sl takes the row pairs rp = sl + 448k (rows 2rp, 2rp + 1): per slice one 16-byte load of codes
+// (wd_t: per (layer, slice), 2048 rows x 8 bytes), per 128-column group one 8-byte load of scale | min << 16
+struct DownRegs {
+    u4_t c[kRP][kMaxSlices];
+    u2_t sm[kRP][2];  // the block's slices span at most two groups
+};
+
+RK_DEV void down_issue(const Params& p, int l, const Work& wk, DownRegs& dr) {
+    const int sl = threadIdx.x - 64;
+    const int nsl = p.inter / 16, ngd = p.inter / 128;
+    const int gb = wk.sb / 8, ge = (wk.se - 1) / 8;
 #pragma unroll
-    for (int r = 0; r < REP; ++r)
-        qv[r] = as_h2(ld_coh(reinterpret_cast<const uint32_t*>(p.qbuf + (size_t)(g * REP + r) * kHD) + lane));
-    float m[REP], lsum[REP];
-    float2 acc[REP];
+    for (int k = 0; k < kRP; ++k) {
+        const int rp = sl + kSLanes * k;
 #pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        m[r] = -INFINITY;
-        lsum[r] = 0.f;
-        acc[r] = make_float2(0.f, 0.f);
+        for (int i = 0; i < kMaxSlices; ++i) dr.c[k][i] = u4_t{0u, 0u, 0u, 0u};
+        dr.sm[k][0] = dr.sm[k][1] = u2_t{0u, 0u};
+        if (rp < kH / 2) {
+#pragma unroll
+            for (int i = 0; i < kMaxSlices; ++i)
+                if (wk.sb + i < wk.se)
+                    dr.c[k][i] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wd_t) +
+                                                            ((size_t)l * nsl + wk.sb + i) * (kH / 2) + rp);
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                if (gb + q <= ge)
+                    dr.sm[k][q] = *reinterpret_cast<const u2_t*>(p.wd_sm + ((size_t)l * ngd + gb + q) * kH + 2 * rp);
+        }
     }
-    const size_t base = (((size_t)l * p.NKV + g) * p.S) * kHD;
+}
+
+// partial down output of this block's channels for all 2048 rows, published tagged (tdp[block][row])
+RK_DEV void down_compute(const Params& p, uint32_t tag, const Work& wk, const DownRegs& dr, const Lds& S) {
+    const int sl = threadIdx.x - 64;
+    const Int4Masks km = int4_masks();
+    const int gb = wk.sb / 8;
+    uint32_t xp[kMaxSlices][8];
+    float asum[kMaxSlices];
+#pragma unroll
+    for (int i = 0; i < kMaxSlices; ++i) {
+        asum[i] = 0.f;
+        const float* a = S.act + 16 * i;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)  // dword e holds codes 8e..8e+7: pairs (a0, a4), (a1, a5), ...
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xp[i][4 * e + k] = pack_h2(a[8 * e + k], a[8 * e + k + 4]);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) asum[i] += a[c];
+    }
+    uint64_t* out = reinterpret_cast<uint64_t*>(p.tdp + (size_t)blockIdx.x * kH);
+#pragma unroll
+    for (int k = 0; k < kRP; ++k) {
+        const int rp = sl + kSLanes * k;
+        if (rp < kH / 2) {
+            float d[2] = {0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < kMaxSlices; ++i) {
+                if (wk.sb + i < wk.se) {
+                    const int q = (wk.sb + i) / 8 - gb;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {  // row 2rp + h: dwords 2h, 2h + 1
+                        float dot = 0.f;
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            h2_t pr[4];
+                            dequant_pairs(dr.c[k][i][2 * h + e], km, pr);
+#pragma unroll
+                            for (int kk = 0; kk < 4; ++kk) dot = dot2(pr[kk], as_h2(xp[i][4 * e + kk]), dot);
+                        }
+                        const uint32_t sm = q == 0 ? dr.sm[k][0][h] : dr.sm[k][1][h];
+                        d[h] = __builtin_fmaf(dot, h16((uint16_t)sm),
+                                              __builtin_fmaf(h16((uint16_t)(sm >> 16)), asum[i], d[h]));
+                    }
+                }
+            }
+            st_coh64(out + rp, tpair(d[0], d[1], tag));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- attention
+RK_DEV int split_chunk(int n, int nsp) { return ((n + nsp - 1) / nsp + 7) & ~7; }
+
+struct Split {
+    bool att;           // this block runs a split
+    int g, sp, start, end, n, ch;
+};
+
+RK_DEV Split split_of(const Params& p, int64_t pos) {
+    Split s;
+    s.att = (int)blockIdx.x < p.NKV * p.nsp;
+    s.g = s.att ? blockIdx.x / p.nsp : 0;
+    s.sp = s.att ? blockIdx.x % p.nsp : 0;
+    s.n = (int)min<int64_t>(pos + 1, (int64_t)p.S);
+    s.ch = split_chunk(s.n, p.nsp);
+    s.start = s.sp * s.ch;
+    s.end = s.att ? min(s.start + s.ch, s.n) : s.start;
+    return s;
+}
+
+struct KVRegs {
+    uint32_t k[kKVPre], v[kKVPre];
+};
+
+// cached slots start + sw + 7u (u < kKVPre) of this block's split; slot pos is read from the tagged copy
+RK_DEV void kv_issue(const Params& p, int l, int64_t pos, KVRegs& kv) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
+    const Split s = split_of(p, pos);
+    const size_t base = (((size_t)l * p.NKV + s.g) * p.S) * kHD;
     const uint32_t* kr = reinterpret_cast<const uint32_t*>(p.kc + base);
     const uint32_t* vr = reinterpret_cast<const uint32_t*>(p.vc + base);
-    constexpr int kB = 8;  // slots per wave whose K / V loads are in flight together
-    for (int tb = start + wave; tb < end; tb += kB * kWaves) {
-        uint32_t kw[kB], vw[kB];
 #pragma unroll
-        for (int u = 0; u < kB; ++u) {
-            const int t = tb + u * kWaves;
-            const size_t o = (size_t)min(t, end - 1) * (kHD / 2) + lane;
-            // slot pos was written in this step by another block: read it coherently; older slots: plain loads
-            kw[u] = t == pos ? ld_coh(kr + o) : kr[o];
-            vw[u] = t == pos ? ld_coh(vr + o) : vr[o];
+    for (int u = 0; u < kKVPre; ++u) {
+        const int t = s.start + sw + kStreamers * u;
+        kv.k[u] = kv.v[u] = 0u;
+        if (t < s.end && t != pos) {
+            kv.k[u] = kr[(size_t)t * (kHD / 2) + lane];
+            kv.v[u] = vr[(size_t)t * (kHD / 2) + lane];
         }
+    }
+}
+
+// wave 0: q of the block's KV head (REP heads) and, when the split holds pos, k / v at pos -> LDS
+RK_DEV bool q_poll(const Params& p, int rep, int64_t pos, uint32_t tag, Lds& S) {
+    const int lane = threadIdx.x & 63;
+    const Split s = split_of(p, pos);
+    if (!s.att) return true;
+    const bool has_pos = s.start <= pos && pos < s.end;
+    const uint64_t* tq = reinterpret_cast<const uint64_t*>(p.tq);
+    const uint64_t* tkv = reinterpret_cast<const uint64_t*>(p.tkv);
+    uint32_t v[kMaxRep + 2];
+    const bool ok = poll_pairs<kMaxRep + 2>(
+        p, tag,
+        [&](int k) -> const uint64_t* {
+            if (k < kMaxRep) return k < rep ? tq + (size_t)(s.g * rep + k) * (kHD / 2) + lane : nullptr;
+            if (!has_pos) return nullptr;
+            return tkv + (size_t)((k - kMaxRep) * p.NKV + s.g) * (kHD / 2) + lane;
+        },
+        v);
 #pragma unroll
-        for (int u = 0; u < kB; ++u) {
-            const int t = tb + u * kWaves;
-            if (t >= end) break;
-            const h2_t kp = as_h2(kw[u]), vp = as_h2(vw[u]);
+    for (int k = 0; k < kMaxRep; ++k)
+        if (k < rep) S.qs[k][lane] = v[k];
+    if (has_pos) {
+        S.knew[lane] = v[kMaxRep];
+        S.vnew[lane] = v[kMaxRep + 1];
+    }
+    return ok;
+}
+
+// streamers: online softmax over the split's slots for the REP heads, merged over the streamers in LDS, then the
+// normalized partial (o / l, m, l) of each head published tagged
+template <int REP>
+RK_DEV void attention(const Params& p, int l, int64_t pos, uint32_t tag, const KVRegs& kv, Lds& S) {
+    const int tid = threadIdx.x, lane = tid & 63, sw = (tid >> 6) - 1;
+    const Split s = split_of(p, pos);
+    if (sw >= 0) {
+        h2_t qv[REP];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) qv[r] = as_h2(S.qs[r][lane]);
+        float m[REP], lsum[REP];
+        float2 acc[REP];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+            m[r] = -INFINITY;
+            lsum[r] = 0.f;
+            acc[r] = make_float2(0.f, 0.f);
+        }
+        const size_t base = (((size_t)l * p.NKV + s.g) * p.S) * kHD;
+        const uint32_t* kr = reinterpret_cast<const uint32_t*>(p.kc + base);
+        const uint32_t* vr = reinterpret_cast<const uint32_t*>(p.vc + base);
+        for (int u = 0; s.start + sw + kStreamers * u < s.end; ++u) {
+            const int t = s.start + sw + kStreamers * u;
+            uint32_t kw, vw;
+            if (t == pos) {
+                kw = S.knew[lane];
+                vw = S.vnew[lane];
+            } else if (u < kKVPre) {
+                kw = kv.k[0];
+                vw = kv.v[0];
+#pragma unroll
+                for (int uu = 1; uu < kKVPre; ++uu)
+                    if (u == uu) {
+                        kw = kv.k[uu];
+                        vw = kv.v[uu];
+                    }
+            } else {  // beyond the prefetched slots (long contexts with few splits)
+                kw = kr[(size_t)t * (kHD / 2) + lane];
+                vw = vr[(size_t)t * (kHD / 2) + lane];
+            }
+            const h2_t kp = as_h2(kw), vp = as_h2(vw);
             float sc[REP];
 #pragma unroll
             for (int r = 0; r < REP; ++r) sc[r] = dot2(qv[r], kp, 0.f);
@@ -484,175 +597,239 @@ RK_DEV void attention_split(const Params& p, int l, int64_t pos, Lds& S) {
                 m[r] = mn;
             }
         }
-    }
 #pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        if (lane == 0) {
-            S.s_m[wave][r] = m[r];
-            S.s_l[wave][r] = lsum[r];
+        for (int r = 0; r < REP; ++r) {
+            if (lane == 0) {
+                S.s_m[sw][r] = m[r];
+                S.s_l[sw][r] = lsum[r];
+            }
+            S.s_acc[sw][r][lane] = acc[r];
         }
-        S.s_acc[wave][r][lane] = acc[r];
     }
     __syncthreads();
-    for (int r = wave; r < REP; r += kWaves) {
+    if (!s.att) return;
+    for (int e = tid - 64; e >= 0 && e < REP * 64; e += kSLanes) {  // streamer thread = (head r, dim pair d2)
+        const int r = e >> 6, d2 = e & 63;
         float M = -INFINITY;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, S.s_m[w2][r]);
+        for (int w = 0; w < kStreamers; ++w) M = fmaxf(M, S.s_m[w][r]);
         float Lt = 0.f, ax = 0.f, ay = 0.f;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
-            const float wt = S.s_m[w2][r] == -INFINITY ? 0.f : __expf(S.s_m[w2][r] - M);
-            Lt += wt * S.s_l[w2][r];
-            ax += wt * S.s_acc[w2][r][lane].x;
-            ay += wt * S.s_acc[w2][r][lane].y;
+        for (int w = 0; w < kStreamers; ++w) {
+            const float wt = S.s_m[w][r] == -INFINITY ? 0.f : __expf(S.s_m[w][r] - M);
+            Lt += wt * S.s_l[w][r];
+            ax += wt * S.s_acc[w][r][d2].x;
+            ay += wt * S.s_acc[w][r][d2].y;
         }
-        const size_t pi = (size_t)(g * REP + r) * nsp + sp;
-        st_coh64(reinterpret_cast<uint64_t*>(p.po + pi * kHD) + lane, pack_f2(ax, ay));
-        if (lane == 0) {
-            st_coh_f(p.pm + pi, M);
-            st_coh_f(p.pl + pi, Lt);
+        const size_t pi = (size_t)(s.g * REP + r) * p.nsp + s.sp;
+        const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
+        st_coh64(reinterpret_cast<uint64_t*>(p.tpo + pi * kHD) + d2, tpair(ax * inv, ay * inv, tag));
+        if (d2 == 0) {
+            st_coh64(reinterpret_cast<uint64_t*>(p.tml) + 2 * pi,
+                     (uint64_t)__builtin_bit_cast(uint32_t, M) | ((uint64_t)tag << 32));
+            st_coh64(reinterpret_cast<uint64_t*>(p.tml) + 2 * pi + 1,
+                     (uint64_t)__builtin_bit_cast(uint32_t, Lt) | ((uint64_t)tag << 32));
         }
     }
-    // ---- the last block of this KV head merges the nsp partials of its REP heads
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(p.grp_ctr + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        S.flag = old == (unsigned)(nsp - 1);
-        if (S.flag) __hip_atomic_store(p.grp_ctr + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!S.flag) return;
-    // wave w merges splits part, part + kParts, ... of head r (kParts waves per head, one dim pair per lane); every
-    // load of a batch is independent of the others, so a batch costs one memory round trip
-    constexpr int kParts = kWaves / REP;
-    const int na = min(nsp, (n + ch - 1) / ch);  // splits holding at least one slot
-    const int r = wave / kParts, part = wave % kParts;
-    const size_t hb = (size_t)(g * REP + r) * nsp;
-    const uint64_t* po2 = reinterpret_cast<const uint64_t*>(p.po + hb * kHD) + lane;
-    float M = -INFINITY, den = 0.f, nx = 0.f, ny = 0.f;
-    constexpr int kCB = 8;
-    for (int i0 = part; i0 < na; i0 += kCB * kParts) {
-        float mi[kCB], li[kCB];
-        uint64_t oi[kCB];
+}
+
+// wave 0 of head h's combiner: out = sum_i w_i o_i / sum_i w_i, w_i = exp(m_i - max m) * l_i over the splits
+// holding at least one slot; published tagged
+RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
+    const int lane = threadIdx.x & 63;
+    const int nsp = p.nsp;
+    const int n = (int)min<int64_t>(pos + 1, (int64_t)p.S);
+    const int ch = split_chunk(n, nsp);
+    const int na = min(nsp, (n + ch - 1) / ch);
+    const size_t hb = (size_t)h * nsp;
+    const uint64_t* tml = reinterpret_cast<const uint64_t*>(p.tml);
+    const uint64_t* po = reinterpret_cast<const uint64_t*>(p.tpo + hb * kHD) + lane;
+    const uint64_t t0 = wall_clock64();
+    // (m, l) of the splits lane, lane + 64, ... (nsp <= 256), then the o pairs of every split in batches of 32
+    float mi[4], li[4];
+    {
+        uint32_t pending = 0;
 #pragma unroll
-        for (int u = 0; u < kCB; ++u) {
-            const int i = min(i0 + u * kParts, na - 1);
-            mi[u] = ld_coh_f(p.pm + hb + i);
-            li[u] = ld_coh_f(p.pl + hb + i);
-            oi[u] = ld_coh64(po2 + (size_t)i * (kHD / 2));
+        for (int k = 0; k < 4; ++k) {
+            mi[k] = -INFINITY;
+            li[k] = 0.f;
+            if (lane + 64 * k < na) pending |= 1u << k;
         }
-        float bm = M;
+        while (true) {
 #pragma unroll
-        for (int u = 0; u < kCB; ++u)
-            if (i0 + u * kParts < na) bm = fmaxf(bm, mi[u]);
-        if (bm == -INFINITY) continue;  // only empty splits so far
-        const float a = __expf(M - bm);
-        den *= a;
-        nx *= a;
-        ny *= a;
+            for (int k = 0; k < 4; ++k) {
+                if (pending & (1u << k)) {
+                    const uint64_t a = ld_coh64(tml + 2 * (hb + lane + 64 * k));
+                    const uint64_t b = ld_coh64(tml + 2 * (hb + lane + 64 * k) + 1);
+                    if ((uint32_t)(a >> 32) == tag && (uint32_t)(b >> 32) == tag) {
+                        mi[k] = __builtin_bit_cast(float, (uint32_t)a);
+                        li[k] = __builtin_bit_cast(float, (uint32_t)b);
+                        pending &= ~(1u << k);
+                    }
+                }
+            }
+            if (__all(pending == 0)) break;
+            if (!wait_more(p, t0)) return false;
+        }
+    }
+    float M = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < kCB; ++u) {
-            if (i0 + u * kParts < na && mi[u] != -INFINITY) {
-                const float wt = __expf(mi[u] - bm);
-                den += wt * li[u];
-                nx += wt * __builtin_bit_cast(float, (uint32_t)oi[u]);
-                ny += wt * __builtin_bit_cast(float, (uint32_t)(oi[u] >> 32));
+    for (int k = 0; k < 4; ++k) M = fmaxf(M, mi[k]);
+    M = wave_max(M);
+    float wt[4], den = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        wt[k] = mi[k] == -INFINITY ? 0.f : __expf(mi[k] - M) * li[k];
+        den += wt[k];
+    }
+    den = wave_sum(den);
+    // o pairs of splits i0 .. i0 + 31 per batch: polled until every tag matches, staged in LDS, then summed in
+    // split order (the result does not depend on arrival order)
+    float ox = 0.f, oy = 0.f;
+    for (int i0 = 0; i0 < na; i0 += 32) {
+        uint32_t pending = 0;
+#pragma unroll
+        for (int k = 0; k < 32; ++k)
+            if (i0 + k < na) pending |= 1u << k;
+        while (true) {
+            uint64_t q[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k)
+                if (pending & (1u << k)) q[k] = ld_coh64(po + (size_t)(i0 + k) * (kHD / 2));
+#pragma unroll
+            for (int k = 0; k < 32; ++k)
+                if ((pending & (1u << k)) && pair_ok(q[k], tag)) {
+                    S.cst[k][lane] = pair_val(q[k]);
+                    pending &= ~(1u << k);
+                }
+            if (__all(pending == 0)) break;
+            if (!wait_more(p, t0)) return false;
+        }
+        const int kq = i0 >> 6;  // the wt register holding splits i0 .. i0 + 31 (i0 is a multiple of 32)
+        float wq = wt[0];
+#pragma unroll
+        for (int k = 1; k < 4; ++k)
+            if (kq == k) wq = wt[k];
+        for (int k = 0; k < 32 && i0 + k < na; ++k) {
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wq), (i0 & 63) + k));
+            const h2_t o = as_h2(S.cst[k][lane]);
+            ox = __builtin_fmaf(w, (float)o.x, ox);
+            oy = __builtin_fmaf(w, (float)o.y, oy);
+        }
+    }
+    const float inv = 1.0f / den;
+    st_coh64(reinterpret_cast<uint64_t*>(p.tob + (size_t)h * kHD) + lane, tpair(ox * inv, oy * inv, tag));
+    return true;
+}
+
+// wave 0: this block's 8 rows of the down partials of all blocks, summed -> S.drow
+RK_DEV bool down_gather(const Params& p, uint32_t tag, Lds& S) {
+    const int lane = threadIdx.x & 63;
+    float d[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) d[r] = 0.f;
+    const int nb = gridDim.x;
+    bool ok = true;
+    for (int c0 = 0; c0 < nb && ok; c0 += 256) {  // producers c = c0 + lane + 64k: 4 qwords (8 rows) each
+        uint32_t v[16];
+        ok = poll_pairs<16>(
+            p, tag,
+            [&](int k) -> const uint64_t* {
+                const int c = c0 + lane + 64 * (k >> 2);
+                return c < nb ? reinterpret_cast<const uint64_t*>(p.tdp + (size_t)c * kH + 8 * blockIdx.x) + (k & 3)
+                              : nullptr;
+            },
+            v);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            if (c0 + lane + 64 * (k >> 2) < nb) {
+                const h2_t h = as_h2(v[k]);
+                d[2 * (k & 3)] += (float)h.x;
+                d[2 * (k & 3) + 1] += (float)h.y;
             }
         }
-        M = bm;
     }
-    S.s_acc[wave][0][lane] = make_float2(nx, ny);
-    if (lane == 0) {
-        S.c_m[wave] = M;
-        S.c_l[wave] = den;
+    wave_reduce_rows<8>(d);
+    const int r = row_of_lane<8>(lane);
+    if (lane == writer_lane<8>(r)) S.drow[r] = d[0];
+    return ok;
+}
+
+// wave 0: the attention output (all heads) -> permuted pairs per 8 columns + per-32-column sums
+RK_DEV bool ob_poll(const Params& p, uint32_t tag, Lds& S) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t* tob = reinterpret_cast<const uint64_t*>(p.tob);
+    uint32_t v[16];
+    const bool ok = poll_pairs<16>(
+        p, tag, [&](int k) -> const uint64_t* { return tob + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v);
+    const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = lane + 64 * k;  // 8-column block
+        const u4_t d = {v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+        uint32_t hp[4];
+        pair_permute(d, hp);
+        S.vecp[i] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+        float sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
+        sum += dpp<0xB1>(sum);  // 4 consecutive 8-blocks (lanes) = one 32-column chunk
+        sum += dpp<0x4E>(sum);
+        if ((lane & 3) == 0) S.vsum[i >> 2] = sum;
     }
-    __syncthreads();
-    if (tid < REP * 64) {  // thread = (head r2, dim pair d2): merge the kParts waves of the head
-        const int r2 = tid >> 6, d2 = tid & 63;
-        float Mx = -INFINITY;
+    return ok;
+}
+
+// ---------------------------------------------------------------------------------------------- w_o rows
+// streamer sw owns row 8b + sw; streamer 0 also row 8b + 7. wo_sm: per (layer, row, group) scale | min << 16.
+struct ORegs {
+    u4_t w[2];
+    uint32_t sm[2];
+};
+
+RK_DEV void o_issue(const Params& p, int l, ORegs& o) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
+    const int K = p.NH * kHD, ng = K / 128;
 #pragma unroll
-        for (int k = 0; k < kParts; ++k) Mx = fmaxf(Mx, S.c_m[r2 * kParts + k]);
-        float dd = 0.f, ox = 0.f, oy = 0.f;
-#pragma unroll
-        for (int k = 0; k < kParts; ++k) {
-            const int w2 = r2 * kParts + k;
-            const float wt = S.c_m[w2] == -INFINITY ? 0.f : __expf(S.c_m[w2] - Mx);
-            dd += wt * S.c_l[w2];
-            ox += wt * S.s_acc[w2][0][d2].x;
-            oy += wt * S.s_acc[w2][0][d2].y;
+    for (int k = 0; k < 2; ++k) {
+        o.w[k] = u4_t{0u, 0u, 0u, 0u};
+        o.sm[k] = 0u;
+        if (k == 0 || sw == 0) {
+            const int row = 8 * blockIdx.x + (k == 0 ? sw : 7);
+            const size_t rr = (size_t)l * kH + row;
+            o.w[k] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wo_q + rr * (K / 2)) + lane);
+            o.sm[k] = p.wo_sm[rr * ng + (lane >> 2)];
         }
-        const float inv = 1.0f / dd;
-        st_coh(reinterpret_cast<uint32_t*>(p.ob) + ((size_t)(g * REP + r2) * kHD) / 2 + d2, pack_h2(ox * inv, oy * inv));
     }
 }
 
-constexpr int kDownNJ = 6;  // ceil(11008 / 32 / 64): chunks per lane of one down row
-
-// at most one row of w_down / w_o per wave (rpb <= kWaves is checked at launch)
-RK_DEV int own_row(int& row) {
-    const int rpb = (kH + gridDim.x - 1) / gridDim.x, wave = threadIdx.x >> 6;
-    row = blockIdx.x * rpb + wave;
-    return wave < rpb && row < kH;
-}
-
-RK_DEV void down_issue(const Params& p, int l, RowPrefetch<kDownNJ>& rp) {
-    int row;
-    const int inter = p.inter;
-    if (own_row(row))
-        row_prefetch<kDownNJ>(rp, p.wd_q + (size_t)l * kH * (inter / 2), p.wd_s + (size_t)l * kH * (inter / 128),
-                              p.wd_m + (size_t)l * kH * (inter / 128), row, inter);
-}
-
-template <int REP>
-RK_DEV void phase_b(const Params& p, int l, int64_t pos, const RowPrefetch<kDownNJ>& rp, Lds& S) {
-    attention_split<REP>(p, l, pos, S);
-    __syncthreads();
-    stage_vec_pairs(p.act, p.inter, S);
-    __syncthreads();
+RK_DEV void o_compute(const ORegs& o, Lds& S) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
     const Int4Masks km = int4_masks();
-    int row;
-    if (own_row(row)) {
-        const float d = row_dot<kDownNJ>(rp, p.inter, S, km);
-        if ((threadIdx.x & 63) == 0) S.drow[threadIdx.x >> 6] = d;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        if (k == 0 || sw == 0) {
+            uint32_t xp[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = S.vecp[lane * 4 + q];
+                xp[4 * q] = v.x; xp[4 * q + 1] = v.y; xp[4 * q + 2] = v.z; xp[4 * q + 3] = v.w;
+            }
+            const float d = chunk_dot_int4(o.w[k], xp, km);
+            float acc = __builtin_fmaf(d, h16((uint16_t)o.sm[k]), h16((uint16_t)(o.sm[k] >> 16)) * S.vsum[lane]);
+            acc = wave_sum(acc);
+            if (lane == 0) S.orow[k == 0 ? sw : 7] = acc;
+        }
     }
-}
-
-// ---------------------------------------------------------------------------------------------- phase C
-RK_DEV void o_issue(const Params& p, int l, RowPrefetch<1>& rp) {
-    int row;
-    const int K = p.NH * kHD;
-    if (own_row(row))
-        row_prefetch<1>(rp, p.wo_q + (size_t)l * kH * (K / 2), p.wo_s + (size_t)l * kH * (K / 128),
-                        p.wo_m + (size_t)l * kH * (K / 128), row, K);
-}
-
-RK_DEV void phase_c(const Params& p, const RowPrefetch<1>& rp, Lds& S) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int rpb = (kH + gridDim.x - 1) / gridDim.x;
-    const int K = p.NH * kHD;
-    stage_vec_pairs(p.ob, K, S);
-    __syncthreads();
-    const Int4Masks km = int4_masks();
-    int row;
-    if (own_row(row)) {
-        const float o = row_dot<1>(rp, K, S, km);
-        if (lane == 0) S.xrow[wave] = rnd16(S.xrow[wave] + rnd16(o) + rnd16(S.drow[wave]));
-    }
-    __syncthreads();
-    if (tid < rpb / 2)  // rows 2t, 2t+1 of this block as one dword
-        st_coh(reinterpret_cast<uint32_t*>(p.x) + (blockIdx.x * rpb) / 2 + tid,
-               pack_h2(S.xrow[2 * tid], S.xrow[2 * tid + 1]));
 }
 
 // ---------------------------------------------------------------------------------------------- head
-// int8 audio head: block b owns rows [b * per, (b + 1) * per), wave w rows r0 + w + 8k. The first batch of a
-// wave's rows is issued before the last barrier.
-constexpr int kHeadB = 8;  // rows per wave per batch
+// The head rows are loaded into the tile registers (free after the last layer's tiles): streamer sw's row k
+// (r0 + sw + 7k, k < kHeadRows) half j goes to flat entry 2k + j of TileRegs::w.
+static_assert(2 * kHeadRows <= kGPW * kMaxTiles, "head rows fit the tile registers");
 
-struct HeadLoad {
-    u4_t w[kHeadB][2];
-};
+RK_DEV u4_t& head_slot(TileRegs& tr, int e) { return tr.w[e / kMaxTiles][e % kMaxTiles]; }
+RK_DEV const u4_t& head_slot(const TileRegs& tr, int e) { return tr.w[e / kMaxTiles][e % kMaxTiles]; }
 
 RK_DEV void head_rows(const Params& p, int& r0, int& r1) {
     const int per = (p.n_audio + gridDim.x - 1) / gridDim.x;
@@ -660,55 +837,145 @@ RK_DEV void head_rows(const Params& p, int& r0, int& r1) {
     r1 = min(p.n_audio, r0 + per);
 }
 
-RK_DEV void head_load(const Params& p, int first, int r1, HeadLoad& hl) {
-    const int lane = threadIdx.x & 63;
+RK_DEV void head_issue(const Params& p, TileRegs& tr) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
+    int r0, r1;
+    head_rows(p, r0, r1);
 #pragma unroll
-    for (int k = 0; k < kHeadB; ++k) {
-        const int r = first + kWaves * k;
+    for (int e = 0; e < kGPW * kMaxTiles; ++e) head_slot(tr, e) = u4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < kHeadRows; ++k) {
+        const int r = r0 + sw + kStreamers * k;
         if (r < r1) {
             const u4_t* qr = reinterpret_cast<const u4_t*>(p.head_q + (size_t)r * kH);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) hl.w[k][j] = __builtin_nontemporal_load(qr + lane + 64 * j);
+            for (int j = 0; j < 2; ++j) head_slot(tr, 2 * k + j) = __builtin_nontemporal_load(qr + lane + 64 * j);
         }
     }
 }
 
-RK_DEV void head_phase(const Params& p, HeadLoad& hl, Lds& S) {
-    if (threadIdx.x < 64) {  // wave 0: final LayerNorm, natural pairs of h in LDS
-        XWave xw;
-        x_load(p, xw);
-        layernorm_wave(xw, p.norm_w, p.eps);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float* v = xw.v[k];
-            S.vecp[threadIdx.x + 64 * k] = make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
-                                                      pack_h2(v[6], v[7]));
-        }
-    }
-    __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
     int r0, r1;
     head_rows(p, r0, r1);
-    for (int first = r0 + wave; first < r1; first += kWaves * kHeadB) {
-        if (first != r0 + wave) head_load(p, first, r1, hl);
+    for (int k = 0; r0 + sw + kStreamers * k < r1; ++k) {
+        const int r = r0 + sw + kStreamers * k;
+        u4_t w[2];
+        if (k < kHeadRows) {
+            w[0] = head_slot(tr, 0);
+            w[1] = head_slot(tr, 1);
 #pragma unroll
-        for (int k = 0; k < kHeadB; ++k) {
-            const int r = first + kWaves * k;
-            if (r >= r1) break;
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {  // 128 chunks of 16 columns
-                const int c = lane + 64 * j;
-                uint32_t xp[8];
-                const uint4 a = S.vecp[2 * c], b = S.vecp[2 * c + 1];
-                xp[0] = a.x; xp[1] = a.y; xp[2] = a.z; xp[3] = a.w;
-                xp[4] = b.x; xp[5] = b.y; xp[6] = b.z; xp[7] = b.w;
-                acc += chunk_dot_int8<true>(hl.w[k][j], xp);
-            }
-            acc = wave_sum(acc);
-            if (lane == 0) p.logits[r] = acc * h16(p.head_s[r]);
+            for (int kk = 1; kk < kHeadRows; ++kk)
+                if (k == kk) {
+                    w[0] = head_slot(tr, 2 * kk);
+                    w[1] = head_slot(tr, 2 * kk + 1);
+                }
+        } else {
+            const u4_t* qr = reinterpret_cast<const u4_t*>(p.head_q + (size_t)r * kH);
+            w[0] = qr[lane];
+            w[1] = qr[lane + 64];
         }
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {  // 128 chunks of 16 columns
+            const int c = lane + 64 * j;
+            uint32_t xp[8];
+            const uint4 a = S.vecp[2 * c], b = S.vecp[2 * c + 1];
+            xp[0] = a.x; xp[1] = a.y; xp[2] = a.z; xp[3] = a.w;
+            xp[4] = b.x; xp[5] = b.y; xp[6] = b.z; xp[7] = b.w;
+            acc += chunk_dot_int8<true>(w[j], xp);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) p.logits[r] = acc * h16(p.head_s[r]);
     }
+}
+
+// ---------------------------------------------------------------------------------------------- the step
+// Wave 0 and the streamers run separate code (so each role's registers are allocated for its own peak, not the
+// sum) and meet at the same sequence of block barriers per layer:
+//   B1 h staged | B2 tile partials | B3 tile outputs (inside tile_epilogue) | B4 epilogue done | B5 q staged,
+//   down partials published | B6 attention partials (inside attention) | B7 attention output staged |
+//   B8 o rows  -- then wave 0 updates and publishes x.  Head: B9 h staged.
+// Streamer issue order (each wait covers only older loads): down(l) after the tile epilogue, consumed after
+// attention(l); then O(l), K/V(l + 1), and after the down partials tiles(l + 1) (the head rows after the last
+// layer), which then have the attention-output and x hops (~5 us) to land. At most ~50 vector-memory instructions
+// are in flight per streamer, and the tile and down prefetches are never live together.
+
+template <int REP>
+RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok, const Work& wk, Lds& S) {
+    const int lane = threadIdx.x & 63;
+    for (int l = 0; l < p.L; ++l) {
+        const uint32_t tag = tag_of(step, l);
+        XWave xw;
+        if (l == 0) {
+            x_from_embedding(p, tok, xw);
+        } else {
+            x_poll(p, tag_of(step, l - 1), xw);
+            if (l == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;  // every block has read pos
+        }
+        layernorm_wave(xw, p.ln_w + (size_t)l * kH, p.eps);
+        stage_h_frag(xw, S);
+        __syncthreads();                          // B1
+        __syncthreads();                          // B2
+        tile_epilogue(p, l, pos, tag, wk, S);     // B3 inside
+        __syncthreads();                          // B4
+        q_poll(p, REP, pos, tag, S);
+        __syncthreads();                          // B5
+        __syncthreads();                          // B6
+        if (wk.comb >= 0) combine(p, wk.comb, pos, tag, S);
+        down_gather(p, tag, S);
+        ob_poll(p, tag, S);
+        __syncthreads();                          // B7
+        __syncthreads();                          // B8
+        if (lane < 8) S.xrow[lane] = rnd16(S.xrow[lane] + rnd16(S.orow[lane]) + rnd16(S.drow[lane]));
+        if (lane < 4)
+            st_coh64(reinterpret_cast<uint64_t*>(p.tx) + 4 * blockIdx.x + lane,
+                     tpair(S.xrow[2 * lane], S.xrow[2 * lane + 1], tag));
+    }
+    // final LayerNorm, h as natural pairs for the int8 head
+    XWave xw;
+    x_poll(p, tag_of(step, p.L - 1), xw);
+    if (p.L == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;
+    layernorm_wave(xw, p.norm_w, p.eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float* v = xw.v[k];
+        S.vecp[lane + 64 * k] =
+            make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7]));
+    }
+    __syncthreads();                              // B9
+}
+
+template <int REP>
+RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Work& wk, Lds& S) {
+    TileRegs tr;
+    DownRegs dr;
+    KVRegs kv;
+    ORegs orr;
+    tile_issue(p, 0, S, wk, tr);
+    kv_issue(p, 0, pos, kv);
+    for (int l = 0; l < p.L; ++l) {
+        const uint32_t tag = tag_of(step, l);
+        const bool last = l + 1 == p.L;
+        __syncthreads();                          // B1
+        tile_compute(tr, wk, S);
+        __syncthreads();                          // B2
+        tile_epilogue(p, l, pos, tag, wk, S);     // B3 inside
+        __syncthreads();                          // B4
+        down_issue(p, l, wk, dr);
+        __syncthreads();                          // B5
+        attention<REP>(p, l, pos, tag, kv, S);    // B6 inside
+        o_issue(p, l, orr);
+        if (!last) kv_issue(p, l + 1, pos, kv);
+        down_compute(p, tag, wk, dr, S);
+        if (!last) tile_issue(p, l + 1, S, wk, tr);
+        else head_issue(p, tr);
+        __syncthreads();                          // B7
+        o_compute(orr, S);
+        __syncthreads();                          // B8
+    }
+    __syncthreads();                              // B9
+    head_compute(p, tr, S);
 }
 
 template <int REP>
@@ -718,54 +985,20 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     const int tid = threadIdx.x;
     const int64_t pos = p.pos[0];
     const int64_t tok = p.tok[0];
-    if (pos < 0 || pos >= p.S) {  // no cache slot for this position: every block leaves before any barrier
+    if (pos < 0 || pos >= p.S) {  // no cache slot for this position: every block leaves at once
         if (blockIdx.x == 0 && tid == 0) atomicOr(p.status, kBadPos);
         return;
     }
-    unsigned epoch = ld_coh(p.flags + blockIdx.x);
-    const int rpb = (kH + gridDim.x - 1) / gridDim.x;
-    const bool poller = tid < 64;
-
-    // Each phase's weights are issued between the block's arrival at the barrier in front of the phase and the
-    // wait for its release, so they stream in while the grid synchronizes: layer 0's w_in tiles right away.
-    TileLoad tl;
-    tile_issue(p, 0, tl);
-    // this block's rows of the residual stream, x = round(emb_q[tok] * emb_s[tok]), kept in LDS across layers
-    if (tid < rpb) S.xrow[tid] = rnd16((float)p.emb_q[(size_t)tok * kH + blockIdx.x * rpb + tid] * h16(p.emb_s[tok]));
-
-    for (int l = 0; l < p.L; ++l) {
-        phase_a(p, l, tl, tok, pos, S);
-        RowPrefetch<kDownNJ> rd;
-        grid_arrive(p, ++epoch);
-        if (!poller) down_issue(p, l, rd);
-        grid_wait(p, epoch);
-        if (poller) down_issue(p, l, rd);
-        if (l == 0 && blockIdx.x == 0 && tid == 0) p.pos[0] = pos + 1;  // every block has read pos by now
-
-        phase_b<REP>(p, l, pos, rd, S);
-        RowPrefetch<1> ro;
-        grid_arrive(p, ++epoch);
-        if (!poller) o_issue(p, l, ro);
-        grid_wait(p, epoch);
-        if (poller) o_issue(p, l, ro);
-
-        phase_c(p, ro, S);
-        if (l + 1 == p.L) break;
-        grid_arrive(p, ++epoch);
-        if (!poller) tile_issue(p, l + 1, tl);
-        grid_wait(p, epoch);
-        if (poller) tile_issue(p, l + 1, tl);
-    }
-
-    // final LayerNorm + audio head
-    HeadLoad hl;
-    int r0, r1;
-    head_rows(p, r0, r1);
-    grid_arrive(p, ++epoch);
-    if (!poller) head_load(p, r0 + (tid >> 6), r1, hl);
-    grid_wait(p, epoch);
-    if (poller) head_load(p, r0, r1, hl);
-    head_phase(p, hl, S);
+    const uint32_t step = p.ctr[blockIdx.x];
+    if (tid < kWork) S.work[tid] = p.work[(size_t)blockIdx.x * kWork + tid];
+    if (tid < 8) S.xrow[tid] = rnd16((float)p.emb_q[(size_t)tok * kH + 8 * blockIdx.x + tid] * h16(p.emb_s[tok]));
+    __syncthreads();
+    const Work wk = work_of(S);
+    if (tid < 64)
+        poller_main<REP>(p, step, pos, tok, wk, S);
+    else
+        streamer_main<REP>(p, pos, step, wk, S);
+    if (tid == 0) p.ctr[blockIdx.x] = step + 1;
 }
 
 // can `nblocks` blocks of the kernel be resident on the current device at the same time?
@@ -794,13 +1027,16 @@ extern "C" int rk_decode_step_persistent(const rk_decode_params* params, int nbl
     if (p.L <= 0 || p.L > 64 || p.NKV <= 0 || p.NH % p.NKV || p.NH * kHD != kH || p.S <= 0) return RK_ERR_SHAPE;
     const int rep = p.NH / p.NKV;
     if (!(rep == 1 || rep == 2 || rep == 4 || rep == 8)) return RK_ERR_SHAPE;
-    if (p.inter <= 0 || p.inter % 128 || p.inter > 11008 || (p.inter + 2047) / 2048 > 6) return RK_ERR_SHAPE;
-    if (nblocks <= 0 || nblocks % p.NKV || nblocks / p.NKV != p.nsp || p.nsp > 256) return RK_ERR_BLOCK;
-    if ((kH + nblocks - 1) / nblocks > kWaves) return RK_ERR_BLOCK;  // each wave owns one row of down / O
-    if (!p.tok || !p.pos || !p.emb_q || !p.emb_s || !p.win_q || !p.wo_q || !p.wd_q || !p.kc || !p.vc ||
-        !p.head_q || !p.logits || !p.x || !p.flags || !p.status || !p.grp_ctr)
+    if (p.inter <= 0 || p.inter % 128 || p.inter > 11008) return RK_ERR_SHAPE;
+    if (nblocks <= 0 || nblocks * 8 != kH) return RK_ERR_BLOCK;  // block b owns rows [8b, 8b + 8)
+    if (p.nsp <= 0 || p.nsp > 256 || p.NKV * p.nsp > nblocks || p.inter / 16 > kMaxSlices * nblocks)
+        return RK_ERR_BLOCK;
+    if (!p.tok || !p.pos || !p.emb_q || !p.emb_s || !p.win_t || !p.win_sm || !p.wo_q || !p.wo_sm ||
+        !p.wd_t || !p.wd_sm || !p.ln_w || !p.norm_w || !p.cos_t || !p.sin_t || !p.kc || !p.vc || !p.head_q ||
+        !p.head_s || !p.logits || !p.work || !p.tx || !p.tq || !p.tkv || !p.tob || !p.tdp || !p.tpo || !p.tml ||
+        !p.ctr || !p.status)
         return RK_ERR_NULL;
-    if (!co_resident(rep, nblocks)) return RK_ERR_BLOCK;  // the grid barriers need every block resident at once
+    if (!co_resident(rep, nblocks)) return RK_ERR_BLOCK;  // the waits need every block resident at once
     hipStream_t st = (hipStream_t)stream;
     switch (rep) {
         case 1: hipLaunchKernelGGL(decode_step_kernel<1>, dim3(nblocks), dim3(kThreads), sizeof(Lds), st, p); break;

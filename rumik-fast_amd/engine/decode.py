@@ -154,9 +154,12 @@ class RkDecodeParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("L", "NH", "NKV", "inter", "S", "n_audio", "nsp")] + [
         ("eps", ctypes.c_float), ("scale", ctypes.c_float), ("sliding", ctypes.c_ulonglong)] + [
         (n, ctypes.c_void_p) for n in (
-            "tok", "pos", "emb_q", "emb_s", "win_q", "win_s", "win_m", "wo_q", "wo_s", "wo_m", "wd_q", "wd_s", "wd_m",
-            "ln_w", "norm_w", "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "x", "qbuf", "act", "ob",
-            "po", "pm", "pl", "grp_ctr", "flags", "status")]
+            "tok", "pos", "emb_q", "emb_s", "win_t", "win_sm", "wo_q", "wo_sm", "wd_t", "wd_sm", "ln_w", "norm_w",
+            "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "work", "tx", "tq", "tkv", "tob", "tdp",
+            "tpo", "tml", "ctr", "status")]
+
+
+MAX_TILES, MAX_SLICES, WORK = 7, 3, 16   # kMaxTiles, kMaxSlices, kWork of csrc/decode_persistent.hip
 
 
 def interleave_gate_up(t, cfg):
@@ -168,43 +171,98 @@ def interleave_gate_up(t, cfg):
     return torch.cat([t[:a], gu.reshape(2 * cfg.inter, -1)]).contiguous()
 
 
+def pack_scale_min(s, m):
+    """fp16 scale, min [..] -> int32 scale | min << 16 (the kernel's per-(row, group) word)."""
+    lo = s.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+    hi = m.contiguous().view(torch.int16).to(torch.int32) << 16
+    return (lo | hi).contiguous()
+
+
+def tile_layout(q):
+    """w_in codes [n_in, 1024] -> per (tile, 128-column group) the 16 rows x 64 bytes in lane order: lane j + 16s
+    holds row j's bytes [16s, 16s + 16) of the group. Returns [n_in / 16, 16, 64, 16] uint8."""
+    nt = q.shape[0] // 16
+    return q.reshape(nt, 16, 16, 4, 16).permute(0, 2, 3, 1, 4).contiguous().reshape(nt, 16, 64, 16)
+
+
+def down_layout(q):
+    """w_down codes [2048, inter / 2] -> per 16-column slice the 2048 rows x 8 bytes: [inter / 16, 2048, 8]."""
+    return q.reshape(q.shape[0], -1, 8).permute(1, 0, 2).contiguous()
+
+
+def work_table(cfg, nblocks, nsp):
+    """Per block: its w_in tiles (q / k / v tiles first, then the gate / up tiles of its MLP channels), its w_down
+    slices [sb, se) (16 channels each; a block owns both gate / up tiles of each of its slices) and the head it
+    combines. Returns int16 [nblocks, 16]."""
+    qkv_tiles = (cfg.NH + 2 * cfg.NKV) * cfg.HD // 16
+    nsl = cfg.inter // 16
+    tiles = [[] for _ in range(nblocks)]
+    ranges = []
+    for b in range(nblocks):
+        sb, se = b * nsl // nblocks, (b + 1) * nsl // nblocks
+        if se - sb > MAX_SLICES:
+            raise ValueError("too many MLP channels per block")
+        ranges.append((sb, se))
+        for k in range(sb, se):
+            tiles[b] += [qkv_tiles + 2 * k, qkv_tiles + 2 * k + 1]
+    qkv = [[] for _ in range(nblocks)]
+    for t in range(qkv_tiles):  # each q / k / v tile to the block with the fewest tiles so far
+        b = min(range(nblocks), key=lambda i: (len(tiles[i]) + len(qkv[i]), len(qkv[i]), i))
+        qkv[b].append(t)
+    table = torch.full((nblocks, WORK), -1, dtype=torch.int16)
+    for b in range(nblocks):
+        tl = qkv[b] + tiles[b]
+        if len(tl) > MAX_TILES:
+            raise ValueError(f"block {b} would hold {len(tl)} tiles (at most {MAX_TILES})")
+        table[b, :len(tl)] = torch.tensor(tl, dtype=torch.int16)
+        table[b, 8], table[b, 9] = ranges[b]
+    natt = cfg.NKV * nsp
+    spare = list(range(natt, nblocks)) or list(range(nblocks))
+    for h in range(cfg.NH):  # combiners on blocks without an attention split where there are enough
+        table[spare[h * len(spare) // cfg.NH], 10] = h
+    return table
+
+
 class PersistentDecode:
     """The decode step as one persistent kernel launch (csrc/decode_persistent.hip). Same weights, state and
-    outputs as DecodeStep; needs hidden 2048 and head dim 128. `weights` as from random_weights; they are
-    re-laid out (stacked over layers, gate / up interleaved) and the per-layer copies can then be dropped."""
+    outputs as DecodeStep; needs hidden 2048 and head dim 128 and one block per 8 rows of the hidden state
+    (256 blocks, one per CU on MI355X). `weights` as from random_weights; they are re-laid out once (stacked over
+    layers, gate / up interleaved, tile / slice layouts) and the per-layer copies can then be dropped."""
 
-    def __init__(self, cfg: Config, weights, device="cuda", nblocks=None, keep_layer_weights=False):
+    def __init__(self, cfg: Config, weights, device="cuda", nsp=None, keep_layer_weights=False):
         if cfg.H != 2048 or cfg.HD != 128 or cfg.NH * cfg.HD != 2048:
             raise ValueError("the persistent step is built for hidden 2048 / head dim 128")
         self.cfg, self.dev = cfg, torch.device(device)
         d = self.dev
-        if nblocks is None:
-            nblocks = torch.cuda.get_device_properties(d).multi_processor_count
-        nblocks -= nblocks % cfg.NKV
-        self.nblocks, self.nsp = nblocks, nblocks // cfg.NKV
+        self.nblocks = 2048 // 8
+        self.nsp = nsp or min(32, self.nblocks // cfg.NKV)
         lib = HL.lib()
         if lib.rk_decode_params_size() != ctypes.sizeof(RkDecodeParams):
             raise RuntimeError("rk_decode_params layout mismatch between the library and decode.py")
-        w = weights
-        self.win = [torch.stack([interleave_gate_up(t[k], cfg) for t in w["w_in"]]) for k in range(3)]
-        self.wo = [torch.stack([t[k] for t in w["w_o"]]) for k in range(3)]
-        self.wd = [torch.stack([t[k] for t in w["w_down"]]) for k in range(3)]
+        w, c = weights, cfg
+        stack = lambda f, key: torch.stack([f(t) for t in w[key]]).contiguous()  # noqa: E731
+        self.win_t = stack(lambda t: tile_layout(interleave_gate_up(t[0], c)), "w_in")
+        self.win_sm = stack(lambda t: pack_scale_min(interleave_gate_up(t[1], c), interleave_gate_up(t[2], c)), "w_in")
+        self.wo_q = stack(lambda t: t[0], "w_o")
+        self.wo_sm = stack(lambda t: pack_scale_min(t[1], t[2]), "w_o")
+        self.wd_t = stack(lambda t: down_layout(t[0]), "w_down")
+        self.wd_sm = stack(lambda t: pack_scale_min(t[1], t[2]).t().contiguous(), "w_down")
         self.ln = torch.stack(w["ln"]).contiguous()
         self.norm, self.emb, self.head = w["norm"], w["emb"], w["head"]
         if not keep_layer_weights:
             for k in ("w_in", "w_o", "w_down"):
                 w[k].clear()
+        self.work = work_table(c, self.nblocks, self.nsp).to(d)
         f16, f32, i32 = torch.float16, torch.float32, torch.int32
-        c = cfg
-        self.x = torch.zeros(2048, dtype=f16, device=d)
-        self.qbuf = torch.zeros(c.NH * c.HD, dtype=f16, device=d)
-        self.act = torch.zeros(c.inter, dtype=f16, device=d)
-        self.ob = torch.zeros(c.NH * c.HD, dtype=f16, device=d)
-        self.po = torch.zeros(c.NH, self.nsp, c.HD, dtype=f32, device=d)
-        self.pm = torch.zeros(c.NH, self.nsp, dtype=f32, device=d)
-        self.pl = torch.zeros(c.NH, self.nsp, dtype=f32, device=d)
-        self.grp_ctr = torch.zeros(c.NKV, dtype=i32, device=d)
-        self.flags = torch.zeros(nblocks * 32, dtype=i32, device=d)  # one 128-byte line per block
+        nb = self.nblocks
+        self.tx = torch.zeros(2048, dtype=i32, device=d)
+        self.tq = torch.zeros(c.NH * c.HD, dtype=i32, device=d)
+        self.tkv = torch.zeros(2 * c.NKV * c.HD, dtype=i32, device=d)
+        self.tob = torch.zeros(c.NH * c.HD, dtype=i32, device=d)
+        self.tdp = torch.zeros(nb * 2048, dtype=i32, device=d)
+        self.tpo = torch.zeros(c.NH * self.nsp * c.HD, dtype=i32, device=d)
+        self.tml = torch.zeros(c.NH * self.nsp * 2, dtype=torch.int64, device=d)
+        self.ctr = torch.zeros(nb, dtype=i32, device=d)
         self.status = torch.zeros(1, dtype=i32, device=d)
         self.logits = torch.zeros(c.n_audio, dtype=f32, device=d)
         self.kc = torch.zeros(c.L, c.NKV, c.S, c.HD, dtype=f16, device=d)
@@ -216,19 +274,28 @@ class PersistentDecode:
         P = RkDecodeParams(L=c.L, NH=c.NH, NKV=c.NKV, inter=c.inter, S=c.S, n_audio=c.n_audio, nsp=self.nsp,
                            eps=c.eps, scale=c.HD ** -0.5, sliding=sliding)
         for name, t in (("tok", self.tok), ("pos", self.pos), ("emb_q", self.emb[0]), ("emb_s", self.emb[1]),
-                        ("win_q", self.win[0]), ("win_s", self.win[1]), ("win_m", self.win[2]),
-                        ("wo_q", self.wo[0]), ("wo_s", self.wo[1]), ("wo_m", self.wo[2]),
-                        ("wd_q", self.wd[0]), ("wd_s", self.wd[1]), ("wd_m", self.wd[2]),
-                        ("ln_w", self.ln), ("norm_w", self.norm), ("cos_t", self.cos), ("sin_t", self.sin),
-                        ("kc", self.kc), ("vc", self.vc), ("head_q", self.head[0]), ("head_s", self.head[1]),
-                        ("logits", self.logits), ("x", self.x), ("qbuf", self.qbuf), ("act", self.act),
-                        ("ob", self.ob), ("po", self.po), ("pm", self.pm), ("pl", self.pl),
-                        ("grp_ctr", self.grp_ctr), ("flags", self.flags), ("status", self.status)):
+                        ("win_t", self.win_t), ("win_sm", self.win_sm), ("wo_q", self.wo_q), ("wo_sm", self.wo_sm),
+                        ("wd_t", self.wd_t), ("wd_sm", self.wd_sm), ("ln_w", self.ln), ("norm_w", self.norm),
+                        ("cos_t", self.cos), ("sin_t", self.sin), ("kc", self.kc), ("vc", self.vc),
+                        ("head_q", self.head[0]), ("head_s", self.head[1]), ("logits", self.logits),
+                        ("work", self.work), ("tx", self.tx), ("tq", self.tq), ("tkv", self.tkv), ("tob", self.tob),
+                        ("tdp", self.tdp), ("tpo", self.tpo), ("tml", self.tml), ("ctr", self.ctr),
+                        ("status", self.status)):
             if not t.is_contiguous() or t.device != d:
                 raise RuntimeError(f"{name} must be a contiguous tensor on {d}")
             setattr(P, name, t.data_ptr())
         self.params = P
         self.graph = None
+
+    @property
+    def x(self):
+        """the residual stream after the last layer of the last step (fp16, decoded from the tagged words)"""
+        return self.tx.view(torch.float16)[0::2]
+
+    def reset(self):
+        """Zero the exchange buffers, step counters and status (needed after a nonzero status)."""
+        for t in (self.tx, self.tq, self.tkv, self.tob, self.tdp, self.tpo, self.tml, self.ctr, self.status):
+            t.zero_()
 
     def set_state(self, tok: int, pos: int):
         self.tok.fill_(tok)
@@ -244,14 +311,14 @@ class PersistentDecode:
                  "decode_step_persistent")
 
     def capture(self):
-        saved = (self.x.clone(), self.kc.clone(), self.vc.clone(), self.pos.clone())
+        saved = (self.kc.clone(), self.vc.clone(), self.pos.clone())
         self.step()
         torch.cuda.synchronize(self.dev)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.step()
         torch.cuda.synchronize(self.dev)
-        self.x.copy_(saved[0]); self.kc.copy_(saved[1]); self.vc.copy_(saved[2]); self.pos.copy_(saved[3])
+        self.kc.copy_(saved[0]); self.vc.copy_(saved[1]); self.pos.copy_(saved[2])
         torch.cuda.synchronize(self.dev)
         self.graph = g
         return g
@@ -260,5 +327,5 @@ class PersistentDecode:
         self.graph.replay()
 
     def status_word(self) -> int:
-        """0 when every grid barrier of every step so far completed in time."""
+        """0 when every wait of every step so far completed in time."""
         return int(self.status.item())

@@ -136,7 +136,8 @@ int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_str
  * Weights are stacked over layers and re-laid out once at load time:
  *   w_in rows are [q | k | v | per 8 MLP channels: 8 gate rows, 8 up rows]; tile T = rows [16T, 16T + 16);
  *   win_t holds, per (layer, tile, 128-column group), the 16 rows x 64 bytes of codes in lane order (lane j + 16s:
- *   row j, bytes [16s, 16s + 16) of the group); win_sm per (layer, tile, row) the 16 groups' scale | min << 16;
+ *   row j, bytes [16s, 16s + 16) of the group); win_sm per (layer, tile, wave w = 0..7, row) the two scale |
+ *   min << 16 words of wave w's column groups (waves 1..7: 2(w - 1), 2(w - 1) + 1; wave 0: 14, 15);
  *   wd_t holds w_down by 16-column slices: per (layer, slice), 2048 rows x 8 bytes; wd_sm per (layer, group) the
  *   2048 rows' scale | min << 16; w_o keeps the reference code layout, wo_sm its scale | min << 16.
  * Blocks exchange fp16 values as tagged 32-bit words (value | tag << 16, tag = 1 + (step * 64 + layer) % 65535,
@@ -154,7 +155,7 @@ typedef struct rk_decode_params {
     const int8_t* emb_q;    /* [vocab, 2048] */
     const uint16_t* emb_s;  /* [vocab] fp16 */
     const uint8_t* win_t;   /* [L, n_in/16, 16, 64, 16 B] */
-    const uint32_t* win_sm; /* [L, n_in/16, 16 rows, 16 groups] */
+    const uint32_t* win_sm; /* [L, n_in/16, 8 waves, 16 rows, 2] */
     const uint8_t* wo_q;    /* [L, 2048, NH*64] */
     const uint32_t* wo_sm;  /* [L, 2048, NH]: scale | min << 16 */
     const uint8_t* wd_t;    /* [L, inter/16, 2048, 8 B] */

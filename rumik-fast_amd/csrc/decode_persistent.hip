@@ -46,12 +46,14 @@ constexpr int kHD = 128;                   // head dim
 constexpr int kNG = kH / 128;              // column groups of a w_in row
 constexpr int kMaxRep = 8;
 constexpr int kMaxTiles = 7;               // w_in tiles per block
-constexpr int kGPW = 3;                    // column groups per streamer (16 = 3 + 3 + 2 * 5)
+constexpr int kGPW = 2;                    // column groups per wave (8 waves x 2 = 16)
+constexpr int kTileSplit = 3;              // next-layer tiles [0, 3) are issued after the tile compute, the rest later
 constexpr int kMaxSlices = 3;              // w_down 16-column slices per block
 constexpr int kRP = (kH / 2 + kSLanes - 1) / kSLanes;  // down row pairs per streamer lane (3)
-constexpr int kKVPre = 10;                 // cached slots per streamer whose K / V are loaded ahead
-constexpr int kHeadRows = 10;              // head rows per streamer loaded ahead
+constexpr int kKVPre = 5;                  // cached slots per streamer whose K / V are loaded ahead (7 x 5 >= 2048 / 64)
+constexpr int kHeadRows = 7;               // head rows per streamer loaded ahead (the rest load when used)
 constexpr int kWork = 16;                  // int16 entries per block in the work table
+constexpr int kPreDown = 2, kPreOb = 1;    // ~0.5 us waits before the down-partial and attention-output polls
 constexpr uint64_t kWaitTicks = 20000000ull;  // 200 ms at the 100 MHz wall clock
 constexpr unsigned kAbort = 1u, kTimeout = 2u, kBadPos = 4u;
 
@@ -101,11 +103,19 @@ RK_DEV bool wait_more(const Params& p, uint64_t t0) {
     return true;
 }
 
+// Every poller first waits `pre` x ~0.5 us (s_sleep 20): measured on 256 blocks, all-to-all exchanges complete
+// fastest when the first poll comes ~0.5 us after the data is written and polls then follow back to back; polls
+// sent long before the data exists only load the coherent path that every other exchange shares.
+RK_DEV void pre_wait(int pre) {
+    for (int i = 0; i < pre; ++i) __builtin_amdgcn_s_sleep(20);
+}
+
 // Poll N tagged fp16 pairs per lane (qword addresses from addr(k); nullptr = not needed) until every tag matches;
 // val[k] receives the packed pair. Wave-uniform control flow; false after an abort or a timeout.
 template <int N, class Addr>
-RK_DEV bool poll_pairs(const Params& p, uint32_t tag, Addr addr, uint32_t (&val)[N]) {
+RK_DEV bool poll_pairs(const Params& p, uint32_t tag, Addr addr, uint32_t (&val)[N], int pre = 1) {
     static_assert(N <= 32, "pending mask");
+    pre_wait(pre);
     uint32_t pending = 0;
 #pragma unroll
     for (int k = 0; k < N; ++k)
@@ -131,7 +141,7 @@ RK_DEV bool poll_pairs(const Params& p, uint32_t tag, Addr addr, uint32_t (&val)
 struct Lds {
     uint4 hfrag[kH / 8];                      // MFMA A fragments of h
     float hsum[kNG];                          // per-group sums of h
-    float tpart[kStreamers][kMaxTiles][16];   // K-split partial dots of the block's tiles
+    float tpart[kWaves][kMaxTiles][16];       // K-split partial dots of the block's tiles
     float ty[kMaxTiles][16];                  // the tiles' projection outputs (rounded)
     float act[kMaxSlices * 16];               // act of the block's MLP channels
     uint32_t qs[kMaxRep][64];                 // q pairs of the block's KV head
@@ -142,6 +152,10 @@ struct Lds {
     float vsum[kH / 32];                      // per-32-column sums of the attention output
     uint32_t cst[32][64];                     // the combine's validated split outputs (one batch)
     float orow[8], drow[8], xrow[8];          // this block's rows of o, down and the residual stream
+    float rcos[kHD / 2], rsin[kHD / 2];       // RoPE cos / sin of pair i at pos
+    uint4 xraw[kH / 8];                       // x (fp16, 8 per entry) for the block-wide LayerNorm
+    uint4 lnw[kH / 8];                        // its weights
+    float ln_mean, ln_rstd;
     int16_t work[kWork];
 };
 
@@ -163,9 +177,10 @@ RK_DEV Work work_of(const Lds& S) {
     return w;
 }
 
-// streamer sw's column groups of every tile: {0, 1, 2}, {3, 4, 5}, then pairs {2sw + 2, 2sw + 3}
-RK_DEV int group0(int sw) { return sw < 2 ? 3 * sw : 2 * sw + 2; }
-RK_DEV int n_groups(int sw) { return sw < 2 ? 3 : 2; }
+// wave w's two column groups of every tile: streamers (w = 1..7) groups 2(w - 1), 2(w - 1) + 1, wave 0 groups 14,
+// 15 (it computes them while it would otherwise wait for the streamers)
+RK_DEV int wave_id() { return threadIdx.x >> 6; }
+RK_DEV int group0(int w) { return 2 * ((w + kWaves - 1) % kWaves); }
 
 // ---------------------------------------------------------------------------------------------- x / h (wave 0)
 // lane holds the 8-column blocks i = lane + 64k, k < 4
@@ -190,7 +205,8 @@ RK_DEV void x_from_embedding(const Params& p, int64_t tok, XWave& xw) {
 
 RK_DEV bool x_poll(const Params& p, uint32_t tag, XWave& xw) {
     const int lane = threadIdx.x & 63;
-    const uint64_t* tx = reinterpret_cast<const uint64_t*>(p.tx);
+    // the opaque zero keeps the addresses from being hoisted out of the layer loop (they would pin ~30 VGPRs)
+    const uint64_t* tx = reinterpret_cast<const uint64_t*>(p.tx) + opaque_vgpr(0u);
     uint32_t v[16];
     const bool ok = poll_pairs<16>(
         p, tag, [&](int k) -> const uint64_t* { return tx + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v);
@@ -205,9 +221,15 @@ RK_DEV bool x_poll(const Params& p, uint32_t tag, XWave& xw) {
     return ok;
 }
 
-// h = round(LN(x) * w) (biased variance, the reference's LayerNorm, engine/rumik_int4.py:38-43)
-RK_DEV void layernorm_wave(XWave& xw, const uint16_t* w, float eps) {
+// LayerNorm (the reference's, engine/rumik_int4.py:38-43: biased variance, no bias), split over the block:
+// wave 0 holds x after its poll, computes mean and rstd and stages x and the weights in LDS (ln_stats); then
+// threads 0..255 normalize one 8-column block each and stage it (ln_apply_frag for the MFMA fragments of h,
+// ln_apply_pairs for the head's natural pairs).
+RK_DEV void ln_stats(const XWave& xw, const uint16_t* w, float eps, Lds& S) {
     const int lane = threadIdx.x & 63;
+    u4_t wv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wv[k] = reinterpret_cast<const u4_t*>(w)[lane + 64 * k];
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -225,37 +247,60 @@ RK_DEV void layernorm_wave(XWave& xw, const uint16_t* w, float eps) {
     const float rstd = 1.0f / sqrtf(wave_sum(ss) * (1.0f / kH) + eps);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const u4_t wv = reinterpret_cast<const u4_t*>(w)[lane + 64 * k];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint16_t wb = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
-            xw.v[k][e] = rnd16((xw.v[k][e] - mean) * rstd * h16(wb));
-        }
+        const float* v = xw.v[k];
+        S.xraw[lane + 64 * k] =
+            make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7]));
+        S.lnw[lane + 64 * k] = make_uint4(wv[k][0], wv[k][1], wv[k][2], wv[k][3]);
+    }
+    if (lane == 0) {
+        S.ln_mean = mean;
+        S.ln_rstd = rstd;
     }
 }
 
-// h -> MFMA A fragments (pairs permuted as the dequant orders the codes) + per-group sums
-RK_DEV void stage_h_frag(const XWave& xw, Lds& S) {
-    const int lane = threadIdx.x & 63;
+// thread i < 256: h of 8-column block i = round((x - mean) * rstd * w)
+RK_DEV void ln_block(const Lds& S, int i, float (&h)[8]) {
+    const uint4 xv = S.xraw[i], wv = S.lnw[i];
+    const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w}, ws[4] = {wv.x, wv.y, wv.z, wv.w};
+    const float mean = S.ln_mean, rstd = S.ln_rstd;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = lane + 64 * k;
-        u4_t d;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) d[e] = pack_h2(xw.v[k][2 * e], xw.v[k][2 * e + 1]);
-        uint32_t hp[4];
-        pair_permute(d, hp);
-        const int g = i >> 4, r = i & 15, s = r >> 2, t = r & 3;
-        S.hfrag[g * 16 + t * 4 + s] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-        float sum = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum += xw.v[k][e];
-        sum += dpp<0x128>(sum);  // 16 lanes = one 128-column group, inside one DPP row
-        sum += dpp<0x124>(sum);
-        sum += dpp<0x122>(sum);
-        sum += dpp<0x121>(sum);
-        if ((lane & 15) == 0) S.hsum[i >> 4] = sum;
+    for (int e = 0; e < 4; ++e) {
+        const h2_t xh = as_h2(xs[e]), wh = as_h2(ws[e]);
+        h[2 * e] = rnd16(((float)xh.x - mean) * rstd * (float)wh.x);
+        h[2 * e + 1] = rnd16(((float)xh.y - mean) * rstd * (float)wh.y);
     }
+}
+
+// h -> MFMA A fragments (pairs permuted as the dequant orders the codes) + per-group sums; threads 0..255
+RK_DEV void ln_apply_frag(Lds& S) {
+    const int i = threadIdx.x;
+    if (i >= kH / 8) return;
+    float h[8];
+    ln_block(S, i, h);
+    u4_t d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d[e] = pack_h2(h[2 * e], h[2 * e + 1]);
+    uint32_t hp[4];
+    pair_permute(d, hp);
+    const int g = i >> 4, r = i & 15, sq = r >> 2, t = r & 3;
+    S.hfrag[g * 16 + t * 4 + sq] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += h[e];
+    sum += dpp<0x128>(sum);  // 16 threads = one 128-column group, inside one DPP row
+    sum += dpp<0x124>(sum);
+    sum += dpp<0x122>(sum);
+    sum += dpp<0x121>(sum);
+    if ((i & 15) == 0) S.hsum[g] = sum;
+}
+
+// h -> natural fp16 pairs per 8 columns (the int8 head's input); threads 0..255
+RK_DEV void ln_apply_pairs(Lds& S) {
+    const int i = threadIdx.x;
+    if (i >= kH / 8) return;
+    float h[8];
+    ln_block(S, i, h);
+    S.vecp[i] = make_uint4(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]), pack_h2(h[4], h[5]), pack_h2(h[6], h[7]));
 }
 
 // ---------------------------------------------------------------------------------------------- w_in tiles
@@ -266,90 +311,80 @@ struct TileRegs {
 
 RK_DEV size_t n_tiles(const Params& p) { return ((size_t)(p.NH + 2 * p.NKV) * kHD + 2 * p.inter) / 16; }
 
-// win_t: per (layer, tile, group) 1 KiB of codes in lane order; win_sm: per (layer, tile, row) the 16 groups'
-// scale | min << 16, so a streamer's consecutive groups of one row come in one or two loads
-RK_DEV void tile_issue(const Params& p, int l, const Lds& S, const Work& wk, TileRegs& tr) {
-    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
-    const int g0 = group0(sw), ng = n_groups(sw);
+// Streamer prefetches are branch-free with a fixed instruction count (addresses clamped to valid data that is then
+// ignored): the compiler can then wait for exactly the loads a computation needs. With data-dependent branches
+// around loads it cannot count the loads issued after a prefetch and waits for all of them, so e.g. the attention
+// would wait for the down-projection burst issued just before it.
+//
+// win_t: per (layer, tile, group) 1 KiB of codes in lane order. win_sm: per (layer, tile, wave, row) the two
+// scale | min << 16 words of the wave's groups, one 8-byte load per tile.
+RK_DEV void tile_issue(const Params& p, int l, const Lds& S, const Work& wk, TileRegs& tr, int tb, int te) {
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int g0 = group0(w);
     const size_t base = (size_t)l * n_tiles(p);
-    // every register is written on every path (zero when unused), so no value lives across iterations
+    const int t_fallback = wk.nt > 0 ? S.work[0] : 0;
 #pragma unroll
     for (int t = 0; t < kMaxTiles; ++t) {
+        if (t < tb || t >= te) continue;  // compile-time after inlining
+        const size_t T = base + (t < wk.nt ? S.work[t] : t_fallback);
 #pragma unroll
-        for (int k = 0; k < kGPW; ++k) {
-            tr.w[k][t] = u4_t{0u, 0u, 0u, 0u};
-            tr.sm[k][t] = 0u;
-        }
-        if (t < wk.nt) {
-            const size_t T = base + S.work[t];
-#pragma unroll
-            for (int k = 0; k < kGPW; ++k)
-                if (k < ng)
-                    tr.w[k][t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.win_t) +
-                                                            (T * kNG + g0 + k) * 64 + lane);
-            const uint32_t* sm = p.win_sm + (T * 16 + (lane & 15)) * kNG + g0;
-            if (sw == 1) {  // groups 3 | 4, 5
-                tr.sm[0][t] = sm[0];
-                const u2_t v = *reinterpret_cast<const u2_t*>(sm + 1);
-                tr.sm[1][t] = v.x;
-                tr.sm[2][t] = v.y;
-            } else {  // groups g0, g0 + 1 (| g0 + 2 for streamer 0)
-                const u2_t v = *reinterpret_cast<const u2_t*>(sm);
-                tr.sm[0][t] = v.x;
-                tr.sm[1][t] = v.y;
-                if (sw == 0) tr.sm[2][t] = sm[2];
-            }
-        }
+        for (int k = 0; k < kGPW; ++k)
+            tr.w[k][t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.win_t) + (T * kNG + g0 + k) * 64 + lane);
+        const u2_t sm = *(reinterpret_cast<const u2_t*>(p.win_sm) + (T * kWaves + w) * 16 + (lane & 15));
+        tr.sm[0][t] = sm.x;
+        tr.sm[1][t] = sm.y;
     }
 }
 
-// the streamer's groups of every tile -> S.tpart[sw][t][row]
+// the wave's groups of every tile -> S.tpart[w][t][row]. Per group the four 32-column chunks are the outer
+// loop and the tiles the inner one, so up to 7 independent MFMA accumulations are in flight.
+template <int TB, int TE>
 RK_DEV void tile_compute(const TileRegs& tr, const Work& wk, Lds& S) {
-    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1, s = lane >> 4;
-    const int g0 = group0(sw), ng = n_groups(sw);
+    const int lane = threadIdx.x & 63, w = wave_id(), s = lane >> 4;
+    const int g0 = group0(w), ng = kGPW;
     const Int4Masks km = int4_masks();
     float acc[kMaxTiles];
 #pragma unroll
-    for (int t = 0; t < kMaxTiles; ++t) acc[t] = 0.f;
+    for (int t = TB; t < TE; ++t) acc[t] = 0.f;
 #pragma unroll
     for (int k = 0; k < kGPW; ++k) {
         if (k < ng) {
             const int g = g0 + k;
-            h8_t A[4];
+            f4_t d[kMaxTiles];
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) A[t4] = __builtin_bit_cast(h8_t, S.hfrag[g * 16 + t4 * 4 + s]);
+            for (int t = TB; t < TE; ++t) d[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) {
+                const h8_t A = __builtin_bit_cast(h8_t, S.hfrag[g * 16 + t4 * 4 + s]);
+#pragma unroll
+                for (int t = TB; t < TE; ++t)  // tiles beyond the block's count hold zero codes
+                    d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag(tr.w[k][t][t4], km), d[t], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);  // one chunk's fragments live at a time
+            }
             const float hs = S.hsum[g];
 #pragma unroll
-            for (int t = 0; t < kMaxTiles; ++t) {
-                if (t < wk.nt) {
-                    f4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int t4 = 0; t4 < 4; ++t4)
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t4], dequant_frag(tr.w[k][t][t4], km), d, 0, 0,
-                                                                   0);
-                    const uint32_t sm = tr.sm[k][t];
-                    acc[t] = __builtin_fmaf(d[0], h16((uint16_t)sm),
-                                            __builtin_fmaf(h16((uint16_t)(sm >> 16)), hs, acc[t]));
-                    __builtin_amdgcn_sched_barrier(0);  // one (group, tile) chain's fragments live at a time
-                }
+            for (int t = TB; t < TE; ++t) {
+                const uint32_t sm = tr.sm[k][t];
+                acc[t] = __builtin_fmaf(d[t][0], h16((uint16_t)sm), __builtin_fmaf(h16((uint16_t)(sm >> 16)), hs, acc[t]));
             }
         }
     }
     if (lane < 16)
 #pragma unroll
-        for (int t = 0; t < kMaxTiles; ++t)
-            if (t < wk.nt) S.tpart[sw][t][lane] = acc[t];
+        for (int t = TB; t < TE; ++t)
+            if (t < wk.nt) S.tpart[w][t][lane] = acc[t];
 }
 
-// thread (t, j): the tile row's output, its epilogue and its publication
-RK_DEV void tile_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, const Work& wk, Lds& S) {
+// thread (t - tb, j): tile t's row j output, its epilogue and its publication, for tiles [tb, te)
+RK_DEV void tile_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, const Work& wk, Lds& S, int tb,
+                          int te) {
     const int tid = threadIdx.x;
-    const int t = tid >> 4, j = tid & 15;
-    const bool mine = t < wk.nt;
+    const int t = tb + (tid >> 4), j = tid & 15;
+    const bool mine = t < te && t < wk.nt;
     if (mine) {
         float y = 0.f;
 #pragma unroll
-        for (int w = 0; w < kStreamers; ++w) y += S.tpart[w][t][j];
+        for (int w = 0; w < kWaves; ++w) y += S.tpart[w][t][j];
         S.ty[t][j] = rnd16(y);  // the projection output in fp16 (the reference's buf_in)
     }
     __syncthreads();
@@ -363,8 +398,7 @@ RK_DEV void tile_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, con
         float out = y;
         if ((p.sliding >> l) & 1ull) {  // interleaved RoPE: pairs (2i, 2i + 1)
             const int dd = row % kHD;
-            const float c = h16(p.cos_t[(size_t)pos * kHD + (dd & ~1)]);
-            const float sn = h16(p.sin_t[(size_t)pos * kHD + (dd & ~1)]);
+            const float c = S.rcos[dd >> 1], sn = S.rsin[dd >> 1];
             const float partner = S.ty[t][j ^ 1];
             out = (dd & 1) ? (y * c + partner * sn) : (y * c - partner * sn);
         }
@@ -398,24 +432,17 @@ struct DownRegs {
 RK_DEV void down_issue(const Params& p, int l, const Work& wk, DownRegs& dr) {
     const int sl = threadIdx.x - 64;
     const int nsl = p.inter / 16, ngd = p.inter / 128;
-    const int gb = wk.sb / 8, ge = (wk.se - 1) / 8;
+    const int gb = wk.sb / 8;
 #pragma unroll
     for (int k = 0; k < kRP; ++k) {
-        const int rp = sl + kSLanes * k;
+        const int rp = min(sl + kSLanes * k, kH / 2 - 1);
 #pragma unroll
-        for (int i = 0; i < kMaxSlices; ++i) dr.c[k][i] = u4_t{0u, 0u, 0u, 0u};
-        dr.sm[k][0] = dr.sm[k][1] = u2_t{0u, 0u};
-        if (rp < kH / 2) {
+        for (int i = 0; i < kMaxSlices; ++i)
+            dr.c[k][i] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wd_t) +
+                                                    ((size_t)l * nsl + min(wk.sb + i, nsl - 1)) * (kH / 2) + rp);
 #pragma unroll
-            for (int i = 0; i < kMaxSlices; ++i)
-                if (wk.sb + i < wk.se)
-                    dr.c[k][i] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wd_t) +
-                                                            ((size_t)l * nsl + wk.sb + i) * (kH / 2) + rp);
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-                if (gb + q <= ge)
-                    dr.sm[k][q] = *reinterpret_cast<const u2_t*>(p.wd_sm + ((size_t)l * ngd + gb + q) * kH + 2 * rp);
-        }
+        for (int q = 0; q < 2; ++q)
+            dr.sm[k][q] = *reinterpret_cast<const u2_t*>(p.wd_sm + ((size_t)l * ngd + min(gb + q, ngd - 1)) * kH + 2 * rp);
     }
 }
 
@@ -440,8 +467,8 @@ RK_DEV void down_compute(const Params& p, uint32_t tag, const Work& wk, const Do
     uint64_t* out = reinterpret_cast<uint64_t*>(p.tdp + (size_t)blockIdx.x * kH);
 #pragma unroll
     for (int k = 0; k < kRP; ++k) {
-        const int rp = sl + kSLanes * k;
-        if (rp < kH / 2) {
+        const int rp = min(sl + kSLanes * k, kH / 2 - 1);  // the clamped lanes rewrite the last pair's own value
+        {
             float d[2] = {0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < kMaxSlices; ++i) {
@@ -492,7 +519,8 @@ struct KVRegs {
     uint32_t k[kKVPre], v[kKVPre];
 };
 
-// cached slots start + sw + 7u (u < kKVPre) of this block's split; slot pos is read from the tagged copy
+// cached slots start + sw + 7u (u < kKVPre) of this block's split; slot pos is read from the tagged copy. Every
+// lane loads kKVPre slots (clamped into the cache), used or not.
 RK_DEV void kv_issue(const Params& p, int l, int64_t pos, KVRegs& kv) {
     const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
     const Split s = split_of(p, pos);
@@ -501,12 +529,9 @@ RK_DEV void kv_issue(const Params& p, int l, int64_t pos, KVRegs& kv) {
     const uint32_t* vr = reinterpret_cast<const uint32_t*>(p.vc + base);
 #pragma unroll
     for (int u = 0; u < kKVPre; ++u) {
-        const int t = s.start + sw + kStreamers * u;
-        kv.k[u] = kv.v[u] = 0u;
-        if (t < s.end && t != pos) {
-            kv.k[u] = kr[(size_t)t * (kHD / 2) + lane];
-            kv.v[u] = vr[(size_t)t * (kHD / 2) + lane];
-        }
+        const int t = min(s.start + sw + kStreamers * u, p.S - 1);
+        kv.k[u] = kr[(size_t)t * (kHD / 2) + lane];
+        kv.v[u] = vr[(size_t)t * (kHD / 2) + lane];
     }
 }
 
@@ -516,8 +541,9 @@ RK_DEV bool q_poll(const Params& p, int rep, int64_t pos, uint32_t tag, Lds& S) 
     const Split s = split_of(p, pos);
     if (!s.att) return true;
     const bool has_pos = s.start <= pos && pos < s.end;
-    const uint64_t* tq = reinterpret_cast<const uint64_t*>(p.tq);
-    const uint64_t* tkv = reinterpret_cast<const uint64_t*>(p.tkv);
+    const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
+    const uint64_t* tq = reinterpret_cast<const uint64_t*>(p.tq) + z;
+    const uint64_t* tkv = reinterpret_cast<const uint64_t*>(p.tkv) + z;
     uint32_t v[kMaxRep + 2];
     const bool ok = poll_pairs<kMaxRep + 2>(
         p, tag,
@@ -634,7 +660,9 @@ RK_DEV void attention(const Params& p, int l, int64_t pos, uint32_t tag, const K
 }
 
 // wave 0 of head h's combiner: out = sum_i w_i o_i / sum_i w_i, w_i = exp(m_i - max m) * l_i over the splits
-// holding at least one slot; published tagged
+// holding at least one slot (at most 64); published tagged. Polling loops of 32 splits gather the o pairs (the
+// first also split lane's (m, l)); validated pairs are staged in LDS and summed in split order (the result does
+// not depend on arrival order).
 RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
     const int lane = threadIdx.x & 63;
     const int nsp = p.nsp;
@@ -642,79 +670,55 @@ RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
     const int ch = split_chunk(n, nsp);
     const int na = min(nsp, (n + ch - 1) / ch);
     const size_t hb = (size_t)h * nsp;
-    const uint64_t* tml = reinterpret_cast<const uint64_t*>(p.tml);
-    const uint64_t* po = reinterpret_cast<const uint64_t*>(p.tpo + hb * kHD) + lane;
+    const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
+    const uint64_t* tml = reinterpret_cast<const uint64_t*>(p.tml) + 2 * (hb + lane) + z;
+    const uint64_t* po = reinterpret_cast<const uint64_t*>(p.tpo + hb * kHD) + lane + z;
+    pre_wait(1);
     const uint64_t t0 = wall_clock64();
-    // (m, l) of the splits lane, lane + 64, ... (nsp <= 256), then the o pairs of every split in batches of 32
-    float mi[4], li[4];
-    {
-        uint32_t pending = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            mi[k] = -INFINITY;
-            li[k] = 0.f;
-            if (lane + 64 * k < na) pending |= 1u << k;
-        }
-        while (true) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (pending & (1u << k)) {
-                    const uint64_t a = ld_coh64(tml + 2 * (hb + lane + 64 * k));
-                    const uint64_t b = ld_coh64(tml + 2 * (hb + lane + 64 * k) + 1);
-                    if ((uint32_t)(a >> 32) == tag && (uint32_t)(b >> 32) == tag) {
-                        mi[k] = __builtin_bit_cast(float, (uint32_t)a);
-                        li[k] = __builtin_bit_cast(float, (uint32_t)b);
-                        pending &= ~(1u << k);
-                    }
-                }
-            }
-            if (__all(pending == 0)) break;
-            if (!wait_more(p, t0)) return false;
-        }
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) M = fmaxf(M, mi[k]);
-    M = wave_max(M);
-    float wt[4], den = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        wt[k] = mi[k] == -INFINITY ? 0.f : __expf(mi[k] - M) * li[k];
-        den += wt[k];
-    }
-    den = wave_sum(den);
-    // o pairs of splits i0 .. i0 + 31 per batch: polled until every tag matches, staged in LDS, then summed in
-    // split order (the result does not depend on arrival order)
-    float ox = 0.f, oy = 0.f;
+    // splits in batches of 32, wave-uniform pending bits: split k counts as arrived when every lane sees its tag;
+    // the first batch also brings split lane's (m, l)
+    bool ml_done = lane >= na;
+    float mi = -INFINITY, li = 0.f, wt = 0.f, den = 0.f, ox = 0.f, oy = 0.f;
     for (int i0 = 0; i0 < na; i0 += 32) {
-        uint32_t pending = 0;
-#pragma unroll
-        for (int k = 0; k < 32; ++k)
-            if (i0 + k < na) pending |= 1u << k;
+        uint32_t pending = na - i0 >= 32 ? ~0u : ((1u << (na - i0)) - 1);
         while (true) {
             uint64_t q[32];
 #pragma unroll
             for (int k = 0; k < 32; ++k)
                 if (pending & (1u << k)) q[k] = ld_coh64(po + (size_t)(i0 + k) * (kHD / 2));
+            uint64_t qm = 0, ql = 0;
+            if (!__all(ml_done)) {
+                qm = ld_coh64(tml);
+                ql = ld_coh64(tml + 1);
+            }
 #pragma unroll
             for (int k = 0; k < 32; ++k)
-                if ((pending & (1u << k)) && pair_ok(q[k], tag)) {
+                if ((pending & (1u << k)) && __all(pair_ok(q[k], tag))) {
                     S.cst[k][lane] = pair_val(q[k]);
                     pending &= ~(1u << k);
                 }
-            if (__all(pending == 0)) break;
+            if (!ml_done && (uint32_t)(qm >> 32) == tag && (uint32_t)(ql >> 32) == tag) {
+                mi = __builtin_bit_cast(float, (uint32_t)qm);
+                li = __builtin_bit_cast(float, (uint32_t)ql);
+                ml_done = true;
+            }
+            if (pending == 0 && __all(ml_done)) break;
             if (!wait_more(p, t0)) return false;
         }
-        const int kq = i0 >> 6;  // the wt register holding splits i0 .. i0 + 31 (i0 is a multiple of 32)
-        float wq = wt[0];
+        if (i0 == 0) {
+            const float M = wave_max(mi);
+            wt = (lane < na && mi != -INFINITY) ? __expf(mi - M) * li : 0.f;
+            den = wave_sum(wt);
+        }
 #pragma unroll
-        for (int k = 1; k < 4; ++k)
-            if (kq == k) wq = wt[k];
-        for (int k = 0; k < 32 && i0 + k < na; ++k) {
-            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wq), (i0 & 63) + k));
-            const h2_t o = as_h2(S.cst[k][lane]);
-            ox = __builtin_fmaf(w, (float)o.x, ox);
-            oy = __builtin_fmaf(w, (float)o.y, oy);
+        for (int k = 0; k < 32; ++k) {  // fixed trip count: the LDS reads are all in flight together
+            if (i0 + k < na) {
+                const float w =
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), (i0 + k) & 63));
+                const h2_t o = as_h2(S.cst[k][lane]);
+                ox = __builtin_fmaf(w, (float)o.x, ox);
+                oy = __builtin_fmaf(w, (float)o.y, oy);
+            }
         }
     }
     const float inv = 1.0f / den;
@@ -722,57 +726,51 @@ RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
     return true;
 }
 
-// wave 0: this block's 8 rows of the down partials of all blocks, summed -> S.drow
-RK_DEV bool down_gather(const Params& p, uint32_t tag, Lds& S) {
+// wave 0: this block's 8 rows of the down partials of all blocks (summed -> S.drow), then the attention output of
+// all heads (-> permuted pairs per 8 columns + per-32-column sums in LDS). The down partials are ready ~one hop
+// after attention, the attention output ~two, so they are polled in that order.
+RK_DEV bool gather_down_and_ob(const Params& p, uint32_t tag, Lds& S, int pre_down, int pre_ob) {
     const int lane = threadIdx.x & 63;
+    const int nb = gridDim.x;  // at most 256 producers: lane + 64k, k < 4, 4 qwords (8 rows) each
+    const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
+    const uint64_t* tob = reinterpret_cast<const uint64_t*>(p.tob) + z;
+    const uint32_t* tdp = p.tdp + z;
+    uint32_t v[16];
+    bool ok = poll_pairs<16>(
+        p, tag,
+        [&](int k) -> const uint64_t* {
+            const int c = lane + 64 * (k >> 2);
+            return c < nb ? reinterpret_cast<const uint64_t*>(tdp + (size_t)c * kH + 8 * blockIdx.x) + (k & 3)
+                          : nullptr;
+        },
+        v, pre_down);
     float d[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) d[r] = 0.f;
-    const int nb = gridDim.x;
-    bool ok = true;
-    for (int c0 = 0; c0 < nb && ok; c0 += 256) {  // producers c = c0 + lane + 64k: 4 qwords (8 rows) each
-        uint32_t v[16];
-        ok = poll_pairs<16>(
-            p, tag,
-            [&](int k) -> const uint64_t* {
-                const int c = c0 + lane + 64 * (k >> 2);
-                return c < nb ? reinterpret_cast<const uint64_t*>(p.tdp + (size_t)c * kH + 8 * blockIdx.x) + (k & 3)
-                              : nullptr;
-            },
-            v);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            if (c0 + lane + 64 * (k >> 2) < nb) {
-                const h2_t h = as_h2(v[k]);
-                d[2 * (k & 3)] += (float)h.x;
-                d[2 * (k & 3) + 1] += (float)h.y;
-            }
+    for (int k = 0; k < 16; ++k) {
+        if (lane + 64 * (k >> 2) < nb) {
+            const h2_t h = as_h2(v[k]);
+            d[2 * (k & 3)] += (float)h.x;
+            d[2 * (k & 3) + 1] += (float)h.y;
         }
     }
     wave_reduce_rows<8>(d);
     const int r = row_of_lane<8>(lane);
     if (lane == writer_lane<8>(r)) S.drow[r] = d[0];
-    return ok;
-}
-
-// wave 0: the attention output (all heads) -> permuted pairs per 8 columns + per-32-column sums
-RK_DEV bool ob_poll(const Params& p, uint32_t tag, Lds& S) {
-    const int lane = threadIdx.x & 63;
-    const uint64_t* tob = reinterpret_cast<const uint64_t*>(p.tob);
-    uint32_t v[16];
-    const bool ok = poll_pairs<16>(
-        p, tag, [&](int k) -> const uint64_t* { return tob + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v);
+    ok &= poll_pairs<16>(
+        p, tag, [&](int k) -> const uint64_t* { return tob + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v, pre_ob);
     const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int i = lane + 64 * k;  // 8-column block
-        const u4_t d = {v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+        const u4_t dd = {v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
         uint32_t hp[4];
-        pair_permute(d, hp);
+        pair_permute(dd, hp);
         S.vecp[i] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
         float sum = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
+        for (int e = 0; e < 4; ++e) sum = dot2(as_h2(dd[e]), one, sum);
         sum += dpp<0xB1>(sum);  // 4 consecutive 8-blocks (lanes) = one 32-column chunk
         sum += dpp<0x4E>(sum);
         if ((lane & 3) == 0) S.vsum[i >> 2] = sum;
@@ -791,15 +789,11 @@ RK_DEV void o_issue(const Params& p, int l, ORegs& o) {
     const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
     const int K = p.NH * kHD, ng = K / 128;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        o.w[k] = u4_t{0u, 0u, 0u, 0u};
-        o.sm[k] = 0u;
-        if (k == 0 || sw == 0) {
-            const int row = 8 * blockIdx.x + (k == 0 ? sw : 7);
-            const size_t rr = (size_t)l * kH + row;
-            o.w[k] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wo_q + rr * (K / 2)) + lane);
-            o.sm[k] = p.wo_sm[rr * ng + (lane >> 2)];
-        }
+    for (int k = 0; k < 2; ++k) {  // streamers 1..6 load their own row again as the second one (unused)
+        const int row = 8 * blockIdx.x + (k == 1 && sw == 0 ? 7 : sw);
+        const size_t rr = (size_t)l * kH + row;
+        o.w[k] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wo_q + rr * (K / 2)) + lane);
+        o.sm[k] = p.wo_sm[rr * ng + (lane >> 2)];
     }
 }
 
@@ -842,15 +836,11 @@ RK_DEV void head_issue(const Params& p, TileRegs& tr) {
     int r0, r1;
     head_rows(p, r0, r1);
 #pragma unroll
-    for (int e = 0; e < kGPW * kMaxTiles; ++e) head_slot(tr, e) = u4_t{0u, 0u, 0u, 0u};
-#pragma unroll
     for (int k = 0; k < kHeadRows; ++k) {
-        const int r = r0 + sw + kStreamers * k;
-        if (r < r1) {
-            const u4_t* qr = reinterpret_cast<const u4_t*>(p.head_q + (size_t)r * kH);
+        const int r = min(r0 + sw + kStreamers * k, p.n_audio - 1);
+        const u4_t* qr = reinterpret_cast<const u4_t*>(p.head_q + (size_t)r * kH);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) head_slot(tr, 2 * k + j) = __builtin_nontemporal_load(qr + lane + 64 * j);
-        }
+        for (int j = 0; j < 2; ++j) head_slot(tr, 2 * k + j) = __builtin_nontemporal_load(qr + lane + 64 * j);
     }
 }
 
@@ -893,17 +883,22 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
 // ---------------------------------------------------------------------------------------------- the step
 // Wave 0 and the streamers run separate code (so each role's registers are allocated for its own peak, not the
 // sum) and meet at the same sequence of block barriers per layer:
-//   B1 h staged | B2 tile partials | B3 tile outputs (inside tile_epilogue) | B4 epilogue done | B5 q staged,
-//   down partials published | B6 attention partials (inside attention) | B7 attention output staged |
-//   B8 o rows  -- then wave 0 updates and publishes x.  Head: B9 h staged.
-// Streamer issue order (each wait covers only older loads): down(l) after the tile epilogue, consumed after
-// attention(l); then O(l), K/V(l + 1), and after the down partials tiles(l + 1) (the head rows after the last
-// layer), which then have the attention-output and x hops (~5 us) to land. At most ~50 vector-memory instructions
-// are in flight per streamer, and the tile and down prefetches are never live together.
+//   B0 x + LN statistics staged | B1 h staged | B2 partials of tiles [0, 3) | B3 (epilogue) | B4 q / k / v of
+//   those tiles published | B5 partials of tiles [3, 7), q staged | B6 (epilogue) | B7 act staged |
+//   B8 (attention) | B9 attention output + down rows staged | B10 o rows  -- then wave 0 publishes x.
+//   Head: H0 LN statistics staged | H1 h staged.
+// The work table lists a block's q / k / v tiles first (at most 3), so they are computed and published in the
+// first pass and the q / k / v hop overlaps the second pass.
+// Streamer issue order (each wait covers only older loads, see tile_issue): tiles(l + 1) [0, 3) after the first
+// epilogue; after attention(l) and the down partials: O(l), K/V(l + 1), tiles(l + 1) [3, 7), down(l + 1). The
+// loop's back edge and its preheader leave the same sequence outstanding. At most ~57 vector-memory instructions
+// are in flight per streamer (the hardware counter holds 63).
 
 template <int REP>
 RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok, const Work& wk, Lds& S) {
     const int lane = threadIdx.x & 63;
+    TileRegs tr;  // wave 0's two column groups of the block's tiles, issued a layer ahead (before the x poll)
+    tile_issue(p, 0, S, wk, tr, 0, kMaxTiles);
     for (int l = 0; l < p.L; ++l) {
         const uint32_t tag = tag_of(step, l);
         XWave xw;
@@ -913,37 +908,38 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
             x_poll(p, tag_of(step, l - 1), xw);
             if (l == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;  // every block has read pos
         }
-        layernorm_wave(xw, p.ln_w + (size_t)l * kH, p.eps);
-        stage_h_frag(xw, S);
-        __syncthreads();                          // B1
-        __syncthreads();                          // B2
-        tile_epilogue(p, l, pos, tag, wk, S);     // B3 inside
-        __syncthreads();                          // B4
+        ln_stats(xw, p.ln_w + (size_t)l * kH, p.eps, S);
+        __syncthreads();                                      // B0
+        ln_apply_frag(S);
+        __syncthreads();                                      // B1
+        tile_compute<0, kTileSplit>(tr, wk, S);
+        __syncthreads();                                      // B2
+        tile_epilogue(p, l, pos, tag, wk, S, 0, kTileSplit);  // B3 inside
+        __syncthreads();                                      // B4
+        tile_compute<kTileSplit, kMaxTiles>(tr, wk, S);
         q_poll(p, REP, pos, tag, S);
-        __syncthreads();                          // B5
-        __syncthreads();                          // B6
+        __syncthreads();                                      // B5
+        tile_epilogue(p, l, pos, tag, wk, S, kTileSplit, kMaxTiles);  // B6 inside
+        __syncthreads();                                      // B7
+        __syncthreads();                                      // B8
         if (wk.comb >= 0) combine(p, wk.comb, pos, tag, S);
-        down_gather(p, tag, S);
-        ob_poll(p, tag, S);
-        __syncthreads();                          // B7
-        __syncthreads();                          // B8
+        gather_down_and_ob(p, tag, S, kPreDown, kPreOb);
+        __syncthreads();                                      // B9
+        __syncthreads();                                      // B10
         if (lane < 8) S.xrow[lane] = rnd16(S.xrow[lane] + rnd16(S.orow[lane]) + rnd16(S.drow[lane]));
         if (lane < 4)
             st_coh64(reinterpret_cast<uint64_t*>(p.tx) + 4 * blockIdx.x + lane,
                      tpair(S.xrow[2 * lane], S.xrow[2 * lane + 1], tag));
+        tile_issue(p, l + 1 < p.L ? l + 1 : l, S, wk, tr, 0, kMaxTiles);
     }
     // final LayerNorm, h as natural pairs for the int8 head
     XWave xw;
     x_poll(p, tag_of(step, p.L - 1), xw);
     if (p.L == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;
-    layernorm_wave(xw, p.norm_w, p.eps);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float* v = xw.v[k];
-        S.vecp[lane + 64 * k] =
-            make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7]));
-    }
-    __syncthreads();                              // B9
+    ln_stats(xw, p.norm_w, p.eps, S);
+    __syncthreads();                                          // H0
+    ln_apply_pairs(S);
+    __syncthreads();                                          // H1
 }
 
 template <int REP>
@@ -952,29 +948,40 @@ RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Wor
     DownRegs dr;
     KVRegs kv;
     ORegs orr;
-    tile_issue(p, 0, S, wk, tr);
+    // the same outstanding sequence the loop leaves behind at its back edge: tiles [0, 3), K/V, tiles [3, 7), down
+    tile_issue(p, 0, S, wk, tr, 0, kTileSplit);
     kv_issue(p, 0, pos, kv);
+    tile_issue(p, 0, S, wk, tr, kTileSplit, kMaxTiles);
+    down_issue(p, 0, wk, dr);
     for (int l = 0; l < p.L; ++l) {
         const uint32_t tag = tag_of(step, l);
-        const bool last = l + 1 == p.L;
-        __syncthreads();                          // B1
-        tile_compute(tr, wk, S);
-        __syncthreads();                          // B2
-        tile_epilogue(p, l, pos, tag, wk, S);     // B3 inside
-        __syncthreads();                          // B4
-        down_issue(p, l, wk, dr);
-        __syncthreads();                          // B5
-        attention<REP>(p, l, pos, tag, kv, S);    // B6 inside
-        o_issue(p, l, orr);
-        if (!last) kv_issue(p, l + 1, pos, kv);
+        const int ln = l + 1 < p.L ? l + 1 : l;  // the last layer re-issues its own (cache-resident) weights
+        __syncthreads();                                      // B0
+        ln_apply_frag(S);
+        __syncthreads();                                      // B1
+        tile_compute<0, kTileSplit>(tr, wk, S);
+        __syncthreads();                                      // B2
+        tile_epilogue(p, l, pos, tag, wk, S, 0, kTileSplit);  // B3 inside
+        __syncthreads();                                      // B4
+        tile_issue(p, ln, S, wk, tr, 0, kTileSplit);          // next layer's tiles, first part
+        tile_compute<kTileSplit, kMaxTiles>(tr, wk, S);
+        __syncthreads();                                      // B5
+        tile_epilogue(p, l, pos, tag, wk, S, kTileSplit, kMaxTiles);  // B6 inside
+        __syncthreads();                                      // B7
+        attention<REP>(p, l, pos, tag, kv, S);                // B8 inside
         down_compute(p, tag, wk, dr, S);
-        if (!last) tile_issue(p, l + 1, S, wk, tr);
-        else head_issue(p, tr);
-        __syncthreads();                          // B7
+        o_issue(p, l, orr);
+        kv_issue(p, ln, pos, kv);
+        tile_issue(p, ln, S, wk, tr, kTileSplit, kMaxTiles);  // second part
+        down_issue(p, ln, wk, dr);
+        __syncthreads();                                      // B9
         o_compute(orr, S);
-        __syncthreads();                          // B8
+        __syncthreads();                                      // B10
     }
-    __syncthreads();                              // B9
+    head_issue(p, tr);
+    __syncthreads();                                          // H0
+    ln_apply_pairs(S);
+    __syncthreads();                                          // H1
     head_compute(p, tr, S);
 }
 
@@ -991,6 +998,10 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     }
     const uint32_t step = p.ctr[blockIdx.x];
     if (tid < kWork) S.work[tid] = p.work[(size_t)blockIdx.x * kWork + tid];
+    if (tid < kHD / 2) {  // the table holds each angle twice (pair elements 2i, 2i + 1)
+        S.rcos[tid] = h16(p.cos_t[(size_t)pos * kHD + 2 * tid]);
+        S.rsin[tid] = h16(p.sin_t[(size_t)pos * kHD + 2 * tid]);
+    }
     if (tid < 8) S.xrow[tid] = rnd16((float)p.emb_q[(size_t)tok * kH + 8 * blockIdx.x + tid] * h16(p.emb_s[tok]));
     __syncthreads();
     const Work wk = work_of(S);
@@ -1029,7 +1040,8 @@ extern "C" int rk_decode_step_persistent(const rk_decode_params* params, int nbl
     if (!(rep == 1 || rep == 2 || rep == 4 || rep == 8)) return RK_ERR_SHAPE;
     if (p.inter <= 0 || p.inter % 128 || p.inter > 11008) return RK_ERR_SHAPE;
     if (nblocks <= 0 || nblocks * 8 != kH) return RK_ERR_BLOCK;  // block b owns rows [8b, 8b + 8)
-    if (p.nsp <= 0 || p.nsp > 256 || p.NKV * p.nsp > nblocks || p.inter / 16 > kMaxSlices * nblocks)
+    if (p.nsp <= 0 || p.nsp > 64 || p.NKV * p.nsp > nblocks || p.inter / 16 > kMaxSlices * nblocks ||
+        (p.S + p.nsp - 1) / p.nsp > kStreamers * kKVPre)  // every cached slot of a split is prefetched
         return RK_ERR_BLOCK;
     if (!p.tok || !p.pos || !p.emb_q || !p.emb_s || !p.win_t || !p.win_sm || !p.wo_q || !p.wo_sm ||
         !p.wd_t || !p.wd_sm || !p.ln_w || !p.norm_w || !p.cos_t || !p.sin_t || !p.kc || !p.vc || !p.head_q ||

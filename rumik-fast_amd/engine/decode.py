@@ -160,6 +160,7 @@ class RkDecodeParams(ctypes.Structure):
 
 
 MAX_TILES, MAX_SLICES, WORK = 7, 3, 16   # kMaxTiles, kMaxSlices, kWork of csrc/decode_persistent.hip
+FIRST_PASS = 3                           # kTileSplit: a block's q / k / v tiles are computed in its first pass
 
 
 def interleave_gate_up(t, cfg):
@@ -176,6 +177,15 @@ def pack_scale_min(s, m):
     lo = s.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
     hi = m.contiguous().view(torch.int16).to(torch.int32) << 16
     return (lo | hi).contiguous()
+
+
+def wave_scale_min(sm):
+    """per-(row, group) scale | min words [n_in, 16] -> per (tile, wave, row) the two words of the wave's groups:
+    waves 1..7 hold groups 2(w - 1), 2(w - 1) + 1, wave 0 groups 14, 15. Returns int32 [n_in / 16, 8, 16, 2]."""
+    nt = sm.shape[0] // 16
+    per_group = sm.reshape(nt, 16, 8, 2)            # [tile, row, group pair, 2]
+    order = torch.tensor([7, 0, 1, 2, 3, 4, 5, 6])  # wave w -> group pair (w + 7) % 8
+    return per_group[:, :, order].permute(0, 2, 1, 3).contiguous()
 
 
 def tile_layout(q):
@@ -211,6 +221,8 @@ def work_table(cfg, nblocks, nsp):
         qkv[b].append(t)
     table = torch.full((nblocks, WORK), -1, dtype=torch.int16)
     for b in range(nblocks):
+        if len(qkv[b]) > FIRST_PASS:
+            raise ValueError(f"block {b} would hold {len(qkv[b])} q/k/v tiles (at most {FIRST_PASS})")
         tl = qkv[b] + tiles[b]
         if len(tl) > MAX_TILES:
             raise ValueError(f"block {b} would hold {len(tl)} tiles (at most {MAX_TILES})")
@@ -235,14 +247,17 @@ class PersistentDecode:
         self.cfg, self.dev = cfg, torch.device(device)
         d = self.dev
         self.nblocks = 2048 // 8
-        self.nsp = nsp or min(32, self.nblocks // cfg.NKV)
+        self.nsp = nsp or min(64, self.nblocks // cfg.NKV)
+        if self.nsp > 64:
+            raise ValueError("at most 64 attention splits per KV head")
         lib = HL.lib()
         if lib.rk_decode_params_size() != ctypes.sizeof(RkDecodeParams):
             raise RuntimeError("rk_decode_params layout mismatch between the library and decode.py")
         w, c = weights, cfg
         stack = lambda f, key: torch.stack([f(t) for t in w[key]]).contiguous()  # noqa: E731
         self.win_t = stack(lambda t: tile_layout(interleave_gate_up(t[0], c)), "w_in")
-        self.win_sm = stack(lambda t: pack_scale_min(interleave_gate_up(t[1], c), interleave_gate_up(t[2], c)), "w_in")
+        self.win_sm = stack(lambda t: wave_scale_min(pack_scale_min(interleave_gate_up(t[1], c),
+                                                                     interleave_gate_up(t[2], c))), "w_in")
         self.wo_q = stack(lambda t: t[0], "w_o")
         self.wo_sm = stack(lambda t: pack_scale_min(t[1], t[2]), "w_o")
         self.wd_t = stack(lambda t: down_layout(t[0]), "w_down")

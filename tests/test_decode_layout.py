@@ -15,6 +15,11 @@ def test_work_table_covers_every_tile_once(cfg_kw):
     n_tiles = qkv_tiles + 2 * cfg.inter // 16
     tiles = t[:, :8]
     assert (tiles >= 0).sum(1).max() <= decode.MAX_TILES
+    # q / k / v tiles come first and fit the first pass
+    for b in range(nb):
+        row = [int(v) for v in tiles[b] if v >= 0]
+        nq = sum(v < qkv_tiles for v in row)
+        assert nq <= decode.FIRST_PASS and all(v < qkv_tiles for v in row[:nq])
     got = sorted(int(v) for v in tiles.flatten() if v >= 0)
     assert got == list(range(n_tiles))
     # slices are contiguous, cover all MLP channels, and each block owns the gate/up tiles of its slices

@@ -170,11 +170,11 @@ typedef struct rk_decode_params {
     const uint16_t* head_s; /* [n_audio] fp16 */
     float* logits;          /* [n_audio] */
     const int16_t* work;    /* [nblocks, 16]: w_in tiles (8, -1 = none), slice begin, slice end, combined head (-1 = none) */
-    uint32_t* tx;           /* [2048] */
+    uint32_t* tx;           /* [16, 2048]: 16 copies */
     uint32_t* tq;           /* [NH*128] */
     uint32_t* tkv;          /* [2, NKV*128] (k, v of the current layer at pos) */
-    uint32_t* tob;          /* [NH*128] */
-    uint32_t* tdp;          /* [nblocks, 2048] down-projection partials */
+    uint32_t* tob;          /* [16, NH*128]: 16 copies */
+    uint32_t* tdp;          /* [nblocks (consumer), nblocks (producer), 8] down-projection partials */
     uint32_t* tpo;          /* [NH, nsp, 128] normalized split outputs */
     unsigned long long* tml; /* [NH, nsp, 2] */
     unsigned* ctr;          /* [nblocks] step counters */

@@ -54,6 +54,10 @@ constexpr int kKVPre = 5;                  // cached slots per streamer whose K 
 constexpr int kHeadRows = 7;               // head rows per streamer loaded ahead (the rest load when used)
 constexpr int kWork = 16;                  // int16 entries per block in the work table
 constexpr int kPreDown = 2, kPreOb = 1;    // ~0.5 us waits before the down-partial and attention-output polls
+// x and the attention output are polled by every block: they are published in kXRep copies 8 KB apart and block b
+// polls copy b % kXRep, so no 8 KB stretch of memory serves more than 16 pollers
+constexpr int kXRep = 16;
+constexpr int kRepQwords = kH / 2;         // qwords per copy (2048 tagged fp16 words)
 constexpr uint64_t kWaitTicks = 20000000ull;  // 200 ms at the 100 MHz wall clock
 constexpr unsigned kAbort = 1u, kTimeout = 2u, kBadPos = 4u;
 
@@ -92,9 +96,10 @@ RK_DEV bool pair_ok(uint64_t q, uint32_t tag) {
 // the two fp16 values of a tagged pair as one packed fp16x2 dword
 RK_DEV uint32_t pair_val(uint64_t q) { return (uint32_t)(q & 0xFFFFu) | ((uint32_t)(q >> 16) & 0xFFFF0000u); }
 
-// true while a wait may go on; on expiry raise the abort bit
-RK_DEV bool wait_more(const Params& p, uint64_t t0) {
-    if (ld_coh(p.status) & kAbort) return false;
+// true while a wait may go on; on expiry raise the abort bit. `status` is the status word loaded in the same batch
+// as the poll it belongs to (one round trip per poll iteration).
+RK_DEV bool wait_more(const Params& p, uint64_t t0, uint32_t status) {
+    if (status & kAbort) return false;
     if (wall_clock64() - t0 > kWaitTicks) {
         if ((threadIdx.x & 63) == 0) atomicOr(p.status, kAbort | kTimeout);
         return false;
@@ -111,11 +116,16 @@ RK_DEV void pre_wait(int pre) {
 }
 
 // Poll N tagged fp16 pairs per lane (qword addresses from addr(k); nullptr = not needed) until every tag matches;
-// val[k] receives the packed pair. Wave-uniform control flow; false after an abort or a timeout.
+// val[k] receives the packed pair. Every iteration loads all N words and the status word unconditionally, so they
+// are one batch with a single wait: reloading a word already validated is harmless, because its next value is
+// written only after every consumer has finished this poll (the exchanges' dataflow order), and its first
+// validated value is the one kept. Wave-uniform control flow; false after an abort or a timeout.
 template <int N, class Addr>
 RK_DEV bool poll_pairs(const Params& p, uint32_t tag, Addr addr, uint32_t (&val)[N], int pre = 1) {
     static_assert(N <= 32, "pending mask");
     pre_wait(pre);
+    // a valid, lane-varying address for the unneeded slots (a uniform one is turned into scalar moves and waits)
+    const uint64_t* dummy = reinterpret_cast<const uint64_t*>(p.tx) + (threadIdx.x & 63);
     uint32_t pending = 0;
 #pragma unroll
     for (int k = 0; k < N; ++k)
@@ -124,8 +134,11 @@ RK_DEV bool poll_pairs(const Params& p, uint32_t tag, Addr addr, uint32_t (&val)
     while (true) {
         uint64_t q[N];
 #pragma unroll
-        for (int k = 0; k < N; ++k)
-            if (pending & (1u << k)) q[k] = ld_coh64(addr(k));
+        for (int k = 0; k < N; ++k) {
+            const uint64_t* a = addr(k);
+            q[k] = ld_coh64(a ? a : dummy);
+        }
+        const uint32_t st = ld_coh(p.status);
 #pragma unroll
         for (int k = 0; k < N; ++k)
             if ((pending & (1u << k)) && pair_ok(q[k], tag)) {
@@ -133,7 +146,7 @@ RK_DEV bool poll_pairs(const Params& p, uint32_t tag, Addr addr, uint32_t (&val)
                 pending &= ~(1u << k);
             }
         if (__all(pending == 0)) return true;
-        if (!wait_more(p, t0)) return false;
+        if (!wait_more(p, t0, st)) return false;
     }
 }
 
@@ -206,7 +219,8 @@ RK_DEV void x_from_embedding(const Params& p, int64_t tok, XWave& xw) {
 RK_DEV bool x_poll(const Params& p, uint32_t tag, XWave& xw) {
     const int lane = threadIdx.x & 63;
     // the opaque zero keeps the addresses from being hoisted out of the layer loop (they would pin ~30 VGPRs)
-    const uint64_t* tx = reinterpret_cast<const uint64_t*>(p.tx) + opaque_vgpr(0u);
+    const uint64_t* tx =
+        reinterpret_cast<const uint64_t*>(p.tx) + (blockIdx.x % kXRep) * kRepQwords + opaque_vgpr(0u);
     uint32_t v[16];
     const bool ok = poll_pairs<16>(
         p, tag, [&](int k) -> const uint64_t* { return tx + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v);
@@ -446,7 +460,9 @@ RK_DEV void down_issue(const Params& p, int l, const Work& wk, DownRegs& dr) {
     }
 }
 
-// partial down output of this block's channels for all 2048 rows, published tagged (tdp[block][row])
+// partial down output of this block's channels for all 2048 rows, published tagged. tdp is laid out
+// [consumer block][producer block][8 rows]: a consumer's rows from all producers form one contiguous 8 KB run, so
+// its polls touch 64 cache lines instead of one line per producer.
 RK_DEV void down_compute(const Params& p, uint32_t tag, const Work& wk, const DownRegs& dr, const Lds& S) {
     const int sl = threadIdx.x - 64;
     const Int4Masks km = int4_masks();
@@ -464,7 +480,7 @@ RK_DEV void down_compute(const Params& p, uint32_t tag, const Work& wk, const Do
 #pragma unroll
         for (int c = 0; c < 16; ++c) asum[i] += a[c];
     }
-    uint64_t* out = reinterpret_cast<uint64_t*>(p.tdp + (size_t)blockIdx.x * kH);
+    uint64_t* out = reinterpret_cast<uint64_t*>(p.tdp) + (size_t)blockIdx.x * 4;  // + (consumer * nb) * 4 + pair
 #pragma unroll
     for (int k = 0; k < kRP; ++k) {
         const int rp = min(sl + kSLanes * k, kH / 2 - 1);  // the clamped lanes rewrite the last pair's own value
@@ -490,7 +506,7 @@ RK_DEV void down_compute(const Params& p, uint32_t tag, const Work& wk, const Do
                     }
                 }
             }
-            st_coh64(out + rp, tpair(d[0], d[1], tag));
+            st_coh64(out + (size_t)(rp >> 2) * gridDim.x * 4 + (rp & 3), tpair(d[0], d[1], tag));
         }
     }
 }
@@ -679,18 +695,16 @@ RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
     // the first batch also brings split lane's (m, l)
     bool ml_done = lane >= na;
     float mi = -INFINITY, li = 0.f, wt = 0.f, den = 0.f, ox = 0.f, oy = 0.f;
+    const uint64_t* tml_l = lane < nsp ? tml : reinterpret_cast<const uint64_t*>(p.tml);  // lanes past nsp: any valid
     for (int i0 = 0; i0 < na; i0 += 32) {
         uint32_t pending = na - i0 >= 32 ? ~0u : ((1u << (na - i0)) - 1);
         while (true) {
+            // one batch per iteration (see poll_pairs): every split's pair, the (m, l) words and the status
             uint64_t q[32];
 #pragma unroll
-            for (int k = 0; k < 32; ++k)
-                if (pending & (1u << k)) q[k] = ld_coh64(po + (size_t)(i0 + k) * (kHD / 2));
-            uint64_t qm = 0, ql = 0;
-            if (!__all(ml_done)) {
-                qm = ld_coh64(tml);
-                ql = ld_coh64(tml + 1);
-            }
+            for (int k = 0; k < 32; ++k) q[k] = ld_coh64(po + (size_t)min(i0 + k, nsp - 1) * (kHD / 2));
+            const uint64_t qm = ld_coh64(tml_l), ql = ld_coh64(tml_l + 1);
+            const uint32_t st = ld_coh(p.status);
 #pragma unroll
             for (int k = 0; k < 32; ++k)
                 if ((pending & (1u << k)) && __all(pair_ok(q[k], tag))) {
@@ -703,26 +717,30 @@ RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
                 ml_done = true;
             }
             if (pending == 0 && __all(ml_done)) break;
-            if (!wait_more(p, t0)) return false;
+            if (!wait_more(p, t0, st)) return false;
         }
         if (i0 == 0) {
             const float M = wave_max(mi);
             wt = (lane < na && mi != -INFINITY) ? __expf(mi - M) * li : 0.f;
             den = wave_sum(wt);
         }
+        // unconditional LDS reads (all in flight together); entries past the last split are masked to zero
+        uint32_t c[32];
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {  // fixed trip count: the LDS reads are all in flight together
-            if (i0 + k < na) {
-                const float w =
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), (i0 + k) & 63));
-                const h2_t o = as_h2(S.cst[k][lane]);
-                ox = __builtin_fmaf(w, (float)o.x, ox);
-                oy = __builtin_fmaf(w, (float)o.y, oy);
-            }
+        for (int k = 0; k < 32; ++k) c[k] = S.cst[k][lane];
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const float w =
+                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), (i0 + k) & 63));
+            const h2_t o = as_h2(i0 + k < na ? c[k] : 0u);
+            ox = __builtin_fmaf(w, (float)o.x, ox);
+            oy = __builtin_fmaf(w, (float)o.y, oy);
         }
     }
     const float inv = 1.0f / den;
-    st_coh64(reinterpret_cast<uint64_t*>(p.tob + (size_t)h * kHD) + lane, tpair(ox * inv, oy * inv, tag));
+    const uint64_t o = tpair(ox * inv, oy * inv, tag);
+#pragma unroll
+    for (int r = 0; r < kXRep; ++r) st_coh64(reinterpret_cast<uint64_t*>(p.tob) + r * kRepQwords + h * (kHD / 2) + lane, o);
     return true;
 }
 
@@ -731,33 +749,38 @@ RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
 // after attention, the attention output ~two, so they are polled in that order.
 RK_DEV bool gather_down_and_ob(const Params& p, uint32_t tag, Lds& S, int pre_down, int pre_ob) {
     const int lane = threadIdx.x & 63;
-    const int nb = gridDim.x;  // at most 256 producers: lane + 64k, k < 4, 4 qwords (8 rows) each
+    const int nb = gridDim.x;  // at most 256 producers, 4 qwords (8 rows) each: 16 qwords per lane
     const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
-    const uint64_t* tob = reinterpret_cast<const uint64_t*>(p.tob) + z;
+    const uint64_t* tob = reinterpret_cast<const uint64_t*>(p.tob) + (blockIdx.x % kXRep) * kRepQwords + z;
     const uint32_t* tdp = p.tdp + z;
     uint32_t v[16];
+    // qword q = 64k + lane of this block's run: producer q / 4, rows 2(q % 4), 2(q % 4) + 1
+    const uint64_t* run = reinterpret_cast<const uint64_t*>(tdp) + (size_t)blockIdx.x * nb * 4;
     bool ok = poll_pairs<16>(
-        p, tag,
-        [&](int k) -> const uint64_t* {
-            const int c = lane + 64 * (k >> 2);
-            return c < nb ? reinterpret_cast<const uint64_t*>(tdp + (size_t)c * kH + 8 * blockIdx.x) + (k & 3)
-                          : nullptr;
-        },
-        v, pre_down);
-    float d[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) d[r] = 0.f;
+        p, tag, [&](int k) -> const uint64_t* { return 64 * k + lane < 4 * nb ? run + 64 * k + lane : nullptr; }, v,
+        pre_down);
+    float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        if (lane + 64 * (k >> 2) < nb) {
+        if (64 * k + lane < 4 * nb) {
             const h2_t h = as_h2(v[k]);
-            d[2 * (k & 3)] += (float)h.x;
-            d[2 * (k & 3) + 1] += (float)h.y;
+            d0 += (float)h.x;
+            d1 += (float)h.y;
         }
     }
-    wave_reduce_rows<8>(d);
-    const int r = row_of_lane<8>(lane);
-    if (lane == writer_lane<8>(r)) S.drow[r] = d[0];
+    // sum over the lanes that share lane % 4
+    d0 += xor_lane<4>(d0);
+    d1 += xor_lane<4>(d1);
+    d0 += xor_lane<8>(d0);
+    d1 += xor_lane<8>(d1);
+    d0 += xor_lane<16>(d0);
+    d1 += xor_lane<16>(d1);
+    d0 += xor_lane<32>(d0);
+    d1 += xor_lane<32>(d1);
+    if (lane < 4) {
+        S.drow[2 * lane] = d0;
+        S.drow[2 * lane + 1] = d1;
+    }
     ok &= poll_pairs<16>(
         p, tag, [&](int k) -> const uint64_t* { return tob + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v, pre_ob);
     const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
@@ -927,9 +950,10 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
         __syncthreads();                                      // B9
         __syncthreads();                                      // B10
         if (lane < 8) S.xrow[lane] = rnd16(S.xrow[lane] + rnd16(S.orow[lane]) + rnd16(S.drow[lane]));
-        if (lane < 4)
-            st_coh64(reinterpret_cast<uint64_t*>(p.tx) + 4 * blockIdx.x + lane,
-                     tpair(S.xrow[2 * lane], S.xrow[2 * lane + 1], tag));
+        static_assert(4 * kXRep <= 64, "one store per lane");
+        if (lane < 4 * kXRep)  // lane = copy * 4 + pair
+            st_coh64(reinterpret_cast<uint64_t*>(p.tx) + (lane >> 2) * kRepQwords + 4 * blockIdx.x + (lane & 3),
+                     tpair(S.xrow[2 * (lane & 3)], S.xrow[2 * (lane & 3) + 1], tag));
         tile_issue(p, l + 1 < p.L ? l + 1 : l, S, wk, tr, 0, kMaxTiles);
     }
     // final LayerNorm, h as natural pairs for the int8 head

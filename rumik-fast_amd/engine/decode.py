@@ -161,6 +161,7 @@ class RkDecodeParams(ctypes.Structure):
 
 MAX_TILES, MAX_SLICES, WORK = 7, 3, 16   # kMaxTiles, kMaxSlices, kWork of csrc/decode_persistent.hip
 FIRST_PASS = 3                           # kTileSplit: a block's q / k / v tiles are computed in its first pass
+X_COPIES = 16                            # kXRep: x and the attention output are published in 16 copies
 
 
 def interleave_gate_up(t, cfg):
@@ -270,10 +271,10 @@ class PersistentDecode:
         self.work = work_table(c, self.nblocks, self.nsp).to(d)
         f16, f32, i32 = torch.float16, torch.float32, torch.int32
         nb = self.nblocks
-        self.tx = torch.zeros(2048, dtype=i32, device=d)
+        self.tx = torch.zeros(X_COPIES * 2048, dtype=i32, device=d)
         self.tq = torch.zeros(c.NH * c.HD, dtype=i32, device=d)
         self.tkv = torch.zeros(2 * c.NKV * c.HD, dtype=i32, device=d)
-        self.tob = torch.zeros(c.NH * c.HD, dtype=i32, device=d)
+        self.tob = torch.zeros(X_COPIES * c.NH * c.HD, dtype=i32, device=d)
         self.tdp = torch.zeros(nb * 2048, dtype=i32, device=d)
         self.tpo = torch.zeros(c.NH * self.nsp * c.HD, dtype=i32, device=d)
         self.tml = torch.zeros(c.NH * self.nsp * 2, dtype=torch.int64, device=d)
@@ -305,7 +306,7 @@ class PersistentDecode:
     @property
     def x(self):
         """the residual stream after the last layer of the last step (fp16, decoded from the tagged words)"""
-        return self.tx.view(torch.float16)[0::2]
+        return self.tx[:2048].view(torch.float16)[0::2]
 
     def reset(self):
         """Zero the exchange buffers, step counters and status (needed after a nonzero status)."""

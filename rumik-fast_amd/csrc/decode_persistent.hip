@@ -163,7 +163,8 @@ struct Lds {
     float2 s_acc[kStreamers][kMaxRep][64];    // per-streamer attention partials
     uint4 vecp[kH / 8];                       // attention output (permuted pairs) / h (natural pairs, head)
     float vsum[kH / 32];                      // per-32-column sums of the attention output
-    uint32_t cst[32][64];                     // the combine's validated split outputs (one batch)
+    float2 cpa[kStreamers][64];               // the combine's per-streamer parts: sum of w_i o_i per dim pair,
+    float cpm[kStreamers], cpl[kStreamers];   //   the streamer's max m and sum of w_i
     float orow[8], drow[8], xrow[8];          // this block's rows of o, down and the residual stream
     float rcos[kHD / 2], rsin[kHD / 2];       // RoPE cos / sin of pair i at pos
     uint4 xraw[kH / 8];                       // x (fp16, 8 per entry) for the block-wide LayerNorm
@@ -239,11 +240,20 @@ RK_DEV bool x_poll(const Params& p, uint32_t tag, XWave& xw) {
 // wave 0 holds x after its poll, computes mean and rstd and stages x and the weights in LDS (ln_stats); then
 // threads 0..255 normalize one 8-column block each and stage it (ln_apply_frag for the MFMA fragments of h,
 // ln_apply_pairs for the head's natural pairs).
-RK_DEV void ln_stats(const XWave& xw, const uint16_t* w, float eps, Lds& S) {
+// the LayerNorm weights of one row, 4 x 16 bytes per lane; loaded before the x poll so that their round trip
+// overlaps it
+struct LnW {
+    u4_t v[4];
+};
+RK_DEV void ln_w_issue(const uint16_t* w, LnW& wv) {
     const int lane = threadIdx.x & 63;
-    u4_t wv[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) wv[k] = reinterpret_cast<const u4_t*>(w)[lane + 64 * k];
+    for (int k = 0; k < 4; ++k) wv.v[k] = reinterpret_cast<const u4_t*>(w)[lane + 64 * k];
+}
+
+RK_DEV void ln_stats(const XWave& xw, const LnW& lw, float eps, Lds& S) {
+    const int lane = threadIdx.x & 63;
+    const u4_t* wv = lw.v;
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -287,7 +297,7 @@ RK_DEV void ln_block(const Lds& S, int i, float (&h)[8]) {
 
 // h -> MFMA A fragments (pairs permuted as the dequant orders the codes) + per-group sums; threads 0..255
 RK_DEV void ln_apply_frag(Lds& S) {
-    const int i = threadIdx.x;
+    const int i = (int)opaque_vgpr(threadIdx.x);  // recomputed per call: a hoisted LDS address would be spilled
     if (i >= kH / 8) return;
     float h[8];
     ln_block(S, i, h);
@@ -512,7 +522,10 @@ RK_DEV void down_compute(const Params& p, uint32_t tag, const Work& wk, const Do
 }
 
 // ---------------------------------------------------------------------------------------------- attention
-RK_DEV int split_chunk(int n, int nsp) { return ((n + nsp - 1) / nsp + 7) & ~7; }
+// slots per attention split: n / nsp rounded up to 8, at least kMinChunk (short contexts use fewer, fuller splits,
+// so the combine waits on fewer blocks)
+constexpr int kMinChunk = 16;
+RK_DEV int split_chunk(int n, int nsp) { return max(kMinChunk, ((n + nsp - 1) / nsp + 7) & ~7); }
 
 struct Split {
     bool att;           // this block runs a split
@@ -568,7 +581,7 @@ RK_DEV bool q_poll(const Params& p, int rep, int64_t pos, uint32_t tag, Lds& S) 
             if (!has_pos) return nullptr;
             return tkv + (size_t)((k - kMaxRep) * p.NKV + s.g) * (kHD / 2) + lane;
         },
-        v);
+        v, 0);  // no pre-wait: the poll starts after the second tile pass, well after q was written
 #pragma unroll
     for (int k = 0; k < kMaxRep; ++k)
         if (k < rep) S.qs[k][lane] = v[k];
@@ -675,40 +688,48 @@ RK_DEV void attention(const Params& p, int l, int64_t pos, uint32_t tag, const K
     }
 }
 
-// wave 0 of head h's combiner: out = sum_i w_i o_i / sum_i w_i, w_i = exp(m_i - max m) * l_i over the splits
-// holding at least one slot (at most 64); published tagged. Polling loops of 32 splits gather the o pairs (the
-// first also split lane's (m, l)); validated pairs are staged in LDS and summed in split order (the result does
-// not depend on arrival order).
-RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
-    const int lane = threadIdx.x & 63;
-    const int nsp = p.nsp;
+// Head h's combine: out = sum_i w_i o_i / sum_i w_i, w_i = exp(m_i - max m) * l_i over the splits holding at least
+// one slot (at most 64). The streamers of the combining block share the polling: streamer sw polls splits
+// [kCombPer * sw, kCombPer * (sw + 1)) in one batch per iteration and leaves (M = its max m, L = sum of its w_i taken
+// against M, sum of w_i o_i) in LDS; after a block barrier wave 0 merges the 7 parts (comb_merge). The sums run in split order within a wave and in
+// wave order across waves, so the result does not depend on arrival order.
+RK_DEV int comb_splits(const Params& p, int64_t pos) {
     const int n = (int)min<int64_t>(pos + 1, (int64_t)p.S);
-    const int ch = split_chunk(n, nsp);
-    const int na = min(nsp, (n + ch - 1) / ch);
-    const size_t hb = (size_t)h * nsp;
-    const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
-    const uint64_t* tml = reinterpret_cast<const uint64_t*>(p.tml) + 2 * (hb + lane) + z;
-    const uint64_t* po = reinterpret_cast<const uint64_t*>(p.tpo + hb * kHD) + lane + z;
-    pre_wait(1);
-    const uint64_t t0 = wall_clock64();
-    // splits in batches of 32, wave-uniform pending bits: split k counts as arrived when every lane sees its tag;
-    // the first batch also brings split lane's (m, l)
-    bool ml_done = lane >= na;
-    float mi = -INFINITY, li = 0.f, wt = 0.f, den = 0.f, ox = 0.f, oy = 0.f;
-    const uint64_t* tml_l = lane < nsp ? tml : reinterpret_cast<const uint64_t*>(p.tml);  // lanes past nsp: any valid
-    for (int i0 = 0; i0 < na; i0 += 32) {
-        uint32_t pending = na - i0 >= 32 ? ~0u : ((1u << (na - i0)) - 1);
+    const int ch = split_chunk(n, p.nsp);
+    return min(p.nsp, (n + ch - 1) / ch);
+}
+
+constexpr int kCombPer = 10;  // splits per streamer (7 x 10 >= 64)
+
+RK_DEV bool comb_part(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
+    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
+    const int nsp = p.nsp, i0 = kCombPer * sw;
+    const int cnt = min(max(comb_splits(p, pos) - i0, 0), kCombPer);
+    float M = -INFINITY, L = 0.f, ax = 0.f, ay = 0.f;
+    bool ok = true;
+    if (cnt > 0) {
+        const size_t hb = (size_t)h * nsp;
+        const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
+        const uint64_t* po = reinterpret_cast<const uint64_t*>(p.tpo + hb * kHD) + lane + z;
+        // lane j < kCombPer brings split i0 + j's (m, l); the other lanes repeat one of those loads
+        const int jl = lane % kCombPer;
+        const uint64_t* tml = reinterpret_cast<const uint64_t*>(p.tml) + 2 * (hb + min(i0 + jl, nsp - 1)) + z;
+        const uint64_t t0 = wall_clock64();
+        uint32_t pending = (1u << cnt) - 1;
+        bool ml_done = jl >= cnt;
+        float mi = -INFINITY, li = 0.f;
+        uint32_t val[kCombPer];
         while (true) {
-            // one batch per iteration (see poll_pairs): every split's pair, the (m, l) words and the status
-            uint64_t q[32];
+            // one batch per iteration (see poll_pairs): the splits' pairs, the (m, l) words and the status
+            uint64_t q[kCombPer];
 #pragma unroll
-            for (int k = 0; k < 32; ++k) q[k] = ld_coh64(po + (size_t)min(i0 + k, nsp - 1) * (kHD / 2));
-            const uint64_t qm = ld_coh64(tml_l), ql = ld_coh64(tml_l + 1);
+            for (int k = 0; k < kCombPer; ++k) q[k] = ld_coh64(po + (size_t)min(i0 + k, nsp - 1) * (kHD / 2));
+            const uint64_t qm = ld_coh64(tml), ql = ld_coh64(tml + 1);
             const uint32_t st = ld_coh(p.status);
 #pragma unroll
-            for (int k = 0; k < 32; ++k)
+            for (int k = 0; k < kCombPer; ++k)
                 if ((pending & (1u << k)) && __all(pair_ok(q[k], tag))) {
-                    S.cst[k][lane] = pair_val(q[k]);
+                    val[k] = pair_val(q[k]);
                     pending &= ~(1u << k);
                 }
             if (!ml_done && (uint32_t)(qm >> 32) == tag && (uint32_t)(ql >> 32) == tag) {
@@ -717,31 +738,55 @@ RK_DEV bool combine(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S) {
                 ml_done = true;
             }
             if (pending == 0 && __all(ml_done)) break;
-            if (!wait_more(p, t0, st)) return false;
+            if (!wait_more(p, t0, st)) {
+                ok = false;
+                break;
+            }
         }
-        if (i0 == 0) {
-            const float M = wave_max(mi);
-            wt = (lane < na && mi != -INFINITY) ? __expf(mi - M) * li : 0.f;
-            den = wave_sum(wt);
-        }
-        // unconditional LDS reads (all in flight together); entries past the last split are masked to zero
-        uint32_t c[32];
+        if (ok) {
+            // lanes 0..kCombPer-1 hold the splits' (m, l): the max, then each split's weight, broadcast by readlane
+            M = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) c[k] = S.cst[k][lane];
+            for (int k = 0; k < kCombPer; ++k)
+                if (k < cnt) M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mi), k)));
+            const float wl = (jl < cnt && mi != -INFINITY) ? __expf(mi - M) * li : 0.f;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
-            const float w =
-                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), (i0 + k) & 63));
-            const h2_t o = as_h2(i0 + k < na ? c[k] : 0u);
-            ox = __builtin_fmaf(w, (float)o.x, ox);
-            oy = __builtin_fmaf(w, (float)o.y, oy);
+            for (int k = 0; k < kCombPer; ++k) {
+                const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k));
+                const h2_t o = as_h2(k < cnt ? val[k] : 0u);
+                ax = __builtin_fmaf(wk, (float)o.x, ax);
+                ay = __builtin_fmaf(wk, (float)o.y, ay);
+                L += wk;
+            }
         }
     }
-    const float inv = 1.0f / den;
+    S.cpa[sw][lane] = make_float2(ax, ay);
+    if (lane == 0) {
+        S.cpm[sw] = M;
+        S.cpl[sw] = L;
+    }
+    return ok;
+}
+
+// wave 0, after the barrier that follows the streamers' comb_part: merge the parts, publish in kXRep copies
+RK_DEV void comb_merge(const Params& p, int h, uint32_t tag, const Lds& S) {
+    const int lane = threadIdx.x & 63;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kStreamers; ++w) M = fmaxf(M, S.cpm[w]);
+    float den = 0.f, ox = 0.f, oy = 0.f;
+#pragma unroll
+    for (int w = 0; w < kStreamers; ++w) {
+        const float f = S.cpm[w] == -INFINITY ? 0.f : __expf(S.cpm[w] - M);
+        const float2 a = S.cpa[w][lane];
+        den = __builtin_fmaf(f, S.cpl[w], den);
+        ox = __builtin_fmaf(f, a.x, ox);
+        oy = __builtin_fmaf(f, a.y, oy);
+    }
+    const float inv = den > 0.f ? 1.0f / den : 0.f;
     const uint64_t o = tpair(ox * inv, oy * inv, tag);
 #pragma unroll
     for (int r = 0; r < kXRep; ++r) st_coh64(reinterpret_cast<uint64_t*>(p.tob) + r * kRepQwords + h * (kHD / 2) + lane, o);
-    return true;
 }
 
 // wave 0: this block's 8 rows of the down partials of all blocks (summed -> S.drow), then the attention output of
@@ -908,7 +953,8 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
 // sum) and meet at the same sequence of block barriers per layer:
 //   B0 x + LN statistics staged | B1 h staged | B2 partials of tiles [0, 3) | B3 (epilogue) | B4 q / k / v of
 //   those tiles published | B5 partials of tiles [3, 7), q staged | B6 (epilogue) | B7 act staged |
-//   B8 (attention) | B9 attention output + down rows staged | B10 o rows  -- then wave 0 publishes x.
+//   B8 (attention) | BC (combining blocks only) combine parts staged | B9 attention output + down rows staged |
+//   B10 o rows  -- then wave 0 publishes x.
 //   Head: H0 LN statistics staged | H1 h staged.
 // The work table lists a block's q / k / v tiles first (at most 3), so they are computed and published in the
 // first pass and the q / k / v hop overlaps the second pass.
@@ -925,13 +971,15 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
     for (int l = 0; l < p.L; ++l) {
         const uint32_t tag = tag_of(step, l);
         XWave xw;
+        LnW lw;
+        ln_w_issue(p.ln_w + (size_t)l * kH, lw);
         if (l == 0) {
             x_from_embedding(p, tok, xw);
         } else {
             x_poll(p, tag_of(step, l - 1), xw);
             if (l == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;  // every block has read pos
         }
-        ln_stats(xw, p.ln_w + (size_t)l * kH, p.eps, S);
+        ln_stats(xw, lw, p.eps, S);
         __syncthreads();                                      // B0
         ln_apply_frag(S);
         __syncthreads();                                      // B1
@@ -945,7 +993,10 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
         tile_epilogue(p, l, pos, tag, wk, S, kTileSplit, kMaxTiles);  // B6 inside
         __syncthreads();                                      // B7
         __syncthreads();                                      // B8
-        if (wk.comb >= 0) combine(p, wk.comb, pos, tag, S);
+        if (wk.comb >= 0) {  // block-uniform: the streamers poll the splits, wave 0 merges
+            __syncthreads();                                  // BC
+            comb_merge(p, wk.comb, tag, S);
+        }
         gather_down_and_ob(p, tag, S, kPreDown, kPreOb);
         __syncthreads();                                      // B9
         __syncthreads();                                      // B10
@@ -958,9 +1009,11 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
     }
     // final LayerNorm, h as natural pairs for the int8 head
     XWave xw;
+    LnW lw;
+    ln_w_issue(p.norm_w, lw);
     x_poll(p, tag_of(step, p.L - 1), xw);
     if (p.L == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;
-    ln_stats(xw, p.norm_w, p.eps, S);
+    ln_stats(xw, lw, p.eps, S);
     __syncthreads();                                          // H0
     ln_apply_pairs(S);
     __syncthreads();                                          // H1
@@ -994,6 +1047,10 @@ RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Wor
         __syncthreads();                                      // B7
         attention<REP>(p, l, pos, tag, kv, S);                // B8 inside
         down_compute(p, tag, wk, dr, S);
+        if (wk.comb >= 0) {  // this block's share of the combine (wave 0 merges after BC)
+            comb_part(p, wk.comb, pos, tag, S);
+            __syncthreads();                                  // BC
+        }
         o_issue(p, l, orr);
         kv_issue(p, ln, pos, kv);
         tile_issue(p, ln, S, wk, tr, kTileSplit, kMaxTiles);  // second part

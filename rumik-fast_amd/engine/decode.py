@@ -201,24 +201,42 @@ def down_layout(q):
     return q.reshape(q.shape[0], -1, 8).permute(1, 0, 2).contiguous()
 
 
+def combiner_blocks(cfg, nblocks, nsp):
+    """The block that combines each head's attention splits: blocks without an attention split where there are
+    enough, else the blocks holding the last splits of each KV head (empty at short contexts)."""
+    natt = cfg.NKV * nsp
+    spare = list(range(natt, nblocks))
+    if len(spare) >= cfg.NH:
+        return [spare[h * len(spare) // cfg.NH] for h in range(cfg.NH)]
+    return [(h % cfg.NKV) * nsp + nsp - 1 - (h // cfg.NKV) % nsp for h in range(cfg.NH)]
+
+
 def work_table(cfg, nblocks, nsp):
     """Per block: its w_in tiles (q / k / v tiles first, then the gate / up tiles of its MLP channels), its w_down
     slices [sb, se) (16 channels each; a block owns both gate / up tiles of each of its slices) and the head it
-    combines. Returns int16 [nblocks, 16]."""
+    combines. Combining blocks get no MLP channels when the others can hold them all, so their streamers start the
+    combine right after attention. Returns int16 [nblocks, 16]."""
     qkv_tiles = (cfg.NH + 2 * cfg.NKV) * cfg.HD // 16
     nsl = cfg.inter // 16
+    comb = combiner_blocks(cfg, nblocks, nsp)
+    others = [b for b in range(nblocks) if b not in set(comb)]
+    if nsl > MAX_SLICES * len(others):
+        others = list(range(nblocks))
     tiles = [[] for _ in range(nblocks)]
-    ranges = []
-    for b in range(nblocks):
-        sb, se = b * nsl // nblocks, (b + 1) * nsl // nblocks
+    ranges = [(0, 0)] * nblocks
+    for i, b in enumerate(others):
+        sb, se = i * nsl // len(others), (i + 1) * nsl // len(others)
         if se - sb > MAX_SLICES:
             raise ValueError("too many MLP channels per block")
-        ranges.append((sb, se))
+        ranges[b] = (sb, se)
         for k in range(sb, se):
             tiles[b] += [qkv_tiles + 2 * k, qkv_tiles + 2 * k + 1]
     qkv = [[] for _ in range(nblocks)]
-    for t in range(qkv_tiles):  # each q / k / v tile to the block with the fewest tiles so far
-        b = min(range(nblocks), key=lambda i: (len(tiles[i]) + len(qkv[i]), len(qkv[i]), i))
+    for t in range(qkv_tiles):  # each q / k / v tile to the block with the fewest tiles so far (FIRST_PASS at most)
+        b = min((i for i in range(nblocks) if len(qkv[i]) < FIRST_PASS),
+                key=lambda i: (len(tiles[i]) + len(qkv[i]), len(qkv[i]), i), default=None)
+        if b is None:
+            raise ValueError("too many q/k/v tiles for the blocks' first passes")
         qkv[b].append(t)
     table = torch.full((nblocks, WORK), -1, dtype=torch.int16)
     for b in range(nblocks):
@@ -227,12 +245,11 @@ def work_table(cfg, nblocks, nsp):
         tl = qkv[b] + tiles[b]
         if len(tl) > MAX_TILES:
             raise ValueError(f"block {b} would hold {len(tl)} tiles (at most {MAX_TILES})")
-        table[b, :len(tl)] = torch.tensor(tl, dtype=torch.int16)
+        if tl:
+            table[b, :len(tl)] = torch.tensor(tl, dtype=torch.int16)
         table[b, 8], table[b, 9] = ranges[b]
-    natt = cfg.NKV * nsp
-    spare = list(range(natt, nblocks)) or list(range(nblocks))
-    for h in range(cfg.NH):  # combiners on blocks without an attention split where there are enough
-        table[spare[h * len(spare) // cfg.NH], 10] = h
+    for h, b in enumerate(comb):
+        table[b, 10] = h
     return table
 
 

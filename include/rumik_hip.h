@@ -139,9 +139,11 @@ int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_str
  *   row j, bytes [16s, 16s + 16) of the group); win_sm per (layer, tile, wave w = 0..7, row) the two scale |
  *   min << 16 words of wave w's column groups (waves 1..7: 2(w - 1), 2(w - 1) + 1; wave 0: 14, 15);
  *   wd_t holds w_down by 16-column slices: per (layer, slice), 2048 rows x 8 bytes; wd_sm per (layer, group) the
- *   2048 rows' scale | min << 16; w_o keeps the reference code layout, wo_sm its scale | min << 16.
+ *   2048 rows' scale | min << 16; wo_q holds w_o per (layer, head h, row group r of 128 rows) as 512 items of 16
+ *   bytes (item i: row 128r + i / 4, the codes of columns 128h + 32(i % 4) .. + 32); wo_sm per (layer, row, head)
+ *   its scale | min << 16. Block b = (head b / 16, row group b % 16) computes that slice of the o projection.
  * Blocks exchange fp16 values as tagged 32-bit words (value | tag << 16, tag = 1 + (step * 64 + layer) % 65535,
- * step = the block's ctr entry) and poll the words themselves: tx, tq, tkv, tob, tdp, tpo (fp16 words) and tml
+ * step = the block's ctr entry) and poll the words themselves: tx, tq, tkv, top, tdp, tpo (fp16 words) and tml
  * (fp32 m / l | tag << 32). All exchange buffers, ctr and status start at zero; after a nonzero status, re-zero them.
  * status bit 1 = a wait exceeded 200 ms (the step finishes early with garbage); bit 2 = pos outside [0, S)
  * (nothing is computed or written, pos is not advanced).
@@ -156,7 +158,7 @@ typedef struct rk_decode_params {
     const uint16_t* emb_s;  /* [vocab] fp16 */
     const uint8_t* win_t;   /* [L, n_in/16, 16, 64, 16 B] */
     const uint32_t* win_sm; /* [L, n_in/16, 8 waves, 16 rows, 2] */
-    const uint8_t* wo_q;    /* [L, 2048, NH*64] */
+    const uint8_t* wo_q;    /* [L, NH, 16, 512, 16 B] */
     const uint32_t* wo_sm;  /* [L, 2048, NH]: scale | min << 16 */
     const uint8_t* wd_t;    /* [L, inter/16, 2048, 8 B] */
     const uint32_t* wd_sm;  /* [L, inter/128, 2048] */
@@ -169,11 +171,11 @@ typedef struct rk_decode_params {
     const int8_t* head_q;   /* [n_audio, 2048] */
     const uint16_t* head_s; /* [n_audio] fp16 */
     float* logits;          /* [n_audio] */
-    const int16_t* work;    /* [nblocks, 16]: w_in tiles (8, -1 = none), slice begin, slice end, combined head (-1 = none) */
+    const int16_t* work;    /* [nblocks, 16]: w_in tiles (8, -1 = none), slice begin, slice end, 5 unused */
     uint32_t* tx;           /* [16, 2048]: 16 copies */
     uint32_t* tq;           /* [NH*128] */
     uint32_t* tkv;          /* [2, NKV*128] (k, v of the current layer at pos) */
-    uint32_t* tob;          /* [16, NH*128]: 16 copies */
+    uint32_t* top;          /* [nblocks (consumer), NH, 8] o-projection partials */
     uint32_t* tdp;          /* [nblocks (consumer), nblocks (producer), 8] down-projection partials */
     uint32_t* tpo;          /* [NH, nsp, 128] normalized split outputs */
     unsigned long long* tml; /* [NH, nsp, 2] */

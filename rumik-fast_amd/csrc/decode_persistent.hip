@@ -9,7 +9,8 @@
 // 32-bit word (fp16 value | tag << 16; the tag names the step and the layer) with an agent-scope atomic store, and
 // the consumer polls the words themselves with agent-scope atomic loads (coherent across the XCDs' L2s). One
 // cross-block edge then costs one store-to-load hop (measured 0.75 us idle, ~1.5 us while HBM streams) instead of
-// a barrier's two plus a data load.
+// a barrier's two plus a data load. Every poll loads all its words and the status word as one batch: one round
+// trip per poll iteration.
 //
 // Roles inside a block: wave 0 only polls, gathers and stages exchanged data in LDS. It never has weight loads in
 // flight: vector-memory results return in issue order, so a poll behind a weight burst would wait for the burst.
@@ -26,9 +27,11 @@
 //     2048 rows, published tagged (each x-row owner sums the partials of all blocks for its rows)
 //   wave 0: q of its KV head (+ k, v at pos) -> LDS;  streamers: one flash-decoding split over the cached slots,
 //     partial (m, l, o / l) published tagged
-//   wave 0 of head h's combiner block: merges the head's split partials -> attention output, published tagged
-//   wave 0: its 8 rows of the down partials of all blocks; the attention output (all heads) -> LDS
-//   streamers: its 8 rows of w_o . attn;  wave 0: x rows = x + o + d (each rounded once, as add_ln), published
+//   block b = (head h = b / 16, row group r = b % 16): the streamers poll head h's split partials, wave 0 merges
+//     them -> h's attention output in LDS; streamers: w_o[128r .. 128r + 128, h's 128 columns] . attn -> o partials
+//     of those rows, published tagged (no separate combiner and no all-to-all of the attention output)
+//   wave 0: its 8 rows of the down partials of all blocks and of the o partials of all heads, one poll batch;
+//     x rows = x + o + d (each rounded once, as add_ln), published
 // After the last layer: final LayerNorm and the int8 audio head (rows split over blocks); pos += 1.
 //
 // Every wait is bounded by wall-clock time (200 ms): on expiry the kernel sets an abort bit in `status`, every
@@ -53,9 +56,9 @@ constexpr int kRP = (kH / 2 + kSLanes - 1) / kSLanes;  // down row pairs per str
 constexpr int kKVPre = 5;                  // cached slots per streamer whose K / V are loaded ahead (7 x 5 >= 2048 / 64)
 constexpr int kHeadRows = 7;               // head rows per streamer loaded ahead (the rest load when used)
 constexpr int kWork = 16;                  // int16 entries per block in the work table
-constexpr int kPreDown = 2, kPreOb = 1;    // ~0.5 us waits before the down-partial and attention-output polls
-// x and the attention output are polled by every block: they are published in kXRep copies 8 KB apart and block b
-// polls copy b % kXRep, so no 8 KB stretch of memory serves more than 16 pollers
+constexpr int kPreRows = 1;                // ~0.5 us wait before the down / o partial poll
+// x is polled by every block: it is published in kXRep copies 8 KB apart and block b polls copy b % kXRep, so no
+// 8 KB stretch of memory serves more than 16 pollers
 constexpr int kXRep = 16;
 constexpr int kRepQwords = kH / 2;         // qwords per copy (2048 tagged fp16 words)
 constexpr uint64_t kWaitTicks = 20000000ull;  // 200 ms at the 100 MHz wall clock
@@ -161,8 +164,9 @@ struct Lds {
     uint32_t knew[64], vnew[64];              // k, v at pos of that KV head
     float s_m[kStreamers][kMaxRep], s_l[kStreamers][kMaxRep];
     float2 s_acc[kStreamers][kMaxRep][64];    // per-streamer attention partials
-    uint4 vecp[kH / 8];                       // attention output (permuted pairs) / h (natural pairs, head)
-    float vsum[kH / 32];                      // per-32-column sums of the attention output
+    uint4 vecp[kH / 8];                       // h as natural pairs (the int8 head's input)
+    uint32_t attn[kHD / 2];                   // head (block / 16)'s attention output, natural fp16 pairs
+    float asum;                               //   and the sum of its 128 values
     float2 cpa[kStreamers][64];               // the combine's per-streamer parts: sum of w_i o_i per dim pair,
     float cpm[kStreamers], cpl[kStreamers];   //   the streamer's max m and sum of w_i
     float orow[8], drow[8], xrow[8];          // this block's rows of o, down and the residual stream
@@ -177,7 +181,6 @@ struct Lds {
 struct Work {
     int nt;     // w_in tiles
     int sb, se; // down slices [sb, se)
-    int comb;   // head this block combines (-1: none)
 };
 
 RK_DEV Work work_of(const Lds& S) {
@@ -187,7 +190,6 @@ RK_DEV Work work_of(const Lds& S) {
     for (int t = 0; t < kMaxTiles; ++t) w.nt += S.work[t] >= 0;
     w.sb = S.work[8];
     w.se = S.work[9];
-    w.comb = S.work[10];
     return w;
 }
 
@@ -689,7 +691,7 @@ RK_DEV void attention(const Params& p, int l, int64_t pos, uint32_t tag, const K
 }
 
 // Head h's combine: out = sum_i w_i o_i / sum_i w_i, w_i = exp(m_i - max m) * l_i over the splits holding at least
-// one slot (at most 64). The streamers of the combining block share the polling: streamer sw polls splits
+// one slot (at most 64). The streamers of each of the head's 16 blocks share the polling: streamer sw polls splits
 // [kCombPer * sw, kCombPer * (sw + 1)) in one batch per iteration and leaves (M = its max m, L = sum of its w_i taken
 // against M, sum of w_i o_i) in LDS; after a block barrier wave 0 merges the 7 parts (comb_merge). The sums run in split order within a wave and in
 // wave order across waves, so the result does not depend on arrival order.
@@ -768,8 +770,10 @@ RK_DEV bool comb_part(const Params& p, int h, int64_t pos, uint32_t tag, Lds& S)
     return ok;
 }
 
-// wave 0, after the barrier that follows the streamers' comb_part: merge the parts, publish in kXRep copies
-RK_DEV void comb_merge(const Params& p, int h, uint32_t tag, const Lds& S) {
+// wave 0, after the barrier that follows the streamers' comb_part: merge the parts into head h's attention output,
+// rounded to fp16 (the reference keeps it in the activation dtype), staged as natural pairs with the sum of its 128
+// values (for the min term of the o projection)
+RK_DEV void comb_merge(Lds& S) {
     const int lane = threadIdx.x & 63;
     float M = -INFINITY;
 #pragma unroll
@@ -784,26 +788,91 @@ RK_DEV void comb_merge(const Params& p, int h, uint32_t tag, const Lds& S) {
         oy = __builtin_fmaf(f, a.y, oy);
     }
     const float inv = den > 0.f ? 1.0f / den : 0.f;
-    const uint64_t o = tpair(ox * inv, oy * inv, tag);
-#pragma unroll
-    for (int r = 0; r < kXRep; ++r) st_coh64(reinterpret_cast<uint64_t*>(p.tob) + r * kRepQwords + h * (kHD / 2) + lane, o);
+    const float a0 = rnd16(ox * inv), a1 = rnd16(oy * inv);
+    S.attn[lane] = pack_h2(a0, a1);
+    const float sum = wave_sum(a0 + a1);
+    if (lane == 0) S.asum = sum;
 }
 
-// wave 0: this block's 8 rows of the down partials of all blocks (summed -> S.drow), then the attention output of
-// all heads (-> permuted pairs per 8 columns + per-32-column sums in LDS). The down partials are ready ~one hop
-// after attention, the attention output ~two, so they are polled in that order.
-RK_DEV bool gather_down_and_ob(const Params& p, uint32_t tag, Lds& S, int pre_down, int pre_ob) {
+// ---------------------------------------------------------------------------------------------- w_o partials
+// Block b = (head h = b / 16, row group r = b % 16) computes the o projection of head h's attention output for
+// rows [128r, 128r + 128): 512 items (row i / 4, 32-column chunk i % 4 of the head's 128 columns), one 16-byte load
+// each. Streamer lane s takes item s, streamer 0's lanes also item 448 + lane. The head's 128 columns are one
+// quantization group, so each row has one scale | min word (wo_sm[layer][row][head]).
+constexpr int kOItems = 512;
+
+struct ORegs {
+    u4_t w[2];
+    uint32_t sm[2];
+};
+
+static_assert(kH / kHD == 16 && kH / 128 == 16, "16 heads x 16 row groups of 128 = the 256 blocks");
+RK_DEV int o_head() { return blockIdx.x >> 4; }
+RK_DEV int o_rgroup() { return blockIdx.x & 15; }
+
+RK_DEV void o_issue(const Params& p, int l, ORegs& o) {
+    const int ls = threadIdx.x - 64;
+    const int h = o_head(), r = o_rgroup();
+    const u4_t* base = reinterpret_cast<const u4_t*>(p.wo_q) + ((size_t)(l * p.NH + h) * 16 + r) * kOItems;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // lanes without a second item load their first one again (unused)
+        const int i = k == 1 && ls < kOItems - kSLanes ? ls + kSLanes : ls;
+        o.w[k] = __builtin_nontemporal_load(base + i);
+        o.sm[k] = p.wo_sm[((size_t)l * kH + 128 * r + (i >> 2)) * p.NH + h];
+    }
+}
+
+// the items' dots, summed per row over the 4 lanes of its chunks; lanes i % 8 == 0 publish rows (i/4, i/4 + 1) as
+// one tagged pair to top[consumer block][head][8 rows]
+RK_DEV void o_part(const Params& p, uint32_t tag, const ORegs& o, const Lds& S) {
+    const int ls = threadIdx.x - 64, lane = threadIdx.x & 63;
+    const int h = o_head(), r = o_rgroup();
+    const Int4Masks km = int4_masks();
+    uint64_t* top = reinterpret_cast<uint64_t*>(p.top);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        if (k == 1 && ls >= kOItems - kSLanes) break;  // wave-uniform: only streamer 0 has a second item
+        const int i = ls + k * kSLanes, c = i & 3;
+        uint32_t xp[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // natural pairs of 8 columns -> the dequant's pair order
+            const u4_t d = {S.attn[16 * c + 4 * q], S.attn[16 * c + 4 * q + 1], S.attn[16 * c + 4 * q + 2],
+                            S.attn[16 * c + 4 * q + 3]};
+            uint32_t hp[4];
+            pair_permute(d, hp);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xp[4 * q + e] = hp[e];
+        }
+        float v = chunk_dot_int4(o.w[k], xp, km);
+        v += dpp<0xB1>(v);  // the row's 4 chunks sit in lanes 4j .. 4j + 3
+        v += dpp<0x4E>(v);
+        v = __builtin_fmaf(v, h16((uint16_t)o.sm[k]), h16((uint16_t)(o.sm[k] >> 16)) * S.asum);
+        const float nxt = __shfl_down(v, 4);  // the next row's total (lane + 4)
+        if ((lane & 7) == 0) {
+            const int row = 128 * r + (i >> 2);  // even
+            st_coh64(top + ((size_t)(row >> 3) * p.NH + h) * 4 + ((row & 7) >> 1), tpair(v, nxt, tag));
+        }
+    }
+}
+
+// wave 0: this block's 8 rows of the down partials of all blocks and of the o partials of all heads, one poll
+// batch; each summed over its producers (-> S.drow, S.orow)
+RK_DEV bool gather_rows(const Params& p, uint32_t tag, Lds& S, int pre) {
     const int lane = threadIdx.x & 63;
-    const int nb = gridDim.x;  // at most 256 producers, 4 qwords (8 rows) each: 16 qwords per lane
+    const int nb = gridDim.x;  // at most 256 down producers, 4 qwords (8 rows) each: 16 qwords per lane
     const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
-    const uint64_t* tob = reinterpret_cast<const uint64_t*>(p.tob) + (blockIdx.x % kXRep) * kRepQwords + z;
-    const uint32_t* tdp = p.tdp + z;
-    uint32_t v[16];
-    // qword q = 64k + lane of this block's run: producer q / 4, rows 2(q % 4), 2(q % 4) + 1
-    const uint64_t* run = reinterpret_cast<const uint64_t*>(tdp) + (size_t)blockIdx.x * nb * 4;
-    bool ok = poll_pairs<16>(
-        p, tag, [&](int k) -> const uint64_t* { return 64 * k + lane < 4 * nb ? run + 64 * k + lane : nullptr; }, v,
-        pre_down);
+    // down: qword q = 64k + lane of this block's run: producer q / 4, rows 2(q % 4), 2(q % 4) + 1;
+    // o: lane = head * 4 + pair (16 heads)
+    const uint64_t* run = reinterpret_cast<const uint64_t*>(p.tdp + z) + (size_t)blockIdx.x * nb * 4;
+    const uint64_t* orun = reinterpret_cast<const uint64_t*>(p.top + z) + (size_t)blockIdx.x * p.NH * 4;
+    uint32_t v[17];
+    const bool ok = poll_pairs<17>(
+        p, tag,
+        [&](int k) -> const uint64_t* {
+            if (k == 16) return lane < 4 * p.NH ? orun + lane : nullptr;
+            return 64 * k + lane < 4 * nb ? run + 64 * k + lane : nullptr;
+        },
+        v, pre);
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -813,76 +882,27 @@ RK_DEV bool gather_down_and_ob(const Params& p, uint32_t tag, Lds& S, int pre_do
             d1 += (float)h.y;
         }
     }
+    float o0 = 0.f, o1 = 0.f;
+    if (lane < 4 * p.NH) {
+        const h2_t h = as_h2(v[16]);
+        o0 = (float)h.x;
+        o1 = (float)h.y;
+    }
     // sum over the lanes that share lane % 4
-    d0 += xor_lane<4>(d0);
-    d1 += xor_lane<4>(d1);
-    d0 += xor_lane<8>(d0);
-    d1 += xor_lane<8>(d1);
-    d0 += xor_lane<16>(d0);
-    d1 += xor_lane<16>(d1);
-    d0 += xor_lane<32>(d0);
-    d1 += xor_lane<32>(d1);
+#pragma unroll
+    for (int m = 4; m < 64; m *= 2) {
+        d0 += __shfl_xor(d0, m);
+        d1 += __shfl_xor(d1, m);
+        o0 += __shfl_xor(o0, m);
+        o1 += __shfl_xor(o1, m);
+    }
     if (lane < 4) {
         S.drow[2 * lane] = d0;
         S.drow[2 * lane + 1] = d1;
-    }
-    ok &= poll_pairs<16>(
-        p, tag, [&](int k) -> const uint64_t* { return tob + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v, pre_ob);
-    const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = lane + 64 * k;  // 8-column block
-        const u4_t dd = {v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
-        uint32_t hp[4];
-        pair_permute(dd, hp);
-        S.vecp[i] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-        float sum = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sum = dot2(as_h2(dd[e]), one, sum);
-        sum += dpp<0xB1>(sum);  // 4 consecutive 8-blocks (lanes) = one 32-column chunk
-        sum += dpp<0x4E>(sum);
-        if ((lane & 3) == 0) S.vsum[i >> 2] = sum;
+        S.orow[2 * lane] = o0;
+        S.orow[2 * lane + 1] = o1;
     }
     return ok;
-}
-
-// ---------------------------------------------------------------------------------------------- w_o rows
-// streamer sw owns row 8b + sw; streamer 0 also row 8b + 7. wo_sm: per (layer, row, group) scale | min << 16.
-struct ORegs {
-    u4_t w[2];
-    uint32_t sm[2];
-};
-
-RK_DEV void o_issue(const Params& p, int l, ORegs& o) {
-    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
-    const int K = p.NH * kHD, ng = K / 128;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {  // streamers 1..6 load their own row again as the second one (unused)
-        const int row = 8 * blockIdx.x + (k == 1 && sw == 0 ? 7 : sw);
-        const size_t rr = (size_t)l * kH + row;
-        o.w[k] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wo_q + rr * (K / 2)) + lane);
-        o.sm[k] = p.wo_sm[rr * ng + (lane >> 2)];
-    }
-}
-
-RK_DEV void o_compute(const ORegs& o, Lds& S) {
-    const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 1;
-    const Int4Masks km = int4_masks();
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        if (k == 0 || sw == 0) {
-            uint32_t xp[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = S.vecp[lane * 4 + q];
-                xp[4 * q] = v.x; xp[4 * q + 1] = v.y; xp[4 * q + 2] = v.z; xp[4 * q + 3] = v.w;
-            }
-            const float d = chunk_dot_int4(o.w[k], xp, km);
-            float acc = __builtin_fmaf(d, h16((uint16_t)o.sm[k]), h16((uint16_t)(o.sm[k] >> 16)) * S.vsum[lane]);
-            acc = wave_sum(acc);
-            if (lane == 0) S.orow[k == 0 ? sw : 7] = acc;
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------------------------- head
@@ -953,15 +973,15 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
 // sum) and meet at the same sequence of block barriers per layer:
 //   B0 x + LN statistics staged | B1 h staged | B2 partials of tiles [0, 3) | B3 (epilogue) | B4 q / k / v of
 //   those tiles published | B5 partials of tiles [3, 7), q staged | B6 (epilogue) | B7 act staged |
-//   B8 (attention) | BC (combining blocks only) combine parts staged | B9 attention output + down rows staged |
-//   B10 o rows  -- then wave 0 publishes x.
+//   B8 (attention) | BC combine parts of head b / 16 staged | BO its attention output staged | B9 down and o rows
+//   staged  -- then wave 0 publishes x.
 //   Head: H0 LN statistics staged | H1 h staged.
 // The work table lists a block's q / k / v tiles first (at most 3), so they are computed and published in the
 // first pass and the q / k / v hop overlaps the second pass.
 // Streamer issue order (each wait covers only older loads, see tile_issue): tiles(l + 1) [0, 3) after the first
-// epilogue; after attention(l) and the down partials: O(l), K/V(l + 1), tiles(l + 1) [3, 7), down(l + 1). The
-// loop's back edge and its preheader leave the same sequence outstanding. At most ~57 vector-memory instructions
-// are in flight per streamer (the hardware counter holds 63).
+// epilogue; after the o partials of layer l: O(l + 1), K/V(l + 1), tiles(l + 1) [3, 7), down(l + 1). The loop's
+// back edge and its preheader leave the same sequence outstanding. At most ~57 vector-memory instructions are in
+// flight per streamer (the hardware counter holds 63).
 
 template <int REP>
 RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok, const Work& wk, Lds& S) {
@@ -993,13 +1013,11 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
         tile_epilogue(p, l, pos, tag, wk, S, kTileSplit, kMaxTiles);  // B6 inside
         __syncthreads();                                      // B7
         __syncthreads();                                      // B8
-        if (wk.comb >= 0) {  // block-uniform: the streamers poll the splits, wave 0 merges
-            __syncthreads();                                  // BC
-            comb_merge(p, wk.comb, tag, S);
-        }
-        gather_down_and_ob(p, tag, S, kPreDown, kPreOb);
+        __syncthreads();                                      // BC
+        comb_merge(S);
+        __syncthreads();                                      // BO
+        gather_rows(p, tag, S, kPreRows);
         __syncthreads();                                      // B9
-        __syncthreads();                                      // B10
         if (lane < 8) S.xrow[lane] = rnd16(S.xrow[lane] + rnd16(S.orow[lane]) + rnd16(S.drow[lane]));
         static_assert(4 * kXRep <= 64, "one store per lane");
         if (lane < 4 * kXRep)  // lane = copy * 4 + pair
@@ -1025,8 +1043,10 @@ RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Wor
     DownRegs dr;
     KVRegs kv;
     ORegs orr;
-    // the same outstanding sequence the loop leaves behind at its back edge: tiles [0, 3), K/V, tiles [3, 7), down
+    // the same outstanding sequence the loop leaves behind at its back edge: tiles [0, 3), O, K/V, tiles [3, 7),
+    // down
     tile_issue(p, 0, S, wk, tr, 0, kTileSplit);
+    o_issue(p, 0, orr);
     kv_issue(p, 0, pos, kv);
     tile_issue(p, 0, S, wk, tr, kTileSplit, kMaxTiles);
     down_issue(p, 0, wk, dr);
@@ -1047,17 +1067,15 @@ RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Wor
         __syncthreads();                                      // B7
         attention<REP>(p, l, pos, tag, kv, S);                // B8 inside
         down_compute(p, tag, wk, dr, S);
-        if (wk.comb >= 0) {  // this block's share of the combine (wave 0 merges after BC)
-            comb_part(p, wk.comb, pos, tag, S);
-            __syncthreads();                                  // BC
-        }
-        o_issue(p, l, orr);
+        comb_part(p, o_head(), pos, tag, S);
+        __syncthreads();                                      // BC
+        __syncthreads();                                      // BO
+        o_part(p, tag, orr, S);
+        o_issue(p, ln, orr);
         kv_issue(p, ln, pos, kv);
         tile_issue(p, ln, S, wk, tr, kTileSplit, kMaxTiles);  // second part
         down_issue(p, ln, wk, dr);
         __syncthreads();                                      // B9
-        o_compute(orr, S);
-        __syncthreads();                                      // B10
     }
     head_issue(p, tr);
     __syncthreads();                                          // H0
@@ -1126,7 +1144,7 @@ extern "C" int rk_decode_step_persistent(const rk_decode_params* params, int nbl
         return RK_ERR_BLOCK;
     if (!p.tok || !p.pos || !p.emb_q || !p.emb_s || !p.win_t || !p.win_sm || !p.wo_q || !p.wo_sm ||
         !p.wd_t || !p.wd_sm || !p.ln_w || !p.norm_w || !p.cos_t || !p.sin_t || !p.kc || !p.vc || !p.head_q ||
-        !p.head_s || !p.logits || !p.work || !p.tx || !p.tq || !p.tkv || !p.tob || !p.tdp || !p.tpo || !p.tml ||
+        !p.head_s || !p.logits || !p.work || !p.tx || !p.tq || !p.tkv || !p.top || !p.tdp || !p.tpo || !p.tml ||
         !p.ctr || !p.status)
         return RK_ERR_NULL;
     if (!co_resident(rep, nblocks)) return RK_ERR_BLOCK;  // the waits need every block resident at once

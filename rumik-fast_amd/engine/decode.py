@@ -155,13 +155,13 @@ class RkDecodeParams(ctypes.Structure):
         ("eps", ctypes.c_float), ("scale", ctypes.c_float), ("sliding", ctypes.c_ulonglong)] + [
         (n, ctypes.c_void_p) for n in (
             "tok", "pos", "emb_q", "emb_s", "win_t", "win_sm", "wo_q", "wo_sm", "wd_t", "wd_sm", "ln_w", "norm_w",
-            "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "work", "tx", "tq", "tkv", "tob", "tdp",
+            "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "work", "tx", "tq", "tkv", "top", "tdp",
             "tpo", "tml", "ctr", "status")]
 
 
 MAX_TILES, MAX_SLICES, WORK = 7, 3, 16   # kMaxTiles, kMaxSlices, kWork of csrc/decode_persistent.hip
 FIRST_PASS = 3                           # kTileSplit: a block's q / k / v tiles are computed in its first pass
-X_COPIES = 16                            # kXRep: x and the attention output are published in 16 copies
+X_COPIES = 16                            # kXRep: x is published in 16 copies
 
 
 def interleave_gate_up(t, cfg):
@@ -201,34 +201,26 @@ def down_layout(q):
     return q.reshape(q.shape[0], -1, 8).permute(1, 0, 2).contiguous()
 
 
-def combiner_blocks(cfg, nblocks, nsp):
-    """The block that combines each head's attention splits: blocks without an attention split where there are
-    enough, else the blocks holding the last splits of each KV head (empty at short contexts)."""
-    natt = cfg.NKV * nsp
-    spare = list(range(natt, nblocks))
-    if len(spare) >= cfg.NH:
-        return [spare[h * len(spare) // cfg.NH] for h in range(cfg.NH)]
-    return [(h % cfg.NKV) * nsp + nsp - 1 - (h // cfg.NKV) % nsp for h in range(cfg.NH)]
+def o_layout(q, nh):
+    """w_o codes [2048, nh * 64] -> per (head h, row group r of 128 rows) 512 items of 16 bytes, item i = row
+    128r + i / 4, the codes of columns 128h + 32(i % 4) .. + 32: [nh, 16, 512, 16]."""
+    rows = q.shape[0]
+    return q.reshape(rows // 128, 128, nh, 4, 16).permute(2, 0, 1, 3, 4).reshape(nh, rows // 128, 512, 16).contiguous()
 
 
 def work_table(cfg, nblocks, nsp):
-    """Per block: its w_in tiles (q / k / v tiles first, then the gate / up tiles of its MLP channels), its w_down
-    slices [sb, se) (16 channels each; a block owns both gate / up tiles of each of its slices) and the head it
-    combines. Combining blocks get no MLP channels when the others can hold them all, so their streamers start the
-    combine right after attention. Returns int16 [nblocks, 16]."""
+    """Per block: its w_in tiles (q / k / v tiles first, then the gate / up tiles of its MLP channels) and its
+    w_down slices [sb, se) (16 channels each; a block owns both gate / up tiles of each of its slices).
+    Returns int16 [nblocks, 16] (columns 10..15 unused)."""
     qkv_tiles = (cfg.NH + 2 * cfg.NKV) * cfg.HD // 16
     nsl = cfg.inter // 16
-    comb = combiner_blocks(cfg, nblocks, nsp)
-    others = [b for b in range(nblocks) if b not in set(comb)]
-    if nsl > MAX_SLICES * len(others):
-        others = list(range(nblocks))
     tiles = [[] for _ in range(nblocks)]
-    ranges = [(0, 0)] * nblocks
-    for i, b in enumerate(others):
-        sb, se = i * nsl // len(others), (i + 1) * nsl // len(others)
+    ranges = []
+    for b in range(nblocks):
+        sb, se = b * nsl // nblocks, (b + 1) * nsl // nblocks
         if se - sb > MAX_SLICES:
             raise ValueError("too many MLP channels per block")
-        ranges[b] = (sb, se)
+        ranges.append((sb, se))
         for k in range(sb, se):
             tiles[b] += [qkv_tiles + 2 * k, qkv_tiles + 2 * k + 1]
     qkv = [[] for _ in range(nblocks)]
@@ -240,16 +232,12 @@ def work_table(cfg, nblocks, nsp):
         qkv[b].append(t)
     table = torch.full((nblocks, WORK), -1, dtype=torch.int16)
     for b in range(nblocks):
-        if len(qkv[b]) > FIRST_PASS:
-            raise ValueError(f"block {b} would hold {len(qkv[b])} q/k/v tiles (at most {FIRST_PASS})")
         tl = qkv[b] + tiles[b]
         if len(tl) > MAX_TILES:
             raise ValueError(f"block {b} would hold {len(tl)} tiles (at most {MAX_TILES})")
         if tl:
             table[b, :len(tl)] = torch.tensor(tl, dtype=torch.int16)
         table[b, 8], table[b, 9] = ranges[b]
-    for h, b in enumerate(comb):
-        table[b, 10] = h
     return table
 
 
@@ -276,7 +264,7 @@ class PersistentDecode:
         self.win_t = stack(lambda t: tile_layout(interleave_gate_up(t[0], c)), "w_in")
         self.win_sm = stack(lambda t: wave_scale_min(pack_scale_min(interleave_gate_up(t[1], c),
                                                                      interleave_gate_up(t[2], c))), "w_in")
-        self.wo_q = stack(lambda t: t[0], "w_o")
+        self.wo_q = stack(lambda t: o_layout(t[0], c.NH), "w_o")
         self.wo_sm = stack(lambda t: pack_scale_min(t[1], t[2]), "w_o")
         self.wd_t = stack(lambda t: down_layout(t[0]), "w_down")
         self.wd_sm = stack(lambda t: pack_scale_min(t[1], t[2]).t().contiguous(), "w_down")
@@ -291,7 +279,7 @@ class PersistentDecode:
         self.tx = torch.zeros(X_COPIES * 2048, dtype=i32, device=d)
         self.tq = torch.zeros(c.NH * c.HD, dtype=i32, device=d)
         self.tkv = torch.zeros(2 * c.NKV * c.HD, dtype=i32, device=d)
-        self.tob = torch.zeros(X_COPIES * c.NH * c.HD, dtype=i32, device=d)
+        self.top = torch.zeros(nb * c.NH * 8, dtype=i32, device=d)
         self.tdp = torch.zeros(nb * 2048, dtype=i32, device=d)
         self.tpo = torch.zeros(c.NH * self.nsp * c.HD, dtype=i32, device=d)
         self.tml = torch.zeros(c.NH * self.nsp * 2, dtype=torch.int64, device=d)
@@ -311,7 +299,7 @@ class PersistentDecode:
                         ("wd_t", self.wd_t), ("wd_sm", self.wd_sm), ("ln_w", self.ln), ("norm_w", self.norm),
                         ("cos_t", self.cos), ("sin_t", self.sin), ("kc", self.kc), ("vc", self.vc),
                         ("head_q", self.head[0]), ("head_s", self.head[1]), ("logits", self.logits),
-                        ("work", self.work), ("tx", self.tx), ("tq", self.tq), ("tkv", self.tkv), ("tob", self.tob),
+                        ("work", self.work), ("tx", self.tx), ("tq", self.tq), ("tkv", self.tkv), ("top", self.top),
                         ("tdp", self.tdp), ("tpo", self.tpo), ("tml", self.tml), ("ctr", self.ctr),
                         ("status", self.status)):
             if not t.is_contiguous() or t.device != d:
@@ -327,7 +315,7 @@ class PersistentDecode:
 
     def reset(self):
         """Zero the exchange buffers, step counters and status (needed after a nonzero status)."""
-        for t in (self.tx, self.tq, self.tkv, self.tob, self.tdp, self.tpo, self.tml, self.ctr, self.status):
+        for t in (self.tx, self.tq, self.tkv, self.top, self.tdp, self.tpo, self.tml, self.ctr, self.status):
             t.zero_()
 
     def set_state(self, tok: int, pos: int):

@@ -41,7 +41,7 @@ def test_binding_table_covers_the_header():
 
 def test_version_and_status_strings():
     lib = HL.lib()
-    assert lib.rk_abi_version() == 2
+    assert lib.rk_abi_version() == 3
     texts = {0: "ok", -1: "shape", -2: "unsupported block shape", -3: "unsupported dtype", -4: "null pointer",
              -6: "kernel launch failed"}
     for code, t in texts.items():

@@ -22,23 +22,26 @@ def test_work_table_covers_every_tile_once(cfg_kw):
         assert nq <= decode.FIRST_PASS and all(v < qkv_tiles for v in row[:nq])
     got = sorted(int(v) for v in tiles.flatten() if v >= 0)
     assert got == list(range(n_tiles))
-    # the blocks holding slices cover all MLP channels contiguously in block order, and each block owns the
-    # gate/up tiles of its slices
+    # slices are contiguous, cover all MLP channels, and each block owns the gate/up tiles of its slices
     sb, se = t[:, 8].tolist(), t[:, 9].tolist()
-    held = [b for b in range(nb) if se[b] > sb[b]]
-    assert sb[held[0]] == 0 and se[held[-1]] == cfg.inter // 16
-    assert all(se[a] == sb[b] for a, b in zip(held, held[1:]))
+    assert sb[0] == 0 and se[-1] == cfg.inter // 16 and all(se[b] == sb[b + 1] for b in range(nb - 1))
     assert max(e - s for s, e in zip(sb, se)) <= decode.MAX_SLICES
     for b in range(nb):
         own = set(int(v) for v in tiles[b] if v >= qkv_tiles)
         assert own == {qkv_tiles + 2 * k + h for k in range(sb[b], se[b]) for h in (0, 1)}
-    # every head has exactly one combiner
-    heads = sorted(int(v) for v in t[:, 10] if v >= 0)
-    assert heads == list(range(cfg.NH))
-    # combining blocks hold no MLP channels when the other blocks can take them all
-    comb = [b for b in range(nb) if t[b, 10] >= 0]
-    if cfg.inter // 16 <= decode.MAX_SLICES * (nb - len(comb)):
-        assert all(se[b] == sb[b] for b in comb)
+    assert (t[:, 10:] == -1).all()
+
+
+def test_o_layout_items():
+    """item i of (head h, row group r) holds row 128r + i // 4, the codes of columns 128h + 32(i % 4) .. + 32"""
+    g = torch.Generator().manual_seed(1)
+    nh = 16
+    q = torch.randint(0, 256, (2048, nh * 64), generator=g, dtype=torch.uint8)
+    o = decode.o_layout(q, nh)
+    assert o.shape == (nh, 16, 512, 16)
+    for h, r, i in ((0, 0, 0), (3, 5, 7), (15, 15, 511), (9, 2, 130)):
+        row, c = 128 * r + i // 4, i % 4
+        assert torch.equal(o[h, r, i], q[row, 64 * h + 16 * c: 64 * h + 16 * c + 16])
 
 
 def test_tile_layout_lane_order():

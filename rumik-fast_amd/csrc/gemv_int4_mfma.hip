@@ -61,49 +61,80 @@ RK_DEV h8_t dequant8(uint32_t w, const Consts& k) {
 
 // Stage x in LDS: fragment f = g*16 + t*4 + s holds the 8 values of columns 128g + 32s + 8t + (0,4,1,5,2,6,3,7)
 // as fp16; xsum[g] = fp32 sum of the group's 128 values. Every thread of the block takes part.
-RK_DEV void stage_x(const void* __restrict__ x, int xdt, int K, uint4* __restrict__ frag, float* __restrict__ xsum) {
-    const int nb = K >> 3;  // 8-column blocks
-    for (int base = 0; base < nb; base += blockDim.x) {
-        const int i = base + threadIdx.x;
-        float sum = 0.f;
-        if (i < nb) {
-            const u4_t d = reinterpret_cast<const u4_t*>(x)[i];
-            uint32_t h[4];
-            if (xdt == RK_BF16) {
-                float f[8];
+// kXPre 8-column blocks per thread are loaded into registers before the weights (x_issue), so that staging them
+// (stage_x) waits for x only: vector-memory results return in issue order. Longer x (more than kXPre blocks per
+// thread) is loaded in the staging loop itself.
+constexpr int kXPre = 2;
+
+struct XRegs {
+    u4_t d[kXPre];
+};
+
+RK_DEV void x_issue(const void* __restrict__ x, int K, XRegs& xr) {
+    const int nb = K >> 3;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    f[2 * e] = __builtin_bit_cast(float, d[e] << 16);
-                    f[2 * e + 1] = __builtin_bit_cast(float, d[e] & 0xffff0000u);
-                }
+    for (int k = 0; k < kXPre; ++k)  // clamped, unconditional: a fixed number of loads in flight
+        xr.d[k] = reinterpret_cast<const u4_t*>(x)[min((int)threadIdx.x + k * (int)blockDim.x, nb - 1)];
+}
+
+// one 8-column block: fp16 pairs in dequant order (or bf16 converted) + its fp32 sum -> LDS fragment; the
+// 16 threads of a group then sum their parts inside a 16-lane DPP row
+RK_DEV void stage_block(int i, int nb, int xdt, u4_t d, uint4* __restrict__ frag, float* __restrict__ xsum) {
+    float sum = 0.f;
+    if (i < nb) {
+        uint32_t h[4];
+        const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+        if (xdt == RK_BF16) {
+            float f[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) sum += f[e];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    h2_t p;
-                    p.x = (_Float16)f[e];
-                    p.y = (_Float16)f[e + 4];
-                    h[e] = as_u32(p);
-                }
-            } else {
-                h[0] = perm(d.z, d.x, 0x05040100u);  // (x0, x4)
-                h[1] = perm(d.z, d.x, 0x07060302u);  // (x1, x5)
-                h[2] = perm(d.w, d.y, 0x05040100u);  // (x2, x6)
-                h[3] = perm(d.w, d.y, 0x07060302u);  // (x3, x7)
-                const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
+            for (int e = 0; e < 4; ++e) {
+                f[2 * e] = __builtin_bit_cast(float, d[e] << 16);
+                f[2 * e + 1] = __builtin_bit_cast(float, d[e] & 0xffff0000u);
             }
-            const int g = i >> 4, r = i & 15;  // column offset in the group: 8r = 32s + 8t
-            const int s = r >> 2, t = r & 3;
-            frag[g * 16 + t * 4 + s] = make_uint4(h[0], h[1], h[2], h[3]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += f[e];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h2_t p;
+                p.x = (_Float16)f[e];
+                p.y = (_Float16)f[e + 4];
+                h[e] = as_u32(p);
+            }
+        } else {
+            h[0] = perm(d.z, d.x, 0x05040100u);  // (x0, x4)
+            h[1] = perm(d.z, d.x, 0x07060302u);  // (x1, x5)
+            h[2] = perm(d.w, d.y, 0x05040100u);  // (x2, x6)
+            h[3] = perm(d.w, d.y, 0x07060302u);  // (x3, x7)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
         }
-        // 16 consecutive threads hold one group: sum them inside their 16-lane DPP row
-        sum += dpp<0x128>(sum);  // row_ror:8
-        sum += dpp<0x124>(sum);  // row_ror:4
-        sum += dpp<0x122>(sum);  // row_ror:2
-        sum += dpp<0x121>(sum);  // row_ror:1
-        if (i < nb && (i & 15) == 0) xsum[i >> 4] = sum;
+        const int g = i >> 4, r = i & 15;  // column offset in the group: 8r = 32s + 8t
+        const int s = r >> 2, t = r & 3;
+        frag[g * 16 + t * 4 + s] = make_uint4(h[0], h[1], h[2], h[3]);
+    }
+    sum += dpp<0x128>(sum);  // 16 consecutive threads hold one group: sum inside their 16-lane DPP row (row_ror:8)
+    sum += dpp<0x124>(sum);  // row_ror:4
+    sum += dpp<0x122>(sum);  // row_ror:2
+    sum += dpp<0x121>(sum);  // row_ror:1
+    if (i < nb && (i & 15) == 0) xsum[i >> 4] = sum;
+}
+
+// XREG (K / 8 <= kXPre * blockDim, chosen on the host): every block of x is in registers already. It is a template
+// parameter so that the x loads are not sunk into a branch behind the weight loads.
+template <bool XREG>
+RK_DEV void stage_x(const void* __restrict__ x, int xdt, int K, const XRegs& xr, uint4* __restrict__ frag,
+                    float* __restrict__ xsum) {
+    const int nb = K >> 3;  // 8-column blocks
+    if constexpr (XREG) {
+#pragma unroll
+        for (int k = 0; k < kXPre; ++k)
+            if (k * (int)blockDim.x < nb) stage_block(threadIdx.x + k * blockDim.x, nb, xdt, xr.d[k], frag, xsum);
+    } else {
+        for (int base = 0; base < nb; base += blockDim.x) {
+            const int i = base + threadIdx.x;
+            const u4_t d = i < nb ? reinterpret_cast<const u4_t*>(x)[i] : u4_t{0u, 0u, 0u, 0u};
+            stage_block(i, nb, xdt, d, frag, xsum);
+        }
     }
 }
 
@@ -113,16 +144,10 @@ struct Batch {
     uint16_t sv[kGB], mv[kGB];
 };
 
+// VEC_SM (16-byte aligned rows and batch starts, every batch full): one load for 8 scales, one for 8 mins
 template <bool VEC_SM>
-RK_DEV void load_batch(Batch& b, const uint8_t* qrow, const uint16_t* srow, const uint16_t* mrow, int gb, int g1) {
-    const bool full = gb + kGB <= g1;
-#pragma unroll
-    for (int e = 0; e < kGB; ++e) {
-        const int g = gb + e;
-        if (g < g1) b.w[e] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(qrow + (size_t)g * 64));
-        else b.w[e] = u4_t{0u, 0u, 0u, 0u};
-    }
-    if (VEC_SM && full) {  // 16-byte aligned rows and batch starts: one load for 8 scales, one for 8 mins
+RK_DEV void load_batch_sm(Batch& b, const uint16_t* srow, const uint16_t* mrow, int gb, int g1) {
+    if constexpr (VEC_SM) {
         const u4_t s8 = *reinterpret_cast<const u4_t*>(srow + gb);
         const u4_t m8 = *reinterpret_cast<const u4_t*>(mrow + gb);
 #pragma unroll
@@ -133,36 +158,71 @@ RK_DEV void load_batch(Batch& b, const uint8_t* qrow, const uint16_t* srow, cons
     } else {
 #pragma unroll
         for (int e = 0; e < kGB; ++e) {
-            const int g = gb + e;
-            b.sv[e] = g < g1 ? srow[g] : (uint16_t)0;
-            b.mv[e] = g < g1 ? mrow[g] : (uint16_t)0;
+            const int g = min(gb + e, g1 - 1);
+            b.sv[e] = srow[g];
+            b.mv[e] = mrow[g];
         }
     }
 }
 
-// dequant + 4 MFMAs per group, then the group affine into acc. FULL batches have no per-group checks, so the
-// compiler can interleave the independent MFMA chains of different groups.
+// Scales / mins first, then the codes in group order: the compute of group e then waits only for the loads up to
+// its own (results return in issue order), so it starts while later groups are still in flight. Groups past g1
+// reload group g1 - 1 (fixed load count; their results are never used).
+template <bool VEC_SM>
+RK_DEV void load_batch(Batch& b, const uint8_t* qrow, const uint16_t* srow, const uint16_t* mrow, int gb, int g1) {
+    load_batch_sm<VEC_SM>(b, srow, mrow, gb, g1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order: scales before codes
+#pragma unroll
+    for (int e = 0; e < kGB; ++e) {
+        const int g = min(gb + e, g1 - 1);
+        b.w[e] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(qrow + (size_t)g * 64));
+    }
+}
+
+// dequant + 4 MFMAs per group (each group waits only for its own codes; the next group's x fragments are read from
+// LDS while the current group's MFMAs run), then the group affines into acc once the batch's scales / mins are in
+// (whatever order the compiler issued them in): acc += scale * dot + min * xsum_g. FULL batches have no per-group
+// checks.
 template <bool FULL>
 RK_DEV void compute_batch(const Batch& b, const uint4* frag, const float* xsum, int s, int gb, int g1,
                           const Consts& kc, float& acc) {
+    float dg[kGB];
+    h8_t A[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) A[t] = __builtin_bit_cast(h8_t, frag[min(gb, g1 - 1) * 16 + t * 4 + s]);
+#pragma unroll
+    for (int e = 0; e < kGB; ++e) {
+        const int g = gb + e;
+        h8_t An[4];
+        if (e + 1 < kGB) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) An[t] = __builtin_bit_cast(h8_t, frag[min(g + 1, g1 - 1) * 16 + t * 4 + s]);
+        }
+        dg[e] = 0.f;
+        if (FULL || g < g1) {
+            f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t], dequant8(b.w[e][t], kc), d, 0, 0, 0);
+            dg[e] = d[0];
+        }
+        if (e + 1 < kGB) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) A[t] = An[t];
+        }
+    }
 #pragma unroll
     for (int e = 0; e < kGB; ++e) {
         const int g = gb + e;
         if (FULL || g < g1) {
-            const uint4* fg = frag + g * 16 + s;
-            f4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const h8_t A = __builtin_bit_cast(h8_t, fg[t * 4]);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant8(b.w[e][t], kc), d, 0, 0, 0);
-            }
-            acc = __builtin_fmaf(d[0], f16_bits_to_f32(b.sv[e]), __builtin_fmaf(f16_bits_to_f32(b.mv[e]), xsum[g], acc));
+            acc = __builtin_fmaf(dg[e], f16_bits_to_f32(b.sv[e]), __builtin_fmaf(f16_bits_to_f32(b.mv[e]), xsum[g], acc));
         }
     }
 }
 
-template <int KS, bool VEC_SM>
-__global__ __launch_bounds__(256) void gemv_int4_mfma_kernel(const void* __restrict__ x, int xdt,
+// 3 waves per SIMD (<= 168 VGPRs): the 688 blocks of the gate+up projection are all resident at once
+template <int KS, bool VEC_SM, bool XREG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemv_int4_mfma_kernel(const void* __restrict__ x, int xdt,
                                                               const uint8_t* __restrict__ q,
                                                               const uint16_t* __restrict__ sc,
                                                               const uint16_t* __restrict__ mn,
@@ -185,16 +245,21 @@ __global__ __launch_bounds__(256) void gemv_int4_mfma_kernel(const void* __restr
     const uint16_t* srow = sc + (size_t)row * NG;
     const uint16_t* mrow = mn + (size_t)row * NG;
 
-    // the first batch of weights goes out before x is staged: its HBM latency overlaps the staging
+    // x, then the first batch of scales and codes: the HBM latency of the weights overlaps the staging of x
+    XRegs xr;
+    if constexpr (XREG) x_issue(x, K, xr);
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order: x before the weights
     Batch cur;
     load_batch<VEC_SM>(cur, qrow, srow, mrow, g0, g1);
 
-    stage_x(x, xdt, K, frag, xsum);
+    stage_x<XREG>(x, xdt, K, xr, frag, xsum);
     __syncthreads();
 
     const Consts kc = {opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
     float acc = 0.f;
-    for (int gb = g0; gb < g1; gb += kGB) {
+    if (g1 - g0 == kGB) {  // wave-uniform: one full batch, nothing more to load (straight-line waits)
+        compute_batch<true>(cur, frag, xsum, s, g0, g1, kc, acc);
+    } else for (int gb = g0; gb < g1; gb += kGB) {
         Batch nxt;
         const bool more = gb + kGB < g1;
         if (more) load_batch<VEC_SM>(nxt, qrow, srow, mrow, gb + kGB, g1);  // prefetch while computing
@@ -225,9 +290,14 @@ hipError_t launch_mfma(const void* x, int xdt, const uint8_t* q, const uint16_t*
                        int ydt, int N, int K, int teams, hipStream_t st) {
     const int tiles = (N + 15) / 16;
     const int blocks = (tiles + teams - 1) / teams;
+    const int threads = 64 * KS * teams;
     const size_t lds = (size_t)K * 2 + (size_t)(K / 128) * 4 + (size_t)teams * KS * 16 * 4;
-    hipLaunchKernelGGL((gemv_int4_mfma_kernel<KS, VEC>), dim3(blocks), dim3(64 * KS * teams), lds, st, x, xdt, q, s,
-                       m, y, ydt, N, K);
+    if (K / 8 <= kXPre * threads)
+        hipLaunchKernelGGL((gemv_int4_mfma_kernel<KS, VEC, true>), dim3(blocks), dim3(threads), lds, st, x, xdt, q, s,
+                           m, y, ydt, N, K);
+    else
+        hipLaunchKernelGGL((gemv_int4_mfma_kernel<KS, VEC, false>), dim3(blocks), dim3(threads), lds, st, x, xdt, q,
+                           s, m, y, ydt, N, K);
     return hipGetLastError();
 }
 

@@ -24,13 +24,23 @@ namespace {
 
 constexpr int kMaxThreads = 1024;
 
-// Load the 32 x values of chunk c as 16 fp16 pairs in dequant order, and their fp32 sum.
-RK_DEV void load_x_chunk(const void* __restrict__ x, int xdt, int c, uint32_t (&xp)[16], float& xs) {
+// The 32 x values of chunk c (4 x 16 bytes), loaded raw: issued before the weights so that processing them waits for
+// x only (vector-memory results return in issue order).
+struct XChunk {
+    u4_t d[4];
+};
+RK_DEV void load_x_raw(const void* __restrict__ x, int c, XChunk& xc) {
     const u4_t* xv = reinterpret_cast<const u4_t*>(x) + (size_t)c * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xc.d[i] = xv[i];
+}
+
+// chunk c's x as 16 fp16 pairs in dequant order, and their fp32 sum
+RK_DEV void process_x_chunk(const XChunk& xc, int xdt, uint32_t (&xp)[16], float& xs) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        u4_t d = xv[i];  // 8 consecutive 16-bit values: d.x = (x0,x1), d.y = (x2,x3), d.z = (x4,x5), d.w = (x6,x7)
+        u4_t d = xc.d[i];  // 8 consecutive 16-bit values: d.x = (x0,x1), d.y = (x2,x3), d.z = (x4,x5), d.w = (x6,x7)
         if (xdt == RK_BF16) {
             // bf16 -> fp32 (exact, summed) -> fp16 (round to nearest even) pairs
             float f[8];
@@ -121,41 +131,40 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_int4_kernel(const void* __re
 
     // K is walked in passes of 64*KS*NJ chunks (one pass whenever the plan allows it)
     for (int c0 = 0; c0 < nch; c0 += 64 * KS * NJ) {
-        // ---- loads first: R rows x NJ chunks of codes, then their scales / mins (all independent, all in flight)
-        u4_t w[R][NJ];
+        // ---- loads, in the order they are consumed: x (from L2), the scales / mins, then R rows x NJ chunks of
+        // codes. Every load is unconditional (chunks past K re-read the last chunk, rows past N the last row) so the
+        // compiler can wait for each one alone; the duplicates meet zeroed x and add nothing.
+        XChunk xc[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) load_x_raw(x, min(c0 + t + j * 64 * KS, nch - 1), xc[j]);
         uint16_t s16[R][NJ], m16[R][NJ];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int row = min(row0 + r, N - 1);  // rows past N re-read the last row; their result is dropped
-            const u4_t* qr = reinterpret_cast<const u4_t*>(q + (size_t)row * (size_t)(K >> 1));
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int c = c0 + t + j * 64 * KS;
-                if (c < nch) w[r][j] = __builtin_nontemporal_load(qr + c);
-                else w[r][j] = u4_t{0u, 0u, 0u, 0u};
-            }
-        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int row = min(row0 + r, N - 1);
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const int c = c0 + t + j * 64 * KS;
+                const int c = min(c0 + t + j * 64 * KS, nch - 1);
                 const size_t gi = (size_t)row * ng + (c >> 2);
-                if (c < nch) { s16[r][j] = sc[gi]; m16[r][j] = mn[gi]; }
-                else { s16[r][j] = 0; m16[r][j] = 0; }
+                s16[r][j] = sc[gi];
+                m16[r][j] = mn[gi];
             }
         }
+        u4_t w[R][NJ];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, N - 1);  // rows past N re-read the last row; their result is dropped
+            const u4_t* qr = reinterpret_cast<const u4_t*>(q + (size_t)row * (size_t)(K >> 1));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) w[r][j] = __builtin_nontemporal_load(qr + min(c0 + t + j * 64 * KS, nch - 1));
+        }
 
-        // ---- x chunks (from L2: the same small vector for every wave)
+        // ---- x chunks as dequant-ordered pairs (zero past K)
         uint32_t xp[NJ][16];
         float xs[NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const int c = c0 + t + j * 64 * KS;
-            if (c < nch) {
-                load_x_chunk(x, xdt, c, xp[j], xs[j]);
-            } else {
+            process_x_chunk(xc[j], xdt, xp[j], xs[j]);
+            if (c0 + t + j * 64 * KS >= nch) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) xp[j][e] = 0u;
                 xs[j] = 0.f;

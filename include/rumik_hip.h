@@ -131,8 +131,9 @@ int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_str
  * ~260 launches of RumikFused._step, engine/rumik_fused.py:97-121, plus the audio head of _logits, :84-89).
  * Hidden size 2048 and head dim 128 are fixed; NH * 128 == 2048; NH / NKV in {1, 2, 4, 8}; inter % 128 == 0 and
  * inter <= 11008. One block per CU (nblocks = 256 on MI355X, co-residency is checked); block b owns rows
- * [8b, 8b + 8) of the residual stream and of w_o, the w_in tiles and w_down column slices its `work` row lists, and
- * attention split b % nsp of KV head b / nsp (b < NKV * nsp).
+ * [8b, 8b + 8) of the residual stream, the w_in tiles and w_down column slices its `work` row lists, attention
+ * split b % nsp of KV head b / nsp (b < NKV * nsp), and the combine of head b / 16 with its w_o slice (rows of
+ * group b % 16).
  * Weights are stacked over layers and re-laid out once at load time:
  *   w_in rows are [q | k | v | per 8 MLP channels: 8 gate rows, 8 up rows]; tile T = rows [16T, 16T + 16);
  *   win_t holds, per (layer, tile, 128-column group), the 16 rows x 64 bytes of codes in lane order (lane j + 16s:

@@ -132,29 +132,35 @@ __global__ __launch_bounds__(256) void mm_int4_kernel(const void* __restrict__ X
 #pragma unroll
         for (int nt = 0; nt < WN; ++nt) acc[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int g = 0; g < NG; ++g) {
+    // one group's operands; the next group's are loaded while the current one computes (software pipelining)
+    struct Stage {
         u4_t wq[WN];
         uint16_t sv[WN], mv[WN];
+        u4_t xa[WM][4];
+    };
+    auto load = [&](Stage& st, int g) {
 #pragma unroll
         for (int nt = 0; nt < WN; ++nt) {
-            wq[nt] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(qrow[nt] + (size_t)g * 64));
-            sv[nt] = srow[nt][g];
-            mv[nt] = mrow[nt][g];
+            st.sv[nt] = srow[nt][g];
+            st.mv[nt] = mrow[nt][g];
         }
-        u4_t xa[WM][4];
 #pragma unroll
         for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xa[mt][t] = reinterpret_cast<const u4_t*>(xrow[mt] + 128 * g)[t];
+            for (int t = 0; t < 4; ++t) st.xa[mt][t] = reinterpret_cast<const u4_t*>(xrow[mt] + 128 * g)[t];
+#pragma unroll
+        for (int nt = 0; nt < WN; ++nt) st.wq[nt] = reinterpret_cast<const u4_t*>(qrow[nt] + (size_t)g * 64)[0];
+    };
+    auto compute = [&](const Stage& st, int g) {
         h8_t A[WM][4], B[WN][4];
 #pragma unroll
         for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) A[mt][t] = afrag(xa[mt][t], xdt);
+            for (int t = 0; t < 4; ++t) A[mt][t] = afrag(st.xa[mt][t], xdt);
 #pragma unroll
         for (int nt = 0; nt < WN; ++nt)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) B[nt][t] = dequant8(wq[nt][t], kc);
+            for (int t = 0; t < 4; ++t) B[nt][t] = dequant8(st.wq[nt][t], kc);
 #pragma unroll
         for (int mt = 0; mt < WM; ++mt) {
             // this lane's 4 D rows are m0 + mt*16 + 4s + e: their group sums are 4 consecutive floats
@@ -164,12 +170,21 @@ __global__ __launch_bounds__(256) void mm_int4_kernel(const void* __restrict__ X
                 f4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int t = 0; t < 4; ++t) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt][t], B[nt][t], c, 0, 0, 0);
-                const float scl = f16_bits_to_f32(sv[nt]), mnv = f16_bits_to_f32(mv[nt]);
+                const float scl = f16_bits_to_f32(st.sv[nt]), mnv = f16_bits_to_f32(st.mv[nt]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[mt][nt][e] = __builtin_fmaf(c[e], scl, __builtin_fmaf(xs[e], mnv, acc[mt][nt][e]));
             }
         }
+    };
+    Stage cur, nxt;
+    load(cur, 0);
+    int g = 0;
+    for (; g + 1 < NG; ++g) {
+        load(nxt, g + 1);
+        compute(cur, g);
+        cur = nxt;
     }
+    compute(cur, g);
 
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
@@ -183,6 +198,204 @@ __global__ __launch_bounds__(256) void mm_int4_kernel(const void* __restrict__ X
                 if (m < M) store_act(Y, ydt, (size_t)m * ldy + n, acc[mt][nt][e]);
             }
         }
+}
+
+// ---------------------------------------------------------------------------------------------- LDS-tiled kernel
+// Block = 4 waves (2 x 2), tile BM x BN = (2*WM*16) x (2*WN*16). Per 128-column K step (one quantization group) the
+// One K step (128-column group) of a block tile staged in LDS, double-buffered: the X rows as fp16 MFMA A
+// fragments (dequant pair order) with each row's fp32 sum over the group, the code rows dequantised to exact fp16
+// codes as B fragments. MFMA t of a step covers columns 32s + 8t .. + 7 of the group in lane group s, as in the
+// GEMV kernels.
+template <int BM, int BN>
+struct MmStage {
+    // a[m tile][t][slot]: the A fragment of MFMA t for 16 rows; lane (row i, quarter s) sits in slot
+    // 16 s + (i ^ (4 s + t)), so that both the 16-lane reads of a quarter and the writes of one row's 16 chunks
+    // (all s, t) touch 16 distinct 16-byte bank groups
+    uint4 a[BM / 16][4][64];
+    uint4 b[BN / 16][4][64];  // b[n tile][t][lane]: lane (column j, quarter s)
+    float xs[BM];
+};
+
+// Block tile BM x BN = (GM WM 16) x (GN WN 16): GM x GN waves, each holding WM x WN 16 x 16 MFMA tiles. Per
+// 128-column group g (one K step): the block's X rows and code rows are loaded into registers two steps ahead,
+// converted into one of two LDS stages, and every wave runs its 4 x WM x WN MFMAs from LDS into per-step sums c,
+// then applies the group's affine: acc += c * scale[n] + rowsum(X)[m] * min[n] (fp32), as the reference's Triton
+// kernel does. With eight waves (two per SIMD) one wave's conversion and affine overlap another's MFMAs.
+// BF16: activations are bf16 (else fp16), a template parameter so the staging has no per-chunk dtype branches
+template <int WM, int WN, int GM, int GN, bool BF16>
+__global__ __launch_bounds__(64 * GM * GN) void mm_int4_lds_kernel(const void* __restrict__ X, int ldx,
+                                                                   const uint8_t* __restrict__ q,
+                                                                   const uint16_t* __restrict__ sc,
+                                                                   const uint16_t* __restrict__ mn, void* __restrict__ Y,
+                                                                   int ydt, int ldy, int M, int N, int K) {
+    constexpr int NT = 64 * GM * GN;
+    constexpr int BM = GM * WM * 16, BN = GN * WN * 16;
+    constexpr int XCH = BM * 16 / NT;  // 16-byte X chunks per thread per step (row r, 8-column block c)
+    constexpr int WCH = BN * 4 / NT;   // 16-byte code chunks per thread per step (row n, quarter s)
+    static_assert(XCH >= 1 && WCH >= 1 && BM * 16 % NT == 0 && BN * 4 % NT == 0, "tile does not fit the threads");
+    using Stage = MmStage<BM, BN>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    Stage* stg = reinterpret_cast<Stage*>(smem);  // [2]
+    const int NG = K >> 7;
+    uint32_t* smw = reinterpret_cast<uint32_t*>(stg + 2);  // [BN][NG]: scale | min << 16 of the block's rows
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / GN, wn = wave % GN;
+    const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
+    const DqConsts kc = {opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u)};
+
+    for (int i = tid; i < BN * NG; i += NT) {
+        const int n = min(nb + i / NG, N - 1), g = i % NG;
+        smw[i] = (uint32_t)sc[(size_t)n * NG + g] | ((uint32_t)mn[(size_t)n * NG + g] << 16);
+    }
+    // this thread's staging slots: X chunk i -> row r = idx / 16, 8-column block c = idx % 16 (a row's 256 bytes
+    // in 16 consecutive lanes, so its sum is a 16-lane DPP reduction); code chunk i -> row r = idx % 16 +
+    // 16 (idx / 64), quarter s = idx / 16 % 4 (16 consecutive lanes write one quarter of 16 rows: no bank conflict)
+    struct Regs {
+        u4_t xr[XCH], wr[WCH];
+    };
+    Regs R0, R1;  // two steps in flight: step g + 2 is loaded while step g computes
+    auto load = [&](Regs& R, int g) {
+        auto& xr = R.xr; auto& wr = R.wr;
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int idx = tid + NT * i, r = idx >> 4, c = idx & 15;
+            const int m = min(mb + r, M - 1);
+            xr[i] = *reinterpret_cast<const u4_t*>(reinterpret_cast<const uint16_t*>(X) + (size_t)m * ldx + 128 * g + 8 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < WCH; ++i) {
+            const int idx = tid + NT * i, r = (idx & 15) | ((idx >> 6) << 4), qq = (idx >> 4) & 3;
+            const int n = min(nb + r, N - 1);
+            wr[i] = *reinterpret_cast<const u4_t*>(q + (size_t)n * (size_t)(K >> 1) + 64 * g + 16 * qq);
+        }
+    };
+    auto store = [&](const Regs& R, Stage& st) {
+        const auto& xr = R.xr; const auto& wr = R.wr;
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int idx = tid + NT * i, r = idx >> 4, c = idx & 15;
+            // 8-column block c = 32s + 8t: quarter s = c / 4, MFMA t = c % 4, swizzle 4 s + t = c
+            st.a[r >> 4][c & 3][16 * (c >> 2) + ((r & 15) ^ c)] =
+                __builtin_bit_cast(uint4, afrag(xr[i], BF16 ? RK_BF16 : RK_F16));
+            float sum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (BF16) {
+                    sum += __builtin_bit_cast(float, xr[i][e] << 16) + __builtin_bit_cast(float, xr[i][e] & 0xffff0000u);
+                } else {
+                    const h2_t v = as_h2(xr[i][e]);
+                    sum += (float)v.x + (float)v.y;
+                }
+            }
+            sum += dpp<0x128>(sum);  // the row's 16 chunks sit in 16 consecutive lanes (one DPP row)
+            sum += dpp<0x124>(sum);
+            sum += dpp<0x122>(sum);
+            sum += dpp<0x121>(sum);
+            if (c == 0) st.xs[r] = sum;
+        }
+#pragma unroll
+        for (int i = 0; i < WCH; ++i) {
+            const int idx = tid + NT * i, r = (idx & 15) | ((idx >> 6) << 4), qq = (idx >> 4) & 3;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                st.b[r >> 4][t][(r & 15) + 16 * qq] = __builtin_bit_cast(uint4, dequant8(wr[i][t], kc));
+        }
+    };
+
+    f4_t acc[WM][WN];
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < WN; ++nt) acc[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    // A fragment slot of this lane for MFMA t (the swizzle of the stores)
+    int aslot[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) aslot[t] = 16 * (lane >> 4) + ((lane & 15) ^ (4 * (lane >> 4) + t));
+
+    load(R0, 0);
+    load(R1, min(1, NG - 1));
+    store(R0, stg[0]);
+    __syncthreads();
+    // one K step: reload Rn (it held step g, already in LDS) with step g + 2, compute step g from LDS, store step
+    // g + 1 (in Rs since one step ago) into the other buffer
+    auto step = [&](int g, Regs& Rn, const Regs& Rs) {
+        const Stage& st = stg[g & 1];
+        load(Rn, min(g + 2, NG - 1));  // unconditional (the last steps reload the last group, unused): a conditional
+                                       // load would make the compiler wait for every load in flight
+        f4_t c[WM][WN];
+#pragma unroll
+        for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < WN; ++nt) c[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            h8_t A[WM], B[WN];
+#pragma unroll
+            for (int mt = 0; mt < WM; ++mt) A[mt] = __builtin_bit_cast(h8_t, st.a[wm * WM + mt][t][aslot[t]]);
+#pragma unroll
+            for (int nt = 0; nt < WN; ++nt) B[nt] = __builtin_bit_cast(h8_t, st.b[wn * WN + nt][t][lane]);
+#pragma unroll
+            for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < WN; ++nt)
+                    c[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], B[nt], c[mt][nt], 0, 0, 0);
+        }
+        // D[i][j] in lane j + 16 (i / 4), element i % 4: column n = tile + lane % 16, rows 4 (lane / 16) + e
+#pragma unroll
+        for (int nt = 0; nt < WN; ++nt) {
+            const uint32_t w = smw[((wn * WN + nt) * 16 + (lane & 15)) * NG + g];
+            const float scl = f16_bits_to_f32((uint16_t)w), mnv = f16_bits_to_f32((uint16_t)(w >> 16));
+#pragma unroll
+            for (int mt = 0; mt < WM; ++mt) {
+                const f4_t xs = *reinterpret_cast<const f4_t*>(&st.xs[(wm * WM + mt) * 16 + 4 * (lane >> 4)]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[mt][nt][e] = __builtin_fmaf(c[mt][nt][e], scl, __builtin_fmaf(xs[e], mnv, acc[mt][nt][e]));
+            }
+        }
+        if (g + 1 < NG) store(Rs, stg[(g + 1) & 1]);  // the other buffer: last read one step ago, before the barrier
+        __syncthreads();
+    };
+    int g = 0;
+    for (; g + 1 < NG; g += 2) {  // unrolled by two so each register set has a fixed role; no optional step inside
+        step(g, R0, R1);
+        step(g + 1, R1, R0);
+    }
+    if (g < NG) step(g, R0, R1);
+
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < WN; ++nt) {
+            const int n = nb + (wn * WN + nt) * 16 + (lane & 15);
+            if (n >= N) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = mb + (wm * WM + mt) * 16 + 4 * (lane >> 4) + e;
+                if (m < M) store_act(Y, ydt, (size_t)m * ldy + n, acc[mt][nt][e]);
+            }
+        }
+}
+
+template <int WM, int WN, int GM, int GN>
+size_t mm_lds_bytes(int K) {
+    constexpr int BM = GM * WM * 16, BN = GN * WN * 16;
+    return 2 * sizeof(MmStage<BM, BN>) + (size_t)BN * (K / 128) * 4;
+}
+
+template <int WM, int WN, int GM, int GN>
+hipError_t launch_mm_lds(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s, const uint16_t* m,
+                         void* Y, int ydt, int ldy, int M, int N, int K, hipStream_t st) {
+    constexpr int BM = GM * WM * 16, BN = GN * WN * 16;
+    const size_t lds = mm_lds_bytes<WM, WN, GM, GN>(K);
+    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+    if (xdt == RK_BF16)
+        hipLaunchKernelGGL((mm_int4_lds_kernel<WM, WN, GM, GN, true>), grid, dim3(64 * GM * GN), lds, st, X, ldx, q, s,
+                           m, Y, ydt, ldy, M, N, K);
+    else
+        hipLaunchKernelGGL((mm_int4_lds_kernel<WM, WN, GM, GN, false>), grid, dim3(64 * GM * GN), lds, st, X, ldx, q,
+                           s, m, Y, ydt, ldy, M, N, K);
+    return hipGetLastError();
 }
 
 template <int WM, int WN>
@@ -207,8 +420,13 @@ extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_
     if (((uintptr_t)X & 15) || ((uintptr_t)q & 15) || (ldx % 8)) return RK_ERR_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t e;
-    // short prompts: 32-row blocks (memory-bound, keep the grid wide); longer: 64 x 64 blocks
-    if (M <= 32) e = launch_mm<1, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
-    else e = launch_mm<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
+    // LDS-tiled kernel: 128 x 128 tiles when that still gives every CU a block (and fits LDS), else 64 x 64
+    const long big = (long)((N + 127) / 128) * ((M + 127) / 128);
+    if (M > 64 && big >= 256 && mm_lds_bytes<4, 2, 2, 4>(K) <= 160 * 1024)
+        e = launch_mm_lds<4, 2, 2, 4>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
+    else if (mm_lds_bytes<2, 2, 2, 2>(K) <= 160 * 1024)
+        e = launch_mm_lds<2, 2, 2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
+    else
+        e = launch_mm<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }

@@ -86,6 +86,19 @@ int rk_gemv_int8_rows(const void* x, int x_dtype, const void* q, int q_kind, con
 int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
                     const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, rk_stream_t stream);
 
+/* Bytes of fp32 workspace rk_mm_int4_g128_ws uses for this shape (0: it needs none). Shapes whose output tiles
+ * alone leave CUs idle (few rows and columns, long K) are split over K into fp32 partial sums that a second kernel
+ * adds in a fixed order. Part of the same drop-in for mm_int4 (reference kernels/mm_int4.py:59-73), which
+ * allocates its output per call; the Python wrapper allocates this workspace the same way. */
+size_t rk_mm_int4_workspace_bytes(int M, int N, int K);
+
+/* rk_mm_int4_g128 with a caller-provided workspace of at least rk_mm_int4_workspace_bytes(M, N, K) bytes
+ * (16-byte aligned; may be NULL when that is 0); RK_ERR_SHAPE if it is smaller. Same results as rk_mm_int4_g128 up
+ * to fp32 summation order. Calls that share one workspace must be ordered on one stream. */
+int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
+                       const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, void* workspace,
+                       size_t workspace_bytes, rk_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------------------
  * Decode-step glue (reference engine/fused.py). Activations of one decode step are vectors of `act_dtype`
  * (fp16 or bf16); the KV cache is [NKV, S, HD] per layer in act_dtype; `pos` is an int64 on the device, read by

@@ -203,8 +203,7 @@ __global__ __launch_bounds__(256) void mm_int4_kernel(const void* __restrict__ X
 // ---------------------------------------------------------------------------------------------- LDS-tiled kernel
 // Block = 4 waves (2 x 2), tile BM x BN = (2*WM*16) x (2*WN*16). Per 128-column K step (one quantization group) the
 // One K step (128-column group) of a block tile staged in LDS, double-buffered: the X rows as fp16 MFMA A
-// fragments (dequant pair order) with each row's fp32 sum over the group, the code rows dequantised to exact fp16
-// codes as B fragments. MFMA t of a step covers columns 32s + 8t .. + 7 of the group in lane group s, as in the
+// fragments (dequant pair order), the code rows dequantised to exact fp16 codes as B fragments. MFMA t of a step covers columns 32s + 8t .. + 7 of the group in lane group s, as in the
 // GEMV kernels.
 template <int BM, int BN>
 struct MmStage {
@@ -213,94 +212,117 @@ struct MmStage {
     // (all s, t) touch 16 distinct 16-byte bank groups
     uint4 a[BM / 16][4][64];
     uint4 b[BN / 16][4][64];  // b[n tile][t][lane]: lane (column j, quarter s)
-    float xs[BM];
 };
 
-// Block tile BM x BN = (GM WM 16) x (GN WN 16): GM x GN waves, each holding WM x WN 16 x 16 MFMA tiles. Per
-// 128-column group g (one K step): the block's X rows and code rows are loaded into registers two steps ahead,
-// converted into one of two LDS stages, and every wave runs its 4 x WM x WN MFMAs from LDS into per-step sums c,
-// then applies the group's affine: acc += c * scale[n] + rowsum(X)[m] * min[n] (fp32), as the reference's Triton
-// kernel does. With eight waves (two per SIMD) one wave's conversion and affine overlap another's MFMAs.
+// Block tile BM x BN = (2 WM 16) x (2 WN 16) with eight waves in two roles. Waves 0..3 (2 x 2) each hold WM x WN
+// 16 x 16 MFMA tiles: per 128-column group g (one K step) they run 4 x WM x WN MFMAs from LDS stage g % 2 into
+// per-step sums c, 4 x WM more against an all-ones B for the rows' sums of X over the group (exact products, fp32
+// accumulation, already in the accumulator layout), and apply the group's affine, acc += c * scale[n] +
+// rowsum(X)[m] * min[n] (fp32, as the reference's Triton kernel does). Waves 4..7 stage: they keep the X rows and
+// code rows of the next two steps in registers and, during step g, convert step g + 1 into the other LDS stage
+// (X -> fp16 fragments, codes -> exact fp16). One barrier per step; the two roles run on every SIMD at once, so
+// the staging conversions overlap the MFMAs instead of following them.
+// Split K (splits > 1): block (tile, split) covers groups [split NG / splits, (split + 1) NG / splits) and writes
+// its fp32 sums to part[split][M][N] for mm_splitk_reduce; with splits == 1 the block writes Y directly.
 // BF16: activations are bf16 (else fp16), a template parameter so the staging has no per-chunk dtype branches
-template <int WM, int WN, int GM, int GN, bool BF16>
-__global__ __launch_bounds__(64 * GM * GN) void mm_int4_lds_kernel(const void* __restrict__ X, int ldx,
-                                                                   const uint8_t* __restrict__ q,
-                                                                   const uint16_t* __restrict__ sc,
-                                                                   const uint16_t* __restrict__ mn, void* __restrict__ Y,
-                                                                   int ydt, int ldy, int M, int N, int K) {
-    constexpr int NT = 64 * GM * GN;
-    constexpr int BM = GM * WM * 16, BN = GN * WN * 16;
-    constexpr int XCH = BM * 16 / NT;  // 16-byte X chunks per thread per step (row r, 8-column block c)
-    constexpr int WCH = BN * 4 / NT;   // 16-byte code chunks per thread per step (row n, quarter s)
-    static_assert(XCH >= 1 && WCH >= 1 && BM * 16 % NT == 0 && BN * 4 % NT == 0, "tile does not fit the threads");
+template <int WM, int WN, bool BF16>
+__global__ __launch_bounds__(512) void mm_int4_lds_kernel(const void* __restrict__ X, int ldx,
+                                                          const uint8_t* __restrict__ q, const uint16_t* __restrict__ sc,
+                                                          const uint16_t* __restrict__ mn, void* __restrict__ Y,
+                                                          int ydt, int ldy, int M, int N, int K,
+                                                          float* __restrict__ part, int splits) {
+    constexpr int BM = 2 * WM * 16, BN = 2 * WN * 16;
+    constexpr int XCH = BM * 16 / 256;  // 16-byte X chunks per staging thread per step (row r, 8-column block c)
+    constexpr int WCH = BN * 4 / 256;   // 16-byte code chunks per staging thread per step (row n, quarter s)
+    static_assert(XCH >= 1 && WCH >= 1, "tile too small for 256 staging threads");
     using Stage = MmStage<BM, BN>;
     extern __shared__ __align__(16) uint8_t smem[];
     Stage* stg = reinterpret_cast<Stage*>(smem);  // [2]
-    const int NG = K >> 7;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: role branches are scalar
+    const bool stager = wave >= 4;
+    const int sid = tid - 256;  // staging thread index (stager waves)
+    const int wm = (wave & 3) >> 1, wn = wave & 1;
+    // 1-D grid: workgroups go round-robin to the 8 XCDs, so virtual id (L % 8) * (G / 8) + L / 8 gives each XCD a
+    // contiguous range, walked row block fastest: the row blocks sharing one code tile run together on one L2
+    const int G = gridDim.x, L = blockIdx.x, GY = (M + BM - 1) / BM;
+    const int Lv = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
+    const int split = Lv % splits, tile = Lv / splits;
+    const int mb = (tile % GY) * BM, nb = (tile / GY) * BN;
+    const int NGT = K >> 7;                                                   // groups of a row
+    const int g0 = split * NGT / splits, NG = (split + 1) * NGT / splits - g0;  // this block's groups
     uint32_t* smw = reinterpret_cast<uint32_t*>(stg + 2);  // [BN][NG]: scale | min << 16 of the block's rows
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / GN, wn = wave % GN;
-    const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
-    const DqConsts kc = {opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u)};
 
-    for (int i = tid; i < BN * NG; i += NT) {
-        const int n = min(nb + i / NG, N - 1), g = i % NG;
-        smw[i] = (uint32_t)sc[(size_t)n * NG + g] | ((uint32_t)mn[(size_t)n * NG + g] << 16);
+    for (int i = tid; i < BN * NG; i += 512) {
+        const int n = min(nb + i / NG, N - 1), g = g0 + i % NG;
+        smw[i] = (uint32_t)sc[(size_t)n * NGT + g] | ((uint32_t)mn[(size_t)n * NGT + g] << 16);
     }
-    // this thread's staging slots: X chunk i -> row r = idx / 16, 8-column block c = idx % 16 (a row's 256 bytes
-    // in 16 consecutive lanes, so its sum is a 16-lane DPP reduction); code chunk i -> row r = idx % 16 +
-    // 16 (idx / 64), quarter s = idx / 16 % 4 (16 consecutive lanes write one quarter of 16 rows: no bank conflict)
+    // staging slots: X chunk i -> row r = idx / 16, 8-column block c = idx % 16 (a row's 256 bytes in 16
+    // consecutive lanes); code chunk i -> row r = idx % 16 + 16 (idx / 64),
+    // quarter s = idx / 16 % 4 (16 consecutive lanes write one quarter of 16 rows: no bank conflict)
     struct Regs {
         u4_t xr[XCH], wr[WCH];
     };
-    Regs R0, R1;  // two steps in flight: step g + 2 is loaded while step g computes
     auto load = [&](Regs& R, int g) {
         auto& xr = R.xr; auto& wr = R.wr;
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int idx = tid + NT * i, r = idx >> 4, c = idx & 15;
+            const int idx = sid + 256 * i, r = idx >> 4, c = idx & 15;
             const int m = min(mb + r, M - 1);
-            xr[i] = *reinterpret_cast<const u4_t*>(reinterpret_cast<const uint16_t*>(X) + (size_t)m * ldx + 128 * g + 8 * c);
+            xr[i] = *reinterpret_cast<const u4_t*>(reinterpret_cast<const uint16_t*>(X) + (size_t)m * ldx +
+                                                   128 * (g0 + g) + 8 * c);
         }
 #pragma unroll
         for (int i = 0; i < WCH; ++i) {
-            const int idx = tid + NT * i, r = (idx & 15) | ((idx >> 6) << 4), qq = (idx >> 4) & 3;
+            const int idx = sid + 256 * i, r = (idx & 15) | ((idx >> 6) << 4), qq = (idx >> 4) & 3;
             const int n = min(nb + r, N - 1);
-            wr[i] = *reinterpret_cast<const u4_t*>(q + (size_t)n * (size_t)(K >> 1) + 64 * g + 16 * qq);
+            wr[i] = *reinterpret_cast<const u4_t*>(q + (size_t)n * (size_t)(K >> 1) + 64 * (g0 + g) + 16 * qq);
         }
     };
     auto store = [&](const Regs& R, Stage& st) {
+        const DqConsts kc = {opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u)};
         const auto& xr = R.xr; const auto& wr = R.wr;
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int idx = tid + NT * i, r = idx >> 4, c = idx & 15;
+            const int idx = sid + 256 * i, r = idx >> 4, c = idx & 15;
             // 8-column block c = 32s + 8t: quarter s = c / 4, MFMA t = c % 4, swizzle 4 s + t = c
             st.a[r >> 4][c & 3][16 * (c >> 2) + ((r & 15) ^ c)] =
                 __builtin_bit_cast(uint4, afrag(xr[i], BF16 ? RK_BF16 : RK_F16));
-            float sum = 0.f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if constexpr (BF16) {
-                    sum += __builtin_bit_cast(float, xr[i][e] << 16) + __builtin_bit_cast(float, xr[i][e] & 0xffff0000u);
-                } else {
-                    const h2_t v = as_h2(xr[i][e]);
-                    sum += (float)v.x + (float)v.y;
-                }
-            }
-            sum += dpp<0x128>(sum);  // the row's 16 chunks sit in 16 consecutive lanes (one DPP row)
-            sum += dpp<0x124>(sum);
-            sum += dpp<0x122>(sum);
-            sum += dpp<0x121>(sum);
-            if (c == 0) st.xs[r] = sum;
         }
 #pragma unroll
         for (int i = 0; i < WCH; ++i) {
-            const int idx = tid + NT * i, r = (idx & 15) | ((idx >> 6) << 4), qq = (idx >> 4) & 3;
+            const int idx = sid + 256 * i, r = (idx & 15) | ((idx >> 6) << 4), qq = (idx >> 4) & 3;
 #pragma unroll
             for (int t = 0; t < 4; ++t)
                 st.b[r >> 4][t][(r & 15) + 16 * qq] = __builtin_bit_cast(uint4, dequant8(wr[i][t], kc));
         }
     };
+
+    // The two roles run separate loops with the same number of barriers (two before the K loop, one per step), so
+    // neither holds the other's registers.
+    if (stager) {
+        Regs R0, R1;  // two steps in flight: step g + 2 is loaded while step g + 1 is converted
+        load(R0, 0);
+        load(R1, min(1, NG - 1));
+        __syncthreads();  // smw
+        store(R0, stg[0]);
+        __syncthreads();
+        // during step g: reload Rn (it held step g, already in LDS) with step g + 2, store step g + 1 (in Rs since
+        // one step ago) into the other stage, last read by the MFMA waves one step ago, before the barrier
+        auto step = [&](int g, Regs& Rn, const Regs& Rs) {
+            load(Rn, min(g + 2, NG - 1));  // unconditional (the last steps reload the last group, unused): a
+                                           // conditional load would make the compiler wait for every load in flight
+            if (g + 1 < NG) store(Rs, stg[(g + 1) & 1]);
+            __syncthreads();
+        };
+        int g = 0;
+        for (; g + 1 < NG; g += 2) {  // unrolled by two so each register set has a fixed role
+            step(g, R0, R1);
+            step(g + 1, R1, R0);
+        }
+        if (g < NG) step(g, R0, R1);
+        return;
+    }
 
     f4_t acc[WM][WN];
 #pragma unroll
@@ -311,22 +333,18 @@ __global__ __launch_bounds__(64 * GM * GN) void mm_int4_lds_kernel(const void* _
     int aslot[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) aslot[t] = 16 * (lane >> 4) + ((lane & 15) ^ (4 * (lane >> 4) + t));
-
-    load(R0, 0);
-    load(R1, min(1, NG - 1));
-    store(R0, stg[0]);
-    __syncthreads();
-    // one K step: reload Rn (it held step g, already in LDS) with step g + 2, compute step g from LDS, store step
-    // g + 1 (in Rs since one step ago) into the other buffer
-    auto step = [&](int g, Regs& Rn, const Regs& Rs) {
+    __syncthreads();  // smw
+    __syncthreads();  // stage 0
+    const h8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    for (int g = 0; g < NG; ++g) {
         const Stage& st = stg[g & 1];
-        load(Rn, min(g + 2, NG - 1));  // unconditional (the last steps reload the last group, unused): a conditional
-                                       // load would make the compiler wait for every load in flight
-        f4_t c[WM][WN];
+        f4_t c[WM][WN], xs[WM];
 #pragma unroll
-        for (int mt = 0; mt < WM; ++mt)
+        for (int mt = 0; mt < WM; ++mt) {
+            xs[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int nt = 0; nt < WN; ++nt) c[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             h8_t A[WM], B[WN];
@@ -335,10 +353,12 @@ __global__ __launch_bounds__(64 * GM * GN) void mm_int4_lds_kernel(const void* _
 #pragma unroll
             for (int nt = 0; nt < WN; ++nt) B[nt] = __builtin_bit_cast(h8_t, st.b[wn * WN + nt][t][lane]);
 #pragma unroll
-            for (int mt = 0; mt < WM; ++mt)
+            for (int mt = 0; mt < WM; ++mt) {
 #pragma unroll
                 for (int nt = 0; nt < WN; ++nt)
                     c[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], B[nt], c[mt][nt], 0, 0, 0);
+                xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], ones, xs[mt], 0, 0, 0);
+            }
         }
         // D[i][j] in lane j + 16 (i / 4), element i % 4: column n = tile + lane % 16, rows 4 (lane / 16) + e
 #pragma unroll
@@ -346,22 +366,13 @@ __global__ __launch_bounds__(64 * GM * GN) void mm_int4_lds_kernel(const void* _
             const uint32_t w = smw[((wn * WN + nt) * 16 + (lane & 15)) * NG + g];
             const float scl = f16_bits_to_f32((uint16_t)w), mnv = f16_bits_to_f32((uint16_t)(w >> 16));
 #pragma unroll
-            for (int mt = 0; mt < WM; ++mt) {
-                const f4_t xs = *reinterpret_cast<const f4_t*>(&st.xs[(wm * WM + mt) * 16 + 4 * (lane >> 4)]);
+            for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    acc[mt][nt][e] = __builtin_fmaf(c[mt][nt][e], scl, __builtin_fmaf(xs[e], mnv, acc[mt][nt][e]));
-            }
+                    acc[mt][nt][e] = __builtin_fmaf(c[mt][nt][e], scl, __builtin_fmaf(xs[mt][e], mnv, acc[mt][nt][e]));
         }
-        if (g + 1 < NG) store(Rs, stg[(g + 1) & 1]);  // the other buffer: last read one step ago, before the barrier
         __syncthreads();
-    };
-    int g = 0;
-    for (; g + 1 < NG; g += 2) {  // unrolled by two so each register set has a fixed role; no optional step inside
-        step(g, R0, R1);
-        step(g + 1, R1, R0);
     }
-    if (g < NG) step(g, R0, R1);
 
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
@@ -372,29 +383,48 @@ __global__ __launch_bounds__(64 * GM * GN) void mm_int4_lds_kernel(const void* _
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int m = mb + (wm * WM + mt) * 16 + 4 * (lane >> 4) + e;
-                if (m < M) store_act(Y, ydt, (size_t)m * ldy + n, acc[mt][nt][e]);
+                if (m >= M) continue;
+                if (splits == 1)
+                    store_act(Y, ydt, (size_t)m * ldy + n, acc[mt][nt][e]);
+                else
+                    part[((size_t)split * M + m) * N + n] = acc[mt][nt][e];
             }
         }
 }
 
-template <int WM, int WN, int GM, int GN>
-size_t mm_lds_bytes(int K) {
-    constexpr int BM = GM * WM * 16, BN = GN * WN * 16;
-    return 2 * sizeof(MmStage<BM, BN>) + (size_t)BN * (K / 128) * 4;
+// Y[m, n] = sum over splits of part[split][m][n] (fixed order), in Y's dtype
+__global__ __launch_bounds__(256) void mm_splitk_reduce(const float* __restrict__ part, int splits,
+                                                        void* __restrict__ Y, int ydt, int ldy, int M, int N) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, MN = (size_t)M * N;
+    if (i >= MN) return;
+    float v = 0.f;
+    for (int k = 0; k < splits; ++k) v += part[k * MN + i];
+    store_act(Y, ydt, (i / N) * ldy + i % N, v);
 }
 
-template <int WM, int WN, int GM, int GN>
+template <int WM, int WN>
+size_t mm_lds_bytes(int ng) {  // ng: groups of one block
+    constexpr int BM = 2 * WM * 16, BN = 2 * WN * 16;
+    return 2 * sizeof(MmStage<BM, BN>) + (size_t)BN * ng * 4;
+}
+
+template <int WM, int WN>
 hipError_t launch_mm_lds(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s, const uint16_t* m,
-                         void* Y, int ydt, int ldy, int M, int N, int K, hipStream_t st) {
-    constexpr int BM = GM * WM * 16, BN = GN * WN * 16;
-    const size_t lds = mm_lds_bytes<WM, WN, GM, GN>(K);
-    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+                         void* Y, int ydt, int ldy, int M, int N, int K, float* part, int splits, hipStream_t st) {
+    constexpr int BM = 2 * WM * 16, BN = 2 * WN * 16;
+    const size_t lds = mm_lds_bytes<WM, WN>((K / 128 + splits - 1) / splits);
+    dim3 grid(((N + BN - 1) / BN) * ((M + BM - 1) / BM) * splits);
     if (xdt == RK_BF16)
-        hipLaunchKernelGGL((mm_int4_lds_kernel<WM, WN, GM, GN, true>), grid, dim3(64 * GM * GN), lds, st, X, ldx, q, s,
-                           m, Y, ydt, ldy, M, N, K);
+        hipLaunchKernelGGL((mm_int4_lds_kernel<WM, WN, true>), grid, dim3(512), lds, st, X, ldx, q, s, m, Y, ydt, ldy,
+                           M, N, K, part, splits);
     else
-        hipLaunchKernelGGL((mm_int4_lds_kernel<WM, WN, GM, GN, false>), grid, dim3(64 * GM * GN), lds, st, X, ldx, q,
-                           s, m, Y, ydt, ldy, M, N, K);
+        hipLaunchKernelGGL((mm_int4_lds_kernel<WM, WN, false>), grid, dim3(512), lds, st, X, ldx, q, s, m, Y, ydt,
+                           ldy, M, N, K, part, splits);
+    if (splits > 1) {
+        const size_t mn = (size_t)M * N;
+        hipLaunchKernelGGL(mm_splitk_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, splits, Y,
+                           ydt, ldy, M, N);
+    }
     return hipGetLastError();
 }
 
@@ -410,23 +440,76 @@ hipError_t launch_mm(const void* X, int xdt, int ldx, const uint8_t* q, const ui
 
 }  // namespace
 
-extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
-                               const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K,
-                               rk_stream_t stream) {
+namespace {
+
+constexpr size_t kLdsMax = 160 * 1024;
+
+// Kernel choice for one shape: 128 x 128 tiles (cfg 1) when that still gives every CU a block, else 64 x 64 tiles
+// (cfg 2), split over K when a workspace is allowed and the tiles alone leave CUs idle (each split keeps >= 4
+// groups); cfg 0 is the register-staged kernel, for K too long to stage one block's scales in LDS.
+struct MmPlan {
+    int cfg, splits;
+    size_t ws;  // fp32 partial bytes
+};
+
+MmPlan mm_plan(int M, int N, int K, bool allow_ws) {
+    const int NG = K / 128;
+    const long big = (long)((N + 127) / 128) * ((M + 127) / 128);
+    if (M > 64 && big >= 256 && mm_lds_bytes<4, 4>(NG) <= kLdsMax) return {1, 1, 0};
+    const long small = (long)((N + 63) / 64) * ((M + 63) / 64);
+    int splits = 1;
+    if (allow_ws && small < 256) splits = (int)std::max(1L, std::min((256 + small - 1) / small, (long)(NG / 4)));
+    while (allow_ws && mm_lds_bytes<2, 2>((NG + splits - 1) / splits) > kLdsMax && splits < NG) ++splits;
+    if (mm_lds_bytes<2, 2>((NG + splits - 1) / splits) > kLdsMax) return {0, 1, 0};
+    return {2, splits, splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0};
+}
+
+int mm_check(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale, const uint16_t* min,
+             const void* Y, int y_dtype, int ldy, int M, int N, int K) {
     if (!X || !q || !scale || !min || !Y) return RK_ERR_NULL;
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0 || ldx < K || ldy < N) return RK_ERR_SHAPE;
     if (x_dtype != RK_F16 && x_dtype != RK_BF16) return RK_ERR_DTYPE;
     if (y_dtype != RK_F16 && y_dtype != RK_BF16 && y_dtype != RK_F32) return RK_ERR_DTYPE;
     if (((uintptr_t)X & 15) || ((uintptr_t)q & 15) || (ldx % 8)) return RK_ERR_ALIGN;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return RK_OK;
+}
+
+int mm_run(const MmPlan& p, const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
+           const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, float* part, hipStream_t s) {
     hipError_t e;
-    // LDS-tiled kernel: 128 x 128 tiles when that still gives every CU a block (and fits LDS), else 64 x 64
-    const long big = (long)((N + 127) / 128) * ((M + 127) / 128);
-    if (M > 64 && big >= 256 && mm_lds_bytes<4, 2, 2, 4>(K) <= 160 * 1024)
-        e = launch_mm_lds<4, 2, 2, 4>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
-    else if (mm_lds_bytes<2, 2, 2, 2>(K) <= 160 * 1024)
-        e = launch_mm_lds<2, 2, 2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
+    if (p.cfg == 1)
+        e = launch_mm_lds<4, 4>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, nullptr, 1, s);
+    else if (p.cfg == 2)
+        e = launch_mm_lds<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, part, p.splits, s);
     else
         e = launch_mm<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
+                               const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K,
+                               rk_stream_t stream) {
+    const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
+    if (st != RK_OK) return st;
+    return mm_run(mm_plan(M, N, K, false), X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, nullptr,
+                  reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t rk_mm_int4_workspace_bytes(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
+    return mm_plan(M, N, K, true).ws;
+}
+
+extern "C" int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
+                                  const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K,
+                                  void* workspace, size_t workspace_bytes, rk_stream_t stream) {
+    const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
+    if (st != RK_OK) return st;
+    const MmPlan p = mm_plan(M, N, K, true);
+    if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) return RK_ERR_SHAPE;
+    if (p.ws > 0 && ((uintptr_t)workspace & 15)) return RK_ERR_ALIGN;
+    return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, static_cast<float*>(workspace),
+                  reinterpret_cast<hipStream_t>(stream));
 }

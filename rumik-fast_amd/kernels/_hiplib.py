@@ -26,6 +26,8 @@ _SIGS = {
     "rk_gemv_int8_rows": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _p], _i),
     "rk_gemv_int8_rows_ex": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_mm_int4_g128": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_mm_int4_workspace_bytes": ([_i, _i, _i], ctypes.c_size_t),
+    "rk_mm_int4_g128_ws": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, ctypes.c_size_t, _p], _i),
     "rk_embed_ln": ([_p, _p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
     "rk_add_ln": ([_p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
     "rk_post": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),

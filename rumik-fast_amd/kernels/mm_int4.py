@@ -7,8 +7,9 @@ the kernel (weights never leave int4 in HBM), products accumulate in fp32, and e
 
 Same names and arguments as the reference (mm_int4(x, q, s, m, BM=None, BN=64, num_warps=4, num_stages=3), warmup,
 G). The Triton tiling knobs BM / BN / num_warps / num_stages are accepted and validated but do not select anything:
-the HIP kernel picks its own tiles. Extra keyword `out=` writes into a preallocated [T, N] tensor (no allocation,
-graph-capturable). The output dtype is x's dtype (bf16 for the reference engine, as before).
+the HIP kernel picks its own tiles (and, for shapes with few output tiles, a split over K whose fp32 partial sums
+go to a workspace allocated per call from torch's caching allocator, like y). Extra keyword `out=` writes into a
+preallocated [T, N] tensor (graph-capturable). The output dtype is x's dtype (bf16 for the reference engine, as before).
 """
 import torch
 
@@ -40,8 +41,12 @@ def mm_int4(x, q, s, m, BM=None, BN=64, num_warps=4, num_stages=3, out=None):
     if y.shape != (T, N) or y.stride(1) != 1:
         raise AssertionError("out must be [T, N] with unit column stride")
     H.require_gpu(x, q, s, m, y)
-    st = H.lib().rk_mm_int4_g128(H.ptr(x), H.dt(x), x.stride(0), H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(y), H.dt(y),
-                                 y.stride(0), T, N, K, H.stream(x.device))
+    L = H.lib()
+    nws = L.rk_mm_int4_workspace_bytes(T, N, K)
+    # split-K partial sums for shapes with few output tiles (allocated per call like y, from torch's cache)
+    ws = torch.empty(nws, device=x.device, dtype=torch.uint8) if nws else None
+    st = L.rk_mm_int4_g128_ws(H.ptr(x), H.dt(x), x.stride(0), H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(y), H.dt(y),
+                              y.stride(0), T, N, K, H.ptr(ws), nws, H.stream(x.device))
     H.check(st, "mm_int4")
     return y
 

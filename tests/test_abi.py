@@ -49,6 +49,25 @@ def test_version_and_status_strings():
     assert "misaligned" in lib.rk_status_string(-5).decode()
 
 
+@pytest.mark.parametrize("M,N,K,splits", [(34, 2048, 11008, 8), (34, 3072, 2048, 4), (128, 2048, 11008, 4),
+                                          (200, 33, 11008, 21), (34, 22016, 2048, 1), (512, 2048, 11008, 1),
+                                          (512, 22016, 2048, 1), (4, 32, 256, 1)])
+def test_mm_int4_split_k_plan(M, N, K, splits):
+    """fp32 partials only where 64 x 64 output tiles leave CUs idle: splits = min(ceil(256 / tiles), groups / 4)"""
+    nbytes = HL.lib().rk_mm_int4_workspace_bytes(M, N, K)
+    assert nbytes == (splits * M * N * 4 if splits > 1 else 0)
+
+
+def test_mm_int4_ws_rejects_small_workspace():
+    lib = HL.lib()
+    buf = ctypes.c_void_p(256)  # never dereferenced: validation comes first
+    need = lib.rk_mm_int4_workspace_bytes(34, 2048, 11008)
+    args = (buf, HL.F16, 11008, buf, buf, buf, buf, HL.F16, 2048, 34, 2048, 11008)
+    assert lib.rk_mm_int4_g128_ws(*args, buf, need - 4, None) == -1
+    assert lib.rk_mm_int4_g128_ws(*args, None, need, None) == -1
+    assert lib.rk_mm_int4_g128_ws(*args, ctypes.c_void_p(264), need, None) == -5
+
+
 def test_decode_params_struct_matches_the_binding():
     import decode
     assert HL.lib().rk_decode_params_size() == ctypes.sizeof(decode.RkDecodeParams)

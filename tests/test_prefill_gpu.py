@@ -53,6 +53,31 @@ def test_ragged(M, N, K, dev):
     _check(Y, _ref(X, q, s, m), f"M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(34, 2048, 11008), (34, 3072, 2048), (5, 200, 4096), (128, 2048, 11008)])
+def test_split_k_matches_single_pass(M, N, K, dev):
+    """The split-K plan (fp32 partials + ordered sum) against the single-pass kernel of rk_mm_int4_g128 and the
+    oracle; both calls go through the C ABI, the second twice into one workspace."""
+    L = H.lib()
+    nws = L.rk_mm_int4_workspace_bytes(M, N, K)
+    assert nws > 0
+    X, q, s, m = synth.prefill_case(M, N, K, 11)
+    Xd, qd, sd, md = X.to(dev), q.to(dev), s.to(dev), m.to(dev)
+    Y1 = torch.empty(M, N, device=dev, dtype=torch.float32)
+    H.check(L.rk_mm_int4_g128(H.ptr(Xd), H.F16, K, H.ptr(qd), H.ptr(sd), H.ptr(md), H.ptr(Y1), H.F32, N, M, N, K,
+                              H.stream(dev)))
+    ws = torch.full((nws,), 0xFF, device=dev, dtype=torch.uint8)  # stale contents must not matter
+    for _ in range(2):
+        Y2 = torch.full((M, N), 3.0, device=dev, dtype=torch.float32)
+        H.check(L.rk_mm_int4_g128_ws(H.ptr(Xd), H.F16, K, H.ptr(qd), H.ptr(sd), H.ptr(md), H.ptr(Y2), H.F32, N, M,
+                                     N, K, H.ptr(ws), nws, H.stream(dev)))
+        torch.cuda.synchronize()
+        ref = _ref(X, q, s, m)
+        _check(Y1, ref, "single pass")
+        _check(Y2, ref, "split K")
+        # the two differ only in fp32 summation order
+        np.testing.assert_allclose(_np(Y2), _np(Y1), rtol=1e-4, atol=1e-6 * float(np.abs(_np(Y1)).max()))
+
+
 def test_bf16_and_fp32_out(dev):
     X, q, s, m = synth.prefill_case(40, 256, 2048, 5)
     Xb = X.bfloat16()

@@ -5,13 +5,17 @@
 
 Workload (one "step"): config 1 of the benchmark definition — one decoder layer's decode projections at batch 1,
 int4 g128, x fp16 ~N(0,1): fused QKV (2048 -> 3072), O (2048 -> 2048), fused gate+up (2048 -> 2*11008) followed by
-SiLU(gate)*up, down (11008 -> 2048). Each step uses the weights of the next of 16 distinct synthetic layers (665 MB
-in all), so no step is served from the 256 MB Infinity Cache. A step is one hipGraph replay; weights and inputs are
-resident in HBM before timing.
+SiLU(gate)*up, down (11008 -> 2048). The step runs them the way the reference engine does (engine/rumik_fused.py,
+engine/rumik_int4.py:97): QKV and gate+up are one input projection over the rows [q k v | gate | up] (w_in, 25088
+rows), whose epilogue here also applies SiLU(gate)*up (the MLP part of the reference's post), then O, then down:
+three launches. Each step uses the weights of the next of 16 distinct synthetic layers (665 MB in all), so no step
+is served from the 256 MB Infinity Cache. A step is one hipGraph replay; weights and inputs are resident in HBM
+before timing.
 
 value = algorithmic bytes per step (sum over the four projections of N*K/2 + 4*N*K/128 + 2K + 2N) / wall time.
-roofline: the dominant kernel (the gate+up GEMV, 24,001,536 B per launch), its average launch duration measured
-with HIP events on its stream over back-to-back launches with rotated weights.
+roofline: the dominant kernel (the fused w_in + SiLU launch, 27,328,000 B per launch: codes, scales, mins, x and the
+3072 + 11008 outputs), its average launch duration measured with HIP events on its stream over back-to-back
+launches with rotated weights.
 cpu_baseline: the CPU oracle's dequantize-then-matmul of the same step (numpy fp32), on this host's cores.
 Extra fields: the per-projection kernel times, the int8 audio head (config 2) and the int4 prefill (config 3).
 """
@@ -31,6 +35,8 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
 PEAK_FP16_TFLOPS = 2500.0    # MI355X dense fp16 MFMA, published
 H, INTER, NQKV = 2048, 11008, 2048 + 512 + 512
 SHAPES = {"qkv": (NQKV, H), "o": (H, H), "gate_up": (2 * INTER, H), "down": (H, INTER)}
+N_WIN = NQKV + 2 * INTER
+WIN_BYTES = N_WIN * H // 2 + 4 * N_WIN * (H // 128) + 2 * H + 2 * (NQKV + INTER)  # fused w_in + SiLU launch
 N_COPIES = 16
 
 
@@ -81,7 +87,7 @@ def load_traffic():
         return None
     try:
         d = json.loads(f.read_text())
-        return d.get("gemv_int4_gate_up_22016x2048", {}).get("traffic_bytes")
+        return d.get("gemv_int4_w_in_silu_25088x2048", {}).get("traffic_bytes")
     except Exception:
         return None
 
@@ -187,9 +193,16 @@ def main():
     torch.cuda.set_device(dev)
     log(f"[bench] {torch.cuda.get_device_name(dev)}, {torch.cuda.get_device_properties(dev).multi_processor_count} CUs")
 
-    # ---- weights: 16 distinct layers (GPU-side RNG: values are irrelevant to timing)
+    # ---- weights: 16 distinct layers (GPU-side RNG: values are irrelevant to timing); w_in = [qkv | gate+up] rows,
+    # with the separate projections as row slices of it (contiguous views, no copy)
     gen = synth.generator(1, "cuda")
-    layers = [{k: synth.int4_weights(N, K, gen, device=dev) for k, (N, K) in SHAPES.items()} for _ in range(N_COPIES)]
+    layers = []
+    for _ in range(N_COPIES):
+        L = {k: synth.int4_weights(N, K, gen, device=dev) for k, (N, K) in SHAPES.items() if k in ("o", "down")}
+        L["w_in"] = synth.int4_weights(N_WIN, H, gen, device=dev)
+        L["qkv"] = tuple(t[:NQKV] for t in L["w_in"])
+        L["gate_up"] = tuple(t[NQKV:] for t in L["w_in"])
+        layers.append(L)
     x = torch.randn(H, device=dev, generator=gen).half()
     ob = torch.randn(H, device=dev, generator=gen).half()
     y_qkv = torch.empty(NQKV, device=dev, dtype=torch.float16)
@@ -198,14 +211,9 @@ def main():
     act = torch.empty(INTER, device=dev, dtype=torch.float16)
     y_d = torch.empty(H, device=dev, dtype=torch.float16)
 
-    def silu_mul():
-        HL.check(HL.lib().rk_silu_mul(HL.ptr(y_gu), HL.ptr(act), HL.F16, INTER, HL.stream(dev)))
-
     def step_fns(L):
-        return [lambda: cuda_gemv.gemv_int4_cuda(x, *L["qkv"], out=y_qkv),
+        return [lambda: cuda_gemv.gemv_int4_silu_cuda(x, *L["w_in"], NQKV, out=y_qkv, act=act),
                 lambda: cuda_gemv.gemv_int4_cuda(ob, *L["o"], out=y_o),
-                lambda: cuda_gemv.gemv_int4_cuda(x, *L["gate_up"], out=y_gu),
-                silu_mul,
                 lambda: cuda_gemv.gemv_int4_cuda(act, *L["down"], out=y_d)]
 
     graphs = [graph_of(step_fns(L)) for L in layers]
@@ -233,12 +241,17 @@ def main():
         us = time_graph_us(g, N_COPIES)
         proj[k] = {"N": N, "K": K, "us": round(us, 2), "GB_s": round(int4_bytes(N, K) / us / 1e3, 1)}
         del g
+    g = graph_of([lambda L=L: cuda_gemv.gemv_int4_silu_cuda(x, *L["w_in"], NQKV, out=y_qkv, act=act)
+                  for L in layers])
+    win_us = time_graph_us(g, N_COPIES)
+    del g
+    proj["w_in_silu"] = {"N": N_WIN, "K": H, "us": round(win_us, 2), "GB_s": round(WIN_BYTES / win_us / 1e3, 1)}
     log(f"[bench] projections: {proj}")
-    gu_us = proj["gate_up"]["us"]
-    achieved = int4_bytes(*SHAPES["gate_up"]) / gu_us / 1e3
+    achieved = WIN_BYTES / win_us / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": load_traffic(),
-                "kernel": "gemv int4 g128, gate+up N=22016 K=2048", "us_per_launch": gu_us}
+                "kernel": "gemv int4 g128 w_in [qkv | gate | up] N=25088 K=2048 + SiLU*up epilogue",
+                "us_per_launch": round(win_us, 2)}
     del graphs
     del layers
     torch.cuda.empty_cache()
@@ -298,7 +311,8 @@ def main():
         "dtype": "int4 weights x fp16 activations, fp32 accumulate",
         "data": "synthetic (seeded int4 g128 codes / fp16 scale+min, x ~ N(0,1)); 16 distinct weight copies",
         "config": {"workload": "config 1: one decoder layer's decode projections (qkv 3072x2048, o 2048x2048, "
-                               "gate+up 22016x2048 + SiLU*up, down 2048x11008), batch 1",
+                               "gate+up 22016x2048 + SiLU*up, down 2048x11008), batch 1; qkv and gate+up run as "
+                               "the reference engine's one w_in projection with SiLU*up fused: 3 launches",
                    "bytes_per_step": step_bytes, "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2)},
         "roofline": roofline,
         "cpu_baseline": cpu,

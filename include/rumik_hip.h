@@ -72,6 +72,16 @@ int rk_gemv_int4_g128_valu(const void* x, int x_dtype, const uint8_t* q, const u
                            const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
                            rk_stream_t stream);
 
+/* The engine's input projection with the MLP activation fused (decode glue): q holds n_plain ordinary rows,
+ * then `inter` gate rows, then `inter` up rows (the reference's w_in = [q | k | v | gate | up], engine/
+ * rumik_int4.py:97), all int4 g128 over one x. Writes y[0 .. n_plain) and act[c] = silu(gate_c) * up_c for
+ * c < inter, with gate and up rounded to y_dtype first -- exactly what the GEMV followed by the SiLU·up part of
+ * post (reference engine/fused.py:44-84; rk_silu_mul here) produce, in one launch instead of two. Matrix-core
+ * kernel; y may be NULL when n_plain == 0. Same x / q / dtype / alignment rules as rk_gemv_int4_g128_mfma. */
+int rk_gemv_int4_g128_silu(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                           const uint16_t* min, void* y, void* act, int y_dtype, int n_plain, int inter, int K,
+                           int waves, rk_stream_t stream);
+
 /* Batch-1 int8 per-row GEMV: y[n] = scale[n] * sum_k code[n,k] * x[k], fp32 accumulate.
  * Replaces gemv_int8_cuda(x, q, s, out) -> gemv_int8 (reference kernels/cuda_gemv.py:245-249, :188-195).
  * q_kind: RK_Q_S8 or RK_Q_U8; scale dtype RK_F16 or RK_F32; y dtype RK_F32 / RK_BF16 / RK_F16.

@@ -222,13 +222,26 @@ RK_DEV void compute_batch(const Batch& b, const uint4* frag, const float* xsum, 
     }
 }
 
-// 3 waves per SIMD (<= 168 VGPRs): the 688 blocks of the gate+up projection are all resident at once
-template <int KS, bool VEC_SM, bool XREG>
+// the value an output of dtype dt holds for v (what a later kernel reading it back would see)
+RK_DEV float round_as(int dt, float v) {
+    if (dt == RK_F16) return f16_bits_to_f32(f32_to_f16_bits(v));
+    if (dt == RK_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+    return v;
+}
+
+// Rows: the first `plain` rows of the matrix are ordinary outputs y[r]; with inter > 0 they are followed by
+// `inter` gate rows and `inter` up rows, and tile plain_tiles + t holds gate rows 8t .. 8t+7 in its rows 0..7 and
+// the matching up rows in rows 8..15, so its epilogue writes act[8t + j] = silu(gate) * up (the gate and up values
+// rounded to ydt first, as a separate SiLU kernel reading them back would see them).
+// 3 waves per SIMD (<= 168 VGPRs): the 688 blocks of the gate+up projection are all resident at once.
+// PAIRED: the instance with gate / up tiles (a kernel of its own, so profiles tell the two launches apart).
+template <int KS, bool VEC_SM, bool XREG, bool PAIRED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemv_int4_mfma_kernel(const void* __restrict__ x, int xdt,
                                                               const uint8_t* __restrict__ q,
                                                               const uint16_t* __restrict__ sc,
                                                               const uint16_t* __restrict__ mn,
-                                                              void* __restrict__ y, int ydt, int N, int K) {
+                                                              void* __restrict__ y, int ydt, int plain, int inter,
+                                                              void* __restrict__ act, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int NG = K >> 7;
     uint4* frag = reinterpret_cast<uint4*>(smem);
@@ -240,7 +253,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
     const int teams = blockDim.x / (64 * KS);
     const int tile = blockIdx.x * teams + team;
     const int j = lane & 15, s = lane >> 4;
-    const int row = min(tile * 16 + j, N - 1);  // rows past N re-read the last row; never stored
+    const int plain_tiles = (plain + 15) / 16;
+    const bool paired = PAIRED && tile >= plain_tiles;  // wave-uniform
+    const int pc = min(8 * (tile - plain_tiles) + (j & 7), inter - 1);  // channel of a paired tile's row j
+    // rows past the end re-read the last row of their part; never stored
+    const int row = !paired ? min(tile * 16 + j, plain - 1) : plain + (j < 8 ? pc : inter + pc);
     const int gpw = (NG + KS - 1) / KS;         // groups per wave
     const int g0 = kw * gpw, g1 = min(NG, g0 + gpw);
     const uint8_t* qrow = q + (size_t)row * (size_t)(K >> 1) + 16 * s;
@@ -271,9 +288,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
     }
 
     // ---- combine the KS partial sums of the tile, lanes 0..15 store their row
+    auto out = [&](float v) {  // lanes 0..15 of one wave, all active
+        if (!paired) {
+            const int r = tile * 16 + j;
+            if (r < plain) store_act(y, ydt, (size_t)r, v);
+        } else {
+            const float u = round_as(ydt, __shfl_down(v, 8, 16));  // up row j + 8 -> lane j
+            const float g = round_as(ydt, v);
+            const int c = 8 * (tile - plain_tiles) + j;
+            if (j < 8 && c < inter) store_act(act, ydt, (size_t)c, g / (1.0f + __expf(-g)) * u);
+        }
+    };
     if constexpr (KS == 1) {
-        const int r = tile * 16 + j;
-        if (lane < 16 && r < N) store_act(y, ydt, (size_t)r, acc);
+        if (lane < 16) out(acc);
     } else {
         if (lane < 16) red[wave * 16 + lane] = acc;
         __syncthreads();
@@ -281,25 +308,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
             float v = 0.f;
 #pragma unroll
             for (int k = 0; k < KS; ++k) v += red[(team * KS + k) * 16 + lane];
-            const int r = tile * 16 + j;
-            if (r < N) store_act(y, ydt, (size_t)r, v);
+            out(v);
         }
     }
 }
 
 template <int KS, bool VEC>
 hipError_t launch_mfma(const void* x, int xdt, const uint8_t* q, const uint16_t* s, const uint16_t* m, void* y,
-                       int ydt, int N, int K, int teams, hipStream_t st) {
-    const int tiles = (N + 15) / 16;
+                       int ydt, int plain, int inter, void* act, int K, int teams, hipStream_t st) {
+    const int tiles = (plain + 15) / 16 + (inter + 7) / 8;
     const int blocks = (tiles + teams - 1) / teams;
     const int threads = 64 * KS * teams;
     const size_t lds = (size_t)K * 2 + (size_t)(K / 128) * 4 + (size_t)teams * KS * 16 * 4;
-    if (K / 8 <= kXPre * threads)
-        hipLaunchKernelGGL((gemv_int4_mfma_kernel<KS, VEC, true>), dim3(blocks), dim3(threads), lds, st, x, xdt, q, s,
-                           m, y, ydt, N, K);
-    else
-        hipLaunchKernelGGL((gemv_int4_mfma_kernel<KS, VEC, false>), dim3(blocks), dim3(threads), lds, st, x, xdt, q,
-                           s, m, y, ydt, N, K);
+#define RK_LAUNCH(XR, PR)                                                                                          \
+    hipLaunchKernelGGL((gemv_int4_mfma_kernel<KS, VEC, XR, PR>), dim3(blocks), dim3(threads), lds, st, x, xdt, q, s, \
+                       m, y, ydt, plain, inter, act, K)
+    const bool xreg = K / 8 <= kXPre * threads;
+    if (inter > 0) {
+        if (xreg) RK_LAUNCH(true, true); else RK_LAUNCH(false, true);
+    } else {
+        if (xreg) RK_LAUNCH(true, false); else RK_LAUNCH(false, false);
+    }
+#undef RK_LAUNCH
     return hipGetLastError();
 }
 
@@ -308,8 +338,8 @@ hipError_t launch_mfma(const void* x, int xdt, const uint8_t* q, const uint16_t*
 // KS (waves per 16-row tile) and teams (tiles per block) for one call; blocks are 4 waves (KS * teams = 4, or
 // the caller's `waves` when that is smaller). Default KS: enough waves for about two per SIMD of the 256 CUs
 // (tiles * KS >= 2048), at most one group per wave.
-static void plan_mfma(int N, int K, int waves, int* ks_out, int* teams_out) {
-    const int NG = K / 128, tiles = (N + 15) / 16;
+static void plan_mfma(int tiles, int K, int waves, int* ks_out, int* teams_out) {
+    const int NG = K / 128;
     const int w = waves ? waves : 4;
     int ks = 1;
     while (ks < w && ks * 2 <= NG && tiles * ks < 2048) ks *= 2;
@@ -317,11 +347,9 @@ static void plan_mfma(int N, int K, int waves, int* ks_out, int* teams_out) {
     *teams_out = w / ks;
 }
 
-extern "C" int rk_gemv_int4_mfma_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
-                                      const uint16_t* min, void* y, int y_dtype, int N, int K, int waves,
-                                      rk_stream_t stream) {
-    if (!x || !q || !scale || !min || !y) return RK_ERR_NULL;
-    if (N <= 0 || K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
+static int gemv_mfma_run(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale, const uint16_t* min,
+                         void* y, int y_dtype, int plain, int inter, void* act, int K, int waves, hipStream_t s) {
+    if (K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
     if (x_dtype != RK_F16 && x_dtype != RK_BF16) return RK_ERR_DTYPE;
     if (y_dtype != RK_F16 && y_dtype != RK_BF16 && y_dtype != RK_F32) return RK_ERR_DTYPE;
     if (((uintptr_t)x & 15) || ((uintptr_t)q & 15)) return RK_ERR_ALIGN;
@@ -329,16 +357,15 @@ extern "C" int rk_gemv_int4_mfma_impl(const void* x, int x_dtype, const uint8_t*
     if (waves > 4) waves = 4;  // blocks hold at most 4 waves here (each may use up to 168 VGPRs)
     if ((size_t)K * 2 + (size_t)(K / 128) * 4 + 16 * 16 * 4 > 160 * 1024) return RK_ERR_SHAPE;  // x must fit in LDS
     int ks, teams;
-    plan_mfma(N, K, waves, &ks, &teams);
+    plan_mfma((plain + 15) / 16 + (inter + 7) / 8, K, waves, &ks, &teams);
     const int NG = K / 128;
     // 16-byte scale / min loads need 16-byte aligned rows and batch starts
     const bool vec = NG % 8 == 0 && ((NG + ks - 1) / ks) % 8 == 0 && !((uintptr_t)scale & 15) && !((uintptr_t)min & 15);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t e;
 #define RK_KS(KK)                                                                                                  \
     case KK:                                                                                                       \
-        e = vec ? launch_mfma<KK, true>(x, x_dtype, q, scale, min, y, y_dtype, N, K, teams, s)                     \
-                : launch_mfma<KK, false>(x, x_dtype, q, scale, min, y, y_dtype, N, K, teams, s);                   \
+        e = vec ? launch_mfma<KK, true>(x, x_dtype, q, scale, min, y, y_dtype, plain, inter, act, K, teams, s)     \
+                : launch_mfma<KK, false>(x, x_dtype, q, scale, min, y, y_dtype, plain, inter, act, K, teams, s);   \
         break;
     switch (ks) {
         RK_KS(1) RK_KS(2) RK_KS(4)
@@ -346,4 +373,22 @@ extern "C" int rk_gemv_int4_mfma_impl(const void* x, int x_dtype, const uint8_t*
     }
 #undef RK_KS
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+
+extern "C" int rk_gemv_int4_mfma_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                                      const uint16_t* min, void* y, int y_dtype, int N, int K, int waves,
+                                      rk_stream_t stream) {
+    if (!x || !q || !scale || !min || !y) return RK_ERR_NULL;
+    if (N <= 0) return RK_ERR_SHAPE;
+    return gemv_mfma_run(x, x_dtype, q, scale, min, y, y_dtype, N, 0, nullptr, K, waves,
+                         reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int rk_gemv_int4_g128_silu(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                                      const uint16_t* min, void* y, void* act, int y_dtype, int n_plain, int inter,
+                                      int K, int waves, rk_stream_t stream) {
+    if (!x || !q || !scale || !min || !act || (n_plain > 0 && !y)) return RK_ERR_NULL;
+    if (n_plain < 0 || inter <= 0) return RK_ERR_SHAPE;
+    return gemv_mfma_run(x, x_dtype, q, scale, min, y, y_dtype, n_plain, inter, act, K, waves,
+                         reinterpret_cast<hipStream_t>(stream));
 }

@@ -53,6 +53,30 @@ def gemv_int4_cuda(x, q, s, m, out=None, warps=None, rows=None):
     return y
 
 
+def gemv_int4_silu_cuda(x, q, s, m, n_plain, out=None, act=None):
+    """The engine's w_in projection with SiLU(gate) * up fused: q = [n_plain rows | inter gate rows | inter up rows]
+    (int4 g128) -> (y [n_plain] or None, act [inter]), equal to gemv_int4_cuda followed by act = silu(g) * u on the
+    rounded outputs (the MLP part of the reference's post, engine/fused.py:44-84). Outputs in x's dtype by default."""
+    if q.dim() != 2 or q.dtype != torch.uint8 or n_plain < 0 or q.shape[0] <= n_plain or (q.shape[0] - n_plain) % 2:
+        raise RuntimeError("shape")
+    N, K = q.shape[0], q.shape[1] * 2
+    inter = (N - n_plain) // 2
+    a = act if act is not None else torch.empty(inter, device=x.device, dtype=x.dtype)
+    y = out if out is not None else (torch.empty(n_plain, device=x.device, dtype=a.dtype) if n_plain else None)
+    H.require_gpu(x, q, s, m, a, y)
+    if K % G or x.numel() != K or a.numel() < inter or (n_plain and (y.numel() < n_plain or y.dtype != a.dtype)):
+        raise RuntimeError("shape")
+    if s.dtype != torch.float16 or m.dtype != torch.float16 or s.numel() != N * (K // G) or m.numel() != N * (K // G):
+        raise RuntimeError("shape")
+    for t in (x, q, s, m, a) + ((y,) if y is not None else ()):
+        if not t.is_contiguous():
+            raise RuntimeError("shape")
+    st = H.lib().rk_gemv_int4_g128_silu(H.ptr(x), H.dt(x), H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(y), H.ptr(a),
+                                        H.dt(a), n_plain, inter, K, 0, H.stream(x.device))
+    H.check(st)
+    return y, a
+
+
 def quantize_int8_rows(w, pad_to=16):
     """[N, K] -> (uint8 [N', K] = int8 + 128, fp32 scale [N']), rows zero-padded to a multiple of pad_to.
     Symmetric per row: w ~ (q - 128) * scale, scale = max|w| / 127 (reference kernels/cuda_gemv.py:234-242)."""

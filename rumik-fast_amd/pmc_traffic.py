@@ -1,10 +1,11 @@
 #!/usr/bin/env python3
-"""HBM traffic per launch of the gate+up int4 GEMV (N=22016, K=2048), from rocprofv3 hardware counters.
+"""HBM traffic per launch of the fused w_in int4 GEMV + SiLU*up (rows [qkv 3072 | gate 11008 | up 11008], K=2048;
+the dominant kernel of bench.py's step), from rocprofv3 hardware counters.
 
 Two steps:
 
     run        launches a plain elementwise copy of known size (torch.neg over 256 MiB fp16: reads and writes
-               268,435,456 B each) and then the gate+up GEMV over 16 rotated weight copies, eagerly, one dispatch
+               268,435,456 B each) and then the fused w_in GEMV over 16 rotated weight copies, eagerly, one dispatch
                each. Run it under `rocprofv3 --pmc FETCH_SIZE` and again under `rocprofv3 --pmc WRITE_SIZE`.
     summarize  reads the two counter-collection CSVs, scales each counter by what it reads for the copy kernel
                (counter KiB * 1024 / known bytes), and writes profiles/traffic.json (read by bench.py) plus a
@@ -26,9 +27,11 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent.parent
 COPY_BYTES = 256 << 20
-N, K = 22016, 2048
-GEMV_BYTES = N * K // 2 + 4 * N * (K // 128) + 2 * K + 2 * N
+N_PLAIN, INTER, K = 3072, 11008, 2048
+N = N_PLAIN + 2 * INTER
+GEMV_BYTES = N * K // 2 + 4 * N * (K // 128) + 2 * K + 2 * (N_PLAIN + INTER)  # outputs: y [3072] and act [11008]
 N_COPIES = 16
+KEY = "gemv_int4_w_in_silu_25088x2048"
 
 
 def run():
@@ -42,14 +45,15 @@ def run():
     gen = synth.generator(1, "cuda")
     mats = [synth.int4_weights(N, K, gen, device=dev) for _ in range(N_COPIES)]
     x = torch.randn(K, device=dev, generator=gen).half()
-    y = torch.empty(N, device=dev, dtype=torch.float16)
+    y = torch.empty(N_PLAIN, device=dev, dtype=torch.float16)
+    act = torch.empty(INTER, device=dev, dtype=torch.float16)
     torch.cuda.synchronize()
     for _ in range(4):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
     for _ in range(2):
         for w in mats:
-            cuda_gemv.gemv_int4_cuda(x, *w, out=y)
+            cuda_gemv.gemv_int4_silu_cuda(x, *w, N_PLAIN, out=y, act=act)
     torch.cuda.synchronize()
     print("pmc_traffic: run done", flush=True)
 
@@ -88,17 +92,17 @@ def summarize(fetch_dir, write_dir):
     kw = w_copy * 1024 / COPY_BYTES
     fetch_b = f_gemv * 1024 / kf
     write_b = w_gemv * 1024 / kw
-    rec = {"gemv_int4_gate_up_22016x2048": {
+    rec = {KEY: {
         "traffic_bytes": round(fetch_b + write_b), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
         "algorithmic_bytes": GEMV_BYTES, "fetch_scale": round(kf, 4), "write_scale": round(kw, 4),
         "dispatches": {"copy_fetch": nfc, "copy_write": nwc, "gemv_fetch": nfg, "gemv_write": nwg}}}
     (ROOT / "profiles" / "traffic.json").write_text(json.dumps(rec, indent=1) + "\n")
-    r = rec["gemv_int4_gate_up_22016x2048"]
+    r = rec[KEY]
     print("| quantity | value |\n|---|---|")
     print(f"| copy kernel (torch.neg, 256 MiB fp16) FETCH_SIZE / dispatch | {f_copy:.0f} KiB (scale {kf:.4f}) |")
     print(f"| copy kernel WRITE_SIZE / dispatch | {w_copy:.0f} KiB (scale {kw:.4f}) |")
-    print(f"| gate+up GEMV FETCH_SIZE / dispatch | {f_gemv:.0f} KiB -> {fetch_b:,.0f} B |")
-    print(f"| gate+up GEMV WRITE_SIZE / dispatch | {w_gemv:.0f} KiB -> {write_b:,.0f} B |")
+    print(f"| w_in GEMV + SiLU FETCH_SIZE / dispatch | {f_gemv:.0f} KiB -> {fetch_b:,.0f} B |")
+    print(f"| w_in GEMV + SiLU WRITE_SIZE / dispatch | {w_gemv:.0f} KiB -> {write_b:,.0f} B |")
     print(f"| traffic / launch (scaled) | {r['traffic_bytes']:,} B |")
     print(f"| algorithmic bytes / launch | {GEMV_BYTES:,} B (traffic / algorithmic = "
           f"{r['traffic_bytes'] / GEMV_BYTES:.3f}) |")

@@ -182,3 +182,69 @@ def test_graph_capture_replays(dev):
         g.replay()
         torch.cuda.synchronize()
         _assert_parity(y, _oracle(x.cpu(), q.cpu(), s.cpu(), m.cpu()), f"replay {i}")
+
+
+def test_silu_fused_w_in_equals_gemv_then_silu(dev):
+    """The engine's w_in shape ([q k v | gate | up] = 3072 + 2 x 11008 rows): one launch of the fused kernel gives
+    bit-for-bit the GEMV followed by the SiLU·up kernel (same tile plan, same rounding of gate and up)."""
+    n_plain, inter, K = 3072, 11008, 2048
+    x, q, s, m = (t.to(dev) for t in synth.gemv_case(n_plain + 2 * inter, K, 12))
+    y_all = cuda_gemv.gemv_int4_cuda(x, q, s, m, out=torch.empty(n_plain + 2 * inter, device=dev,
+                                                                    dtype=torch.float16))
+    act_ref = torch.empty(inter, device=dev, dtype=torch.float16)
+    H.check(H.lib().rk_silu_mul(H.ptr(y_all[n_plain:]), H.ptr(act_ref), H.F16, inter, H.stream(dev)))
+    y, act = cuda_gemv.gemv_int4_silu_cuda(x, q, s, m, n_plain)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_all[:n_plain])
+    assert torch.equal(act, act_ref)
+    _assert_parity(y, _oracle(x, q[:n_plain], s[:n_plain], m[:n_plain]), "w_in plain rows")
+
+
+@pytest.mark.parametrize("n_plain,inter,K,xdt,ydt", [(40, 100, 256, torch.bfloat16, torch.float32),
+                                                       (0, 8, 128, torch.float16, torch.float16),
+                                                       (16, 1, 2048, torch.float16, torch.bfloat16),
+                                                       (3, 37, 1152, torch.bfloat16, torch.bfloat16)])
+def test_silu_fused_ragged(n_plain, inter, K, xdt, ydt, dev):
+    """Ragged part sizes (plain rows not a multiple of 16, channels not a multiple of 8) and every dtype: y against
+    the oracle's bar, act against silu(gate) * up evaluated in fp32 on the oracle's gate / up (rounded to ydt)."""
+    N = n_plain + 2 * inter
+    x, q, s, m = synth.gemv_case(N, K, 13)
+    x = x.to(xdt)
+    xd, qd, sd, md = x.to(dev), q.to(dev), s.to(dev), m.to(dev)
+    y = torch.full((max(n_plain, 1),), 5.0, device=dev, dtype=ydt)
+    act = torch.full((inter + 3,), 5.0, device=dev, dtype=ydt)  # 3 guard values past the end
+    H.check(H.lib().rk_gemv_int4_g128_silu(H.ptr(xd), H.dt(xd), H.ptr(qd), H.ptr(sd), H.ptr(md), H.ptr(y),
+                                           H.ptr(act), H.dt(act), n_plain, inter, K, 0, H.stream(dev)))
+    torch.cuda.synchronize()
+    ref, floor = _oracle(x, q, s, m)
+    if n_plain:
+        _assert_parity(y[:n_plain], (ref[:n_plain], floor[:n_plain]), "plain rows")
+    else:
+        assert torch.all(y == 5.0)
+    g = torch.tensor(ref[n_plain:n_plain + inter], dtype=torch.float64)
+    u = torch.tensor(ref[n_plain + inter:], dtype=torch.float64)
+    sg = torch.sigmoid(g)
+    want = g * sg * u
+    # first-order bound: d(act) = silu'(g) u dg + silu(g) du (|silu'| <= 1.1), where gate / up each carry the
+    # output rounding (eps, twice: kernel vs reference may round to neighbouring values) plus the GEMV bar's
+    # absolute part (<= the per-output floor), and act its own rounding
+    eps = {torch.float32: 1e-6, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[ydt]
+    eg = 2 * eps * g.abs() + torch.tensor(floor[n_plain:n_plain + inter])
+    eu = 2 * eps * u.abs() + torch.tensor(floor[n_plain + inter:])
+    tol = 1.1 * u.abs() * eg + (g * sg).abs() * eu + 2 * eps * want.abs()
+    got = act[:inter].double().cpu()
+    assert torch.all((got - want).abs() <= tol), float(((got - want).abs() - tol).max())
+    assert torch.all(act[inter:] == 5.0)  # nothing written past inter
+
+
+def test_silu_fused_rejects_bad_arguments(dev):
+    x, q, s, m = (t.to(dev) for t in synth.gemv_case(48, 256, 14))
+    with pytest.raises(RuntimeError):
+        cuda_gemv.gemv_int4_silu_cuda(x, q, s, m, 47)  # 1 row left: not a gate / up pair
+    with pytest.raises(RuntimeError):
+        cuda_gemv.gemv_int4_silu_cuda(x, q, s, m, 48)  # no MLP rows at all
+    L = H.lib()
+    assert L.rk_gemv_int4_g128_silu(H.ptr(x), H.F16, H.ptr(q), H.ptr(s), H.ptr(m), None, H.ptr(x), H.F16, 8, 20,
+                                    256, 0, H.stream(dev)) == -4  # y missing while n_plain > 0
+    assert L.rk_gemv_int4_g128_silu(H.ptr(x), H.F16, H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(x), H.ptr(x), H.F16, 8, 0,
+                                    256, 0, H.stream(dev)) == -1

@@ -248,9 +248,12 @@ struct Int4Plan {
 
 static int plan_int4(int N, int K, int waves, int rows, Int4Plan* p) {
     const int nch = K / 32;
-    // tuned defaults: short rows (K <= 4096) are handled by one wave per row set; long rows are split over 4 waves
-    int w = waves ? waves : 4;
-    int r = rows ? rows : (nch <= 128 ? 4 : 2);
+    // tuned defaults (hipGraph-timed on MI355X, weights rotated past the MALL): short rows (K <= 4096) one wave per
+    // row set, 4 waves per block, 4 rows per wave once N >= 3072 (qkv 3072 x 2048: 3.45 us) and 2 below, so the
+    // 2048-row o projection still fills 256 blocks (3.08 us vs 3.36 with 4 rows); long rows (down, K = 11008) 2 waves
+    // of 2 rows splitting K in two (5.79 us vs 6.25 with 4 waves)
+    int w = waves ? waves : (nch <= 128 ? 4 : 2);
+    int r = rows ? rows : (nch <= 128 ? (N >= 3072 ? 4 : 2) : 2);
     if (!(w == 1 || w == 2 || w == 4 || w == 8 || w == 16)) return RK_ERR_BLOCK;
     if (!(r == 1 || r == 2 || r == 4 || r == 8)) return RK_ERR_BLOCK;
     int ks = nch <= 128 ? 1 : 4;
@@ -262,7 +265,6 @@ static int plan_int4(int N, int K, int waves, int rows, Int4Plan* p) {
     p->rows = r;
     p->ks = ks;
     p->nj = nj;
-    (void)N;
     return RK_OK;
 }
 

@@ -215,6 +215,47 @@ int rk_decode_params_size(void);
 /* pos[0] += 1 on the device (the `self.pos += 1` of the captured step, reference engine/rumik_fused.py:120). */
 int rk_pos_advance(int64_t* pos, rk_stream_t stream);
 
+/* ---- the tail of a decode step: stop predictor + top-k + Gumbel-max sampling + counters
+ * (reference engine/sample.py; maths of RumikInt4._logits_and_stop / _pick, engine/rumik_int4.py:174-191).
+ * Keys: key = (sortable(bits(logit)) << 32) | index with sortable(b) = b ^ ((b >> 31) & 0x7FFFFFFF), sorted
+ * descending (value, then larger index first). Chunks of 512 logits, 32 survivors per chunk, top_k <= 32. */
+
+/* z1[r] = gelu(W1[r] . LayerNorm(h; lnw, lnb, eps) + b1[r]) for r < nz, exact (erf) GELU.
+ * Replaces stop_hidden[(nz // 16,)](h, lnw, lnb, w1, b1, z1, eps, H=, ROWS=16) (reference engine/sample.py:34-49).
+ * h [H] fp16/bf16/fp32; W1 [nz, H] bf16/fp16 (16-byte aligned) or fp32; lnw, lnb [H], b1 [nz], z1 [nz] fp32. */
+int rk_stop_hidden(const void* h, int h_dtype, const float* lnw, const float* lnb, const void* w1, int w1_dtype,
+                   const float* b1, float* z1, float eps, int H, int nz, rk_stream_t stream);
+
+/* keys[512c .. 512c + 512) = chunk c's keys sorted descending, c < ceil(nv / 512); logits past nv count as -inf,
+ * and index end_idx as -inf while step[0] < min_new.
+ * Replaces topk_partial[(nch,)](logits, step, keys, NV, END_IDX, MIN_NEW, CH=512) (reference sample.py:53-61).
+ * logits [nv] fp16/bf16/fp32; step int64 [1] (device); keys int64 [ceil(nv / 512) * 512]. */
+int rk_topk_partial(const void* logits, int logits_dtype, const int64_t* step, int64_t* keys, int nv, int end_idx,
+                    int min_new, rk_stream_t stream);
+
+/* Gathers the first 32 keys of each of the nch chunks (slots past nch * 32 hold -2^62), sorts the nc slots
+ * descending into scratch, samples choice = argmax_{j < topk} (value_j * inv_temp - log(-log(clamp(u_j, 1e-10, 1))))
+ * (first maximum), token = ids[index of choice]; token = end_id if (w2 . z1 + b2 > 0 and step >= min_new);
+ * out[step] = token, tok[0] = token, step[0] += 1.
+ * Replaces pick[(1,)](keys, scratch, u, z1, w2, b2, ids, step, pos, tok, out, inv_temp, END_ID, MIN_NEW, NCH,
+ * CH=512, KEEP=32, NC=, TOPK=, NZ=) (reference sample.py:65-93; pos is unused there and not taken here).
+ * nc: a power of two, nch * 32 <= nc <= 4096; 1 <= topk <= 32; u [>= topk], z1, w2 [nz], b2 [1] fp32;
+ * ids, step, tok, out int64 (device). */
+int rk_pick(const int64_t* keys, int64_t* scratch, const float* u, const float* z1, const float* w2,
+            const float* b2, const int64_t* ids, int64_t* step, int64_t* tok, int64_t* out, float inv_temp,
+            int64_t end_id, int min_new, int nch, int nc, int topk, int nz, rk_stream_t stream);
+
+/* rk_stop_hidden + rk_topk_partial + rk_pick in ONE launch (what FusedSampler.__call__ runs, reference
+ * engine/sample.py:117-127 launches the three kernels): the last block to finish its stop rows or chunk does the
+ * pick. keys / scratch / z1 as above (same contents afterwards); counter: one uint32 of device memory, zero before
+ * the first call, left at zero by every call (so a captured graph needs no reset). Calls sharing a counter must not
+ * overlap. */
+int rk_sample_tail(const void* h, int h_dtype, const float* lnw, const float* lnb, const void* w1, int w1_dtype,
+                   const float* b1, const float* w2, const float* b2, float eps, int H, int nz, const void* logits,
+                   int logits_dtype, int nv, int end_idx, const float* u, const int64_t* ids, int64_t* step,
+                   int64_t* tok, int64_t* out, float inv_temp, int64_t end_id, int min_new, int topk, int64_t* keys,
+                   int64_t* scratch, int nc, float* z1, unsigned* counter, rk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,7 +15,7 @@ F16, BF16, F32 = 0, 1, 2
 Q_S8, Q_U8 = 0, 1
 DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
 
-_p, _i, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+_p, _i, _f, _l = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
 _SIGS = {
     "rk_abi_version": ([], _i),
     "rk_status_string": ([_i], ctypes.c_char_p),
@@ -38,6 +38,11 @@ _SIGS = {
     "rk_silu_mul": ([_p, _p, _i, _i, _p], _i),
     "rk_decode_step_persistent": ([_p, _i, _p], _i),
     "rk_decode_params_size": ([], _i),
+    "rk_stop_hidden": ([_p, _i, _p, _p, _p, _i, _p, _p, _f, _i, _i, _p], _i),
+    "rk_topk_partial": ([_p, _i, _p, _p, _i, _i, _i, _p], _i),
+    "rk_pick": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _f, _l, _i, _i, _i, _i, _i, _p], _i),
+    "rk_sample_tail": ([_p, _i, _p, _p, _p, _i, _p, _p, _p, _f, _i, _i, _p, _i, _i, _i, _p, _p, _p, _p, _p, _f, _l,
+                        _i, _i, _p, _p, _i, _p, _p, _p], _i),
 }
 
 _lib = None

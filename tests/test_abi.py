@@ -107,3 +107,33 @@ def test_decode_step_validates_before_launch():
     assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 256, None) == -1
     p.inter = 11008
     assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 200, None) == -2  # nblocks != NKV * nsp
+
+
+def test_sampler_entry_points_validate_before_any_device_work():
+    """rk_stop_hidden / rk_topk_partial / rk_pick / rk_sample_tail reject bad sizes, dtypes and NULLs on the host
+    (fake, never dereferenced pointers): top_k above 32, a candidate list that is not a power of two or too small
+    or above 4096 slots, unsupported dtypes (reference pick asserts top_k <= 32, engine/sample.py:111)."""
+    lib = HL.lib()
+    P = ctypes.c_void_p(256)
+    S = None
+    # rk_pick(keys, scratch, u, z1, w2, b2, ids, step, tok, out, inv_temp, end_id, min_new, nch, nc, topk, nz, s)
+    pick = lambda nch, nc, topk, nz=512: lib.rk_pick(P, P, P, P, P, P, P, P, P, P, 1.25, 16384, 8, nch, nc, topk,  # noqa: E731
+                                                     nz, S)
+    assert pick(33, 2048, 33) == -1
+    assert pick(33, 2048, 0) == -1
+    assert pick(33, 1024, 30) == -1      # 33 * 32 candidates do not fit
+    assert pick(33, 3000, 30) == -1      # not a power of two
+    assert pick(200, 8192, 30) == -1     # above the LDS candidate list
+    assert pick(33, 2048, 30, nz=0) == -1
+    assert lib.rk_pick(None, P, P, P, P, P, P, P, P, P, 1.0, 1, 8, 33, 2048, 30, 512, S) == -4
+    assert lib.rk_topk_partial(P, 7, P, P, 16385, 16384, 8, S) == -3
+    assert lib.rk_topk_partial(P, 2, P, P, 0, 0, 8, S) == -1
+    assert lib.rk_stop_hidden(P, 1, P, P, P, 5, P, P, 1e-5, 2048, 512, S) == -3
+    assert lib.rk_stop_hidden(P, 1, P, P, P, 1, P, P, 1e-5, 0, 512, S) == -1
+    assert lib.rk_stop_hidden(P, 1, P, P, ctypes.c_void_p(258), 1, P, P, 1e-5, 2048, 512, S) == -5
+    # rk_sample_tail: same checks (nv = 16385 -> 33 chunks need nc >= 1056)
+    tail = lambda nc, topk: lib.rk_sample_tail(P, 1, P, P, P, 1, P, P, P, 1e-5, 2048, 512, P, 2, 16385, 16384, P,  # noqa: E731
+                                               P, P, P, P, 1.25, 16384, 8, topk, P, P, nc, P, P, S)
+    assert tail(1024, 30) == -1 and tail(2048, 40) == -1
+    assert lib.rk_sample_tail(P, 1, P, P, P, 1, P, P, P, 1e-5, 2048, 512, P, 2, 16385, 16384, P, P, P, P, P, 1.25,
+                              16384, 8, 30, P, P, 2048, P, None, S) == -4

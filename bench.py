@@ -17,7 +17,8 @@ roofline: the dominant kernel (the fused w_in + SiLU launch, 27,328,000 B per la
 3072 + 11008 outputs), its average launch duration measured with HIP events on its stream over back-to-back
 launches with rotated weights.
 cpu_baseline: the CPU oracle's dequantize-then-matmul of the same step (numpy fp32), on this host's cores.
-Extra fields: the per-projection kernel times, the int8 audio head (config 2) and the int4 prefill (config 3).
+Extra fields: the per-projection kernel times, the int8 audio head (config 2), the int4 prefill (config 3), the
+sampling tail, and the 36-layer decode step (config 4) with and without sampling inside the graph.
 """
 import argparse
 import json
@@ -136,6 +137,7 @@ def run_decode(dev, steps):
     the timed loop). Timed with HIP events on the engine's stream."""
     import torch
     import decode
+    import synth
     cfg = decode.Config()
     w = decode.random_weights(cfg, 4, device=dev)
     eng = decode.PersistentDecode(cfg, w, device=dev)
@@ -163,9 +165,83 @@ def run_decode(dev, steps):
         out[f"ctx{ctx}"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1),
                             "GB_s": round(nbytes * steps / dt / 1e9, 1), "bytes_per_token": nbytes}
         log(f"[bench] decode ctx {ctx}: {out[f'ctx{ctx}']}")
+    # the same step with the sampling tail inside the graph (a full token: decode, head, stop predictor, top-30,
+    # Gumbel-max pick; the sampled token is the next step's input), ctx 256
+    g = synth.generator(11, "cuda")
+    stop = {"0.weight": torch.ones(cfg.H, device=dev), "0.bias": torch.zeros(cfg.H, device=dev),
+            "1.weight": (torch.randn(512, cfg.H, device=dev, generator=g) / cfg.H ** 0.5).bfloat16(),
+            "1.bias": torch.zeros(512, device=dev), "3.weight": torch.randn(1, 512, device=dev, generator=g) / 512 ** 0.5,
+            "3.bias": torch.tensor([-5.0], device=dev)}
+    ids = torch.arange(cfg.n_audio, dtype=torch.int64) % (cfg.vocab - 1)
+    ids[-1] = cfg.vocab - 1
+    eng.attach_sampler(stop, ids, end_id=cfg.vocab - 1)
+    ctx = 256
+    eng.pos.fill_(ctx - 1)  # the capture's warm-up step needs a cache slot (the last loop left pos at S)
+    eng.capture()
+    for _ in range(10):
+        eng.pos.fill_(ctx - 1); eng.step_i.fill_(9); eng.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        eng.pos.fill_(ctx - 1); eng.step_i.fill_(9); eng.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    dt = e0.elapsed_time(e1) / 1e3
+    if eng.status_word() != 0:
+        raise RuntimeError(f"persistent decode step reported status {eng.status_word()}")
+    out["sampled_ctx256"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1)}
+    log(f"[bench] decode + sampling ctx 256: {out['sampled_ctx256']}")
     del eng, w
     torch.cuda.empty_cache()
     return out
+
+
+def run_sampler(dev):
+    """The sampling tail alone (reference engine/sample.py at the model's sizes: hidden 2048, stop predictor 512 x 2048
+    bf16, 16385 audio logits fp32, top-30): the one-launch FusedSampler call (with its torch.rand) and the
+    reference's three-kernel sequence, each as hipGraph replays."""
+    import types
+    import torch
+    import sample
+    import synth
+    g = synth.generator(12, "cuda")
+    n, H, NZ = 16385, 2048, 512
+    stop = {"0.weight": torch.ones(H, device=dev), "0.bias": torch.zeros(H, device=dev),
+            "1.weight": (torch.randn(NZ, H, device=dev, generator=g) / H ** 0.5).bfloat16(),
+            "1.bias": torch.zeros(NZ, device=dev), "3.weight": torch.randn(1, NZ, device=dev, generator=g) / NZ ** 0.5,
+            "3.bias": torch.tensor([-5.0], device=dev)}
+    e = types.SimpleNamespace(dev=dev, H=H, hn=torch.randn(H, device=dev, generator=g).bfloat16(), stop=stop,
+                              audio_ids=torch.arange(n, dtype=torch.int64, device=dev), end_id=n - 1, top_k=30,
+                              min_new=8, temperature=0.8, step_i=torch.zeros(1, dtype=torch.int64, device=dev),
+                              pos=torch.zeros(1, dtype=torch.int64, device=dev),
+                              tok=torch.zeros(1, dtype=torch.int64, device=dev),
+                              out=torch.zeros(4096, dtype=torch.int64, device=dev))
+    logits = torch.randn(n, device=dev, generator=g) * 3
+    smp = sample.FusedSampler(e, lambda: logits)
+
+    def three():
+        torch.rand(32, device=dev, out=smp.u)
+        sample.stop_hidden(e.hn, smp.lnw, smp.lnb, smp.w1, smp.b1, smp.z1, 1e-5)
+        sample.topk_partial(logits, e.step_i, smp.keys, smp.nv, smp.end_idx, e.min_new)
+        sample.pick(smp.keys, smp.scratch, smp.u, smp.z1, smp.w2, smp.b2, e.audio_ids, e.step_i, e.pos, e.tok, e.out,
+                    1.0 / e.temperature, e.end_id, e.min_new, smp.nch, NC=smp.nc, TOPK=e.top_k)
+
+    res = {"nv": n, "nz": NZ, "H": H, "top_k": 30}
+    for name, fn in (("fused_us", smp), ("three_kernel_us", three)):
+        reps = 20
+        e.step_i.fill_(0)
+        gr = graph_of([fn] * reps)
+        e.step_i.fill_(0)
+        res[name] = round(time_graph_us(gr, reps, reps=5, trials=5), 2)
+        e.step_i.fill_(0)
+        del gr
+    # algorithmic bytes of the fused call: W1 (bf16) + logits + hn + the stop predictor's fp32 vectors
+    nbytes = NZ * H * 2 + n * 4 + H * 2 + (2 * H + 2 * NZ + 1) * 4
+    res["bytes"] = nbytes
+    res["GB_s"] = round(nbytes / res["fused_us"] / 1e3, 1)
+    log(f"[bench] sampler: {res}")
+    return res
 
 
 def main():
@@ -290,6 +366,9 @@ def main():
         torch.cuda.empty_cache()
     log(f"[bench] prefill: {prefill}")
 
+    # ---- the sampling tail (stop predictor + top-30 + Gumbel-max pick + counters)
+    sampler_res = run_sampler(dev)
+
     # ---- config 4: the full 36-layer decode step, hipGraph replays at ctx 256 / 1024 / 2048
     decode_res = run_decode(dev, args.decode_steps) if args.decode_steps > 0 else None
 
@@ -319,6 +398,7 @@ def main():
         "projections": proj,
         "int8_head": head,
         "prefill": prefill,
+        "sampler": sampler_res,
         "decode": decode_res,
     }
     print(json.dumps(rec), flush=True)

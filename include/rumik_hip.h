@@ -205,6 +205,7 @@ typedef struct rk_decode_params {
     unsigned long long* tml; /* [NH, nsp, 2] */
     unsigned* ctr;          /* [nblocks] step counters */
     unsigned* status;
+    uint16_t* hn;           /* [2048] fp16 final LayerNorm output (the sampler's input), or NULL */
 } rk_decode_params;
 
 int rk_decode_step_persistent(const rk_decode_params* params, int nblocks, rk_stream_t stream);
@@ -233,13 +234,15 @@ int rk_stop_hidden(const void* h, int h_dtype, const float* lnw, const float* ln
 int rk_topk_partial(const void* logits, int logits_dtype, const int64_t* step, int64_t* keys, int nv, int end_idx,
                     int min_new, rk_stream_t stream);
 
-/* Gathers the first 32 keys of each of the nch chunks (slots past nch * 32 hold -2^62), sorts the nc slots
- * descending into scratch, samples choice = argmax_{j < topk} (value_j * inv_temp - log(-log(clamp(u_j, 1e-10, 1))))
+/* Selects the top 32 of the nch chunks' top-32 lists into scratch[0 .. 32) in descending key order (the rest of
+ * scratch is not written; the reference sorts all nc slots, of which its pick and sampler check read the first
+ * top_k), samples choice = argmax_{j < topk} (value_j * inv_temp - log(-log(clamp(u_j, 1e-10, 1))))
  * (first maximum), token = ids[index of choice]; token = end_id if (w2 . z1 + b2 > 0 and step >= min_new);
  * out[step] = token, tok[0] = token, step[0] += 1.
  * Replaces pick[(1,)](keys, scratch, u, z1, w2, b2, ids, step, pos, tok, out, inv_temp, END_ID, MIN_NEW, NCH,
  * CH=512, KEEP=32, NC=, TOPK=, NZ=) (reference sample.py:65-93; pos is unused there and not taken here).
- * nc: a power of two, nch * 32 <= nc <= 4096; 1 <= topk <= 32; u [>= topk], z1, w2 [nz], b2 [1] fp32;
+ * nc (the reference's candidate-list length): a power of two, nch * 32 <= nc <= 4096 (so nch <= 128);
+ * 1 <= topk <= 32; u [>= topk], z1, w2 [nz], b2 [1] fp32;
  * ids, step, tok, out int64 (device). */
 int rk_pick(const int64_t* keys, int64_t* scratch, const float* u, const float* z1, const float* w2,
             const float* b2, const int64_t* ids, int64_t* step, int64_t* tok, int64_t* out, float inv_temp,

@@ -13,7 +13,7 @@ extern "C" int rk_gemv_int8_rows_impl(const void* x, int x_dtype, const void* q,
 
 extern "C" {
 
-int rk_abi_version(void) { return 3; }
+int rk_abi_version(void) { return 4; }
 
 const char* rk_status_string(int status) {
     switch (status) {

@@ -1035,6 +1035,8 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
     __syncthreads();                                          // H0
     ln_apply_pairs(S);
     __syncthreads();                                          // H1
+    if (p.hn && blockIdx.x == 0)  // the final hidden state (the sampler's stop predictor reads it)
+        for (int i = lane; i < kH / 8; i += 64) reinterpret_cast<uint4*>(p.hn)[i] = S.vecp[i];
 }
 
 template <int REP>

@@ -8,16 +8,26 @@
 //
 // Top-k ordering (the reference's, sample.py:7-11): each logit and its index are one int64 key,
 //   key = sortable(bits(x)) << 32 | index,  sortable(b) = b ^ ((b >> 31) & 0x7FFFFFFF)
-// so sorting keys sorts values (monotonic also for -inf) and breaks ties by the larger index. Stage 1 sorts each
-// chunk of 512 keys (descending) in LDS with a bitonic network; stage 2 gathers the first 32 of every chunk, sorts
-// them and samples from the first top_k.
+// so key order is value order (monotonic also for -inf) with ties broken by the larger index; keys are unique.
+// Stage 1: one wave per chunk of 512 logits sorts the chunk with a bitonic network held in registers (8 keys per
+// lane, element lane * 8 + e): the 24 stages with partner distance < 8 stay inside a lane, the 21 others exchange
+// all 8 keys of a lane with one partner lane (16 independent 32-bit shuffles per stage). Stage 2: the chunks' top-32
+// lists are merged pairwise in a tree, one wave per merge (a 32-key list and the other reversed form a bitonic
+// sequence of 64, one key per lane; 6 shuffle stages keep the top 32 in order), 16 waves per level. An LDS bitonic
+// sort of the whole chunk / candidate list (what the Triton code's tl.sort does) measured ~1 us per network stage
+// here (98 us per call); a 64-step radix bisection over ballots 48 us; 32 rounds of a 64-bit wave maximum 34 us.
 //
-// Entry points: the reference's three kernels one to one (rk_stop_hidden, rk_topk_partial, rk_pick; buffers and
-// their contents as the reference's: keys = every chunk sorted, scratch = the sorted candidate list), and
-// rk_sample_tail, the same work in ONE launch: blocks [0, nzb) compute the stop predictor's hidden layer, blocks
-// [nzb, nzb + nch) sort one chunk each; every block then bumps a completion counter (release fence + device-scope
-// atomic) and the last block to arrive does the pick (acquire fence first). No block waits for another, so the
-// grid needs no co-residency, and the last block resets the counter, so replays need no memset.
+// Buffers: keys[512c .. 512c + 512) = chunk c sorted in key order (the reference's contents) and scratch[0 .. 32) =
+// the global top 32 in key order, which is what the reference's pick and its sampler check read of the candidate
+// list (sample.py:69-72, check_sample.py:44); the rest of scratch is not written.
+//
+// Entry points: the reference's three kernels one to one (rk_stop_hidden, rk_topk_partial, rk_pick), and
+// rk_sample_tail, the same work in ONE launch: blocks [0, nzb) compute the stop predictor's hidden layer, the next
+// blocks sort one chunk each (wave 0); every block then bumps a completion counter and the last block to arrive
+// does the pick. The exchanged results (keys, z1) are stored and read at agent scope and each block's stores are
+// acknowledged before its count goes up (a device-scope __threadfence per wave writes back L2 and measured 3x
+// slower here). No block waits for another, so the grid needs no co-residency, and the last block resets the
+// counter, so replays need no memset.
 #include <algorithm>
 
 #include "common.h"
@@ -26,9 +36,11 @@ namespace {
 
 constexpr int kCH = 512;       // logits per chunk (reference CH)
 constexpr int kKeep = 32;      // survivors per chunk (reference KEEP, >= top_k)
-constexpr int kMaxNC = 4096;   // candidate slots of the pick (32 KB of LDS)
-constexpr int kStopRows = 4;   // stop-predictor rows per block (one per wave)
-constexpr int kThreads = 256;
+constexpr int kMaxNC = 4096;   // candidate slots of the pick (at most 128 chunks)
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kStopRows = kWaves;  // stop-predictor rows per block (one per wave)
+constexpr int kChunksPerBlock = 1;  // stage 1: wave 0 of a block per chunk (one sort per SIMD: the network is VALU-bound)
 
 RK_DEV int32_t sortable(float x) {
     const int32_t b = __builtin_bit_cast(int32_t, x);
@@ -39,24 +51,88 @@ RK_DEV int64_t make_key(float x, int i) {
     return (int64_t)(((uint64_t)(uint32_t)sortable(x) << 32) | (uint64_t)(uint32_t)i);
 }
 
-// descending bitonic sort of n (a power of two) keys in LDS by the whole block
-RK_DEV void bitonic_desc(int64_t* s, int n) {
-    for (int k = 2; k <= n; k <<= 1) {
+constexpr int64_t kPad = -(int64_t(1) << 62);  // below every real key (the reference's padding value)
+
+// Results another block of the same launch reads (rk_sample_tail) are stored and loaded at agent scope (coherent
+// across the XCDs' L2s, no cache-wide fence needed): the writer waits for its stores' acknowledgements before the
+// block's count goes up, and the last block reads them with agent-scope loads.
+RK_DEV void st_agent(int64_t* p, int64_t v) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), (uint64_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+RK_DEV int64_t ld_agent(const int64_t* p) {
+    return (int64_t)__hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<int64_t*>(p)), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+}
+RK_DEV void st_agent(float* p, float v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+RK_DEV float ld_agent(const float* p) {
+    return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+RK_DEV int64_t shfl_xor64(int64_t v, int m) {
+    const int lo = __shfl_xor((int)(uint32_t)v, m), hi = __shfl_xor((int)(v >> 32), m);
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// one wave sorts the 512 keys of chunk c (element lane * 8 + e) descending and stores them to out[0 .. 512)
+RK_DEV void chunk_sort(const void* logits, int ldt, bool early, int nv, int end_idx, int c, int64_t* out) {
+    const int lane = threadIdx.x & 63;
+    int64_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int i = c * kCH + lane * 8 + e;
+        float x = i < nv ? load_act(logits, ldt, (size_t)i) : -INFINITY;
+        if (early && i == end_idx) x = -INFINITY;  // no </audio> during the first min_new tokens
+        v[e] = make_key(x, i);
+    }
+#pragma unroll
+    for (int k = 2; k <= kCH; k <<= 1) {
+#pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < n; i += blockDim.x) {
-                const int p = i ^ j;
-                if (p > i) {
-                    const int64_t a = s[i], b = s[p];
-                    const bool desc = (i & k) == 0;  // this half of the k-block runs descending
-                    if (desc ? a < b : a > b) {
-                        s[i] = b;
-                        s[p] = a;
+            if (j < 8) {  // partners inside the lane
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int pe = e ^ j;
+                    if (pe > e) {
+                        const bool desc = ((lane * 8 + e) & k) == 0;
+                        const int64_t a = v[e], b = v[pe];
+                        const bool sw = desc ? a < b : a > b;
+                        v[e] = sw ? b : a;
+                        v[pe] = sw ? a : b;
                     }
                 }
+            } else {  // partner lane: lane ^ (j / 8), same slot
+                const int m = j >> 3;
+                const bool lower = (lane & m) == 0;  // this lane holds the lower element of each pair
+                const bool desc = ((lane * 8) & k) == 0;  // the same for all 8 slots (k >= 16)
+                const bool keep_max = lower == desc;
+                int64_t o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = shfl_xor64(v[e], m);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = keep_max ? (o[e] > v[e] ? o[e] : v[e]) : (o[e] < v[e] ? o[e] : v[e]);
             }
-            __syncthreads();
         }
     }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st_agent(out + lane * 8 + e, v[e]);
+}
+
+// one wave: the top 32 of two descending 32-key lists a, b (LDS) into dst[0 .. 32) in order (dst may alias a)
+RK_DEV void merge_top32(const int64_t* a, const int64_t* b, int64_t* dst) {
+    const int lane = threadIdx.x & 63;
+    int64_t x = lane < 32 ? a[lane] : b[63 - lane];  // descending then ascending: bitonic
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) {
+        const int64_t o = shfl_xor64(x, j);
+        const bool lower = (lane & j) == 0;
+        x = lower ? (o > x ? o : x) : (o < x ? o : x);
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < 32) dst[lane] = x;
 }
 
 RK_DEV float block_sum(float v, float* red) {  // red: >= 4 floats of LDS; every thread gets the sum
@@ -74,6 +150,16 @@ RK_DEV float block_sum(float v, float* red) {  // red: >= 4 floats of LDS; every
 // for rows [r0, r0 + kStopRows); every block recomputes the (cheap) LayerNorm of h into LDS. One wave per row.
 RK_DEV void stop_rows(const void* h, int hdt, const float* lnw, const float* lnb, const void* w1, int wdt,
                       const float* b1, float* z1, float eps, int H, int nz, int r0, float* z, float* red) {
+    const int lane = threadIdx.x & 63, r = r0 + (threadIdx.x >> 6);
+    // this wave's W1 row first (up to kRowRegs 16-byte pieces per lane), so its HBM latency overlaps the LayerNorm
+    constexpr int kRowRegs = 8;  // H <= 8192 with 16-bit weights
+    const bool vec = H % 512 == 0 && H <= 64 * 8 * kRowRegs && wdt != RK_F32;
+    uint4 wv[kRowRegs];
+    if (vec) {
+        const uint4* wr = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w1) + (size_t)min(r, nz - 1) * H);
+#pragma unroll
+        for (int k = 0; k < kRowRegs; ++k) wv[k] = wr[min(lane + 64 * k, H / 8 - 1)];
+    }
     float s = 0.f;
     for (int i = threadIdx.x; i < H; i += blockDim.x) {
         const float v = load_act(h, hdt, (size_t)i);
@@ -89,65 +175,67 @@ RK_DEV void stop_rows(const void* h, int hdt, const float* lnw, const float* lnb
     const float rstd = rsqrtf(block_sum(ss, red) / (float)H + eps);
     for (int i = threadIdx.x; i < H; i += blockDim.x) z[i] = (z[i] - mean) * rstd * lnw[i] + lnb[i];
     __syncthreads();
-    const int lane = threadIdx.x & 63, r = r0 + (threadIdx.x >> 6);
     if (r >= nz) return;
     float acc = 0.f;
-    if (H % 512 == 0 && wdt != RK_F32) {  // 8 weights (16 bytes) per lane per step
-        const uint4* wr = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(w1) + (size_t)r * H);
-        for (int c = lane; c < H / 8; c += 64) {
-            const uint4 q = wr[c];
-            const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    if (vec) {  // 8 weights (16 bytes) per lane per piece
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float lo = wdt == RK_BF16 ? bf16_bits_to_f32((uint16_t)d[e]) : f16_bits_to_f32((uint16_t)d[e]);
-                const float hi = wdt == RK_BF16 ? bf16_bits_to_f32((uint16_t)(d[e] >> 16))
-                                                : f16_bits_to_f32((uint16_t)(d[e] >> 16));
-                acc = __builtin_fmaf(lo, z[8 * c + 2 * e], acc);
-                acc = __builtin_fmaf(hi, z[8 * c + 2 * e + 1], acc);
+        for (int k = 0; k < kRowRegs; ++k) {
+            const int c = lane + 64 * k;
+            if (c < H / 8) {
+                const uint32_t d[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = wdt == RK_BF16 ? bf16_bits_to_f32((uint16_t)d[e]) : f16_bits_to_f32((uint16_t)d[e]);
+                    const float hi = wdt == RK_BF16 ? bf16_bits_to_f32((uint16_t)(d[e] >> 16))
+                                                    : f16_bits_to_f32((uint16_t)(d[e] >> 16));
+                    acc = __builtin_fmaf(lo, z[8 * c + 2 * e], acc);
+                    acc = __builtin_fmaf(hi, z[8 * c + 2 * e + 1], acc);
+                }
             }
         }
     } else {
         for (int k = lane; k < H; k += 64) acc = __builtin_fmaf(load_act(w1, wdt, (size_t)r * H + k), z[k], acc);
     }
     acc = wave_sum(acc) + b1[r];
-    if (lane == 0) z1[r] = 0.5f * acc * (1.0f + erff(acc * 0.7071067811865476f));  // exact GELU (F.gelu)
+    if (lane == 0) st_agent(z1 + r, 0.5f * acc * (1.0f + erff(acc * 0.7071067811865476f)));  // exact GELU (F.gelu)
 }
 
-// ---- stage 1 (reference topk_partial, sample.py:53-61): chunk c's keys, sorted descending, into keys[c * 512 ..]
-RK_DEV void topk_chunk(const void* logits, int ldt, const int64_t* step, int64_t* keys, int nv, int end_idx,
-                       int min_new, int c, int64_t* s) {
+// ---- stage 1 (reference topk_partial, sample.py:53-61): wave 0 of block blk sorts chunk blk
+RK_DEV void topk_chunks(const void* logits, int ldt, const int64_t* step, int64_t* keys, int nv, int end_idx,
+                        int min_new, int blk) {
+    const int c = blk * kChunksPerBlock + (threadIdx.x >> 6);
+    if ((threadIdx.x >> 6) >= kChunksPerBlock || c * kCH >= nv) return;
     const bool early = step[0] < (int64_t)min_new;
-    for (int e = threadIdx.x; e < kCH; e += blockDim.x) {
-        const int i = c * kCH + e;
-        float x = i < nv ? load_act(logits, ldt, (size_t)i) : -INFINITY;
-        if (early && i == end_idx) x = -INFINITY;  // no </audio> during the first min_new tokens
-        s[e] = make_key(x, i);
-    }
-    __syncthreads();
-    bitonic_desc(s, kCH);
-    for (int e = threadIdx.x; e < kCH; e += blockDim.x) keys[(size_t)c * kCH + e] = s[e];
+    chunk_sort(logits, ldt, early, nv, end_idx, c, keys + (size_t)c * kCH);
 }
 
-// ---- stage 2 (reference pick, sample.py:65-93): merge the chunks' top 32, sample, stop rule, counters
+// ---- stage 2 (reference pick, sample.py:65-93): the top 32 of the chunks' lists, sample, stop rule, counters.
+// The block stages the lists (nch x 32 keys) and computes the stop logit; wave 0 selects and samples.
 RK_DEV void pick_block(const int64_t* keys, int64_t* scratch, const float* u, const float* z1, const float* w2,
                        const float* b2, const int64_t* ids, int64_t* step_p, int64_t* tok, int64_t* out,
-                       float inv_temp, int64_t end_id, int min_new, int nch, int nc, int topk, int nz, int64_t* s,
+                       float inv_temp, int64_t end_id, int min_new, int nch, int topk, int nz, int64_t* cand,
                        float* red) {
-    for (int c = threadIdx.x; c < nc; c += blockDim.x) {
-        const int ch = c / kKeep;
-        s[c] = ch < nch ? keys[(size_t)ch * kCH + c % kKeep] : -(int64_t(1) << 62);
-    }
+    for (int c = threadIdx.x; c < nch * kKeep; c += blockDim.x)
+        cand[c] = ld_agent(keys + (size_t)(c / kKeep) * kCH + c % kKeep);
     float part = 0.f;
-    for (int r = threadIdx.x; r < nz; r += blockDim.x) part = __builtin_fmaf(z1[r], w2[r], part);
+    for (int r = threadIdx.x; r < nz; r += blockDim.x) part = __builtin_fmaf(ld_agent(z1 + r), w2[r], part);
     const float stop_logit = block_sum(part, red) + b2[0];  // sigmoid(.) > 0.5  <=>  stop_logit > 0
     __syncthreads();
-    bitonic_desc(s, nc);
-    for (int c = threadIdx.x; c < nc; c += blockDim.x) scratch[c] = s[c];
+    // merge tree over the lists (in place): level d merges list i and list i + 2^d for i a multiple of 2^(d+1)
+    const int w = threadIdx.x >> 6;
+    for (int d = 1; d < nch; d <<= 1) {
+        for (int i = 2 * d * w; i < nch; i += 2 * d * kWaves)
+            if (i + d < nch) merge_top32(cand + i * kKeep, cand + (i + d) * kKeep, cand + i * kKeep);
+        __syncthreads();
+    }
     if (threadIdx.x >= 64) return;
-    const int j = threadIdx.x;  // candidate rank (lanes 0..31 hold the top 32, best first)
-    const int64_t top = s[j & 31];
-    const float val = unsortable((int32_t)(top >> 32));
-    const int idx = (int)(uint32_t)(top & 0xFFFFFFFF);
+    const int lane = threadIdx.x;
+    const int64_t top = lane < kKeep ? cand[lane] : kPad;
+    if (lane < kKeep) scratch[lane] = top;
+    const int j = lane;  // candidate rank (lanes 0..31 hold the top 32, best first)
+    const int64_t t = __shfl(top, j & 31);
+    const float val = unsortable((int32_t)(t >> 32));
+    const int idx = (int)(uint32_t)(t & 0xFFFFFFFF);
     const float uu = j < topk ? u[j] : 0.5f;
     const float g = -logf(-logf(fminf(fmaxf(uu, 1e-10f), 1.0f)));
     const float score = j < topk ? val * inv_temp + g : -INFINITY;
@@ -175,19 +263,18 @@ __global__ __launch_bounds__(kThreads) void stop_hidden_kernel(const void* h, in
 
 __global__ __launch_bounds__(kThreads) void topk_partial_kernel(const void* logits, int ldt, const int64_t* step,
                                                                 int64_t* keys, int nv, int end_idx, int min_new) {
-    __shared__ int64_t s[kCH];
-    topk_chunk(logits, ldt, step, keys, nv, end_idx, min_new, blockIdx.x, s);
+    topk_chunks(logits, ldt, step, keys, nv, end_idx, min_new, blockIdx.x);
 }
 
 __global__ __launch_bounds__(kThreads) void pick_kernel(const int64_t* keys, int64_t* scratch, const float* u,
                                                         const float* z1, const float* w2, const float* b2,
                                                         const int64_t* ids, int64_t* step_p, int64_t* tok,
                                                         int64_t* out, float inv_temp, int64_t end_id, int min_new,
-                                                        int nch, int nc, int topk, int nz) {
+                                                        int nch, int topk, int nz) {
     extern __shared__ __align__(16) int64_t ssm[];
     __shared__ float red[16];
-    pick_block(keys, scratch, u, z1, w2, b2, ids, step_p, tok, out, inv_temp, end_id, min_new, nch, nc, topk, nz,
-               ssm, red);
+    pick_block(keys, scratch, u, z1, w2, b2, ids, step_p, tok, out, inv_temp, end_id, min_new, nch, topk, nz, ssm,
+               red);
 }
 
 struct TailArgs {
@@ -202,7 +289,7 @@ struct TailArgs {
     unsigned* counter;
     float eps, inv_temp;
     int64_t end_id;
-    int hdt, wdt, ldt, H, nz, nv, end_idx, min_new, nch, nc, topk, nzb;
+    int hdt, wdt, ldt, H, nz, nv, end_idx, min_new, nch, topk, nzb;
 };
 
 __global__ __launch_bounds__(kThreads) void sample_tail_kernel(TailArgs a) {
@@ -214,17 +301,17 @@ __global__ __launch_bounds__(kThreads) void sample_tail_kernel(TailArgs a) {
         stop_rows(a.h, a.hdt, a.lnw, a.lnb, a.w1, a.wdt, a.b1, a.z1, a.eps, a.H, a.nz, b * kStopRows,
                   reinterpret_cast<float*>(raw), red);
     else
-        topk_chunk(a.logits, a.ldt, a.step, a.keys, a.nv, a.end_idx, a.min_new, b - a.nzb,
-                   reinterpret_cast<int64_t*>(raw));
-    __threadfence();  // release: every thread's z1 / keys stores are visible device-wide before the count
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(a.counter, 1u) == gridDim.x - 1;
+        topk_chunks(a.logits, a.ldt, a.step, a.keys, a.nv, a.end_idx, a.min_new, b - a.nzb);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's agent-scope stores are acknowledged
+    __syncthreads();                // ... and every other wave's of the block
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     __syncthreads();
     if (!last) return;
-    __threadfence();  // acquire: the other blocks' z1 / keys
-    if (threadIdx.x == 0) *a.counter = 0u;  // ready for the next call (stream order)
+    if (threadIdx.x == 0)  // ready for the next call (stream order)
+        __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     pick_block(a.keys, a.scratch, a.u, a.z1, a.w2, a.b2, a.ids, a.step, a.tok, a.out, a.inv_temp, a.end_id,
-               a.min_new, a.nch, a.nc, a.topk, a.nz, reinterpret_cast<int64_t*>(raw), red);
+               a.min_new, a.nch, a.topk, a.nz, reinterpret_cast<int64_t*>(raw), red);
 }
 
 bool pow2(int n) { return n > 0 && (n & (n - 1)) == 0; }
@@ -261,8 +348,9 @@ extern "C" int rk_topk_partial(const void* logits, int logits_dtype, const int64
     if (!logits || !step || !keys) return RK_ERR_NULL;
     if (logits_dtype != RK_F16 && logits_dtype != RK_BF16 && logits_dtype != RK_F32) return RK_ERR_DTYPE;
     if (nv <= 0) return RK_ERR_SHAPE;
-    hipLaunchKernelGGL(topk_partial_kernel, dim3((nv + kCH - 1) / kCH), dim3(kThreads), 0, (hipStream_t)stream,
-                       logits, logits_dtype, step, keys, nv, end_idx, min_new);
+    const int nch = (nv + kCH - 1) / kCH;
+    hipLaunchKernelGGL(topk_partial_kernel, dim3((nch + kChunksPerBlock - 1) / kChunksPerBlock), dim3(kThreads), 0,
+                       (hipStream_t)stream, logits, logits_dtype, step, keys, nv, end_idx, min_new);
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 
@@ -272,9 +360,9 @@ extern "C" int rk_pick(const int64_t* keys, int64_t* scratch, const float* u, co
                        rk_stream_t stream) {
     if (!keys || !scratch || !u || !z1 || !w2 || !b2 || !ids || !step || !tok || !out) return RK_ERR_NULL;
     if (const int e = check_pick(nch, nc, topk, nz)) return e;
-    hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kThreads), (size_t)nc * sizeof(int64_t), (hipStream_t)stream,
-                       keys, scratch, u, z1, w2, b2, ids, step, tok, out, inv_temp, end_id, min_new, nch, nc, topk,
-                       nz);
+    hipLaunchKernelGGL(pick_kernel, dim3(1), dim3(kThreads), (size_t)nch * kKeep * sizeof(int64_t),
+                       (hipStream_t)stream, keys, scratch, u, z1, w2, b2, ids, step, tok, out, inv_temp, end_id,
+                       min_new, nch, topk, nz);
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 
@@ -298,9 +386,9 @@ extern "C" int rk_sample_tail(const void* h, int h_dtype, const float* lnw, cons
     a.logits = logits; a.ids = ids; a.keys = keys; a.scratch = scratch; a.step = step; a.tok = tok; a.out = out;
     a.z1 = z1; a.counter = counter; a.eps = eps; a.inv_temp = inv_temp; a.end_id = end_id;
     a.hdt = h_dtype; a.wdt = w1_dtype; a.ldt = logits_dtype; a.H = H; a.nz = nz; a.nv = nv; a.end_idx = end_idx;
-    a.min_new = min_new; a.nch = nch; a.nc = nc; a.topk = topk; a.nzb = (nz + kStopRows - 1) / kStopRows;
-    const size_t lds = std::max(std::max((size_t)H * sizeof(float), (size_t)kCH * sizeof(int64_t)),
-                                (size_t)nc * sizeof(int64_t));
-    hipLaunchKernelGGL(sample_tail_kernel, dim3(a.nzb + nch), dim3(kThreads), lds, (hipStream_t)stream, a);
+    a.min_new = min_new; a.nch = nch; a.topk = topk; a.nzb = (nz + kStopRows - 1) / kStopRows;
+    const size_t lds = std::max((size_t)H * sizeof(float), (size_t)nch * kKeep * sizeof(int64_t));
+    const int chunk_blocks = (nch + kChunksPerBlock - 1) / kChunksPerBlock;
+    hipLaunchKernelGGL(sample_tail_kernel, dim3(a.nzb + chunk_blocks), dim3(kThreads), lds, (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }

@@ -156,7 +156,7 @@ class RkDecodeParams(ctypes.Structure):
         (n, ctypes.c_void_p) for n in (
             "tok", "pos", "emb_q", "emb_s", "win_t", "win_sm", "wo_q", "wo_sm", "wd_t", "wd_sm", "ln_w", "norm_w",
             "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "work", "tx", "tq", "tkv", "top", "tdp",
-            "tpo", "tml", "ctr", "status")]
+            "tpo", "tml", "ctr", "status", "hn")]
 
 
 MAX_TILES, MAX_SLICES, WORK = 7, 3, 16   # kMaxTiles, kMaxSlices, kWork of csrc/decode_persistent.hip
@@ -286,6 +286,7 @@ class PersistentDecode:
         self.ctr = torch.zeros(nb, dtype=i32, device=d)
         self.status = torch.zeros(1, dtype=i32, device=d)
         self.logits = torch.zeros(c.n_audio, dtype=f32, device=d)
+        self.hn = torch.zeros(c.H, dtype=f16, device=d)  # final LayerNorm output (the sampler's stop predictor input)
         self.kc = torch.zeros(c.L, c.NKV, c.S, c.HD, dtype=f16, device=d)
         self.vc = torch.zeros_like(self.kc)
         self.tok = torch.zeros(1, dtype=torch.int64, device=d)
@@ -301,12 +302,13 @@ class PersistentDecode:
                         ("head_q", self.head[0]), ("head_s", self.head[1]), ("logits", self.logits),
                         ("work", self.work), ("tx", self.tx), ("tq", self.tq), ("tkv", self.tkv), ("top", self.top),
                         ("tdp", self.tdp), ("tpo", self.tpo), ("tml", self.tml), ("ctr", self.ctr),
-                        ("status", self.status)):
+                        ("status", self.status), ("hn", self.hn)):
             if not t.is_contiguous() or t.device != d:
                 raise RuntimeError(f"{name} must be a contiguous tensor on {d}")
             setattr(P, name, t.data_ptr())
         self.params = P
         self.graph = None
+        self.sampler = None
 
     @property
     def x(self):
@@ -327,19 +329,41 @@ class PersistentDecode:
         self.kc[:, :, :ctx].normal_(generator=g)
         self.vc[:, :, :ctx].normal_(generator=g)
 
+    def attach_sampler(self, stop, audio_ids, end_id, top_k=30, min_new=8, temperature=0.8, max_new=1800):
+        """Sample the next token inside the step (reference engine/rumik_fused.py:92-94, engine/sample.py): after
+        the int8 head, the fused sampling tail reads `logits` and `hn`, writes out[step_i] and `tok` (the next
+        step's input token) and advances step_i, so replaying the captured step generates tokens autoregressively
+        on the device. `stop`: the stop predictor's state dict (0.weight, 0.bias, 1.weight, 1.bias, 3.weight,
+        3.bias); `audio_ids` [n_audio] int64 maps head rows to token ids."""
+        import sample
+        self.H = self.cfg.H
+        self.stop = {k: v.to(self.dev) for k, v in stop.items()}
+        self.audio_ids = audio_ids.to(self.dev, torch.int64).contiguous()
+        self.end_id, self.top_k, self.min_new, self.temperature = int(end_id), int(top_k), int(min_new), float(temperature)
+        self.step_i = torch.zeros(1, dtype=torch.int64, device=self.dev)
+        self.out = torch.zeros(max_new + 8, dtype=torch.int64, device=self.dev)
+        self.sampler = sample.FusedSampler(self, lambda: self.logits)
+        return self.sampler
+
     def step(self):
         HL.check(HL.lib().rk_decode_step_persistent(ctypes.byref(self.params), self.nblocks, HL.stream(self.dev)),
                  "decode_step_persistent")
+        if self.sampler is not None:
+            self.sampler()
 
     def capture(self):
-        saved = (self.kc.clone(), self.vc.clone(), self.pos.clone())
+        saved = [self.kc.clone(), self.vc.clone(), self.pos.clone(), self.tok.clone()]
+        if self.sampler is not None:
+            saved += [self.step_i.clone(), self.out.clone()]
         self.step()
         torch.cuda.synchronize(self.dev)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.step()
         torch.cuda.synchronize(self.dev)
-        self.kc.copy_(saved[0]); self.vc.copy_(saved[1]); self.pos.copy_(saved[2])
+        self.kc.copy_(saved[0]); self.vc.copy_(saved[1]); self.pos.copy_(saved[2]); self.tok.copy_(saved[3])
+        if self.sampler is not None:
+            self.step_i.copy_(saved[4]); self.out.copy_(saved[5])
         torch.cuda.synchronize(self.dev)
         self.graph = g
         return g

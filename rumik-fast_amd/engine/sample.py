@@ -3,9 +3,10 @@
 Drop-in for the reference's engine/sample.py (imported by engine/rumik_fused.py:12,38 as `FusedSampler`): the same
 module constants (CH, KEEP), the same three kernels with the same argument order and `kernel[grid](...)` launch
 form (the grid and the Triton tuning keywords ROWS / num_warps are accepted and ignored: each HIP wrapper picks its
-own launch shape), the same buffers with the same contents (`keys`: every 512-logit chunk's packed keys sorted
-descending; `scratch`: the sorted candidate list, whose first top_k entries are the top-k; `z1`: the stop
-predictor's hidden layer), and `FusedSampler(eng, logits_fn)()`, which samples the next token from `eng.hn` and
+own launch shape), the same buffers (`keys`: every 512-logit chunk's packed keys sorted descending; `scratch[:32]`:
+the global top 32 in order, so `scratch[:top_k]` is the top-k -- what the reference's pick and its sampler check
+read of the candidate list; its other slots are not written; `z1`: the stop predictor's hidden layer), and
+`FusedSampler(eng, logits_fn)()`, which samples the next token from `eng.hn` and
 updates `eng.out[step]`, `eng.tok` and `eng.step_i` in place. FusedSampler runs the whole tail as ONE launch
 (rk_sample_tail) instead of three; the uniforms come from torch.rand on the device, as in the reference
 (sample.py:113), so the call stays capturable.
@@ -28,7 +29,7 @@ import _hiplib as HL  # noqa: E402
 
 CH = 512          # logits per stage-1 chunk
 KEEP = 32         # survivors per chunk (>= top_k)
-MAX_NC = 4096     # candidate slots the pick sorts in LDS
+MAX_NC = 4096     # candidate slots of the pick (128 chunks)
 
 
 class _Kernel:

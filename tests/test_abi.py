@@ -41,7 +41,7 @@ def test_binding_table_covers_the_header():
 
 def test_version_and_status_strings():
     lib = HL.lib()
-    assert lib.rk_abi_version() == 3
+    assert lib.rk_abi_version() == 4
     texts = {0: "ok", -1: "shape", -2: "unsupported block shape", -3: "unsupported dtype", -4: "null pointer",
              -6: "kernel launch failed"}
     for code, t in texts.items():
@@ -123,7 +123,7 @@ def test_sampler_entry_points_validate_before_any_device_work():
     assert pick(33, 2048, 0) == -1
     assert pick(33, 1024, 30) == -1      # 33 * 32 candidates do not fit
     assert pick(33, 3000, 30) == -1      # not a power of two
-    assert pick(200, 8192, 30) == -1     # above the LDS candidate list
+    assert pick(200, 8192, 30) == -1     # above 128 chunks
     assert pick(33, 2048, 30, nz=0) == -1
     assert lib.rk_pick(None, P, P, P, P, P, P, P, P, P, 1.0, 1, 8, 33, 2048, 30, 512, S) == -4
     assert lib.rk_topk_partial(P, 7, P, P, 16385, 16384, 8, S) == -3

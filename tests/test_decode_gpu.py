@@ -64,6 +64,9 @@ def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph"):
             assert eng.status_word() == 0, "a grid barrier timed out"
         rx = O.parity_report(_np(eng.x), x)
         rl = O.parity_report(_np(eng.logits), logits)
+        if engine == "persistent":  # the exported final hidden state (the sampler's input)
+            rh = O.parity_report(_np(eng.hn), h)
+            assert rh["norm_rel"] < tol and rh["cosine"] > 0.9999, (s, rh)
         reps.append((rx, rl))
         assert rx["norm_rel"] < tol and rx["cosine"] > 0.9999, (s, rx)
         assert rl["norm_rel"] < tol and rl["cosine"] > 0.9999, (s, rl)
@@ -105,3 +108,60 @@ def test_persistent_small_mlp_and_ctx_edges(dev):
     cfg = decode.Config(L=2, inter=2048, S=256, vocab=32, n_audio=1000)
     _run(cfg, dev, ctx=0, steps=2, use_graph=True, engine="persistent")
     _run(cfg, dev, ctx=254, steps=2, use_graph=False, engine="persistent")
+
+
+def test_persistent_step_with_sampler_token_loop(dev):
+    """Decode step + sampling tail in one captured graph (reference engine/rumik_fused.py:92-94): each replay's
+    sampled token is the next replay's input. Per replay: the token is the sampling oracle's pick on the step's own
+    logits / hidden state and uniforms (oracle/sample.py), and the step itself matches the decode oracle run on the
+    sampled token stream (oracle/glue.py)."""
+    import sample
+    from oracle import sample as OS
+    cfg = decode.Config(L=2, vocab=64, n_audio=700)
+    w = decode.random_weights(cfg, 8, device="cpu", gen_device="cpu")
+    wd = {k: ([tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for v in vv]
+              if isinstance(vv, list) else (tuple(t.to(dev) for t in vv) if isinstance(vv, tuple) else vv.to(dev)))
+          for k, vv in w.items()}
+    eng = decode.PersistentDecode(cfg, wd, device=dev)
+    g = torch.Generator().manual_seed(9)
+    stop = {"0.weight": torch.ones(cfg.H), "0.bias": torch.zeros(cfg.H),
+            "1.weight": (torch.randn(512, cfg.H, generator=g) / cfg.H ** 0.5).bfloat16(),
+            "1.bias": torch.zeros(512), "3.weight": torch.randn(1, 512, generator=g) / 512 ** 0.5,
+            "3.bias": torch.tensor([-5.0])}
+    ids = torch.arange(cfg.n_audio, dtype=torch.int64) % (cfg.vocab - 1)  # head row -> next input token (< vocab)
+    ids[-1] = cfg.vocab - 1
+    eng.attach_sampler(stop, ids, end_id=cfg.vocab - 1, top_k=30, min_new=8, temperature=0.8)
+    ctx = 40
+    kc = torch.zeros(cfg.L, cfg.NKV, cfg.S, cfg.HD, dtype=torch.float16)
+    kc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).half()
+    vc = torch.zeros_like(kc)
+    vc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).half()
+    eng.kc.copy_(kc.to(dev))
+    eng.vc.copy_(vc.to(dev))
+    eng.set_state(5, ctx)
+    eng.capture()
+    md = _oracle_model(cfg, w)
+    okc, ovc = kc.numpy().copy(), vc.numpy().copy()
+    st = {k: v.float().numpy() for k, v in stop.items()}
+    tok = 5
+    for s in range(4):
+        eng.replay()
+        torch.cuda.synchronize()
+        assert eng.status_word() == 0
+        logits, h, x = OG.decode_step(md, tok, ctx + s, okc, ovc)
+        rl = O.parity_report(_np(eng.logits), logits)
+        assert rl["norm_rel"] < 1e-2 and rl["cosine"] > 0.9999, (s, rl)
+        # the sampler's pick on the step's own outputs
+        lg, hn, u = _np(eng.logits), _np(eng.hn), _np(eng.sampler.u)
+        z1 = OS.stop_hidden(hn, st["0.weight"], st["0.bias"], st["1.weight"], st["1.bias"])
+        sl = OS.stop_logit(z1, st["3.weight"].reshape(-1), st["3.bias"])
+        sc, idx = OS.scores(lg, u, s, cfg.n_audio - 1, 8, 30, 0.8)
+        new = int(eng.tok.item())
+        order = np.argsort(-sc, kind="stable")
+        near = [int(ids[idx[j]]) for j in order if sc[order[0]] - sc[j] <= 1e-4]
+        assert new in near and sl < 0, (new, near, sl)
+        assert int(eng.step_i.item()) == s + 1 and int(eng.out[s].item()) == new
+        assert int(eng.pos.item()) == ctx + s + 1
+        tok = new  # the oracle continues on the GPU's token stream
+        eng.kc[:, :, ctx + s].copy_(torch.tensor(okc[:, :, ctx + s]).to(dev))
+        eng.vc[:, :, ctx + s].copy_(torch.tensor(ovc[:, :, ctx + s]).to(dev))

@@ -4,8 +4,9 @@ hidden state, a 512 x 2048 bf16 stop-predictor W1, 16385 audio logits (the last 
 bf16 (bf16 makes ties common), top-30, temperature 0.8, min_new 8, </audio> = the last head row.
 
 What must match (the reference's own sampler check, engine/check_sample.py:19-58, made exact where it can be):
-- keys: every 512-logit chunk's packed keys sorted descending, and scratch: the sorted candidate list, are
-  bit-exact (integer work: the key order is total, ties go to the larger index);
+- keys: every 512-logit chunk's packed keys sorted descending, and scratch[:32]: the global top 32 in order, are
+  bit-exact (integer work: the key order is total, ties go to the larger index; scratch[:32] is what the
+  reference's pick and check read of the candidate list);
 - the top-30 (scratch[:30]) is exactly the oracle's top-30 in key order;
 - z1 (stop predictor hidden layer, fp32 vs the oracle's float64): |diff| <= 1e-4 * (1 + |z1|);
 - the stop decision, whenever the oracle's stop logit is not within 1e-3 of zero;
@@ -81,9 +82,8 @@ def _check_buffers(eng, smp, lg, step, z1_ref):
     keys = OS.make_keys(pad, np.arange(pad.size)).reshape(nch, sample.CH)
     ref_keys = np.sort(keys, axis=1)[:, ::-1]
     assert np.array_equal(_np(smp.keys).reshape(nch, sample.CH), ref_keys)
-    cand = np.full(smp.nc, -(2 ** 62), np.int64)
-    cand[:nch * sample.KEEP] = ref_keys[:, :sample.KEEP].reshape(-1)
-    assert np.array_equal(_np(smp.scratch), np.sort(cand)[::-1])
+    cand = np.sort(ref_keys[:, :sample.KEEP].reshape(-1))[::-1]
+    assert np.array_equal(_np(smp.scratch)[:sample.KEEP], cand[:sample.KEEP])
     assert np.array_equal(_np(smp.scratch)[:eng.top_k], OS.sorted_keys(lg, step, NV - 1, eng.min_new)[:eng.top_k])
     z1 = _np(smp.z1)
     assert np.all(np.abs(z1 - z1_ref) <= 1e-4 * (1 + np.abs(z1_ref))), np.abs(z1 - z1_ref).max()
@@ -138,7 +138,7 @@ def test_fused_tail_matches_three_kernels(dev, ldt):
                     eng.tok, eng.out, 1.0 / eng.temperature, eng.end_id, eng.min_new, smp.nch, NC=smp.nc,
                     TOPK=eng.top_k)
         torch.cuda.synchronize()
-        assert torch.equal(keys, smp.keys) and torch.equal(scratch, smp.scratch) and torch.equal(z1, smp.z1)
+        assert torch.equal(keys, smp.keys) and torch.equal(scratch[:32], smp.scratch[:32]) and torch.equal(z1, smp.z1)
         assert int(eng.tok.item()) == tok
 
 

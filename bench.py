@@ -140,6 +140,7 @@ def run_decode(dev, steps):
     import synth
     cfg = decode.Config()
     w = decode.random_weights(cfg, 4, device=dev)
+    w["head"][0][-1].zero_()  # </audio>'s row: its logit 0 is never sampled, so the generate run below is full length
     eng = decode.PersistentDecode(cfg, w, device=dev)
     out = {"engine": "persistent one-launch step (hipGraph)", "weights_bytes_per_token": cfg.weight_bytes(),
            "layers": cfg.L, "blocks": eng.nblocks}
@@ -170,8 +171,9 @@ def run_decode(dev, steps):
     g = synth.generator(11, "cuda")
     stop = {"0.weight": torch.ones(cfg.H, device=dev), "0.bias": torch.zeros(cfg.H, device=dev),
             "1.weight": (torch.randn(512, cfg.H, device=dev, generator=g) / cfg.H ** 0.5).bfloat16(),
-            "1.bias": torch.zeros(512, device=dev), "3.weight": torch.randn(1, 512, device=dev, generator=g) / 512 ** 0.5,
-            "3.bias": torch.tensor([-5.0], device=dev)}
+            "1.bias": torch.zeros(512, device=dev),
+            "3.weight": torch.randn(1, 512, device=dev, generator=g) / 512 ** 0.5 * 0.01,
+            "3.bias": torch.tensor([-50.0], device=dev)}  # the stop predictor never fires (full-length generation)
     ids = torch.arange(cfg.n_audio, dtype=torch.int64) % (cfg.vocab - 1)
     ids[-1] = cfg.vocab - 1
     eng.attach_sampler(stop, ids, end_id=cfg.vocab - 1)
@@ -192,6 +194,14 @@ def run_decode(dev, steps):
         raise RuntimeError(f"persistent decode step reported status {eng.status_word()}")
     out["sampled_ctx256"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1)}
     log(f"[bench] decode + sampling ctx 256: {out['sampled_ctx256']}")
+    # the host generate loop (frames of 8 replays, pinned read-back, one frame queued ahead): a 4-token prompt, then
+    # 256 generated tokens from position 4
+    import generate
+    gen = generate.Generator(eng, Q=8, max_new=256)
+    gen.generate([1, 2, 3, 4], seed=0)  # warm
+    toks, st = gen.generate([1, 2, 3, 4], seed=0)
+    out["generate"] = {k: st[k] for k in ("prompt_tokens", "tokens", "prefill_ms", "first_frame_ms", "decode_tok_s")}
+    log(f"[bench] generate: {out['generate']}")
     del eng, w
     torch.cuda.empty_cache()
     return out

@@ -1,0 +1,130 @@
+"""The host side of generation on MI355X: prompt, then captured decode steps read back a frame at a time.
+
+Mirrors RumikInt4.generate / to_codes (reference engine/rumik_int4.py:251-324) over PersistentDecode with the sampling
+tail attached (one hipGraph = decode step + sample; the sampled token is the next replay's input):
+- frames of Q tokens (Q = num_quantizers, one Mimi frame): Q graph replays, then an asynchronous copy of the frame's
+  tokens to pinned host memory and an event; the next frame is queued before waiting for the current one (double
+  buffering: the GPU never idles while the host handles a frame), and waiting on the event waits only for the work
+  before it;
+- generation stops at </audio> (tokens after it in the same frame are dropped, a frame queued after it is ignored),
+  at max_new tokens or when the cache is full;
+- to_codes: audio token ids -> [1, Q, frames] Mimi codes, whole frames only, resynchronising on a broken codebook
+  round robin (rumik_int4.py:310-324).
+The prompt: prefill() runs the one-launch decode step once per prompt token (teacher forcing: each replay's input
+is the prompt's next token, its sampled token is discarded except after the last prompt token, which is the first
+generated token). This is the reference's prefill maths token by token; a batched prefill on the int4 matrix cores
+(mm_int4) is a separate component.
+"""
+import time
+
+import torch
+
+
+class Generator:
+    """`eng`: a decode.PersistentDecode with attach_sampler() done. first_unit_id / last_unit_id bound the audio
+    token ids (config.json first_unit_id / last_unit_id); Q = num_quantizers."""
+
+    def __init__(self, eng, Q=8, first_unit_id=None, last_unit_id=None, max_new=None):
+        if eng.sampler is None:
+            raise RuntimeError("attach_sampler() first: the captured step must sample its next token")
+        self.eng, self.Q = eng, int(Q)
+        self.first, self.last = first_unit_id, last_unit_id
+        self.max_new = int(max_new) if max_new is not None else eng.out.shape[0] - 8
+        if self.max_new + self.Q > eng.out.shape[0]:
+            raise ValueError("max_new + Q exceeds the sampler's output buffer")
+        self.max_seq = eng.cfg.S
+        self.host = torch.empty(eng.out.shape[0], dtype=torch.long, pin_memory=True)
+        if eng.graph is None:
+            eng.capture()
+
+    @torch.inference_mode()
+    def prefill(self, ids):
+        """Process the prompt; returns the first generated token (a device scalar, also in eng.tok / eng.out[0])."""
+        e = self.eng
+        T = len(ids)
+        if T < 1 or T + 1 >= self.max_seq:
+            raise ValueError(f"prompt of {T} tokens for a {self.max_seq}-slot cache")
+        ids_t = torch.tensor(list(ids), dtype=torch.long).to(e.dev)
+        e.pos.fill_(0)
+        for i in range(T):
+            e.tok.copy_(ids_t[i:i + 1])
+            e.step_i.zero_()  # every prompt replay samples into out[0]; the last one's is generated token 0
+            e.replay()
+        return e.tok[0]
+
+    @torch.inference_mode()
+    def generate(self, ids, seed=0, on_frame=None):
+        """(tokens, stats) as the reference's generate: the first token from the prompt, then frames of Q."""
+        e = self.eng
+        torch.manual_seed(seed)
+        torch.cuda.synchronize(e.dev)
+        t0 = time.perf_counter()
+        first = int(self.prefill(ids))
+        torch.cuda.synchronize(e.dev)
+        t_prefill = time.perf_counter() - t0
+        pos, n, toks, t_frame0 = len(ids), 1, [first], None
+        done = first == e.end_id
+        host, queued = self.host, []
+
+        def launch():
+            nonlocal pos, n
+            for _ in range(self.Q):
+                e.replay()
+                pos += 1
+            host[n:n + self.Q].copy_(e.out[n:n + self.Q], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            queued.append((n, ev))
+            n += self.Q
+
+        def can_launch():
+            return n < self.max_new and pos + self.Q < self.max_seq
+
+        if not done and can_launch():
+            launch()
+        while queued:
+            if not done and can_launch():
+                launch()                                         # keep one frame ahead
+            k, ev = queued.pop(0)
+            ev.synchronize()
+            new = host[k:k + self.Q].tolist()
+            if t_frame0 is None:
+                t_frame0 = time.perf_counter() - t0
+            if e.end_id in new:
+                new = new[:new.index(e.end_id)]
+                done = True
+            toks += new
+            if on_frame:
+                on_frame(toks)
+            if done:
+                queued.clear()                                   # the frame after </audio> is ignored
+        torch.cuda.synchronize(e.dev)
+        total = time.perf_counter() - t0
+        n_dec = max(len(toks) - 1, 1)
+        return toks, {"prompt_tokens": len(ids), "tokens": len(toks), "prefill_ms": round(t_prefill * 1e3, 1),
+                      "first_frame_ms": round((t_frame0 or total) * 1e3, 1),
+                      "decode_tok_s": round(n_dec / max(total - t_prefill, 1e-9), 1),
+                      "audio_s": round(len(toks) / 100, 2), "total_s": round(total, 2)}
+
+    def to_codes(self, toks):
+        return to_codes(toks, self.first, self.last, self.Q)
+
+
+def to_codes(toks, first, last, Q=8):
+    """audio token ids -> [1, Q, frames] Mimi codes: token t in [first, last] is code (t - first) // Q of codebook
+    (t - first) % Q; a frame is Q tokens with codebooks 0..Q-1 in order; a token out of order restarts the frame
+    (at itself when it is codebook 0), a non-audio token drops the partial frame."""
+    frames, fr = [], []
+    for t in toks:
+        if not first <= t <= last:
+            fr = []
+            continue
+        code, q = divmod(t - first, Q)
+        if q == len(fr):
+            fr.append(code)
+            if len(fr) == Q:
+                frames.append(fr)
+                fr = []
+        else:
+            fr = [code] if q == 0 else []
+    return torch.tensor(frames, dtype=torch.long).reshape(-1, Q).T.unsqueeze(0)

@@ -141,7 +141,7 @@ def run_decode(dev, steps):
     cfg = decode.Config()
     w = decode.random_weights(cfg, 4, device=dev)
     w["head"][0][-1].zero_()  # </audio>'s row: its logit 0 is never sampled, so the generate run below is full length
-    eng = decode.PersistentDecode(cfg, w, device=dev)
+    eng = decode.PersistentDecode(cfg, w, device=dev, keep_layer_weights=True)  # the prefill reads the int4 layout
     out = {"engine": "persistent one-launch step (hipGraph)", "weights_bytes_per_token": cfg.weight_bytes(),
            "layers": cfg.L, "blocks": eng.nblocks}
     eng.fill_cache(cfg.S, seed=5)
@@ -202,6 +202,30 @@ def run_decode(dev, steps):
     toks, st = gen.generate([1, 2, 3, 4], seed=0)
     out["generate"] = {k: st[k] for k in ("prompt_tokens", "tokens", "prefill_ms", "first_frame_ms", "decode_tok_s")}
     log(f"[bench] generate: {out['generate']}")
+    # batched prompt prefill (36 layers: mm_int4, the matrix-core causal attention, row glue), eager, best of 3
+    import prefill as PF
+    pf = PF.Prefill(cfg, w, eng.kc, eng.vc, eng.cos, eng.sin, max_T=512)
+    res = {}
+    for T in (69, 512):
+        ids = [(7 * i) % cfg.vocab for i in range(T)]
+        pf.run(ids)
+        best = math.inf
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            pf.run(ids)
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        res[f"T{T}"] = {"ms": round(best * 1e3, 2), "tok_s": round(T / best, 1)}
+    g = graph_of([lambda: PF.prefill_attn(pf.q, eng.kc[0], eng.vc[0], pf.o, 512, 0, cfg.NH, cfg.NKV, cfg.HD, cfg.S,
+                                          cfg.HD ** -0.5)] * 10)
+    us = time_graph_us(g, 10)
+    fl = 4.0 * cfg.NH * cfg.HD * (512 * 513 / 2)  # QK^T and PV over the causal half
+    res["attn_T512_us"] = round(us, 2)
+    res["attn_T512_mfma_frac"] = round(fl / us / 1e6 / PEAK_FP16_TFLOPS, 4)
+    del g
+    out["prefill"] = res
+    log(f"[bench] prefill (36 layers): {res}")
     del eng, w
     torch.cuda.empty_cache()
     return out

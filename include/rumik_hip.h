@@ -216,6 +216,34 @@ int rk_decode_params_size(void);
 /* pos[0] += 1 on the device (the `self.pos += 1` of the captured step, reference engine/rumik_fused.py:120). */
 int rk_pos_advance(int64_t* pos, rk_stream_t stream);
 
+/* ---- prompt prefill (reference RumikFused.prefill, engine/rumik_fused.py:54-78): the glue between its mm_int4
+ * products for T rows at once, and the causal attention that replaces its torch fp32 _attend. Activations [T, H]
+ * row-major fp16 / bf16 (dt); each stored value is rounded once to dt. */
+
+/* x[t] = dt(emb_q[ids[t]] * emb_s[ids[t]]), h[t] = LayerNorm(x[t]) * ln_w for t < T (the embedding lookup and
+ * cohere_ln of rumik_fused.py:58,63, rumik_int4.py:38-43). ids int64 [T] (device); emb int8 [V, H] + fp16 [V]. */
+int rk_embed_ln_rows(const int64_t* ids, const int8_t* emb_q, const uint16_t* emb_s, const void* ln_w, void* x,
+                     void* h, int dt, int T, int H, float eps, rk_stream_t stream);
+
+/* x[t] = dt(x[t] + a[t] + b[t]), h[t] = LayerNorm(x[t]) * ln_w (rumik_fused.py:74 and the next layer's LN, :63);
+ * b may be NULL. */
+int rk_add_ln_rows(void* x, const void* a, const void* b, const void* ln_w, void* h, int dt, int T, int H, float eps,
+                   rk_stream_t stream);
+
+/* Row t of y [T, ldy] = [q | k | v | gate | up] at position p0 + t: RoPE (interleaved pairs, when rope) on q and k,
+ * q -> q_out [T, NH*HD], k / v -> cache slot p0 + t of kc / vc [NKV, S, HD], act [T, inter] = silu(gate) * up
+ * (rumik_fused.py:64-71). cos / sin [S, HD] in dt. p0 + T <= S. */
+int rk_post_rows(const void* y, int ldy, int p0, const void* cos_t, const void* sin_t, void* kc, void* vc,
+                 void* q_out, void* act, int dt, int T, int NH, int NKV, int HD, int S, int inter, int rope,
+                 rk_stream_t stream);
+
+/* Causal GQA attention for the prompt on the matrix cores: o[t, h] = softmax(q[t, h] . K[g, 0..p0+t]^T * scale)
+ * V[g, 0..p0+t], g = h / (NH / NKV). Replaces _attend (engine/rumik_int4.py:163-171, fp32 scores; here fp32
+ * scores and softmax, P in fp16 for the PV product, fp32 accumulation). q, o [T, NH*128] fp16; kc, vc [NKV, S, 128]
+ * fp16 (one layer), 16-byte aligned; HD = 128, NH / NKV <= 8, p0 + T <= S. */
+int rk_prefill_attn(const void* q, const void* kc, const void* vc, void* o, int dt, int T, int p0, int NH, int NKV,
+                    int HD, int S, float scale, rk_stream_t stream);
+
 /* ---- the tail of a decode step: stop predictor + top-k + Gumbel-max sampling + counters
  * (reference engine/sample.py; maths of RumikInt4._logits_and_stop / _pick, engine/rumik_int4.py:174-191).
  * Keys: key = (sortable(bits(logit)) << 32) | index with sortable(b) = b ^ ((b >> 31) & 0x7FFFFFFF), sorted

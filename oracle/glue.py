@@ -60,6 +60,26 @@ def attend(q, K, V, scale=None):
     return out
 
 
+def causal_attend(q, K, V, p0=0, scale=None):
+    """Prefill attention (engine/rumik_int4.py:163-171: fp32 scores, causal bias, GQA): q [T, NH, HD] of positions
+    p0 .. p0 + T - 1, K / V [NKV, >= p0 + T, HD] -> [T, NH, HD] fp32; query t reads slots 0 .. p0 + t."""
+    q = np.asarray(q, np.float32)
+    T, NH, HD = q.shape
+    NKV = K.shape[0]
+    rep = NH // NKV
+    scale = HD ** -0.5 if scale is None else scale
+    n = p0 + T
+    k = np.asarray(K[:, :n], np.float32)
+    v = np.asarray(V[:, :n], np.float32)
+    bias = np.where(np.arange(n)[None, :] <= (p0 + np.arange(T))[:, None], 0.0, -np.inf).astype(np.float32)
+    out = np.empty((T, NH, HD), np.float32)
+    for h in range(NH):
+        s = (q[:, h] @ k[h // rep].T) * np.float32(scale) + bias
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ v[h // rep]
+    return out
+
+
 def attend_split(q, K, V, nsplit, chunk, scale=None):
     """Flash-decoding as the reference splits it: per split the partial (m, l, acc) over its slots, then the
     combine. Returns (out [NH, HD], m [NH, nsplit], l [NH, nsplit]); empty splits have m = -inf, l = 0."""

@@ -1,0 +1,319 @@
+// Prompt prefill on gfx950: the reference's int4 prefill (engine/rumik_fused.py:54-78) between its mm_int4
+// products, for T prompt rows at once:
+//   embed_ln_rows   x[t] = dt(emb_q[ids[t]] * emb_s[ids[t]]); h[t] = LN(x[t]) * w      (rumik_int4.py:38-43)
+//   post_rows       RoPE on q / k of row t at position p0 + t (interleaved pairs, rumik_int4.py:46-52), K / V
+//                   into the layer's cache slot p0 + t, q to q_out, act = silu(gate) * up
+//   prefill_attn    causal GQA attention of the T queries over cache slots 0 .. p0 + t (rumik_int4.py:163-171)
+//   add_ln_rows     x[t] = dt(x[t] + a[t] + b[t]); h[t] = LN(x[t]) * w (the residual of the parallel block and
+//                   the next layer's LayerNorm)
+// Every stored activation is rounded once to the activation dtype, as in the decode glue.
+//
+// prefill_attn on the matrix cores (v_mfma_f32_16x16x32_f16; operand layouts: A[i][k] in lane i + 16 (k / 8),
+// element k % 8; B[k][j] in lane j + 16 (k / 8); D[i][j] in lane j + 16 (i / 4), element i % 4). Block = (KV head
+// g, tile of 16 queries); wave r = query head g * REP + r. Per key block of 32 slots the block stages K [32 x 128]
+// and V transposed [128 x 32] in LDS once for all REP heads; each wave computes S = Q K^T (2 x 4 MFMAs), the causal
+// mask and an online softmax (row statistics reduced over the 16 lanes of a DPP row), stores P (fp16, the
+// reference's tensor-core PV in 16-bit) to its LDS tile in the A layout and accumulates O += P V (8 MFMAs, fp32).
+#include "common.h"
+
+namespace {
+
+constexpr int kRowThreads = 256;
+constexpr int kMaxPer = 32;  // H <= 8192
+constexpr int kHD = 128;
+constexpr int kKB = 32;      // keys per block step
+constexpr int kQT = 16;      // queries per tile
+
+RK_DEV float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+RK_DEV float round_act(float v, int dt) {
+    if (dt == RK_F16) return (float)(_Float16)v;
+    if (dt == RK_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+    return v;
+}
+
+// LN of the block's register copy of one row, written to h (d = x - mean, h = d * rsqrt(mean(d^2) + eps) * w)
+RK_DEV void ln_row(const float (&xv)[kMaxPer], const void* w, void* h, int dt, int H, float eps, float* red) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k)
+        if (threadIdx.x + k * blockDim.x < (unsigned)H) s += xv[k];
+    const float mean = block_sum(s, red) / (float)H;
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k)
+        if (threadIdx.x + k * blockDim.x < (unsigned)H) {
+            const float d = xv[k] - mean;
+            ss += d * d;
+        }
+    const float rstd = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        if (i < H) store_act(h, dt, (size_t)i, (xv[k] - mean) * rstd * load_act(w, dt, (size_t)i));
+    }
+}
+
+__global__ __launch_bounds__(kRowThreads) void embed_ln_rows_kernel(const int64_t* ids, const int8_t* eq,
+                                                                    const uint16_t* es, const void* w, void* x,
+                                                                    void* h, int dt, int H, float eps) {
+    __shared__ float red[16];
+    const int t = blockIdx.x;
+    const int64_t id = ids[t];
+    const float sc = f16_bits_to_f32(es[id]);
+    const int8_t* row = eq + (size_t)id * H;
+    float xv[kMaxPer];
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        xv[k] = 0.f;
+        if (i < H) {
+            xv[k] = round_act((float)row[i] * sc, dt);
+            store_act(x, dt, (size_t)t * H + i, xv[k]);
+        }
+    }
+    ln_row(xv, w, (char*)h + (size_t)t * H * (dt == RK_F32 ? 4 : 2), dt, H, eps, red);
+}
+
+__global__ __launch_bounds__(kRowThreads) void add_ln_rows_kernel(void* x, const void* a, const void* b,
+                                                                  const void* w, void* h, int dt, int H, float eps) {
+    __shared__ float red[16];
+    const size_t r0 = (size_t)blockIdx.x * H;
+    float xv[kMaxPer];
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        xv[k] = 0.f;
+        if (i < H) {
+            float v = load_act(x, dt, r0 + i) + load_act(a, dt, r0 + i);
+            if (b) v += load_act(b, dt, r0 + i);
+            xv[k] = round_act(v, dt);
+            store_act(x, dt, r0 + i, xv[k]);
+        }
+    }
+    ln_row(xv, w, (char*)h + r0 * (dt == RK_F32 ? 4 : 2), dt, H, eps, red);
+}
+
+// grid (T, NH + 2 NKV + ceil(inter / 256)), 64 threads: block (t, b) as post_kernel of the decode glue for row t
+__global__ __launch_bounds__(64) void post_rows_kernel(const void* y, int ldy, int p0, const void* cos_t,
+                                                       const void* sin_t, void* kc, void* vc, void* qo, void* act,
+                                                       int dt, int NH, int NKV, int HD, int S, int inter, int rope) {
+    const int t = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int pos = p0 + t;
+    const size_t yr = (size_t)t * ldy;
+    if (b < NH + NKV) {
+        for (int j = tid; j < HD / 2; j += 64) {
+            const float xe = load_act(y, dt, yr + (size_t)b * HD + 2 * j);
+            const float xo = load_act(y, dt, yr + (size_t)b * HD + 2 * j + 1);
+            float oe = xe, oo = xo;
+            if (rope) {
+                const float c = load_act(cos_t, dt, (size_t)pos * HD + 2 * j);
+                const float s = load_act(sin_t, dt, (size_t)pos * HD + 2 * j);
+                oe = xe * c - xo * s;
+                oo = xo * c + xe * s;
+            }
+            if (b < NH) {
+                store_act(qo, dt, (size_t)t * NH * HD + (size_t)b * HD + 2 * j, oe);
+                store_act(qo, dt, (size_t)t * NH * HD + (size_t)b * HD + 2 * j + 1, oo);
+            } else {
+                const size_t c0 = ((size_t)(b - NH) * S + pos) * HD;
+                store_act(kc, dt, c0 + 2 * j, oe);
+                store_act(kc, dt, c0 + 2 * j + 1, oo);
+            }
+        }
+    } else if (b < NH + 2 * NKV) {
+        const int hv = b - NH - NKV;
+        for (int j = tid; j < HD; j += 64)
+            store_act(vc, dt, ((size_t)hv * S + pos) * HD + j, load_act(y, dt, yr + (size_t)(NH + NKV + hv) * HD + j));
+    } else {
+        const size_t base = (size_t)(NH + 2 * NKV) * HD;
+        for (int c = (b - NH - 2 * NKV) * 256 + tid; c < min(inter, (b - NH - 2 * NKV + 1) * 256); c += 64) {
+            const float g = load_act(y, dt, yr + base + c), u = load_act(y, dt, yr + base + inter + c);
+            store_act(act, dt, (size_t)t * inter + c, g / (1.0f + __expf(-g)) * u);
+        }
+    }
+}
+
+// all-reduce over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1)
+RK_DEV float row16_max(float v) {
+    v = fmaxf(v, dpp<0x128>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x122>(v));
+    v = fmaxf(v, dpp<0x121>(v));
+    return v;
+}
+RK_DEV float row16_sum(float v) {
+    v += dpp<0x128>(v);
+    v += dpp<0x124>(v);
+    v += dpp<0x122>(v);
+    v += dpp<0x121>(v);
+    return v;
+}
+
+// grid (NKV, ceil(T / 16)), 64 * REP threads. q: [T, NH * 128] fp16 (RoPE applied); kc / vc: the layer's cache
+// [NKV, S, 128] fp16 holding slots 0 .. p0 + T - 1; o: [T, NH * 128] fp16. Query t attends slots 0 .. p0 + t.
+__global__ __launch_bounds__(512) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                                           uint16_t* o, int T, int p0, int NH, int NKV, int S,
+                                                           float scale) {
+    __shared__ __align__(16) uint16_t Ks[kKB][kHD];     // K rows of the key block
+    __shared__ __align__(16) uint16_t Vt[kHD][kKB];     // V transposed: Vt[dim][key]
+    extern __shared__ __align__(16) uint16_t Ps[];      // per wave: P [16 queries][32 keys]
+    const int g = blockIdx.x, q0 = blockIdx.y * kQT;
+    const int lane = threadIdx.x & 63, r = threadIdx.x >> 6, REP = blockDim.x >> 6;
+    const int h = g * REP + r;
+    const int li = lane & 15, lq = lane >> 4;  // A / B fragment: row or column li, k-group lq
+    const int ldq = NH * kHD;
+    uint16_t* P = Ps + r * kQT * kKB;
+    // Q fragments of this wave's head: query q0 + li, dims 32c + 8 lq .. + 8
+    h8_t Qf[4];
+    {
+        const int qi = min(q0 + li, T - 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            Qf[c] = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(q + (size_t)qi * ldq + h * kHD + 32 * c + 8 * lq));
+    }
+    f4_t O[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) O[c] = f4_t{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        m[e] = -INFINITY;
+        l[e] = 0.f;
+    }
+    const uint16_t* kg = kc + (size_t)g * S * kHD;
+    const uint16_t* vg = vc + (size_t)g * S * kHD;
+    const int last = p0 + min(q0 + kQT, T) - 1;  // the last slot any query of the tile sees
+    for (int j0 = 0; j0 <= last; j0 += kKB) {
+        __syncthreads();  // the previous block step's K / V are no longer read
+        for (int e = threadIdx.x; e < kKB * kHD / 8; e += blockDim.x) {
+            const int kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
+            const bool ok = j0 + kj <= last;
+            const uint4 kv = ok ? *reinterpret_cast<const uint4*>(kg + (size_t)(j0 + kj) * kHD + d8) : make_uint4(0, 0, 0, 0);
+            const uint4 vv = ok ? *reinterpret_cast<const uint4*>(vg + (size_t)(j0 + kj) * kHD + d8) : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(&Ks[kj][d8]) = kv;
+            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                Vt[d8 + 2 * u][kj] = (uint16_t)vw[u];
+                Vt[d8 + 2 * u + 1][kj] = (uint16_t)(vw[u] >> 16);
+            }
+        }
+        __syncthreads();
+        // S = Q K^T for keys j0 + 16 hf + li (D layout: row 4 lq + e, key li)
+        f4_t Sd[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Ks[16 * hf + li][32 * c + 8 * lq]));
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Qf[c], B, d, 0, 0, 0);
+            }
+            Sd[hf] = d;
+        }
+        float alpha[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int qpos = p0 + q0 + 4 * lq + e;
+            float s0 = Sd[0][e] * scale, s1 = Sd[1][e] * scale;
+            if (j0 + li > qpos) s0 = -INFINITY;
+            if (j0 + 16 + li > qpos) s1 = -INFINITY;
+            const float mb = row16_max(fmaxf(s0, s1));
+            const float mn = fmaxf(m[e], mb);
+            const float p0v = mn == -INFINITY ? 0.f : __expf(s0 - mn);
+            const float p1v = mn == -INFINITY ? 0.f : __expf(s1 - mn);
+            const _Float16 h0 = (_Float16)p0v, h1 = (_Float16)p1v;
+            alpha[e] = mn == -INFINITY ? 1.f : __expf(m[e] - mn);
+            l[e] = l[e] * alpha[e] + row16_sum((float)h0 + (float)h1);
+            m[e] = mn;
+            P[(4 * lq + e) * kKB + li] = __builtin_bit_cast(uint16_t, h0);
+            P[(4 * lq + e) * kKB + 16 + li] = __builtin_bit_cast(uint16_t, h1);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) O[c][e] *= alpha[e];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // O += P V: A = P[query li][keys 8 lq .. + 8], B = Vt[dim 16 c + li][keys 8 lq .. + 8]
+        const h8_t A = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&P[li * kKB + 8 * lq]));
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Vt[16 * c + li][8 * lq]));
+            O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, O[c], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();  // P is rewritten in the next step only after these reads
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int t = q0 + 4 * lq + e;
+        if (t >= T) continue;
+        const float inv = l[e] > 0.f ? 1.0f / l[e] : 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            o[(size_t)t * ldq + h * kHD + 16 * c + li] = __builtin_bit_cast(uint16_t, (_Float16)(O[c][e] * inv));
+    }
+}
+
+bool act_dt(int dt) { return dt == RK_F16 || dt == RK_BF16; }
+
+}  // namespace
+
+extern "C" int rk_embed_ln_rows(const int64_t* ids, const int8_t* emb_q, const uint16_t* emb_s, const void* ln_w,
+                                void* x, void* h, int dt, int T, int H, float eps, rk_stream_t stream) {
+    if (!ids || !emb_q || !emb_s || !ln_w || !x || !h) return RK_ERR_NULL;
+    if (!act_dt(dt)) return RK_ERR_DTYPE;
+    if (T <= 0 || H <= 0 || H > kRowThreads * kMaxPer) return RK_ERR_SHAPE;
+    hipLaunchKernelGGL(embed_ln_rows_kernel, dim3(T), dim3(kRowThreads), 0, (hipStream_t)stream, ids, emb_q, emb_s,
+                       ln_w, x, h, dt, H, eps);
+    return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+
+extern "C" int rk_add_ln_rows(void* x, const void* a, const void* b, const void* ln_w, void* h, int dt, int T, int H,
+                              float eps, rk_stream_t stream) {
+    if (!x || !a || !ln_w || !h) return RK_ERR_NULL;
+    if (!act_dt(dt)) return RK_ERR_DTYPE;
+    if (T <= 0 || H <= 0 || H > kRowThreads * kMaxPer) return RK_ERR_SHAPE;
+    hipLaunchKernelGGL(add_ln_rows_kernel, dim3(T), dim3(kRowThreads), 0, (hipStream_t)stream, x, a, b, ln_w, h, dt,
+                       H, eps);
+    return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+
+extern "C" int rk_post_rows(const void* y, int ldy, int p0, const void* cos_t, const void* sin_t, void* kc, void* vc,
+                            void* q_out, void* act, int dt, int T, int NH, int NKV, int HD, int S, int inter, int rope,
+                            rk_stream_t stream) {
+    if (!y || !kc || !vc || !q_out || !act || (rope && (!cos_t || !sin_t))) return RK_ERR_NULL;
+    if (!act_dt(dt)) return RK_ERR_DTYPE;
+    if (T <= 0 || NH <= 0 || NKV <= 0 || HD <= 0 || HD % 2 || inter <= 0 || p0 < 0 || p0 + T > S ||
+        ldy < (NH + 2 * NKV) * HD + 2 * inter)
+        return RK_ERR_SHAPE;
+    const dim3 grid(T, NH + 2 * NKV + (inter + 255) / 256);
+    hipLaunchKernelGGL(post_rows_kernel, grid, dim3(64), 0, (hipStream_t)stream, y, ldy, p0, cos_t, sin_t, kc, vc,
+                       q_out, act, dt, NH, NKV, HD, S, inter, rope);
+    return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+
+extern "C" int rk_prefill_attn(const void* q, const void* kc, const void* vc, void* o, int dt, int T, int p0, int NH,
+                               int NKV, int HD, int S, float scale, rk_stream_t stream) {
+    if (!q || !kc || !vc || !o) return RK_ERR_NULL;
+    if (dt != RK_F16) return RK_ERR_DTYPE;
+    if (HD != kHD || NKV <= 0 || NH % NKV || T <= 0 || p0 < 0 || p0 + T > S) return RK_ERR_SHAPE;
+    const int rep = NH / NKV;
+    if (rep > 8) return RK_ERR_SHAPE;
+    if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return RK_ERR_ALIGN;
+    const dim3 grid(NKV, (T + kQT - 1) / kQT);
+    hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(64 * rep), (size_t)rep * kQT * kKB * 2, (hipStream_t)stream,
+                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
+                       scale);
+    return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}

@@ -10,10 +10,10 @@ tail attached (one hipGraph = decode step + sample; the sampled token is the nex
   at max_new tokens or when the cache is full;
 - to_codes: audio token ids -> [1, Q, frames] Mimi codes, whole frames only, resynchronising on a broken codebook
   round robin (rumik_int4.py:310-324).
-The prompt: prefill() runs the one-launch decode step once per prompt token (teacher forcing: each replay's input
-is the prompt's next token, its sampled token is discarded except after the last prompt token, which is the first
-generated token). This is the reference's prefill maths token by token; a batched prefill on the int4 matrix cores
-(mm_int4) is a separate component.
+The prompt: with a prefill.Prefill (all prompt rows of a layer at once: mm_int4 and the matrix-core causal
+attention), then the audio head and the sampling tail; without one, prefill() runs the one-launch decode step once
+per prompt token (teacher forcing: each replay's input is the prompt's next token, its sampled token is discarded
+except after the last prompt token, which is the first generated token).
 """
 import time
 
@@ -24,10 +24,10 @@ class Generator:
     """`eng`: a decode.PersistentDecode with attach_sampler() done. first_unit_id / last_unit_id bound the audio
     token ids (config.json first_unit_id / last_unit_id); Q = num_quantizers."""
 
-    def __init__(self, eng, Q=8, first_unit_id=None, last_unit_id=None, max_new=None):
+    def __init__(self, eng, Q=8, first_unit_id=None, last_unit_id=None, max_new=None, prefill=None):
         if eng.sampler is None:
             raise RuntimeError("attach_sampler() first: the captured step must sample its next token")
-        self.eng, self.Q = eng, int(Q)
+        self.eng, self.Q, self.pf = eng, int(Q), prefill
         self.first, self.last = first_unit_id, last_unit_id
         self.max_new = int(max_new) if max_new is not None else eng.out.shape[0] - 8
         if self.max_new + self.Q > eng.out.shape[0]:
@@ -39,11 +39,21 @@ class Generator:
 
     @torch.inference_mode()
     def prefill(self, ids):
-        """Process the prompt; returns the first generated token (a device scalar, also in eng.tok / eng.out[0])."""
+        """Process the prompt; returns the first generated token (a device scalar, also in eng.tok / eng.out[0]).
+        With a prefill.Prefill: all prompt rows per layer at once on the matrix cores, then the audio head and the
+        sampling tail on hn (rumik_fused.py:54-78); otherwise the decode step once per prompt token."""
         e = self.eng
         T = len(ids)
         if T < 1 or T + 1 >= self.max_seq:
             raise ValueError(f"prompt of {T} tokens for a {self.max_seq}-slot cache")
+        if self.pf is not None:
+            import cuda_gemv
+            self.pf.run(ids, hn=e.hn)
+            e.pos.fill_(T)
+            cuda_gemv.gemv_int8_cuda(e.hn, *e.head, out=e.logits)
+            e.step_i.zero_()
+            e.sampler()  # out[0] = the first token, tok = it, step_i = 1
+            return e.tok[0]
         ids_t = torch.tensor(list(ids), dtype=torch.long).to(e.dev)
         e.pos.fill_(0)
         for i in range(T):

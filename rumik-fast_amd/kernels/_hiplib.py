@@ -38,6 +38,10 @@ _SIGS = {
     "rk_silu_mul": ([_p, _p, _i, _i, _p], _i),
     "rk_decode_step_persistent": ([_p, _i, _p], _i),
     "rk_decode_params_size": ([], _i),
+    "rk_embed_ln_rows": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _f, _p], _i),
+    "rk_add_ln_rows": ([_p, _p, _p, _p, _p, _i, _i, _i, _f, _p], _i),
+    "rk_post_rows": ([_p, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p], _i),
+    "rk_prefill_attn": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _p], _i),
     "rk_stop_hidden": ([_p, _i, _p, _p, _p, _i, _p, _p, _f, _i, _i, _p], _i),
     "rk_topk_partial": ([_p, _i, _p, _p, _i, _i, _i, _p], _i),
     "rk_pick": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _f, _l, _i, _i, _i, _i, _i, _p], _i),

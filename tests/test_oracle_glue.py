@@ -120,3 +120,18 @@ def test_decode_step_residual_identity():
     x0 = (emb[0][2].astype(np.float32) * np.float32(emb[1][2])).astype(np.float16).astype(np.float32)
     np.testing.assert_array_equal(x, x0)
     assert np.any(kc[0, :, 3] != 0) and np.all(kc[0, :, :3] == 0)  # K written at pos only
+
+
+def test_causal_attend_rows_are_decode_attention():
+    """row t of the prefill attention is the decode attention of query t over slots 0..p0+t (the pinned `attend`),
+    and the first row of a fresh prompt is v[0] exactly (one slot)"""
+    rng = np.random.default_rng(12)
+    T, NH, NKV, HD, p0 = 9, 4, 2, 16, 3
+    q = rng.standard_normal((T, NH, HD)).astype(np.float32)
+    K = rng.standard_normal((NKV, p0 + T, HD)).astype(np.float32)
+    V = rng.standard_normal((NKV, p0 + T, HD)).astype(np.float32)
+    out = OG.causal_attend(q, K, V, p0)
+    for t in range(T):
+        np.testing.assert_allclose(out[t], OG.attend(q[t], K[:, :p0 + t + 1], V[:, :p0 + t + 1]), rtol=1e-5, atol=1e-6)
+    first = OG.causal_attend(q[:1], K, V, 0)
+    np.testing.assert_array_equal(first[0], V[np.arange(NH) // 2, 0])

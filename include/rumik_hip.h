@@ -72,6 +72,16 @@ int rk_gemv_int4_g128_valu(const void* x, int x_dtype, const uint8_t* q, const u
                            const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
                            rk_stream_t stream);
 
+/* Two independent int4 g128 GEMVs in one launch, y1 = dequant(q1) x1 and y2 = dequant(q2) x2, each with the
+ * contract of rk_gemv_int4_g128 (tuned default block shapes): the decode layer's o projection (o = attn @ w_o^T) and
+ * down projection (d = act @ w_down^T), which the reference runs as two back-to-back gemv_int4 calls on inputs that
+ * are both ready at that point (engine/rumik_fused.py:115-116). One grid: blocks [0, B1) compute y1, the rest y2.
+ * Shapes with K1 <= 2048 and 4096 < K2 <= 16384 run as the pair kernel; other shapes as two launches. */
+int rk_gemv_int4_g128_pair(const void* x1, int x1_dtype, const uint8_t* q1, const uint16_t* s1, const uint16_t* m1,
+                           void* y1, int y1_dtype, int N1, int K1, const void* x2, int x2_dtype, const uint8_t* q2,
+                           const uint16_t* s2, const uint16_t* m2, void* y2, int y2_dtype, int N2, int K2,
+                           rk_stream_t stream);
+
 /* The engine's input projection with the MLP activation fused (decode glue): q holds n_plain ordinary rows,
  * then `inter` gate rows, then `inter` up rows (the reference's w_in = [q | k | v | gate | up], engine/
  * rumik_int4.py:97), all int4 g128 over one x. Writes y[0 .. n_plain) and act[c] = silu(gate_c) * up_c for

@@ -7,6 +7,11 @@ extern "C" int rk_gemv_int4_g128_impl(const void* x, int x_dtype, const uint8_t*
 extern "C" int rk_gemv_int4_mfma_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
                                       const uint16_t* min, void* y, int y_dtype, int N, int K, int waves,
                                       rk_stream_t stream);
+extern "C" int rk_gemv_int4_g128_pair_impl(const void* x1, int x1_dtype, const uint8_t* q1, const uint16_t* s1,
+                                           const uint16_t* m1, void* y1, int y1_dtype, int N1, int K1,
+                                           const void* x2, int x2_dtype, const uint8_t* q2, const uint16_t* s2,
+                                           const uint16_t* m2, void* y2, int y2_dtype, int N2, int K2,
+                                           rk_stream_t stream);
 extern "C" int rk_gemv_int8_rows_impl(const void* x, int x_dtype, const void* q, int q_kind, const void* scale,
                                       int s_dtype, void* y, int y_dtype, int N, int K, int waves, int rows,
                                       rk_stream_t stream);
@@ -64,6 +69,15 @@ int rk_gemv_int4_g128_subn(const void* x, int x_dtype, const uint8_t* q, const u
                            const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
                            rk_stream_t stream) {
     return rk_gemv_int4_g128_impl(x, x_dtype, q, scale, min, y, y_dtype, N, K, waves, rows, 1, stream);
+}
+
+// Two independent int4 GEMVs (y1 = W1 x1, y2 = W2 x2) in one launch: the layer's o and down projections.
+int rk_gemv_int4_g128_pair(const void* x1, int x1_dtype, const uint8_t* q1, const uint16_t* s1, const uint16_t* m1,
+                           void* y1, int y1_dtype, int N1, int K1, const void* x2, int x2_dtype, const uint8_t* q2,
+                           const uint16_t* s2, const uint16_t* m2, void* y2, int y2_dtype, int N2, int K2,
+                           rk_stream_t stream) {
+    return rk_gemv_int4_g128_pair_impl(x1, x1_dtype, q1, s1, m1, y1, y1_dtype, N1, K1, x2, x2_dtype, q2, s2, m2, y2,
+                                       y2_dtype, N2, K2, stream);
 }
 
 int rk_gemv_int8_rows(const void* x, int x_dtype, const void* q, int q_kind, const void* scale, int s_dtype,

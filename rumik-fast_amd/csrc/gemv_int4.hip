@@ -107,13 +107,11 @@ RK_DEV float chunk_dot(u4_t w, const uint32_t (&xp)[16]) {
     }
 }
 
+// the GEMV of block `blk` (rows [blk * teams * R, ...)); `red`: LDS for the KS-way reduction
 template <int R, int KS, int NJ, bool SUBN>
-__global__ __launch_bounds__(kMaxThreads) void gemv_int4_kernel(const void* __restrict__ x, int xdt,
-                                                                const uint8_t* __restrict__ q,
-                                                                const uint16_t* __restrict__ sc,
-                                                                const uint16_t* __restrict__ mn,
-                                                                void* __restrict__ y, int ydt, int N, int K) {
-    __shared__ float red[kMaxThreads / 64][R];
+RK_DEV void gemv_int4_block(const void* __restrict__ x, int xdt, const uint8_t* __restrict__ q,
+                            const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, void* __restrict__ y,
+                            int ydt, int N, int K, int blk, float (*red)[R]) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int team = wave / KS;
@@ -122,7 +120,7 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_int4_kernel(const void* __re
     const int t = kw * 64 + lane;
     const int nch = K >> 5;
     const int ng = K >> 7;
-    const int row0 = (blockIdx.x * teams + team) * R;  // teams past N (last block only) clamp and store nothing
+    const int row0 = (blk * teams + team) * R;  // teams past N (last block only) clamp and store nothing
 
     const float sfold = SUBN ? 16777216.0f : 1.0f;  // 2^24 undoes the subnormal encoding of the codes
     float acc[R];
@@ -202,6 +200,37 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_int4_kernel(const void* __re
             store_act(y, ydt, (size_t)(row0 + lane), v);
         }
     }
+}
+
+template <int R, int KS, int NJ, bool SUBN>
+__global__ __launch_bounds__(kMaxThreads) void gemv_int4_kernel(const void* __restrict__ x, int xdt,
+                                                                const uint8_t* __restrict__ q,
+                                                                const uint16_t* __restrict__ sc,
+                                                                const uint16_t* __restrict__ mn,
+                                                                void* __restrict__ y, int ydt, int N, int K) {
+    __shared__ float red[kMaxThreads / 64][R];
+    gemv_int4_block<R, KS, NJ, SUBN>(x, xdt, q, sc, mn, y, ydt, N, K, blockIdx.x, red);
+}
+
+// Two independent GEMVs in one launch (blocks [0, nb1) the first, the rest the second), each with its own plan;
+// both run with the same block size. One launch instead of two saves a launch gap and one ramp / drain of the
+// memory stream (the o and down projections of a layer both wait only on the attention and the MLP activation).
+struct GemvArgs {
+    const void* x;
+    const uint8_t* q;
+    const uint16_t *s, *m;
+    void* y;
+    int N, K, xdt, ydt;
+};
+
+template <int R1, int KS1, int NJ1, int R2, int KS2, int NJ2>
+__global__ __launch_bounds__(kMaxThreads) void gemv_int4_pair_kernel(GemvArgs a, GemvArgs b, int nb1) {
+    __shared__ float red1[kMaxThreads / 64][R1];
+    __shared__ float red2[kMaxThreads / 64][R2];
+    if ((int)blockIdx.x < nb1)
+        gemv_int4_block<R1, KS1, NJ1, false>(a.x, a.xdt, a.q, a.s, a.m, a.y, a.ydt, a.N, a.K, blockIdx.x, red1);
+    else
+        gemv_int4_block<R2, KS2, NJ2, false>(b.x, b.xdt, b.q, b.s, b.m, b.y, b.ydt, b.N, b.K, blockIdx.x - nb1, red2);
 }
 
 template <int R, int KS, int NJ, bool SUBN>
@@ -297,4 +326,36 @@ extern "C" int rk_gemv_int4_g128_impl(const void* x, int x_dtype, const uint8_t*
         }
     }
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+
+// o-like (K <= 4096: 4 waves x 2 rows, one pass) + down-like (K <= 16384: 4 waves = 2 teams of 2 splitting K, 2 rows
+// each) in one launch; other shapes run as two launches of the single-GEMV plans.
+extern "C" int rk_gemv_int4_g128_pair_impl(const void* x1, int x1_dtype, const uint8_t* q1, const uint16_t* s1,
+                                           const uint16_t* m1, void* y1, int y1_dtype, int N1, int K1,
+                                           const void* x2, int x2_dtype, const uint8_t* q2, const uint16_t* s2,
+                                           const uint16_t* m2, void* y2, int y2_dtype, int N2, int K2,
+                                           rk_stream_t stream) {
+    if (!x1 || !q1 || !s1 || !m1 || !y1 || !x2 || !q2 || !s2 || !m2 || !y2) return RK_ERR_NULL;
+    if (N1 <= 0 || K1 <= 0 || K1 % 128 || N2 <= 0 || K2 <= 0 || K2 % 128) return RK_ERR_SHAPE;
+    for (int dt : {x1_dtype, x2_dtype})
+        if (dt != RK_F16 && dt != RK_BF16) return RK_ERR_DTYPE;
+    for (int dt : {y1_dtype, y2_dtype})
+        if (dt != RK_F16 && dt != RK_BF16 && dt != RK_F32) return RK_ERR_DTYPE;
+    if (((uintptr_t)x1 | (uintptr_t)q1 | (uintptr_t)x2 | (uintptr_t)q2) & 15) return RK_ERR_ALIGN;
+    const int nch1 = K1 / 32, nch2 = K2 / 32;
+    if (nch1 <= 64 && nch2 > 128 && nch2 <= 512) {
+        const GemvArgs a{x1, q1, s1, m1, y1, N1, K1, x1_dtype, y1_dtype};
+        const GemvArgs b{x2, q2, s2, m2, y2, N2, K2, x2_dtype, y2_dtype};
+        const int nb1 = (N1 + 7) / 8;   // 4 teams of 2 rows
+        const int nb2 = (N2 + 3) / 4;   // 2 teams of 2 rows
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        if (nch2 <= 384)
+            hipLaunchKernelGGL((gemv_int4_pair_kernel<2, 1, 1, 2, 2, 3>), dim3(nb1 + nb2), dim3(256), 0, st, a, b, nb1);
+        else
+            hipLaunchKernelGGL((gemv_int4_pair_kernel<2, 1, 1, 2, 2, 4>), dim3(nb1 + nb2), dim3(256), 0, st, a, b, nb1);
+        return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+    }
+    int e = rk_gemv_int4_g128_impl(x1, x1_dtype, q1, s1, m1, y1, y1_dtype, N1, K1, 0, 0, 0, stream);
+    if (e != RK_OK) return e;
+    return rk_gemv_int4_g128_impl(x2, x2_dtype, q2, s2, m2, y2, y2_dtype, N2, K2, 0, 0, 0, stream);
 }

@@ -2,7 +2,7 @@
 
 Mirrors RumikFused._step (reference engine/rumik_fused.py:97-121) with this build's kernels:
 
-    embed_ln(tok) -> 36 x [ gemv(w_in) -> post -> attn_split -> attn_combine -> gemv(w_o) -> gemv(w_down)
+    embed_ln(tok) -> 36 x [ gemv(w_in) -> post -> attn_split -> attn_combine -> gemv(w_o) + gemv(w_down) (one launch)
                              -> add_ln (next layer's LayerNorm; the final norm after the last layer) ]
     -> pos += 1 -> int8 audio head (fp32 logits)
 
@@ -118,8 +118,8 @@ class DecodeStep:
             fused.attn_split[(c.NKV, c.nsplit)](self.qb, self.kc[i], self.vc[i], self.pos, self.po, self.pm, self.pl,
                                                 c.S, scale, REP=c.NH // c.NKV, HD=c.HD, NSPLIT=c.nsplit)
             fused.attn_combine[(c.NH,)](self.po, self.pm, self.pl, self.pos, self.ob, HD=c.HD, NSPLIT=c.nsplit)
-            cuda_gemv.gemv_int4_cuda(self.ob, *w["w_o"][i], out=self.buf_o)
-            cuda_gemv.gemv_int4_cuda(self.act, *w["w_down"][i], out=self.buf_d)
+            cuda_gemv.gemv_int4_pair_cuda(self.ob, w["w_o"][i], self.act, w["w_down"][i], out1=self.buf_o,
+                                          out2=self.buf_d)
             fused.add_ln[(1,)](self.x, self.buf_o, self.buf_d, w["norm"] if i == c.L - 1 else w["ln"][i + 1], self.h,
                                c.eps, H=c.H)
         fused.pos_advance(self.pos)

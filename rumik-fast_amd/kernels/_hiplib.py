@@ -22,6 +22,7 @@ _SIGS = {
     "rk_gemv_int4_g128": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_mfma": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_valu": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_gemv_int4_g128_pair": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_subn": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_silu": ([_p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int8_rows": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _p], _i),

@@ -53,6 +53,21 @@ def gemv_int4_cuda(x, q, s, m, out=None, warps=None, rows=None):
     return y
 
 
+def gemv_int4_pair_cuda(x1, w1, x2, w2, out1=None, out2=None):
+    """Two independent int4 g128 GEMVs in one launch: (dequant(w1) @ x1, dequant(w2) @ x2), w = (q, s, m); the
+    decode layer's o and down projections (the reference's two gemv_int4 calls, engine/rumik_fused.py:115-116).
+    Same checks and outputs as two gemv_int4_cuda calls."""
+    y1 = out1 if out1 is not None else torch.empty(w1[0].shape[0], device=x1.device, dtype=x1.dtype)
+    y2 = out2 if out2 is not None else torch.empty(w2[0].shape[0], device=x2.device, dtype=x2.dtype)
+    N1, K1 = _check_int4(x1, *w1, y1)
+    N2, K2 = _check_int4(x2, *w2, y2)
+    st = H.lib().rk_gemv_int4_g128_pair(H.ptr(x1), H.dt(x1), H.ptr(w1[0]), H.ptr(w1[1]), H.ptr(w1[2]), H.ptr(y1),
+                                        H.dt(y1), N1, K1, H.ptr(x2), H.dt(x2), H.ptr(w2[0]), H.ptr(w2[1]),
+                                        H.ptr(w2[2]), H.ptr(y2), H.dt(y2), N2, K2, H.stream(x1.device))
+    H.check(st)
+    return y1, y2
+
+
 def gemv_int4_silu_cuda(x, q, s, m, n_plain, out=None, act=None):
     """The engine's w_in projection with SiLU(gate) * up fused: q = [n_plain rows | inter gate rows | inter up rows]
     (int4 g128) -> (y [n_plain] or None, act [inter]), equal to gemv_int4_cuda followed by act = silu(g) * u on the

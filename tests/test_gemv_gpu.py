@@ -248,3 +248,37 @@ def test_silu_fused_rejects_bad_arguments(dev):
                                     256, 0, H.stream(dev)) == -4  # y missing while n_plain > 0
     assert L.rk_gemv_int4_g128_silu(H.ptr(x), H.F16, H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(x), H.ptr(x), H.F16, 8, 0,
                                     256, 0, H.stream(dev)) == -1
+
+
+@pytest.mark.parametrize("N1,K1,N2,K2", [(2048, 2048, 2048, 11008), (17, 256, 5, 11008), (1001, 2048, 63, 16384),
+                                         (300, 4096, 40, 2048)])
+def test_pair_equals_two_gemvs(N1, K1, N2, K2, dev):
+    """rk_gemv_int4_g128_pair (one launch: the o and down projections) against the oracle for both outputs, and
+    bit-equal to rk_gemv_int4_g128_valu with its default plan for each (the last case, K1 = 4096 and K2 = 2048,
+    takes the two-launch fallback)."""
+    x1, q1, s1, m1 = synth.gemv_case(N1, K1, 31)
+    x2, q2, s2, m2 = synth.gemv_case(N2, K2, 32)
+    d1 = tuple(t.to(dev) for t in (x1, q1, s1, m1))
+    d2 = tuple(t.to(dev) for t in (x2, q2, s2, m2))
+    y1, y2 = cuda_gemv.gemv_int4_pair_cuda(d1[0], d1[1:], d2[0], d2[1:])
+    torch.cuda.synchronize()
+    _assert_parity(y1, _oracle(x1, q1, s1, m1), "first")
+    _assert_parity(y2, _oracle(x2, q2, s2, m2), "second")
+    # the same arithmetic per row as the single-GEMV VALU kernel's default plan: equal bits
+    for (x, q, s, m), y in ((d1, y1), (d2, y2)):
+        z = torch.full_like(y, 7.0)
+        H.check(H.lib().rk_gemv_int4_g128_valu(H.ptr(x), H.dt(x), H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(z), H.dt(z),
+                                               q.shape[0], q.shape[1] * 2, 0, 0, H.stream(dev)))
+        torch.cuda.synchronize()
+        assert torch.equal(y, z)
+
+
+def test_pair_rejects_bad_arguments(dev):
+    x, q, s, m = (t.to(dev) for t in synth.gemv_case(48, 256, 14))
+    L = H.lib()
+    args = lambda K2, xdt=H.F16: (H.ptr(x), H.F16, H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(x), H.F16, 48, 256,  # noqa
+                                  H.ptr(x), xdt, H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(x), H.F16, 48, K2, H.stream(dev))
+    assert L.rk_gemv_int4_g128_pair(*args(200)) == -1  # K2 not a multiple of 128: RK_ERR_SHAPE
+    assert L.rk_gemv_int4_g128_pair(*args(256, xdt=H.F32)) == -3  # fp32 x: RK_ERR_DTYPE
+    with pytest.raises(RuntimeError):
+        cuda_gemv.gemv_int4_pair_cuda(x[:128], (q, s, m), x, (q, s, m))

@@ -80,43 +80,45 @@ RK_DEV void x_issue(const void* __restrict__ x, int K, XRegs& xr) {
 // one 8-column block: fp16 pairs in dequant order (or bf16 converted) + its fp32 sum -> LDS fragment; the
 // 16 threads of a group then sum their parts inside a 16-lane DPP row
 RK_DEV void stage_block(int i, int nb, int xdt, u4_t d, uint4* __restrict__ frag, float* __restrict__ xsum) {
+    // the conversion runs unconditionally (only the LDS writes are guarded): a value used only under i < nb would let
+    // the compiler sink its load behind the weight loads, and the staging would then wait for all of them
+    const bool ok = i < nb;
     float sum = 0.f;
-    if (i < nb) {
-        uint32_t h[4];
-        const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-        if (xdt == RK_BF16) {
-            float f[8];
+    uint32_t h[4];
+    const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+    if (xdt == RK_BF16) {
+        float f[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                f[2 * e] = __builtin_bit_cast(float, d[e] << 16);
-                f[2 * e + 1] = __builtin_bit_cast(float, d[e] & 0xffff0000u);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sum += f[e];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                h2_t p;
-                p.x = (_Float16)f[e];
-                p.y = (_Float16)f[e + 4];
-                h[e] = as_u32(p);
-            }
-        } else {
-            h[0] = perm(d.z, d.x, 0x05040100u);  // (x0, x4)
-            h[1] = perm(d.z, d.x, 0x07060302u);  // (x1, x5)
-            h[2] = perm(d.w, d.y, 0x05040100u);  // (x2, x6)
-            h[3] = perm(d.w, d.y, 0x07060302u);  // (x3, x7)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
+        for (int e = 0; e < 4; ++e) {
+            f[2 * e] = __builtin_bit_cast(float, d[e] << 16);
+            f[2 * e + 1] = __builtin_bit_cast(float, d[e] & 0xffff0000u);
         }
-        const int g = i >> 4, r = i & 15;  // column offset in the group: 8r = 32s + 8t
-        const int s = r >> 2, t = r & 3;
-        frag[g * 16 + t * 4 + s] = make_uint4(h[0], h[1], h[2], h[3]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += f[e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            h2_t p;
+            p.x = (_Float16)f[e];
+            p.y = (_Float16)f[e + 4];
+            h[e] = as_u32(p);
+        }
+    } else {
+        h[0] = perm(d.z, d.x, 0x05040100u);  // (x0, x4)
+        h[1] = perm(d.z, d.x, 0x07060302u);  // (x1, x5)
+        h[2] = perm(d.w, d.y, 0x05040100u);  // (x2, x6)
+        h[3] = perm(d.w, d.y, 0x07060302u);  // (x3, x7)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
     }
+    const int g = i >> 4, r = i & 15;  // column offset in the group: 8r = 32s + 8t
+    const int s = r >> 2, t = r & 3;
+    if (ok) frag[g * 16 + t * 4 + s] = make_uint4(h[0], h[1], h[2], h[3]);
+    sum = ok ? sum : 0.f;
     sum += dpp<0x128>(sum);  // 16 consecutive threads hold one group: sum inside their 16-lane DPP row (row_ror:8)
     sum += dpp<0x124>(sum);  // row_ror:4
     sum += dpp<0x122>(sum);  // row_ror:2
     sum += dpp<0x121>(sum);  // row_ror:1
-    if (i < nb && (i & 15) == 0) xsum[i >> 4] = sum;
+    if (ok && (i & 15) == 0) xsum[i >> 4] = sum;
 }
 
 // XREG (K / 8 <= kXPre * blockDim, chosen on the host): every block of x is in registers already. It is a template
@@ -126,8 +128,9 @@ RK_DEV void stage_x(const void* __restrict__ x, int xdt, int K, const XRegs& xr,
                     float* __restrict__ xsum) {
     const int nb = K >> 3;  // 8-column blocks
     if constexpr (XREG) {
+        stage_block(threadIdx.x, nb, xdt, xr.d[0], frag, xsum);  // unguarded: its x load stays ahead of the weights
 #pragma unroll
-        for (int k = 0; k < kXPre; ++k)
+        for (int k = 1; k < kXPre; ++k)
             if (k * (int)blockDim.x < nb) stage_block(threadIdx.x + k * blockDim.x, nb, xdt, xr.d[k], frag, xsum);
     } else {
         for (int base = 0; base < nb; base += blockDim.x) {

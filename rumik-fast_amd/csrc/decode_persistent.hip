@@ -57,6 +57,7 @@ constexpr int kKVPre = 5;                  // cached slots per streamer whose K 
 constexpr int kHeadRows = 7;               // head rows per streamer loaded ahead (the rest load when used)
 constexpr int kWork = 16;                  // int16 entries per block in the work table
 constexpr int kPreRows = 1;                // ~0.5 us wait before the down / o partial poll
+constexpr int kPace = 24;                  // s_sleep(1) units between the streamers' next-layer load groups
 // x is polled by every block: it is published in kXRep copies 8 KB apart and block b polls copy b % kXRep, so no
 // 8 KB stretch of memory serves more than 16 pollers
 constexpr int kXRep = 16;
@@ -114,6 +115,14 @@ RK_DEV bool wait_more(const Params& p, uint64_t t0, uint32_t status) {
 // Every poller first waits `pre` x ~0.5 us (s_sleep 20): measured on 256 blocks, all-to-all exchanges complete
 // fastest when the first poll comes ~0.5 us after the data is written and polls then follow back to back; polls
 // sent long before the data exists only load the coherent path that every other exchange shares.
+// Streamers spread the next layer's loads over the window in which wave 0 gathers the rows, publishes x and polls
+// it back (they have nothing else to do until the next LayerNorm): a CU's memory requests are served in order, so
+// a poll issued behind the whole burst waited for all of it. Measured (36 layers, ctx 256 / 2048 us per token):
+// one burst 688 / 772, kPace 24 684 / 758, 32 680 / 758, 40 728 / 794 (longer than wave 0's window).
+RK_DEV void pace_wait(int n) {
+    for (int i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(1);
+}
+
 RK_DEV void pre_wait(int pre) {
     for (int i = 0; i < pre; ++i) __builtin_amdgcn_s_sleep(20);
 }
@@ -973,14 +982,16 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
 // sum) and meet at the same sequence of block barriers per layer:
 //   B0 x + LN statistics staged | B1 h staged | B2 partials of tiles [0, 3) | B3 (epilogue) | B4 q / k / v of
 //   those tiles published | B5 partials of tiles [3, 7), q staged | B6 (epilogue) | B7 act staged |
-//   B8 (attention) | BC combine parts of head b / 16 staged | BO its attention output staged | B9 down and o rows
-//   staged  -- then wave 0 publishes x.
+//   B8 (attention) | BC combine parts of head b / 16 staged | BO its attention output staged | B9 the streamers'
+//   next-layer loads issued; wave 0 reaches B9 only after its row gather, the x publication, the next layer's x
+//   poll and LayerNorm statistics (so it passes B9 and B0 back to back; nothing in LDS needs B9 earlier).
 //   Head: H0 LN statistics staged | H1 h staged.
 // The work table lists a block's q / k / v tiles first (at most 3), so they are computed and published in the
 // first pass and the q / k / v hop overlaps the second pass.
 // Streamer issue order (each wait covers only older loads, see tile_issue): tiles(l + 1) [0, 3) after the first
-// epilogue; after the o partials of layer l: O(l + 1), K/V(l + 1), tiles(l + 1) [3, 7), down(l + 1). The loop's
-// back edge and its preheader leave the same sequence outstanding. At most ~57 vector-memory instructions are in
+// epilogue; after the o partials of layer l, paced (pace_wait): tiles(l + 1) [3, 7), K/V(l + 1), down(l + 1),
+// O(l + 1) -- the order layer l + 1 consumes them. The loop's back edge and its preheader leave the same sequence
+// outstanding. At most ~57 vector-memory instructions are in
 // flight per streamer (the hardware counter holds 63).
 
 template <int REP>
@@ -1000,6 +1011,8 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
             if (l == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;  // every block has read pos
         }
         ln_stats(xw, lw, p.eps, S);
+        if (l > 0) __syncthreads();                           // B9 of layer l - 1 (after the row gather, the x
+                                                              // publication and this layer's x poll)
         __syncthreads();                                      // B0
         ln_apply_frag(S);
         __syncthreads();                                      // B1
@@ -1017,7 +1030,6 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
         comb_merge(S);
         __syncthreads();                                      // BO
         gather_rows(p, tag, S, kPreRows);
-        __syncthreads();                                      // B9
         if (lane < 8) S.xrow[lane] = rnd16(S.xrow[lane] + rnd16(S.orow[lane]) + rnd16(S.drow[lane]));
         static_assert(4 * kXRep <= 64, "one store per lane");
         if (lane < 4 * kXRep)  // lane = copy * 4 + pair
@@ -1032,6 +1044,7 @@ RK_DEV void poller_main(const Params& p, uint32_t step, int64_t pos, int64_t tok
     x_poll(p, tag_of(step, p.L - 1), xw);
     if (p.L == 1 && blockIdx.x == 0 && lane == 0) p.pos[0] = pos + 1;
     ln_stats(xw, lw, p.eps, S);
+    __syncthreads();                                          // B9 of the last layer
     __syncthreads();                                          // H0
     ln_apply_pairs(S);
     __syncthreads();                                          // H1
@@ -1045,13 +1058,13 @@ RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Wor
     DownRegs dr;
     KVRegs kv;
     ORegs orr;
-    // the same outstanding sequence the loop leaves behind at its back edge: tiles [0, 3), O, K/V, tiles [3, 7),
-    // down
+    // the same outstanding sequence the loop leaves behind at its back edge, in the order the layer consumes it:
+    // tiles [0, 3), tiles [3, 7), K/V, down, O
     tile_issue(p, 0, S, wk, tr, 0, kTileSplit);
-    o_issue(p, 0, orr);
-    kv_issue(p, 0, pos, kv);
     tile_issue(p, 0, S, wk, tr, kTileSplit, kMaxTiles);
+    kv_issue(p, 0, pos, kv);
     down_issue(p, 0, wk, dr);
+    o_issue(p, 0, orr);
     for (int l = 0; l < p.L; ++l) {
         const uint32_t tag = tag_of(step, l);
         const int ln = l + 1 < p.L ? l + 1 : l;  // the last layer re-issues its own (cache-resident) weights
@@ -1073,10 +1086,18 @@ RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Wor
         __syncthreads();                                      // BC
         __syncthreads();                                      // BO
         o_part(p, tag, orr, S);
-        o_issue(p, ln, orr);
+        // the next layer's loads in the order they are consumed, paced (wave 0 meanwhile gathers rows, publishes x,
+        // polls it back and computes the next LayerNorm statistics; it meets the streamers at B9)
+#pragma unroll
+        for (int t = kTileSplit; t < kMaxTiles; ++t) {
+            tile_issue(p, ln, S, wk, tr, t, t + 1);           // second part, one tile at a time
+            pace_wait(kPace);
+        }
         kv_issue(p, ln, pos, kv);
-        tile_issue(p, ln, S, wk, tr, kTileSplit, kMaxTiles);  // second part
+        pace_wait(kPace);
         down_issue(p, ln, wk, dr);
+        pace_wait(kPace);
+        o_issue(p, ln, orr);
         __syncthreads();                                      // B9
     }
     head_issue(p, tr);

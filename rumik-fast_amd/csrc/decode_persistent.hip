@@ -57,7 +57,7 @@ constexpr int kKVPre = 5;                  // cached slots per streamer whose K 
 constexpr int kHeadRows = 7;               // head rows per streamer loaded ahead (the rest load when used)
 constexpr int kWork = 16;                  // int16 entries per block in the work table
 constexpr int kPreRows = 1;                // ~0.5 us wait before the down / o partial poll
-constexpr int kPace = 24;                  // s_sleep(1) units between the streamers' next-layer load groups
+constexpr int kPace = 28;                  // s_sleep(1) units between the streamers' next-layer load groups
 // x is polled by every block: it is published in kXRep copies 8 KB apart and block b polls copy b % kXRep, so no
 // 8 KB stretch of memory serves more than 16 pollers
 constexpr int kXRep = 16;
@@ -118,7 +118,9 @@ RK_DEV bool wait_more(const Params& p, uint64_t t0, uint32_t status) {
 // Streamers spread the next layer's loads over the window in which wave 0 gathers the rows, publishes x and polls
 // it back (they have nothing else to do until the next LayerNorm): a CU's memory requests are served in order, so
 // a poll issued behind the whole burst waited for all of it. Measured (36 layers, ctx 256 / 2048 us per token):
-// one burst 688 / 772, kPace 24 684 / 758, 32 680 / 758, 40 728 / 794 (longer than wave 0's window).
+// one burst 688 / 772, kPace 24 684 / 758, 32 680 / 758, 40 728 / 794 (longer than wave 0's window); with the
+// down prefetch in three pieces (half a pace apart) and no pre-wait before the x poll: kPace 24 684 / 755, 28
+// 666 / 743, 32 672 / 748, 36 694 / 765.
 RK_DEV void pace_wait(int n) {
     for (int i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(1);
 }
@@ -234,8 +236,9 @@ RK_DEV bool x_poll(const Params& p, uint32_t tag, XWave& xw) {
     const uint64_t* tx =
         reinterpret_cast<const uint64_t*>(p.tx) + (blockIdx.x % kXRep) * kRepQwords + opaque_vgpr(0u);
     uint32_t v[16];
+    // no pre-wait: x is polled after the row gather and the x publication, when most rows are out already
     const bool ok = poll_pairs<16>(
-        p, tag, [&](int k) -> const uint64_t* { return tx + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v);
+        p, tag, [&](int k) -> const uint64_t* { return tx + 4 * (lane + 64 * (k >> 2)) + (k & 3); }, v, 0);
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
@@ -464,12 +467,14 @@ struct DownRegs {
     u2_t sm[kRP][2];  // the block's slices span at most two groups
 };
 
+// row-pair sets [KB, KE) of the lane (the whole set at once, or in pieces to pace the issue)
+template <int KB = 0, int KE = kRP>
 RK_DEV void down_issue(const Params& p, int l, const Work& wk, DownRegs& dr) {
     const int sl = threadIdx.x - 64;
     const int nsl = p.inter / 16, ngd = p.inter / 128;
     const int gb = wk.sb / 8;
 #pragma unroll
-    for (int k = 0; k < kRP; ++k) {
+    for (int k = KB; k < KE; ++k) {
         const int rp = min(sl + kSLanes * k, kH / 2 - 1);
 #pragma unroll
         for (int i = 0; i < kMaxSlices; ++i)
@@ -1095,8 +1100,13 @@ RK_DEV void streamer_main(const Params& p, int64_t pos, uint32_t step, const Wor
         }
         kv_issue(p, ln, pos, kv);
         pace_wait(kPace);
-        down_issue(p, ln, wk, dr);
-        pace_wait(kPace);
+        static_assert(kRP == 3, "three down pieces");
+        down_issue<0, 1>(p, ln, wk, dr);
+        pace_wait(kPace / 2);
+        down_issue<1, 2>(p, ln, wk, dr);
+        pace_wait(kPace / 2);
+        down_issue<2, 3>(p, ln, wk, dr);
+        pace_wait(kPace / 2);
         o_issue(p, ln, orr);
         __syncthreads();                                      // B9
     }

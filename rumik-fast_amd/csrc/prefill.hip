@@ -16,6 +16,8 @@
 // reference's tensor-core PV in 16-bit) to its LDS tile in the A layout and accumulates O += P V (8 MFMAs, fp32).
 #include "common.h"
 
+#include <initializer_list>
+
 namespace {
 
 constexpr int kRowThreads = 256;
@@ -103,6 +105,136 @@ __global__ __launch_bounds__(kRowThreads) void add_ln_rows_kernel(void* x, const
     ln_row(xv, w, (char*)h + r0 * (dt == RK_F32 ? 4 : 2), dt, H, eps, red);
 }
 
+// ---- 16-byte vector forms (fp16 / bf16 with H % 8 == 0 and 16-byte aligned rows): a thread holds 8-column chunks
+// c = tid + 256 k of the row; every load of the row is issued before the first use. Same arithmetic as the scalar
+// kernels above (sum in fp32, rounded once; LayerNorm statistics in fp32 over the rounded x).
+constexpr int kVecPer = 4;  // 8-column chunks per thread: H <= 8192
+
+template <bool BF16>
+RK_DEV void unpack8(const u4_t& d, float (&f)[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if constexpr (BF16) {
+            f[2 * e] = __builtin_bit_cast(float, d[e] << 16);
+            f[2 * e + 1] = __builtin_bit_cast(float, d[e] & 0xffff0000u);
+        } else {
+            const h2_t v = as_h2(d[e]);
+            f[2 * e] = (float)v.x;
+            f[2 * e + 1] = (float)v.y;
+        }
+    }
+}
+
+template <bool BF16>
+RK_DEV u4_t pack8(const float (&f)[8]) {
+    u4_t d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if constexpr (BF16)
+            d[e] = (uint32_t)f32_to_bf16_bits(f[2 * e]) | ((uint32_t)f32_to_bf16_bits(f[2 * e + 1]) << 16);
+        else
+            d[e] = (uint32_t)f32_to_f16_bits(f[2 * e]) | ((uint32_t)f32_to_f16_bits(f[2 * e + 1]) << 16);
+    }
+    return d;
+}
+
+// LayerNorm of the thread's chunks (values v, valid chunks c < nc) -> h row (chunk-indexed)
+template <bool BF16>
+RK_DEV void ln_chunks(float (&v)[kVecPer][8], const u4_t (&wd)[kVecPer], u4_t* __restrict__ h4, int nc, int H,
+                      float eps, float* red) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kVecPer; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[k][e];  // zero past the row
+    const float mean = block_sum(s, red) / (float)H;
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kVecPer; ++k)
+        if ((int)threadIdx.x + 256 * k < nc)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = v[k][e] - mean;
+                ss += d * d;
+            }
+    const float rstd = 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps);
+#pragma unroll
+    for (int k = 0; k < kVecPer; ++k) {
+        const int c = threadIdx.x + 256 * k;
+        if (c < nc) {
+            float w[8], o[8];
+            unpack8<BF16>(wd[k], w);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (v[k][e] - mean) * rstd * w[e];
+            h4[c] = pack8<BF16>(o);
+        }
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void add_ln_rows_vec_kernel(u4_t* __restrict__ x, const u4_t* __restrict__ a,
+                                                              const u4_t* __restrict__ b, const u4_t* __restrict__ w,
+                                                              u4_t* __restrict__ h, int H, float eps) {
+    __shared__ float red[16];
+    const int nc = H >> 3;
+    const size_t r0 = (size_t)blockIdx.x * nc;
+    u4_t xd[kVecPer], ad[kVecPer], bd[kVecPer], wd[kVecPer];
+#pragma unroll
+    for (int k = 0; k < kVecPer; ++k) {  // clamped, unconditional loads
+        const int c = min((int)threadIdx.x + 256 * k, nc - 1);
+        xd[k] = x[r0 + c];
+        ad[k] = a[r0 + c];
+        bd[k] = b ? b[r0 + c] : u4_t{0u, 0u, 0u, 0u};
+        wd[k] = w[c];
+    }
+    float v[kVecPer][8];
+#pragma unroll
+    for (int k = 0; k < kVecPer; ++k) {
+        const int c = threadIdx.x + 256 * k;
+        float fx[8], fa[8], fb[8];
+        unpack8<BF16>(xd[k], fx);
+        unpack8<BF16>(ad[k], fa);
+        unpack8<BF16>(bd[k], fb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][e] = c < nc ? round_act(fx[e] + fa[e] + fb[e], BF16 ? RK_BF16 : RK_F16) : 0.f;
+        if (c < nc) x[r0 + c] = pack8<BF16>(v[k]);
+    }
+    ln_chunks<BF16>(v, wd, h + r0, nc, H, eps, red);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void embed_ln_rows_vec_kernel(const int64_t* ids, const int8_t* eq,
+                                                                const uint16_t* es, const u4_t* __restrict__ w,
+                                                                u4_t* __restrict__ x, u4_t* __restrict__ h, int H,
+                                                                float eps) {
+    __shared__ float red[16];
+    const int nc = H >> 3;
+    const size_t r0 = (size_t)blockIdx.x * nc;
+    const int64_t id = ids[blockIdx.x];
+    const float sc = f16_bits_to_f32(es[id]);
+    const uint2* row = reinterpret_cast<const uint2*>(eq + (size_t)id * H);
+    uint2 qd[kVecPer];
+    u4_t wd[kVecPer];
+#pragma unroll
+    for (int k = 0; k < kVecPer; ++k) {
+        const int c = min((int)threadIdx.x + 256 * k, nc - 1);
+        qd[k] = row[c];
+        wd[k] = w[c];
+    }
+    float v[kVecPer][8];
+#pragma unroll
+    for (int k = 0; k < kVecPer; ++k) {
+        const int c = threadIdx.x + 256 * k;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int8_t q = (int8_t)(((e < 4 ? qd[k].x : qd[k].y) >> (8 * (e & 3))) & 0xFF);
+            v[k][e] = c < nc ? round_act((float)q * sc, BF16 ? RK_BF16 : RK_F16) : 0.f;
+        }
+        if (c < nc) x[r0 + c] = pack8<BF16>(v[k]);
+    }
+    ln_chunks<BF16>(v, wd, h + r0, nc, H, eps, red);
+}
+
 // grid (T, NH + 2 NKV + ceil(inter / 256)), 64 threads: block (t, b) as post_kernel of the decode glue for row t
 __global__ __launch_bounds__(64) void post_rows_kernel(const void* y, int ldy, int p0, const void* cos_t,
                                                        const void* sin_t, void* kc, void* vc, void* qo, void* act,
@@ -140,6 +272,55 @@ __global__ __launch_bounds__(64) void post_rows_kernel(const void* y, int ldy, i
             const float g = load_act(y, dt, yr + base + c), u = load_act(y, dt, yr + base + inter + c);
             store_act(act, dt, (size_t)t * inter + c, g / (1.0f + __expf(-g)) * u);
         }
+    }
+}
+
+// post_rows, one block of 256 threads per row t: the q / k heads as 32-bit pairs (RoPE), v and silu(gate) * up as
+// 8-column chunks (shapes with HD % 8 == 0, inter % 8 == 0 and 16-byte aligned rows)
+template <bool BF16>
+__global__ __launch_bounds__(256) void post_rows_vec_kernel(const uint16_t* __restrict__ y, int ldy, int p0,
+                                                            const uint16_t* __restrict__ cos_t,
+                                                            const uint16_t* __restrict__ sin_t,
+                                                            uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                            uint16_t* __restrict__ qo, uint16_t* __restrict__ act,
+                                                            int NH, int NKV, int HD, int S, int inter, int rope) {
+    const int t = blockIdx.x, tid = threadIdx.x, pos = p0 + t;
+    const uint16_t* yr = y + (size_t)t * ldy;
+    const int dt = BF16 ? RK_BF16 : RK_F16;
+    const int hp = HD / 2;
+    for (int pi = tid; pi < (NH + NKV) * hp; pi += 256) {
+        const int hd = pi / hp, j = pi - hd * hp;
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(yr + (size_t)hd * HD + 2 * j);
+        const float xe = load_act(&v, dt, 0), xo = load_act(&v, dt, 1);
+        float oe = xe, oo = xo;
+        if (rope) {
+            const float c = load_act(cos_t, dt, (size_t)pos * HD + 2 * j);
+            const float sn = load_act(sin_t, dt, (size_t)pos * HD + 2 * j);
+            oe = xe * c - xo * sn;
+            oo = xo * c + xe * sn;
+        }
+        uint32_t o;
+        store_act(&o, dt, 0, oe);
+        store_act(&o, dt, 1, oo);
+        uint16_t* dst = hd < NH ? qo + (size_t)t * NH * HD + (size_t)hd * HD + 2 * j
+                                : kc + ((size_t)(hd - NH) * S + pos) * HD + 2 * j;
+        *reinterpret_cast<uint32_t*>(dst) = o;
+    }
+    const u4_t* y4 = reinterpret_cast<const u4_t*>(yr);
+    const int vb = (NH + NKV) * HD / 8, nv = NKV * HD / 8;
+    for (int c = tid; c < nv; c += 256) {
+        const int hv = (8 * c) / HD, off = 8 * c - hv * HD;
+        *reinterpret_cast<u4_t*>(vc + ((size_t)hv * S + pos) * HD + off) = y4[vb + c];
+    }
+    const int gb = (NH + 2 * NKV) * HD / 8, ni = inter / 8;
+    u4_t* a4 = reinterpret_cast<u4_t*>(act + (size_t)t * inter);
+    for (int c = tid; c < ni; c += 256) {
+        float g[8], u[8], o[8];
+        unpack8<BF16>(y4[gb + c], g);
+        unpack8<BF16>(y4[gb + ni + c], u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
+        a4[c] = pack8<BF16>(o);
     }
 }
 
@@ -267,6 +448,14 @@ __global__ __launch_bounds__(512) void prefill_attn_kernel(const uint16_t* q, co
 
 bool act_dt(int dt) { return dt == RK_F16 || dt == RK_BF16; }
 
+// the vector row kernels: rows of H 2-byte values in 8-column chunks, every pointer 16-byte aligned
+bool vec_rows(int H, std::initializer_list<const void*> ptrs) {
+    if (H % 8 || H > 8 * 256 * kVecPer) return false;
+    for (const void* q : ptrs)
+        if ((uintptr_t)q & 15) return false;
+    return true;
+}
+
 }  // namespace
 
 extern "C" int rk_embed_ln_rows(const int64_t* ids, const int8_t* emb_q, const uint16_t* emb_s, const void* ln_w,
@@ -274,8 +463,18 @@ extern "C" int rk_embed_ln_rows(const int64_t* ids, const int8_t* emb_q, const u
     if (!ids || !emb_q || !emb_s || !ln_w || !x || !h) return RK_ERR_NULL;
     if (!act_dt(dt)) return RK_ERR_DTYPE;
     if (T <= 0 || H <= 0 || H > kRowThreads * kMaxPer) return RK_ERR_SHAPE;
-    hipLaunchKernelGGL(embed_ln_rows_kernel, dim3(T), dim3(kRowThreads), 0, (hipStream_t)stream, ids, emb_q, emb_s,
-                       ln_w, x, h, dt, H, eps);
+    const hipStream_t st = (hipStream_t)stream;
+    if (vec_rows(H, {ln_w, x, h}) && H % 8 == 0 && !((uintptr_t)emb_q & 7)) {
+        if (dt == RK_BF16)
+            hipLaunchKernelGGL(embed_ln_rows_vec_kernel<true>, dim3(T), dim3(256), 0, st, ids, emb_q, emb_s,
+                               (const u4_t*)ln_w, (u4_t*)x, (u4_t*)h, H, eps);
+        else
+            hipLaunchKernelGGL(embed_ln_rows_vec_kernel<false>, dim3(T), dim3(256), 0, st, ids, emb_q, emb_s,
+                               (const u4_t*)ln_w, (u4_t*)x, (u4_t*)h, H, eps);
+    } else {
+        hipLaunchKernelGGL(embed_ln_rows_kernel, dim3(T), dim3(kRowThreads), 0, st, ids, emb_q, emb_s, ln_w, x, h, dt,
+                           H, eps);
+    }
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 
@@ -284,8 +483,17 @@ extern "C" int rk_add_ln_rows(void* x, const void* a, const void* b, const void*
     if (!x || !a || !ln_w || !h) return RK_ERR_NULL;
     if (!act_dt(dt)) return RK_ERR_DTYPE;
     if (T <= 0 || H <= 0 || H > kRowThreads * kMaxPer) return RK_ERR_SHAPE;
-    hipLaunchKernelGGL(add_ln_rows_kernel, dim3(T), dim3(kRowThreads), 0, (hipStream_t)stream, x, a, b, ln_w, h, dt,
-                       H, eps);
+    const hipStream_t st = (hipStream_t)stream;
+    if (vec_rows(H, {x, a, ln_w, h}) && (!b || !((uintptr_t)b & 15))) {
+        if (dt == RK_BF16)
+            hipLaunchKernelGGL(add_ln_rows_vec_kernel<true>, dim3(T), dim3(256), 0, st, (u4_t*)x, (const u4_t*)a,
+                               (const u4_t*)b, (const u4_t*)ln_w, (u4_t*)h, H, eps);
+        else
+            hipLaunchKernelGGL(add_ln_rows_vec_kernel<false>, dim3(T), dim3(256), 0, st, (u4_t*)x, (const u4_t*)a,
+                               (const u4_t*)b, (const u4_t*)ln_w, (u4_t*)h, H, eps);
+    } else {
+        hipLaunchKernelGGL(add_ln_rows_kernel, dim3(T), dim3(kRowThreads), 0, st, x, a, b, ln_w, h, dt, H, eps);
+    }
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 
@@ -297,9 +505,26 @@ extern "C" int rk_post_rows(const void* y, int ldy, int p0, const void* cos_t, c
     if (T <= 0 || NH <= 0 || NKV <= 0 || HD <= 0 || HD % 2 || inter <= 0 || p0 < 0 || p0 + T > S ||
         ldy < (NH + 2 * NKV) * HD + 2 * inter)
         return RK_ERR_SHAPE;
-    const dim3 grid(T, NH + 2 * NKV + (inter + 255) / 256);
-    hipLaunchKernelGGL(post_rows_kernel, grid, dim3(64), 0, (hipStream_t)stream, y, ldy, p0, cos_t, sin_t, kc, vc,
-                       q_out, act, dt, NH, NKV, HD, S, inter, rope);
+    const hipStream_t st = (hipStream_t)stream;
+    const bool vec = HD % 8 == 0 && inter % 8 == 0 && ldy % 8 == 0 && !((uintptr_t)y & 15) && !((uintptr_t)vc & 15) &&
+                     !((uintptr_t)act & 15) && !((uintptr_t)kc & 3) && !((uintptr_t)q_out & 3);
+    if (vec) {
+        const auto* y16 = static_cast<const uint16_t*>(y);
+        const auto* c16 = static_cast<const uint16_t*>(cos_t);
+        const auto* s16 = static_cast<const uint16_t*>(sin_t);
+        if (dt == RK_BF16)
+            hipLaunchKernelGGL(post_rows_vec_kernel<true>, dim3(T), dim3(256), 0, st, y16, ldy, p0, c16, s16,
+                               (uint16_t*)kc, (uint16_t*)vc, (uint16_t*)q_out, (uint16_t*)act, NH, NKV, HD, S, inter,
+                               rope);
+        else
+            hipLaunchKernelGGL(post_rows_vec_kernel<false>, dim3(T), dim3(256), 0, st, y16, ldy, p0, c16, s16,
+                               (uint16_t*)kc, (uint16_t*)vc, (uint16_t*)q_out, (uint16_t*)act, NH, NKV, HD, S, inter,
+                               rope);
+    } else {
+        const dim3 grid(T, NH + 2 * NKV + (inter + 255) / 256);
+        hipLaunchKernelGGL(post_rows_kernel, grid, dim3(64), 0, st, y, ldy, p0, cos_t, sin_t, kc, vc, q_out, act, dt,
+                           NH, NKV, HD, S, inter, rope);
+    }
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 

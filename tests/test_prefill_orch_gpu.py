@@ -110,3 +110,87 @@ def test_generate_from_batched_prefill(dev):
     toks, st = gen.generate(prompt, seed=1)
     print(st)
     assert len(toks) == 33 and all(0 <= t < cfg.vocab - 1 for t in toks)
+
+
+# ---- the row kernels on their own (vector path: H % 8 == 0 and 16-byte aligned rows; scalar path otherwise)
+@pytest.mark.parametrize("dtype,H,T,offset", [(torch.float16, 2048, 37, 0), (torch.bfloat16, 2048, 5, 0),
+                                              (torch.float16, 200, 9, 0), (torch.float16, 196, 9, 0),
+                                              (torch.float16, 2048, 3, 1)])
+def test_add_ln_rows(dev, dtype, H, T, offset):
+    """x[t] = dt(x[t] + a[t] + b[t]) exactly; h[t] = LayerNorm(x[t]) * w against the oracle's fp32 LayerNorm.
+    H = 200 takes the vector kernel with a partial last pass, H = 196 (rows not 16-byte aligned) and offset = 1
+    (every buffer shifted by one element) the scalar one."""
+    g = torch.Generator().manual_seed(H + T)
+    x, a, b = (torch.randn(T * H + offset, generator=g).to(dtype) for _ in range(3))
+    w = (torch.rand(H + offset, generator=g) + 0.5).to(dtype)
+    xd, ad, bd, wd = (t.to(dev) for t in (x, a, b, w))
+    hd = torch.empty(T * H + offset, dtype=dtype, device=dev)
+    PF.add_ln_rows(xd[offset:], ad[offset:], bd[offset:], wd[offset:], hd[offset:], T, 1e-5)
+    torch.cuda.synchronize()
+    xs = (x[offset:].float() + a[offset:].float() + b[offset:].float()).to(dtype)
+    assert torch.equal(xd[offset:].cpu(), xs)
+    tol = 2e-3 if dtype == torch.float16 else 1.6e-2
+    wf = w[offset:].float().numpy()
+    for t in range(T):
+        ref = OG.cohere_ln(xs[t * H:(t + 1) * H].float().numpy(), wf)
+        np.testing.assert_allclose(_np(hd[offset + t * H:offset + (t + 1) * H]), ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.float16, 2048), (torch.bfloat16, 2048), (torch.float16, 200),
+                                     (torch.float16, 196)])
+def test_embed_ln_rows(dev, dtype, H):
+    g = torch.Generator().manual_seed(H)
+    eq = torch.randint(-127, 128, (40, H), generator=g, dtype=torch.int8)
+    es = (torch.rand(40, generator=g) * 0.01 + 1e-3).half()
+    w = (torch.rand(H, generator=g) + 0.5).to(dtype)
+    ids = torch.tensor([3, 17, 39, 0, 17], dtype=torch.int64)
+    x = torch.empty(len(ids), H, dtype=dtype, device=dev)
+    h = torch.empty_like(x)
+    PF.embed_ln_rows(ids.to(dev), eq.to(dev), es.to(dev), w.to(dev), x, h, 1e-5)
+    torch.cuda.synchronize()
+    tol = 2e-3 if dtype == torch.float16 else 1.6e-2
+    for t, i in enumerate(ids.tolist()):
+        xr = (eq[i].float() * es[i].float()).to(dtype)
+        assert torch.equal(x[t].cpu(), xr)
+        np.testing.assert_allclose(_np(h[t]), OG.cohere_ln(xr.float().numpy(), w.float().numpy()), rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("dtype,p0,T,rope,act_offset", [(torch.float16, 0, 7, True, 0), (torch.float16, 100, 33, True, 0),
+                                                        (torch.bfloat16, 5, 4, True, 0), (torch.float16, 9, 6, False, 0),
+                                                        (torch.float16, 3, 5, True, 1)])
+def test_post_rows(dev, dtype, p0, T, rope, act_offset):
+    """per row t at position p0 + t: q / k with the interleaved RoPE (oracle.rope), K / V into the cache slot, v
+    copied exactly, act = silu(gate) * up (oracle.silu); act_offset = 1 misaligns act (the scalar kernel)."""
+    NH, NKV, HD, inter, S = 16, 4, 128, 11008, 256
+    n_in = (NH + 2 * NKV) * HD + 2 * inter
+    g = torch.Generator().manual_seed(p0 + T)
+    y = torch.randn(T, n_in, generator=g).to(dtype)
+    cos, sin = (torch.tensor(t).to(dtype) for t in OG.rope_tables(S, HD))
+    kc = torch.zeros(NKV, S, HD, dtype=dtype, device=dev)
+    vc = torch.zeros_like(kc)
+    qo = torch.empty(T, NH * HD, dtype=dtype, device=dev)
+    actb = torch.empty(T * inter + act_offset, dtype=dtype, device=dev)
+    PF.post_rows(y.to(dev), p0, cos.to(dev), sin.to(dev), kc, vc, qo, actb[act_offset:], T, NH, NKV, HD, S, inter,
+                 rope)
+    torch.cuda.synchronize()
+    act = actb[act_offset:].view(T, inter)
+    tol = 2e-3 if dtype == torch.float16 else 1.6e-2
+    for t in range(T):
+        yf = y[t].float().numpy()
+        q = yf[:NH * HD].reshape(NH, HD)
+        k = yf[NH * HD:(NH + NKV) * HD].reshape(NKV, HD)
+        v = yf[(NH + NKV) * HD:(NH + 2 * NKV) * HD].reshape(NKV, HD)
+        gt, up = yf[(NH + 2 * NKV) * HD:][:inter], yf[(NH + 2 * NKV) * HD:][inter:]
+        pos = p0 + t
+        if rope:
+            q = OG.rope(q, cos[pos].float().numpy(), sin[pos].float().numpy())
+            k = OG.rope(k, cos[pos].float().numpy(), sin[pos].float().numpy())
+        else:
+            assert np.array_equal(_np(qo[t]).reshape(NH, HD), q)
+        np.testing.assert_allclose(_np(qo[t]).reshape(NH, HD), q, rtol=tol, atol=tol)
+        np.testing.assert_allclose(_np(kc[:, pos]), k, rtol=tol, atol=tol)
+        assert np.array_equal(_np(vc[:, pos]), v)
+        np.testing.assert_allclose(_np(act[t]), OG.silu(gt) * up, rtol=tol, atol=tol)
+    untouched = torch.ones(S, dtype=torch.bool)
+    untouched[p0:p0 + T] = False
+    assert torch.count_nonzero(kc[:, untouched]) == 0 and torch.count_nonzero(vc[:, untouched]) == 0

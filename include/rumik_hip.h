@@ -250,7 +250,7 @@ int rk_post_rows(const void* y, int ldy, int p0, const void* cos_t, const void* 
 /* Causal GQA attention for the prompt on the matrix cores: o[t, h] = softmax(q[t, h] . K[g, 0..p0+t]^T * scale)
  * V[g, 0..p0+t], g = h / (NH / NKV). Replaces _attend (engine/rumik_int4.py:163-171, fp32 scores; here fp32
  * scores and softmax, P in fp16 for the PV product, fp32 accumulation). q, o [T, NH*128] fp16; kc, vc [NKV, S, 128]
- * fp16 (one layer), 16-byte aligned; HD = 128, NH / NKV <= 8, p0 + T <= S. */
+ * fp16 (one layer), 16-byte aligned; HD = 128, NH / NKV in {1, 2, 4, 8}, p0 + T <= S. */
 int rk_prefill_attn(const void* q, const void* kc, const void* vc, void* o, int dt, int T, int p0, int NH, int NKV,
                     int HD, int S, float scale, rk_stream_t stream);
 

@@ -342,14 +342,49 @@ RK_DEV float row16_sum(float v) {
 
 // grid (NKV, ceil(T / 16)), 64 * REP threads. q: [T, NH * 128] fp16 (RoPE applied); kc / vc: the layer's cache
 // [NKV, S, 128] fp16 holding slots 0 .. p0 + T - 1; o: [T, NH * 128] fp16. Query t attends slots 0 .. p0 + t.
-__global__ __launch_bounds__(512) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                                                           uint16_t* o, int T, int p0, int NH, int NKV, int S,
-                                                           float scale) {
+// the K / V chunks (8 dims of one key) of a key block that thread tid stages: CH = 512 / blockDim per thread
+template <int CH>
+struct KVChunks {
+    u4_t k[CH], v[CH];  // native vectors (HIP's uint4 is a struct with a union, which stays in scratch memory)
+};
+
+// loads of key block j0 (slots past `last` re-read slot `last`: every load valid and unconditional, so the compiler
+// waits for exactly the chunks it stores; those keys are masked out of S and get P = 0)
+template <int CH>
+RK_DEV void kv_load(const uint16_t* kg, const uint16_t* vg, int j0, int last, KVChunks<CH>& c) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+        const int e = threadIdx.x + u * blockDim.x, kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
+        const size_t row = (size_t)min(j0 + kj, last) * kHD + d8;
+        c.k[u] = *reinterpret_cast<const u4_t*>(kg + row);
+        c.v[u] = *reinterpret_cast<const u4_t*>(vg + row);
+    }
+}
+
+template <int CH>
+RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kHD], uint16_t (*Vt)[kKB]) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+        const int e = threadIdx.x + u * blockDim.x, kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
+        *reinterpret_cast<u4_t*>(&Ks[kj][d8]) = c.k[u];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            Vt[d8 + 2 * w][kj] = (uint16_t)c.v[u][w];
+            Vt[d8 + 2 * w + 1][kj] = (uint16_t)(c.v[u][w] >> 16);
+        }
+    }
+}
+
+template <int REP>
+__global__ __launch_bounds__(64 * REP) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc,
+                                                                 const uint16_t* vc, uint16_t* o, int T, int p0,
+                                                                 int NH, int NKV, int S, float scale) {
+    constexpr int CH = kKB * kHD / 8 / (64 * REP);
     __shared__ __align__(16) uint16_t Ks[kKB][kHD];     // K rows of the key block
     __shared__ __align__(16) uint16_t Vt[kHD][kKB];     // V transposed: Vt[dim][key]
     extern __shared__ __align__(16) uint16_t Ps[];      // per wave: P [16 queries][32 keys]
     const int g = blockIdx.x, q0 = blockIdx.y * kQT;
-    const int lane = threadIdx.x & 63, r = threadIdx.x >> 6, REP = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, r = threadIdx.x >> 6;
     const int h = g * REP + r;
     const int li = lane & 15, lq = lane >> 4;  // A / B fragment: row or column li, k-group lq
     const int ldq = NH * kHD;
@@ -374,67 +409,70 @@ __global__ __launch_bounds__(512) void prefill_attn_kernel(const uint16_t* q, co
     const uint16_t* kg = kc + (size_t)g * S * kHD;
     const uint16_t* vg = vc + (size_t)g * S * kHD;
     const int last = p0 + min(q0 + kQT, T) - 1;  // the last slot any query of the tile sees
-    for (int j0 = 0; j0 <= last; j0 += kKB) {
-        __syncthreads();  // the previous block step's K / V are no longer read
-        for (int e = threadIdx.x; e < kKB * kHD / 8; e += blockDim.x) {
-            const int kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
-            const bool ok = j0 + kj <= last;
-            const uint4 kv = ok ? *reinterpret_cast<const uint4*>(kg + (size_t)(j0 + kj) * kHD + d8) : make_uint4(0, 0, 0, 0);
-            const uint4 vv = ok ? *reinterpret_cast<const uint4*>(vg + (size_t)(j0 + kj) * kHD + d8) : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4*>(&Ks[kj][d8]) = kv;
-            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                Vt[d8 + 2 * u][kj] = (uint16_t)vw[u];
-                Vt[d8 + 2 * u + 1][kj] = (uint16_t)(vw[u] >> 16);
-            }
+    // K / V of the next two key blocks are in flight in registers while a block is computed: set A holds the even
+    // steps, set B the odd ones (the loop is unrolled by two so that neither is copied)
+    KVChunks<CH> ka, kb;
+    kv_load<CH>(kg, vg, 0, last, ka);
+    kv_load<CH>(kg, vg, kKB, last, kb);
+    // one key block step (a macro, not a lambda: the register sets must stay promotable to registers)
+#define RK_ATTN_STEP(j0, cur) \
+    __syncthreads();  /* the previous block step's K / V are no longer read */ \
+    kv_store<CH>(cur, Ks, Vt); \
+    __syncthreads(); \
+    kv_load<CH>(kg, vg, j0 + 2 * kKB, last, cur);  /* two steps ahead (clamped: past the end it re-reads `last`) */ \
+    /* S = Q K^T for keys j0 + 16 hf + li (D layout: row 4 lq + e, key li) */ \
+    f4_t Sd[2]; \
+_Pragma("unroll") \
+    for (int hf = 0; hf < 2; ++hf) { \
+        f4_t d = {0.f, 0.f, 0.f, 0.f}; \
+_Pragma("unroll") \
+        for (int c = 0; c < 4; ++c) { \
+            const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Ks[16 * hf + li][32 * c + 8 * lq])); \
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Qf[c], B, d, 0, 0, 0); \
+        } \
+        Sd[hf] = d; \
+    } \
+    float alpha[4]; \
+_Pragma("unroll") \
+    for (int e = 0; e < 4; ++e) { \
+        const int qpos = p0 + q0 + 4 * lq + e; \
+        float s0 = Sd[0][e] * scale, s1 = Sd[1][e] * scale; \
+        if (j0 + li > qpos) s0 = -INFINITY; \
+        if (j0 + 16 + li > qpos) s1 = -INFINITY; \
+        const float mb = row16_max(fmaxf(s0, s1)); \
+        const float mn = fmaxf(m[e], mb); \
+        const float p0v = mn == -INFINITY ? 0.f : __expf(s0 - mn); \
+        const float p1v = mn == -INFINITY ? 0.f : __expf(s1 - mn); \
+        const _Float16 h0 = (_Float16)p0v, h1 = (_Float16)p1v; \
+        alpha[e] = mn == -INFINITY ? 1.f : __expf(m[e] - mn); \
+        l[e] = l[e] * alpha[e] + row16_sum((float)h0 + (float)h1); \
+        m[e] = mn; \
+        P[(4 * lq + e) * kKB + li] = __builtin_bit_cast(uint16_t, h0); \
+        P[(4 * lq + e) * kKB + 16 + li] = __builtin_bit_cast(uint16_t, h1); \
+    } \
+_Pragma("unroll") \
+    for (int c = 0; c < 8; ++c) \
+_Pragma("unroll") \
+        for (int e = 0; e < 4; ++e) O[c][e] *= alpha[e]; \
+    __builtin_amdgcn_wave_barrier(); \
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); \
+    /* O += P V: A = P[query li][keys 8 lq .. + 8], B = Vt[dim 16 c + li][keys 8 lq .. + 8] */ \
+    const h8_t A = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&P[li * kKB + 8 * lq])); \
+_Pragma("unroll") \
+    for (int c = 0; c < 8; ++c) { \
+        const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Vt[16 * c + li][8 * lq])); \
+        O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, O[c], 0, 0, 0); \
+    } \
+    __builtin_amdgcn_wave_barrier();  /* P is rewritten in the next step only after these reads */ \
+     \
+    do {} while (0)
+    for (int j0 = 0; j0 <= last; j0 += 2 * kKB) {
+        RK_ATTN_STEP(j0, ka);
+        if (j0 + kKB <= last) {
+            RK_ATTN_STEP(j0 + kKB, kb);
         }
-        __syncthreads();
-        // S = Q K^T for keys j0 + 16 hf + li (D layout: row 4 lq + e, key li)
-        f4_t Sd[2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            f4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Ks[16 * hf + li][32 * c + 8 * lq]));
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Qf[c], B, d, 0, 0, 0);
-            }
-            Sd[hf] = d;
-        }
-        float alpha[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int qpos = p0 + q0 + 4 * lq + e;
-            float s0 = Sd[0][e] * scale, s1 = Sd[1][e] * scale;
-            if (j0 + li > qpos) s0 = -INFINITY;
-            if (j0 + 16 + li > qpos) s1 = -INFINITY;
-            const float mb = row16_max(fmaxf(s0, s1));
-            const float mn = fmaxf(m[e], mb);
-            const float p0v = mn == -INFINITY ? 0.f : __expf(s0 - mn);
-            const float p1v = mn == -INFINITY ? 0.f : __expf(s1 - mn);
-            const _Float16 h0 = (_Float16)p0v, h1 = (_Float16)p1v;
-            alpha[e] = mn == -INFINITY ? 1.f : __expf(m[e] - mn);
-            l[e] = l[e] * alpha[e] + row16_sum((float)h0 + (float)h1);
-            m[e] = mn;
-            P[(4 * lq + e) * kKB + li] = __builtin_bit_cast(uint16_t, h0);
-            P[(4 * lq + e) * kKB + 16 + li] = __builtin_bit_cast(uint16_t, h1);
-        }
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) O[c][e] *= alpha[e];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // O += P V: A = P[query li][keys 8 lq .. + 8], B = Vt[dim 16 c + li][keys 8 lq .. + 8]
-        const h8_t A = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&P[li * kKB + 8 * lq]));
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Vt[16 * c + li][8 * lq]));
-            O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, O[c], 0, 0, 0);
-        }
-        __builtin_amdgcn_wave_barrier();  // P is rewritten in the next step only after these reads
     }
+#undef RK_ATTN_STEP
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int t = q0 + 4 * lq + e;
@@ -533,12 +571,26 @@ extern "C" int rk_prefill_attn(const void* q, const void* kc, const void* vc, vo
     if (!q || !kc || !vc || !o) return RK_ERR_NULL;
     if (dt != RK_F16) return RK_ERR_DTYPE;
     if (HD != kHD || NKV <= 0 || NH % NKV || T <= 0 || p0 < 0 || p0 + T > S) return RK_ERR_SHAPE;
-    const int rep = NH / NKV;
-    if (rep > 8) return RK_ERR_SHAPE;
+    const int rep = NH / NKV;  // query heads per KV head: 1, 2, 4 or 8 (the staging splits a key block evenly)
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return RK_ERR_SHAPE;
     if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return RK_ERR_ALIGN;
     const dim3 grid(NKV, (T + kQT - 1) / kQT);
-    hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(64 * rep), (size_t)rep * kQT * kKB * 2, (hipStream_t)stream,
+    const size_t lds = (size_t)rep * kQT * kKB * 2;
+    const hipStream_t st = (hipStream_t)stream;
+    switch (rep) {
+        case 1: hipLaunchKernelGGL(prefill_attn_kernel<1>, grid, dim3(64), lds, st,
                        (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
-                       scale);
+                       scale); break;
+        case 2: hipLaunchKernelGGL(prefill_attn_kernel<2>, grid, dim3(128), lds, st,
+                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
+                       scale); break;
+        case 4: hipLaunchKernelGGL(prefill_attn_kernel<4>, grid, dim3(256), lds, st,
+                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
+                       scale); break;
+        case 8: hipLaunchKernelGGL(prefill_attn_kernel<8>, grid, dim3(512), lds, st,
+                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
+                       scale); break;
+        default: return RK_ERR_SHAPE;
+    }
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }

@@ -991,8 +991,11 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
 //   next-layer loads issued; wave 0 reaches B9 only after its row gather, the x publication, the next layer's x
 //   poll and LayerNorm statistics (so it passes B9 and B0 back to back; nothing in LDS needs B9 earlier).
 //   Head: H0 LN statistics staged | H1 h staged.
-// The work table lists a block's q / k / v tiles first (at most 3), so they are computed and published in the
-// first pass and the q / k / v hop overlaps the second pass.
+// The work table lists a block's q / k / v tiles first (at most kTileSplit), so they are computed and published in
+// the first pass and the q / k / v hop overlaps the second pass. This is required, not only faster: a q / k / v tile
+// in the second pass would be published after B5, which waits for wave 0's q poll, which may wait for that very
+// tile in another block -- a circular wait that ends in the timeout. Measured first-pass sizes (ctx 256 / 2048, us
+// per token): 1 726 / 799, 2 697 / 767, 3 664 / 740, 4 692 / 769, 5 712 / 802.
 // Streamer issue order (each wait covers only older loads, see tile_issue): tiles(l + 1) [0, 3) after the first
 // epilogue; after the o partials of layer l, paced (pace_wait): tiles(l + 1) [3, 7), K/V(l + 1), down(l + 1),
 // O(l + 1) -- the order layer l + 1 consumes them. The loop's back edge and its preheader leave the same sequence

@@ -160,7 +160,7 @@ class RkDecodeParams(ctypes.Structure):
 
 
 MAX_TILES, MAX_SLICES, WORK = 7, 3, 16   # kMaxTiles, kMaxSlices, kWork of csrc/decode_persistent.hip
-FIRST_PASS = 3                           # kTileSplit: a block's q / k / v tiles are computed in its first pass
+FIRST_PASS = 3                           # kTileSplit: a block's q / k / v tiles must all be in its first pass
 X_COPIES = 16                            # kXRep: x is published in 16 copies
 
 

@@ -20,6 +20,9 @@
 extern "C" {
 #endif
 
+/* The library is built with hidden visibility; exactly the functions declared in this header are exported. */
+#pragma GCC visibility push(default)
+
 /* dtype codes */
 #define RK_F16 0
 #define RK_BF16 1
@@ -99,12 +102,29 @@ int rk_gemv_int4_g128_silu(const void* x, int x_dtype, const uint8_t* q, const u
 int rk_gemv_int8_rows(const void* x, int x_dtype, const void* q, int q_kind, const void* scale, int s_dtype,
                       void* y, int y_dtype, int N, int K, rk_stream_t stream);
 
+/* rk_gemv_int8_rows with an explicit block shape: waves per block in {1,2,4,8,16} and rows per wave in
+ * {1,2,4,8} (0 = the tuned default; anything else RK_ERR_BLOCK). Same results for every shape; the reference's
+ * gemv_int8 has no such knobs (kernels/cuda_gemv.py:188-195), this entry point exists for block-shape sweeps. */
+int rk_gemv_int8_rows_ex(const void* x, int x_dtype, const void* q, int q_kind, const void* scale, int s_dtype,
+                         void* y, int y_dtype, int N, int K, int waves, int rows, rk_stream_t stream);
+
 /* int4 group-128 matrix product for the prefill: Y[m,n] = sum_k X[m,k] * w[n,k], fp32 accumulate, MFMA.
  * Replaces mm_int4(x, q, s, m) -> _mm_int4 (reference kernels/mm_int4.py:59-73, :24-46).
  * X: [M, K] fp16/bf16 with row stride ldx elements (ldx % 8 == 0, 16-byte aligned rows);
  * Y: [M, N] of y_dtype with row stride ldy. K % 128 == 0; any M >= 1, N >= 1. */
 int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
                     const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, rk_stream_t stream);
+
+/* The kernel plan rk_mm_int4_g128 (use_workspace = 0) or rk_mm_int4_g128_ws (use_workspace = 1) runs for this
+ * shape: *kernel = RK_MM_TILE128 (LDS-staged 128 x 128 tiles), RK_MM_TILE64 (LDS-staged 64 x 64 tiles) or
+ * RK_MM_REGS (register-staged 64 x 64 tiles, for K too long to stage a block's scales in LDS); *splits = the
+ * number of K splits (1 = none; > 1 only with a workspace). Host-only query, no GPU needed; RK_ERR_SHAPE for
+ * sizes rk_mm_int4_g128 rejects. Part of the mm_int4 drop-in (reference kernels/mm_int4.py:59-73 picks its
+ * Triton tile from BM / BN); the reference has no plan query. */
+#define RK_MM_REGS 0
+#define RK_MM_TILE128 1
+#define RK_MM_TILE64 2
+int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits);
 
 /* Bytes of fp32 workspace rk_mm_int4_g128_ws uses for this shape (0: it needs none). Shapes whose output tiles
  * alone leave CUs idle (few rows and columns, long K) are split over K into fp32 partial sums that a second kernel
@@ -223,6 +243,25 @@ int rk_decode_step_persistent(const rk_decode_params* params, int nblocks, rk_st
 /* sizeof(rk_decode_params) as compiled (for bindings that build the struct by hand) */
 int rk_decode_params_size(void);
 
+/* The persistent step's compiled limits, for the host code that builds the work table (no GPU needed).
+ *   max_tiles        w_in tiles one block may list (work[b][0 .. max_tiles), -1 = none)
+ *   first_pass       the block's first tiles computed and published before its q poll: every q / k / v tile a
+ *                    block lists must sit in positions [0, first_pass), else its q poll can wait on a tile that
+ *                    is published only after that poll (a circular wait across blocks)
+ *   max_slices       w_down 16-column slices per block (work[b][slice_begin_col], work[b][slice_end_col])
+ *   work_stride      int16 entries per block row of the work table
+ *   slice_begin_col, slice_end_col   the columns of work[b] holding the block's slice range
+ *   x_copies         copies of the residual stream in tx
+ *   max_splits       attention splits per KV head (nsp)
+ *   max_slots_per_split  cached slots one split may cover (S / nsp rounded up must not exceed it)
+ * No reference counterpart (the reference's step is separate launches, engine/rumik_fused.py:97-121). */
+typedef struct rk_decode_limits {
+    int max_tiles, first_pass, max_slices, work_stride, slice_begin_col, slice_end_col, x_copies, max_splits,
+        max_slots_per_split;
+} rk_decode_limits;
+
+int rk_decode_get_limits(rk_decode_limits* out);
+
 /* pos[0] += 1 on the device (the `self.pos += 1` of the captured step, reference engine/rumik_fused.py:120). */
 int rk_pos_advance(int64_t* pos, rk_stream_t stream);
 
@@ -296,6 +335,8 @@ int rk_sample_tail(const void* h, int h_dtype, const float* lnw, const float* ln
                    int logits_dtype, int nv, int end_idx, const float* u, const int64_t* ids, int64_t* step,
                    int64_t* tok, int64_t* out, float inv_temp, int64_t end_id, int min_new, int topk, int64_t* keys,
                    int64_t* scratch, int nc, float* z1, unsigned* counter, rk_stream_t stream);
+
+#pragma GCC visibility pop
 
 #ifdef __cplusplus
 }

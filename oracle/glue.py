@@ -9,13 +9,29 @@ References (neoandmatrix/rumik-fast):
   post / add_ln    engine/fused.py:30-84 (where the fused step rounds to the activation dtype)
   step             engine/rumik_fused.py:97-121 (embed_ln; per layer gemv(w_in), post, attention, gemv(w_o),
                    gemv(w_down), add_ln; pos += 1; then the audio head)
-Activations are rounded to `dt` (np.float16 here; the reference engine uses bf16) exactly where the fused step
-stores them: the projection outputs, q after RoPE, the K/V cache, act, the attention output, x after the residual
+Activations are rounded to `dt` (np.float16, or "bf16" as the reference engine stores them) exactly where the fused
+step stores them: the projection outputs, q after RoPE, the K/V cache, act, the attention output, x after the residual
 add, and h after each LayerNorm.
 """
 import numpy as np
 
 from . import int4 as I4
+
+
+def round_bf16(v):
+    """float32 -> the nearest bfloat16 (ties to even), returned as float32: bits + 0x7FFF + lsb, then the low 16 bits
+    cleared (the usual round-to-nearest-even on the truncated half); inf / nan pass through."""
+    a = np.asarray(v, np.float32)
+    b = a.view(np.uint32).astype(np.uint64)
+    r = (((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+    return np.where(np.isfinite(a), r, a).astype(np.float32)
+
+
+def round_to(v, dt):
+    """v rounded to the activation dtype dt (np.float16, "bf16" or np.float32), as float32."""
+    if isinstance(dt, str) and dt == "bf16":
+        return round_bf16(v)
+    return np.asarray(v, np.float32).astype(dt).astype(np.float32)
 
 
 def cohere_ln(x, w, eps=1e-5):
@@ -119,23 +135,36 @@ class DecodeModel:
 
     Fields: L, H, NH, NKV, HD, inter, eps; per layer w_in (q|k|v|gate|up rows), w_o, w_down as (q, s, m) and ln [H];
     norm [H]; emb (int8 [V, H], fp16 scale [V]); head (int8 codes [NV, H], fp16 scale [NV]); rope (cos, sin) [S, HD];
-    sliding[L] (RoPE on / off per layer)."""
+    sliding[L] (RoPE on / off per layer). cache_weights=True keeps each dequantized matrix after its first use (the
+    same fp32 dequantize-then-matmul, computed once: for runs of many steps)."""
 
-    def __init__(self, **kw):
+    def __init__(self, cache_weights=False, **kw):
         self.__dict__.update(kw)
+        self.cache = {} if cache_weights else None
+
+
+def _gemv(md, w, x):
+    """dequantize(w) @ x in fp32 (oracle int4.gemv_int4), the dequantized matrix cached when the model asks for it."""
+    if md.cache is None:
+        return I4.gemv_int4(x, *w)
+    key = id(w[0])
+    if key not in md.cache:
+        md.cache[key] = I4.dequantize(*w)
+    return md.cache[key] @ np.asarray(x, np.float32)
 
 
 def decode_step(md: DecodeModel, tok, pos, kc, vc, dt=np.float16):
-    """One decode step at position `pos` for token `tok`; kc / vc [L, NKV, S, HD] are updated in place at `pos`.
-    Returns (logits fp32 [NV], hn [H] (dt), x [H] (dt)). Follows engine/rumik_fused.py:97-121 with the rounding
-    points of engine/fused.py."""
+    """One decode step at position `pos` for token `tok`; kc / vc [L, NKV, S, HD] are updated in place at `pos`
+    (float16 arrays, or float32 arrays holding bf16 values when dt = "bf16"). Returns (logits fp32 [NV], hn [H],
+    x [H]) as float32 holding dt values. Follows engine/rumik_fused.py:97-121 with the rounding points of
+    engine/fused.py."""
     H, NH, NKV, HD, inter = md.H, md.NH, md.NKV, md.HD, md.inter
-    r = lambda v: np.asarray(v, np.float32).astype(dt).astype(np.float32)  # noqa: E731 — round to the act dtype
+    r = lambda v: round_to(v, dt)  # noqa: E731 — round to the act dtype
     x = r(md.emb[0][tok].astype(np.float32) * np.float32(md.emb[1][tok]))                 # fused.py:20-22
     h = r(cohere_ln(x, md.ln[0], md.eps))
     cos, sin = md.rope
     for i in range(md.L):
-        y = r(I4.gemv_int4(h, *md.w_in[i]))                                                  # rumik_fused.py:102
+        y = r(_gemv(md, md.w_in[i], h))                                                      # rumik_fused.py:102
         q = y[:NH * HD].reshape(NH, HD)
         k = y[NH * HD:(NH + NKV) * HD].reshape(NKV, HD)
         v = y[(NH + NKV) * HD:(NH + 2 * NKV) * HD].reshape(NKV, HD)
@@ -143,12 +172,12 @@ def decode_step(md: DecodeModel, tok, pos, kc, vc, dt=np.float16):
         if md.sliding[i]:                                                                    # fused.py:57-65
             q, k = rope(q, cos[pos], sin[pos]), rope(k, cos[pos], sin[pos])
         q, k = r(q), r(k)
-        kc[i, :, pos] = k.astype(dt)
-        vc[i, :, pos] = v.astype(dt)
+        kc[i, :, pos] = k
+        vc[i, :, pos] = v
         act = r(silu(g) * u)                                                                 # fused.py:84
         o = r(attend(q, kc[i, :, :pos + 1].astype(np.float32), vc[i, :, :pos + 1].astype(np.float32)))
-        a = r(I4.gemv_int4(o.reshape(-1), *md.w_o[i]))
-        d = r(I4.gemv_int4(act, *md.w_down[i]))
+        a = r(_gemv(md, md.w_o[i], o.reshape(-1)))
+        d = r(_gemv(md, md.w_down[i], act))
         x = r(x + a + d)                                                                     # fused.py:33-35
         h = r(cohere_ln(x, md.norm if i == md.L - 1 else md.ln[i + 1], md.eps))
     logits = I4.gemv_int8_rows(h, md.head[0], md.head[1], "s8")

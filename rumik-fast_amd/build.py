@@ -23,6 +23,8 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-mcode-object-version=5", "-Wall", "-Wno-unused-function",
+    # export only what include/rumik_hip.h declares (it pushes default visibility around its declarations)
+    "-fvisibility=hidden",
     # packed fp32 ops (v_pk_*_f32) stay off: only scalar fp32 VALU ops are emitted
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",

@@ -1195,3 +1195,17 @@ extern "C" int rk_decode_step_persistent(const rk_decode_params* params, int nbl
 }
 
 extern "C" int rk_decode_params_size(void) { return (int)sizeof(Params); }
+
+extern "C" int rk_decode_get_limits(rk_decode_limits* out) {
+    if (!out) return RK_ERR_NULL;
+    out->max_tiles = kMaxTiles;
+    out->first_pass = kTileSplit;
+    out->max_slices = kMaxSlices;
+    out->work_stride = kWork;
+    out->slice_begin_col = 8;
+    out->slice_end_col = 9;
+    out->x_copies = kXRep;
+    out->max_splits = 64;
+    out->max_slots_per_split = kStreamers * kKVPre;
+    return RK_OK;
+}

@@ -12,13 +12,10 @@
 //     nibbles give 1024 + 16c, brought back to c by one exact packed fma (x 1/16, -64); the same for w >> 8.
 //     v_dot2_f32_f16 multiplies each code pair with the matching x pair and accumulates in fp32, so every product
 //     is exact and only the fp32 sums round (13 VALU ops per 8 weights).
-//     SUBN = true encodes the codes as fp16 subnormals instead ((w & 0x000F000F) = (c0 * 2^-24, c4 * 2^-24),
-//     no de-bias op, 9 ops per 8 weights, powers of two folded into the scale). On gfx950 the dot2 products of
-//     subnormal inputs lose precision (measured error ~10x the default path's), so it is only a variant.
-//   * Per (row, chunk): acc += (scale * 2^24) * dot + min * xsum, in fp32.
+//   * Per (row, chunk): acc += scale * dot + min * xsum, in fp32.
 //   * Rows are reduced over the wave with a transposed butterfly (R + 6 exchanges for R rows, DPP inside 16-lane
 //     rows), then over the KS waves of a team through LDS.
-#include "common.h"
+#include "internal.h"
 
 namespace {
 
@@ -72,43 +69,29 @@ RK_DEV void process_x_chunk(const XChunk& xc, int xdt, uint32_t (&xp)[16], float
     xs = s;
 }
 
-// Dot of one 16-byte code chunk (32 codes) with its x pairs. SUBN: returns sum(code * x) * 2^-24.
-template <bool SUBN>
+// Dot of one 16-byte code chunk (32 codes) with its x pairs.
 RK_DEV float chunk_dot(u4_t w, const uint32_t (&xp)[16]) {
-    if constexpr (SUBN) {
-        float lo = 0.f, hi = 0.f;
+    const h2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    const h2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const h2_t m64 = {(_Float16)-64.f, (_Float16)-64.f};
+    float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t a = w[i], b = a >> 8;
-            lo = dot2(as_h2(a & 0x000F000Fu), as_h2(xp[4 * i + 0]), lo);
-            hi = dot2(as_h2(a & 0x00F000F0u), as_h2(xp[4 * i + 1]), hi);
-            lo = dot2(as_h2(b & 0x000F000Fu), as_h2(xp[4 * i + 2]), lo);
-            hi = dot2(as_h2(b & 0x00F000F0u), as_h2(xp[4 * i + 3]), hi);
-        }
-        return __builtin_fmaf(hi, 0.0625f, lo);  // hi holds 16 * code * 2^-24 * x
-    } else {
-        const h2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
-        const h2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-        const h2_t m64 = {(_Float16)-64.f, (_Float16)-64.f};
-        float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t a = w[i], b = a >> 8;
-            h2_t c04 = as_h2((a & 0x000F000Fu) | 0x64006400u) + m1024;
-            h2_t c15 = as_h2((a & 0x00F000F0u) | 0x64006400u) * s16 + m64;
-            h2_t c26 = as_h2((b & 0x000F000Fu) | 0x64006400u) + m1024;
-            h2_t c37 = as_h2((b & 0x00F000F0u) | 0x64006400u) * s16 + m64;
-            acc0 = dot2(c04, as_h2(xp[4 * i + 0]), acc0);
-            acc1 = dot2(c15, as_h2(xp[4 * i + 1]), acc1);
-            acc0 = dot2(c26, as_h2(xp[4 * i + 2]), acc0);
-            acc1 = dot2(c37, as_h2(xp[4 * i + 3]), acc1);
-        }
-        return acc0 + acc1;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = w[i], b = a >> 8;
+        h2_t c04 = as_h2((a & 0x000F000Fu) | 0x64006400u) + m1024;
+        h2_t c15 = as_h2((a & 0x00F000F0u) | 0x64006400u) * s16 + m64;
+        h2_t c26 = as_h2((b & 0x000F000Fu) | 0x64006400u) + m1024;
+        h2_t c37 = as_h2((b & 0x00F000F0u) | 0x64006400u) * s16 + m64;
+        acc0 = dot2(c04, as_h2(xp[4 * i + 0]), acc0);
+        acc1 = dot2(c15, as_h2(xp[4 * i + 1]), acc1);
+        acc0 = dot2(c26, as_h2(xp[4 * i + 2]), acc0);
+        acc1 = dot2(c37, as_h2(xp[4 * i + 3]), acc1);
     }
+    return acc0 + acc1;
 }
 
 // the GEMV of block `blk` (rows [blk * teams * R, ...)); `red`: LDS for the KS-way reduction
-template <int R, int KS, int NJ, bool SUBN>
+template <int R, int KS, int NJ>
 RK_DEV void gemv_int4_block(const void* __restrict__ x, int xdt, const uint8_t* __restrict__ q,
                             const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, void* __restrict__ y,
                             int ydt, int N, int K, int blk, float (*red)[R]) {
@@ -122,7 +105,6 @@ RK_DEV void gemv_int4_block(const void* __restrict__ x, int xdt, const uint8_t* 
     const int ng = K >> 7;
     const int row0 = (blk * teams + team) * R;  // teams past N (last block only) clamp and store nothing
 
-    const float sfold = SUBN ? 16777216.0f : 1.0f;  // 2^24 undoes the subnormal encoding of the codes
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -175,8 +157,8 @@ RK_DEV void gemv_int4_block(const void* __restrict__ x, int xdt, const uint8_t* 
             float a = acc[r];
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const float d = chunk_dot<SUBN>(w[r][j], xp[j]);
-                const float sv = f16_bits_to_f32(s16[r][j]) * sfold;
+                const float d = chunk_dot(w[r][j], xp[j]);
+                const float sv = f16_bits_to_f32(s16[r][j]);
                 const float mv = f16_bits_to_f32(m16[r][j]);
                 a = __builtin_fmaf(d, sv, __builtin_fmaf(mv, xs[j], a));
             }
@@ -202,14 +184,14 @@ RK_DEV void gemv_int4_block(const void* __restrict__ x, int xdt, const uint8_t* 
     }
 }
 
-template <int R, int KS, int NJ, bool SUBN>
+template <int R, int KS, int NJ>
 __global__ __launch_bounds__(kMaxThreads) void gemv_int4_kernel(const void* __restrict__ x, int xdt,
                                                                 const uint8_t* __restrict__ q,
                                                                 const uint16_t* __restrict__ sc,
                                                                 const uint16_t* __restrict__ mn,
                                                                 void* __restrict__ y, int ydt, int N, int K) {
     __shared__ float red[kMaxThreads / 64][R];
-    gemv_int4_block<R, KS, NJ, SUBN>(x, xdt, q, sc, mn, y, ydt, N, K, blockIdx.x, red);
+    gemv_int4_block<R, KS, NJ>(x, xdt, q, sc, mn, y, ydt, N, K, blockIdx.x, red);
 }
 
 // Two independent GEMVs in one launch (blocks [0, nb1) the first, the rest the second), each with its own plan;
@@ -228,42 +210,42 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_int4_pair_kernel(GemvArgs a,
     __shared__ float red1[kMaxThreads / 64][R1];
     __shared__ float red2[kMaxThreads / 64][R2];
     if ((int)blockIdx.x < nb1)
-        gemv_int4_block<R1, KS1, NJ1, false>(a.x, a.xdt, a.q, a.s, a.m, a.y, a.ydt, a.N, a.K, blockIdx.x, red1);
+        gemv_int4_block<R1, KS1, NJ1>(a.x, a.xdt, a.q, a.s, a.m, a.y, a.ydt, a.N, a.K, blockIdx.x, red1);
     else
-        gemv_int4_block<R2, KS2, NJ2, false>(b.x, b.xdt, b.q, b.s, b.m, b.y, b.ydt, b.N, b.K, blockIdx.x - nb1, red2);
+        gemv_int4_block<R2, KS2, NJ2>(b.x, b.xdt, b.q, b.s, b.m, b.y, b.ydt, b.N, b.K, blockIdx.x - nb1, red2);
 }
 
-template <int R, int KS, int NJ, bool SUBN>
+template <int R, int KS, int NJ>
 hipError_t launch(const void* x, int xdt, const uint8_t* q, const uint16_t* s, const uint16_t* m, void* y, int ydt,
                   int N, int K, int waves, hipStream_t st) {
     const int teams = waves / KS;
     const int rows_per_block = teams * R;
     const int blocks = (N + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((gemv_int4_kernel<R, KS, NJ, SUBN>), dim3(blocks), dim3(waves * 64), 0, st, x, xdt, q, s, m,
+    hipLaunchKernelGGL((gemv_int4_kernel<R, KS, NJ>), dim3(blocks), dim3(waves * 64), 0, st, x, xdt, q, s, m,
                        y, ydt, N, K);
     return hipGetLastError();
 }
 
-template <int R, int KS, bool SUBN>
+template <int R, int KS>
 hipError_t by_nj(int nj, const void* x, int xdt, const uint8_t* q, const uint16_t* s, const uint16_t* m, void* y,
                  int ydt, int N, int K, int waves, hipStream_t st) {
     switch (nj) {
-        case 1: return launch<R, KS, 1, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
-        case 2: return launch<R, KS, 2, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
-        case 3: return launch<R, KS, 3, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
-        case 4: return launch<R, KS, 4, SUBN>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 1: return launch<R, KS, 1>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 2: return launch<R, KS, 2>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 3: return launch<R, KS, 3>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 4: return launch<R, KS, 4>(x, xdt, q, s, m, y, ydt, N, K, waves, st);
         default: return hipErrorInvalidValue;
     }
 }
 
-template <int R, bool SUBN>
+template <int R>
 hipError_t by_ks(int ks, int nj, const void* x, int xdt, const uint8_t* q, const uint16_t* s, const uint16_t* m,
                  void* y, int ydt, int N, int K, int waves, hipStream_t st) {
     switch (ks) {
-        case 1: return by_nj<R, 1, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
-        case 2: return by_nj<R, 2, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
-        case 4: return by_nj<R, 4, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
-        case 8: return by_nj<R, 8, SUBN>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 1: return by_nj<R, 1>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 2: return by_nj<R, 2>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 4: return by_nj<R, 4>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
+        case 8: return by_nj<R, 8>(nj, x, xdt, q, s, m, y, ydt, N, K, waves, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -297,9 +279,9 @@ static int plan_int4(int N, int K, int waves, int rows, Int4Plan* p) {
     return RK_OK;
 }
 
-extern "C" int rk_gemv_int4_g128_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
-                                      const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
-                                      int subn, rk_stream_t stream) {
+int gemv_int4_valu_launch(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                          const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, int rows,
+                          rk_stream_t stream) {
     if (!x || !q || !scale || !min || !y) return RK_ERR_NULL;
     if (N <= 0 || K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
     if (x_dtype != RK_F16 && x_dtype != RK_BF16) return RK_ERR_DTYPE;
@@ -310,31 +292,21 @@ extern "C" int rk_gemv_int4_g128_impl(const void* x, int x_dtype, const uint8_t*
     if (st != RK_OK) return st;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t e;
-    if (subn) {
-        switch (p.rows) {
-            case 1: e = by_ks<1, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-            case 2: e = by_ks<2, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-            case 4: e = by_ks<4, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-            default: e = by_ks<8, true>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-        }
-    } else {
-        switch (p.rows) {
-            case 1: e = by_ks<1, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-            case 2: e = by_ks<2, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-            case 4: e = by_ks<4, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-            default: e = by_ks<8, false>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
-        }
+    switch (p.rows) {
+        case 1: e = by_ks<1>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+        case 2: e = by_ks<2>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+        case 4: e = by_ks<4>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
+        default: e = by_ks<8>(p.ks, p.nj, x, x_dtype, q, scale, min, y, y_dtype, N, K, p.waves, s); break;
     }
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 
 // o-like (K <= 4096: 4 waves x 2 rows, one pass) + down-like (K <= 16384: 4 waves = 2 teams of 2 splitting K, 2 rows
 // each) in one launch; other shapes run as two launches of the single-GEMV plans.
-extern "C" int rk_gemv_int4_g128_pair_impl(const void* x1, int x1_dtype, const uint8_t* q1, const uint16_t* s1,
-                                           const uint16_t* m1, void* y1, int y1_dtype, int N1, int K1,
-                                           const void* x2, int x2_dtype, const uint8_t* q2, const uint16_t* s2,
-                                           const uint16_t* m2, void* y2, int y2_dtype, int N2, int K2,
-                                           rk_stream_t stream) {
+int gemv_int4_pair_launch(const void* x1, int x1_dtype, const uint8_t* q1, const uint16_t* s1,
+                          const uint16_t* m1, void* y1, int y1_dtype, int N1, int K1, const void* x2,
+                          int x2_dtype, const uint8_t* q2, const uint16_t* s2, const uint16_t* m2, void* y2,
+                          int y2_dtype, int N2, int K2, rk_stream_t stream) {
     if (!x1 || !q1 || !s1 || !m1 || !y1 || !x2 || !q2 || !s2 || !m2 || !y2) return RK_ERR_NULL;
     if (N1 <= 0 || K1 <= 0 || K1 % 128 || N2 <= 0 || K2 <= 0 || K2 % 128) return RK_ERR_SHAPE;
     for (int dt : {x1_dtype, x2_dtype})
@@ -355,7 +327,7 @@ extern "C" int rk_gemv_int4_g128_pair_impl(const void* x1, int x1_dtype, const u
             hipLaunchKernelGGL((gemv_int4_pair_kernel<2, 1, 1, 2, 2, 4>), dim3(nb1 + nb2), dim3(256), 0, st, a, b, nb1);
         return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
     }
-    int e = rk_gemv_int4_g128_impl(x1, x1_dtype, q1, s1, m1, y1, y1_dtype, N1, K1, 0, 0, 0, stream);
+    int e = gemv_int4_valu_launch(x1, x1_dtype, q1, s1, m1, y1, y1_dtype, N1, K1, 0, 0, stream);
     if (e != RK_OK) return e;
-    return rk_gemv_int4_g128_impl(x2, x2_dtype, q2, s2, m2, y2, y2_dtype, N2, K2, 0, 0, 0, stream);
+    return gemv_int4_valu_launch(x2, x2_dtype, q2, s2, m2, y2, y2_dtype, N2, K2, 0, 0, stream);
 }

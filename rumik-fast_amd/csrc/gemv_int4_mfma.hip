@@ -21,7 +21,7 @@
 //   * per group: acc += scale * dot + min * xsum_g, fp32; xsum_g comes from LDS;
 //   * KS waves of a block split the groups of the same tile (fills the chip for N = 2048); partial sums are added
 //     through LDS, lanes 0..15 of the first wave store.
-#include "common.h"
+#include "internal.h"
 
 
 namespace {
@@ -378,9 +378,8 @@ static int gemv_mfma_run(const void* x, int x_dtype, const uint8_t* q, const uin
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 
-extern "C" int rk_gemv_int4_mfma_impl(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
-                                      const uint16_t* min, void* y, int y_dtype, int N, int K, int waves,
-                                      rk_stream_t stream) {
+int gemv_int4_mfma_launch(const void* x, int x_dtype, const uint8_t* q, const uint16_t* scale,
+                          const uint16_t* min, void* y, int y_dtype, int N, int K, int waves, rk_stream_t stream) {
     if (!x || !q || !scale || !min || !y) return RK_ERR_NULL;
     if (N <= 0) return RK_ERR_SHAPE;
     return gemv_mfma_run(x, x_dtype, q, scale, min, y, y_dtype, N, 0, nullptr, K, waves,

@@ -6,7 +6,7 @@
 // Dequant, exact: v_perm_b32 places each byte u under 0x64 -> fp16 (1024 + u); a packed add of -1152 gives
 // u - 128, the signed code (signed int8 input is first mapped to u = b ^ 0x80). Products and sums in fp32 via
 // v_dot2_f32_f16; the row scale is applied once after the wave reduction.
-#include "common.h"
+#include "internal.h"
 
 namespace {
 
@@ -159,9 +159,8 @@ hipError_t by_plan8(int rows, int ks, int nj, const void* x, int xdt, const uint
 
 }  // namespace
 
-extern "C" int rk_gemv_int8_rows_impl(const void* x, int x_dtype, const void* q, int q_kind, const void* scale,
-                                      int s_dtype, void* y, int y_dtype, int N, int K, int waves, int rows,
-                                      rk_stream_t stream) {
+int gemv_int8_rows_launch(const void* x, int x_dtype, const void* q, int q_kind, const void* scale,
+                          int s_dtype, void* y, int y_dtype, int N, int K, int waves, int rows, rk_stream_t stream) {
     if (!x || !q || !scale || !y) return RK_ERR_NULL;
     if (N <= 0 || K <= 0 || K % 16 != 0) return RK_ERR_SHAPE;
     if (x_dtype != RK_F16 && x_dtype != RK_BF16) return RK_ERR_DTYPE;

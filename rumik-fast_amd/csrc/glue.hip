@@ -160,8 +160,9 @@ RK_DEV int split_chunk(int n, int nsplit) { return ((n + nsplit - 1) / nsplit + 
 constexpr int kAttnWaves = 4;
 // Flash-decoding partials (reference engine/fused.py:120-169). Block (g, sp): KV head g, slots
 // [sp*ch, min((sp+1)*ch, pos+1)), all REP query heads of g. Wave w takes every kAttnWaves-th slot; lane l holds
-// dims (2l, 2l+1) of q, k, v and of the running acc (HD = 128). Per slot: REP dot products (v_dot2_f32_f16),
-// a transposed lane reduction, an online-softmax update per head. The waves' partials are merged in LDS and
+// dims (2l, 2l+1) of q, k, v and of the running acc (HD = 128). Per slot: REP dot products (fp16: v_dot2_f32_f16,
+// exact products; bf16: fp32 products of the widened values, so no bf16 value is narrowed to fp16 range), a
+// transposed lane reduction, an online-softmax update per head. The waves' partials are merged in LDS and
 // written as (m, l, acc) per head and split; an empty split writes m = -inf, l = 0.
 template <int REP>
 __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(const void* __restrict__ q,
@@ -180,14 +181,16 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(const void*
     const int start = sp * ch, end = min(start + ch, n);
     const int HD = 128;
 
-    // q pairs of the REP heads of this KV head (converted to fp16 pairs for v_dot2)
+    // q pairs of the REP heads of this KV head (fp16 pairs for v_dot2; fp32 pairs for bf16 activations)
     h2_t qv[REP];
+    float2 qf[REP];
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
         const size_t base = (size_t)(g * REP + r) * HD + 2 * lane;
+        qf[r] = make_float2(load_act(q, dt, base), load_act(q, dt, base + 1));
         h2_t p;
-        p.x = (_Float16)load_act(q, dt, base);
-        p.y = (_Float16)load_act(q, dt, base + 1);
+        p.x = (_Float16)qf[r].x;
+        p.y = (_Float16)qf[r].y;
         qv[r] = p;
     }
     float m[REP], l[REP];
@@ -203,12 +206,17 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_split_kernel(const void*
         const size_t o = kv_base + (size_t)t * HD;
         const float k0 = load_act(kc, dt, o), k1 = load_act(kc, dt, o + 1);
         const float v0 = load_act(vc, dt, o), v1 = load_act(vc, dt, o + 1);
-        h2_t kp;
-        kp.x = (_Float16)k0;
-        kp.y = (_Float16)k1;
         float sc[REP];
+        if (dt == RK_BF16) {
 #pragma unroll
-        for (int r = 0; r < REP; ++r) sc[r] = dot2(qv[r], kp, 0.f);
+            for (int r = 0; r < REP; ++r) sc[r] = __builtin_fmaf(qf[r].x, k0, qf[r].y * k1);
+        } else {
+            h2_t kp;
+            kp.x = (_Float16)k0;
+            kp.y = (_Float16)k1;
+#pragma unroll
+            for (int r = 0; r < REP; ++r) sc[r] = dot2(qv[r], kp, 0.f);
+        }
         wave_reduce_rows<REP>(sc);
         // totals: row r sits in lane writer_lane<REP>(r); broadcast each to the whole wave
         float sr[REP];

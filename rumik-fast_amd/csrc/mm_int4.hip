@@ -497,6 +497,14 @@ extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_
                   reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
+    const MmPlan p = mm_plan(M, N, K, use_workspace != 0);
+    if (kernel) *kernel = p.cfg == 1 ? RK_MM_TILE128 : p.cfg == 2 ? RK_MM_TILE64 : RK_MM_REGS;
+    if (splits) *splits = p.splits;
+    return RK_OK;
+}
+
 extern "C" size_t rk_mm_int4_workspace_bytes(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
     return mm_plan(M, N, K, true).ws;

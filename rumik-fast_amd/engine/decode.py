@@ -57,15 +57,16 @@ def rope_tables(S, HD, theta, dtype, device):
 
 
 def random_weights(cfg: Config, seed: int, device, gen_device="cuda"):
-    """Random-init weights of the config's architecture in the reference formats (values irrelevant to speed)."""
+    """Random-init weights of the config's architecture in the reference formats (values irrelevant to speed).
+    LayerNorm weights are drawn per layer (not 1), so a wrong layer index changes the results."""
     g = synth.generator(seed, gen_device)
     w = {"w_in": [], "w_o": [], "w_down": [], "ln": []}
     for _ in range(cfg.L):
         w["w_in"].append(synth.int4_weights(cfg.n_in, cfg.H, g, device=device))
         w["w_o"].append(synth.int4_weights(cfg.H, cfg.NH * cfg.HD, g, device=device))
         w["w_down"].append(synth.int4_weights(cfg.H, cfg.inter, g, device=device))
-        w["ln"].append(torch.ones(cfg.H, dtype=torch.float16, device=device))
-    w["norm"] = torch.ones(cfg.H, dtype=torch.float16, device=device)
+        w["ln"].append(synth.ln_weights(cfg.H, g, device=device))
+    w["norm"] = synth.ln_weights(cfg.H, g, device=device)
     w["emb"] = synth.int8_weights(cfg.vocab, cfg.H, g, device=device)
     w["head"] = synth.int8_weights(cfg.n_audio, cfg.H, g, device=device)
     return w
@@ -159,9 +160,17 @@ class RkDecodeParams(ctypes.Structure):
             "tpo", "tml", "ctr", "status", "hn")]
 
 
-MAX_TILES, MAX_SLICES, WORK = 7, 3, 16   # kMaxTiles, kMaxSlices, kWork of csrc/decode_persistent.hip
-FIRST_PASS = 3                           # kTileSplit: a block's q / k / v tiles must all be in its first pass
-X_COPIES = 16                            # kXRep: x is published in 16 copies
+class RkDecodeLimits(ctypes.Structure):
+    """ctypes mirror of rk_decode_limits (include/rumik_hip.h): the persistent kernel's compiled limits."""
+    _fields_ = [(n, ctypes.c_int) for n in ("max_tiles", "first_pass", "max_slices", "work_stride", "slice_begin_col",
+                                            "slice_end_col", "x_copies", "max_splits", "max_slots_per_split")]
+
+
+def decode_limits() -> RkDecodeLimits:
+    """The limits the library was compiled with (a host-only query: no GPU needed)."""
+    lim = RkDecodeLimits()
+    HL.check(HL.lib().rk_decode_get_limits(ctypes.byref(lim)), "decode_get_limits")
+    return lim
 
 
 def interleave_gate_up(t, cfg):
@@ -208,37 +217,78 @@ def o_layout(q, nh):
     return q.reshape(rows // 128, 128, nh, 4, 16).permute(2, 0, 1, 3, 4).reshape(nh, rows // 128, 512, 16).contiguous()
 
 
-def work_table(cfg, nblocks, nsp):
+def work_table(cfg, nblocks, nsp, lim=None):
     """Per block: its w_in tiles (q / k / v tiles first, then the gate / up tiles of its MLP channels) and its
     w_down slices [sb, se) (16 channels each; a block owns both gate / up tiles of each of its slices).
-    Returns int16 [nblocks, 16] (columns 10..15 unused)."""
+    Returns int16 [nblocks, lim.work_stride]; unused entries are -1."""
+    lim = lim or decode_limits()
     qkv_tiles = (cfg.NH + 2 * cfg.NKV) * cfg.HD // 16
     nsl = cfg.inter // 16
     tiles = [[] for _ in range(nblocks)]
     ranges = []
     for b in range(nblocks):
         sb, se = b * nsl // nblocks, (b + 1) * nsl // nblocks
-        if se - sb > MAX_SLICES:
+        if se - sb > lim.max_slices:
             raise ValueError("too many MLP channels per block")
         ranges.append((sb, se))
         for k in range(sb, se):
             tiles[b] += [qkv_tiles + 2 * k, qkv_tiles + 2 * k + 1]
     qkv = [[] for _ in range(nblocks)]
-    for t in range(qkv_tiles):  # each q / k / v tile to the block with the fewest tiles so far (FIRST_PASS at most)
-        b = min((i for i in range(nblocks) if len(qkv[i]) < FIRST_PASS),
+    for t in range(qkv_tiles):  # each q / k / v tile to the block with the fewest tiles so far (first pass at most)
+        b = min((i for i in range(nblocks) if len(qkv[i]) < lim.first_pass),
                 key=lambda i: (len(tiles[i]) + len(qkv[i]), len(qkv[i]), i), default=None)
         if b is None:
             raise ValueError("too many q/k/v tiles for the blocks' first passes")
         qkv[b].append(t)
-    table = torch.full((nblocks, WORK), -1, dtype=torch.int16)
+    table = torch.full((nblocks, lim.work_stride), -1, dtype=torch.int16)
     for b in range(nblocks):
         tl = qkv[b] + tiles[b]
-        if len(tl) > MAX_TILES:
-            raise ValueError(f"block {b} would hold {len(tl)} tiles (at most {MAX_TILES})")
+        if len(tl) > lim.max_tiles:
+            raise ValueError(f"block {b} would hold {len(tl)} tiles (at most {lim.max_tiles})")
         if tl:
             table[b, :len(tl)] = torch.tensor(tl, dtype=torch.int16)
-        table[b, 8], table[b, 9] = ranges[b]
+        table[b, lim.slice_begin_col], table[b, lim.slice_end_col] = ranges[b]
+    validate_work_table(table, cfg, lim)
     return table
+
+
+def validate_work_table(table, cfg, lim=None):
+    """Raise ValueError unless `table` is a work table the persistent kernel can run without a circular wait:
+    every w_in tile listed exactly once, at most max_tiles per block with no gap before the last one, every q / k / v
+    tile in its block's first pass (positions [0, first_pass): a later one is published after the block's own q
+    poll, which may be waiting for it), the down slices a contiguous partition of the MLP channels with at most
+    max_slices per block, and each block's gate / up tiles exactly those of its slices (the kernel keeps
+    SiLU(gate) * up only for the block's own channels)."""
+    lim = lim or decode_limits()
+    t = torch.as_tensor(table)
+    if t.dim() != 2 or t.shape[1] != lim.work_stride:
+        raise ValueError(f"work table must be [nblocks, {lim.work_stride}]")
+    qkv_tiles = (cfg.NH + 2 * cfg.NKV) * cfg.HD // 16
+    n_tiles = qkv_tiles + 2 * cfg.inter // 16
+    nsl = cfg.inter // 16
+    seen = []
+    prev_end = 0
+    for b in range(t.shape[0]):
+        row = [int(v) for v in t[b, :lim.max_tiles]]
+        n = sum(v >= 0 for v in row)
+        if any(v < 0 for v in row[:n]) or any(v >= 0 for v in row[n:]):
+            raise ValueError(f"block {b}: tiles must fill positions 0 .. n-1")
+        if any(v >= n_tiles for v in row[:n]):
+            raise ValueError(f"block {b}: tile index out of range")
+        if any(v < qkv_tiles for v in row[lim.first_pass:n]):
+            raise ValueError(f"block {b}: a q/k/v tile outside the first {lim.first_pass} positions")
+        seen += row[:n]
+        sb, se = int(t[b, lim.slice_begin_col]), int(t[b, lim.slice_end_col])
+        if sb != prev_end or se < sb or se - sb > lim.max_slices:
+            raise ValueError(f"block {b}: down slices [{sb}, {se}) break the contiguous partition")
+        prev_end = se
+        own = {v for v in row[:n] if v >= qkv_tiles}
+        if own != {qkv_tiles + 2 * k + h for k in range(sb, se) for h in (0, 1)}:
+            raise ValueError(f"block {b}: gate/up tiles differ from those of its slices")
+    if prev_end != nsl:
+        raise ValueError("down slices do not cover every MLP channel")
+    if sorted(seen) != list(range(n_tiles)):
+        raise ValueError("every w_in tile must be listed exactly once")
 
 
 class PersistentDecode:
@@ -254,8 +304,6 @@ class PersistentDecode:
         d = self.dev
         self.nblocks = 2048 // 8
         self.nsp = nsp or min(64, self.nblocks // cfg.NKV)
-        if self.nsp > 64:
-            raise ValueError("at most 64 attention splits per KV head")
         lib = HL.lib()
         if lib.rk_decode_params_size() != ctypes.sizeof(RkDecodeParams):
             raise RuntimeError("rk_decode_params layout mismatch between the library and decode.py")
@@ -273,10 +321,13 @@ class PersistentDecode:
         if not keep_layer_weights:
             for k in ("w_in", "w_o", "w_down"):
                 w[k].clear()
-        self.work = work_table(c, self.nblocks, self.nsp).to(d)
+        self.limits = decode_limits()
+        if self.nsp > self.limits.max_splits or -(-c.S // self.nsp) > self.limits.max_slots_per_split:
+            raise ValueError("cache length / attention splits beyond the kernel's limits")
+        self.work = work_table(c, self.nblocks, self.nsp, self.limits).to(d)
         f16, f32, i32 = torch.float16, torch.float32, torch.int32
         nb = self.nblocks
-        self.tx = torch.zeros(X_COPIES * 2048, dtype=i32, device=d)
+        self.tx = torch.zeros(self.limits.x_copies * 2048, dtype=i32, device=d)
         self.tq = torch.zeros(c.NH * c.HD, dtype=i32, device=d)
         self.tkv = torch.zeros(2 * c.NKV * c.HD, dtype=i32, device=d)
         self.top = torch.zeros(nb * c.NH * 8, dtype=i32, device=d)

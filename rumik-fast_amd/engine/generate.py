@@ -8,6 +8,9 @@ tail attached (one hipGraph = decode step + sample; the sampled token is the nex
   before it;
 - generation stops at </audio> (tokens after it in the same frame are dropped, a frame queued after it is ignored),
   at max_new tokens or when the cache is full;
+- the one-launch step's status word is copied back with every frame (same event): a nonzero status (a wait that
+  timed out, so the step drained with garbage, or a position outside the cache) raises DecodeError after the
+  engine's exchange buffers are reset, instead of emitting tokens sampled from invalid logits;
 - to_codes: audio token ids -> [1, Q, frames] Mimi codes, whole frames only, resynchronising on a broken codebook
   round robin (rumik_int4.py:310-324).
 The prompt: with a prefill.Prefill (all prompt rows of a layer at once: mm_int4 and the matrix-core causal
@@ -18,6 +21,10 @@ except after the last prompt token, which is the first generated token).
 import time
 
 import torch
+
+
+class DecodeError(RuntimeError):
+    """The persistent decode step reported a nonzero status (see PersistentDecode.status_word)."""
 
 
 class Generator:
@@ -34,10 +41,16 @@ class Generator:
             raise ValueError("max_new + Q exceeds the sampler's output buffer")
         self.max_seq = eng.cfg.S
         self.host = torch.empty(eng.out.shape[0], dtype=torch.long, pin_memory=True)
+        self.host_status = torch.zeros(eng.out.shape[0], dtype=torch.int32, pin_memory=True)
         if eng.graph is None:
             eng.capture()
 
     @torch.inference_mode()
+    def _fail(self, status, where):
+        self.eng.reset()
+        raise DecodeError(f"decode step status {status} ({where}): bit 1 = a cross-block wait timed out, bit 2 = "
+                          "position outside the cache; the engine's exchange buffers were reset")
+
     def prefill(self, ids):
         """Process the prompt; returns the first generated token (a device scalar, also in eng.tok / eng.out[0]).
         With a prefill.Prefill: all prompt rows per layer at once on the matrix cores, then the audio head and the
@@ -71,6 +84,8 @@ class Generator:
         t0 = time.perf_counter()
         first = int(self.prefill(ids))
         torch.cuda.synchronize(e.dev)
+        if e.status_word() != 0:
+            self._fail(e.status_word(), "prompt")
         t_prefill = time.perf_counter() - t0
         pos, n, toks, t_frame0 = len(ids), 1, [first], None
         done = first == e.end_id
@@ -82,6 +97,7 @@ class Generator:
                 e.replay()
                 pos += 1
             host[n:n + self.Q].copy_(e.out[n:n + self.Q], non_blocking=True)
+            self.host_status[n:n + 1].copy_(e.status, non_blocking=True)
             ev = torch.cuda.Event()
             ev.record()
             queued.append((n, ev))
@@ -97,6 +113,10 @@ class Generator:
                 launch()                                         # keep one frame ahead
             k, ev = queued.pop(0)
             ev.synchronize()
+            if int(self.host_status[k]) != 0:
+                queued.clear()
+                torch.cuda.synchronize(e.dev)
+                self._fail(int(self.host_status[k]), f"frame at token {k}")
             new = host[k:k + self.Q].tolist()
             if t_frame0 is None:
                 t_frame0 = time.perf_counter() - t0

@@ -23,11 +23,11 @@ _SIGS = {
     "rk_gemv_int4_g128_mfma": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_valu": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_pair": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p], _i),
-    "rk_gemv_int4_g128_subn": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_silu": ([_p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int8_rows": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _p], _i),
     "rk_gemv_int8_rows_ex": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_mm_int4_g128": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_mm_int4_plan": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
     "rk_mm_int4_workspace_bytes": ([_i, _i, _i], ctypes.c_size_t),
     "rk_mm_int4_g128_ws": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, ctypes.c_size_t, _p], _i),
     "rk_embed_ln": ([_p, _p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
@@ -39,6 +39,7 @@ _SIGS = {
     "rk_silu_mul": ([_p, _p, _i, _i, _p], _i),
     "rk_decode_step_persistent": ([_p, _i, _p], _i),
     "rk_decode_params_size": ([], _i),
+    "rk_decode_get_limits": ([_p], _i),
     "rk_embed_ln_rows": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _f, _p], _i),
     "rk_add_ln_rows": ([_p, _p, _p, _p, _p, _i, _i, _i, _f, _p], _i),
     "rk_post_rows": ([_p, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p], _i),
@@ -68,6 +69,16 @@ def lib():
             fn.argtypes, fn.restype = args, ret
         _lib = L
     return _lib
+
+
+MM_REGS, MM_TILE128, MM_TILE64 = 0, 1, 2
+
+
+def mm_plan(M: int, N: int, K: int, use_workspace: bool = True):
+    """(kernel, splits) that rk_mm_int4_g128[_ws] runs for this shape (kernel: MM_REGS / MM_TILE128 / MM_TILE64)."""
+    k, sp = _i(), _i()
+    check(lib().rk_mm_int4_plan(M, N, K, int(use_workspace), ctypes.byref(k), ctypes.byref(sp)), "mm_int4_plan")
+    return k.value, sp.value
 
 
 def exported_symbols():

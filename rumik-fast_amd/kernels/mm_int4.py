@@ -51,12 +51,21 @@ def mm_int4(x, q, s, m, BM=None, BN=64, num_warps=4, num_stages=3, out=None):
     return y
 
 
-def warmup(shapes):
-    """Run every (N, K) shape once so the first real prompt pays no one-time cost (reference
-    kernels/mm_int4.py:49-56; there is no JIT here, this only loads the code object and touches the shapes)."""
+def warmup(shapes, max_T=512):
+    """Run every (N, K) shape once per kernel plan a prompt of up to max_T rows can select (reference
+    kernels/mm_int4.py:49-56 runs its Triton buckets; there is no JIT here, this loads the code objects and touches
+    every plan: the 128 x 128 and 64 x 64 tile kernels, with and without the split over K)."""
     for n, k in shapes:
         q = torch.zeros(n, k // 2, device="cuda", dtype=torch.uint8)
         s = torch.zeros(n, k // G, device="cuda", dtype=torch.float16)
-        for T in (17, 33, 49, 101):
+        for T in plan_lengths(n, k, max_T):
             mm_int4(torch.zeros(T, k, device="cuda", dtype=torch.bfloat16), q, s, s)
     torch.cuda.synchronize()
+
+
+def plan_lengths(n, k, max_T=512):
+    """The shortest prompt length in [1, max_T] for each distinct kernel plan of an (N, K) product."""
+    first = {}
+    for T in range(1, max_T + 1):
+        first.setdefault(H.mm_plan(T, n, k, use_workspace=True), T)
+    return sorted(first.values())

@@ -5,6 +5,7 @@ Distributions (one per configuration of the benchmark definition):
                 scale fp16 ~ U[1e-3, 2e-2] per (row, 128-column group); min fp16 = -7.5*scale + N(0,1)*scale
   int8 head     codes int8 uniform in [-127, 127]; per-row scale fp16 ~ U[1e-3, 1e-2]
   activations   fp16 ~ N(0, 1)
+  LayerNorm w   fp16 ~ U[0.5, 1.5] per layer (the benchmark leaves them unspecified; not 1, so tests see their index)
 Draw order inside one generator: codes, scale, min jitter (then x when asked for). A CPU torch.Generator makes the
 values identical on every host; `device="cuda"` draws on the GPU instead (fast, for benchmarks whose values do not
 matter, not bit-identical to the CPU draw).
@@ -36,6 +37,11 @@ def int8_weights(N: int, K: int, gen: torch.Generator, device="cpu"):
     q = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
     s = (torch.rand(N, generator=gen, device=dev) * (1e-2 - 1e-3) + 1e-3).half()
     return q.to(device), s.to(device)
+
+
+def ln_weights(H: int, gen: torch.Generator, device="cpu"):
+    """LayerNorm weights fp16 [H] ~ U[0.5, 1.5]."""
+    return (torch.rand(H, generator=gen, device=gen.device) + 0.5).half().to(device)
 
 
 def activations(shape, gen: torch.Generator, device="cpu", dtype=torch.float16):

@@ -31,17 +31,19 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     out = subprocess.run(["nm", "-D", "--defined-only", str(HL.LIB_PATH)], capture_output=True, text=True,
                          check=True).stdout
-    exported = set(re.findall(r"\bT (rk_\w+)$", out, flags=re.M))
+    exported = set(re.findall(r"\bT (\w+)$", out, flags=re.M))
     assert set(declared()) <= exported, sorted(set(declared()) - exported)
+    # and nothing else: the library is built with hidden visibility, the header alone decides the exports
+    assert exported == set(declared()), sorted(exported - set(declared()))
 
 
 def test_binding_table_covers_the_header():
-    assert set(declared()) <= set(HL.exported_symbols())
+    assert set(declared()) == set(HL.exported_symbols())
 
 
 def test_version_and_status_strings():
     lib = HL.lib()
-    assert lib.rk_abi_version() == 4
+    assert lib.rk_abi_version() == 5
     texts = {0: "ok", -1: "shape", -2: "unsupported block shape", -3: "unsupported dtype", -4: "null pointer",
              -6: "kernel launch failed"}
     for code, t in texts.items():
@@ -137,3 +139,18 @@ def test_sampler_entry_points_validate_before_any_device_work():
     assert tail(1024, 30) == -1 and tail(2048, 40) == -1
     assert lib.rk_sample_tail(P, 1, P, P, P, 1, P, P, P, 1e-5, 2048, 512, P, 2, 16385, 16384, P, P, P, P, P, 1.25,
                               16384, 8, 30, P, P, 2048, P, None, S) == -4
+
+
+@pytest.mark.parametrize("M,N,K,kernel", [(512, 22016, 2048, HL.MM_TILE128), (201, 25088, 2048, HL.MM_TILE128),
+                                          (512, 2048, 11008, HL.MM_TILE64), (69, 25088, 2048, HL.MM_TILE64),
+                                          (34, 22016, 2048, HL.MM_TILE64), (128, 22016, 2048, HL.MM_TILE64),
+                                          (512, 3072, 2048, HL.MM_TILE64), (4, 32, 200064, HL.MM_REGS)])
+def test_mm_int4_plan_query(M, N, K, kernel):
+    """The plan query names the kernel each shape runs (the GPU tests assert it for the shapes they cover)."""
+    k, sp = HL.mm_plan(M, N, K, use_workspace=False)
+    assert k == kernel and sp == 1
+    k2, sp2 = HL.mm_plan(M, N, K, use_workspace=True)
+    nbytes = HL.lib().rk_mm_int4_workspace_bytes(M, N, K)
+    assert (sp2 > 1) == (nbytes > 0) and nbytes == (sp2 * M * N * 4 if sp2 > 1 else 0)
+    with pytest.raises(RuntimeError):
+        HL.mm_plan(M, N, 100, use_workspace=False)

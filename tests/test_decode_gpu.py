@@ -4,8 +4,9 @@ replayed hipGraph. State is compared after every step (the reference's state-clo
 engine/check_fused.py:20-34).
 
 Tolerances: every activation is stored in fp16 and the step chains ~8 kernels per layer, so results are compared by
-norm-relative error / cosine: hidden state and logits within 1e-2 / 0.9999 per step on the small model and on the
-full-width model (4 layers of the 36-layer shape; each layer is the same computation).
+norm-relative error / cosine: hidden state and logits within 1e-2 / 0.9999 per step on the small model, on the
+full-width model, at the benchmarked contexts (1024 / 2048 slots: all 64 attention splits, up to 32 slots per split)
+and for one whole 36-layer step at the last cache slot.
 """
 import numpy as np
 import pytest
@@ -22,43 +23,49 @@ def _np(t):
     return t.detach().float().cpu().numpy()
 
 
-def _oracle_model(cfg, w):
-    n = lambda t: t.cpu().numpy()  # noqa: E731
+def _oracle_model(cfg, w, dt=np.float16):
+    n = lambda t: t.cpu().float().numpy() if t.dtype == torch.bfloat16 else t.cpu().numpy()  # noqa: E731
     cos, sin = OG.rope_tables(cfg.S, cfg.HD, cfg.rope_theta)
-    return OG.DecodeModel(
+    return OG.DecodeModel(cache_weights=True,
         L=cfg.L, H=cfg.H, NH=cfg.NH, NKV=cfg.NKV, HD=cfg.HD, inter=cfg.inter, eps=cfg.eps,
         w_in=[tuple(map(n, t)) for t in w["w_in"]], w_o=[tuple(map(n, t)) for t in w["w_o"]],
         w_down=[tuple(map(n, t)) for t in w["w_down"]], ln=[n(t) for t in w["ln"]], norm=n(w["norm"]),
         emb=(n(w["emb"][0]), n(w["emb"][1])), head=(n(w["head"][0]), n(w["head"][1])),
-        rope=(cos.astype(np.float16).astype(np.float32), sin.astype(np.float16).astype(np.float32)),
-        sliding=cfg.sliding)
+        rope=(OG.round_to(cos, dt), OG.round_to(sin, dt)), sliding=cfg.sliding)
 
 
-def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph"):
+def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph", dtype=torch.float16):
+    """dtype: the activation / KV-cache dtype of the graph engine (the persistent engine is fp16); for bf16 the
+    LayerNorm weights are bf16 too (as the reference engine's are) and the oracle rounds at bf16."""
     w = decode.random_weights(cfg, seed, device="cpu", gen_device="cpu")
+    if dtype == torch.bfloat16:
+        w["ln"] = [t.bfloat16() for t in w["ln"]]
+        w["norm"] = w["norm"].bfloat16()
     wd = {k: ([tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for v in vv]
               if isinstance(vv, list) else (tuple(t.to(dev) for t in vv) if isinstance(vv, tuple) else vv.to(dev)))
           for k, vv in w.items()}
-    eng = decode.DecodeStep(cfg, wd, device=dev) if engine == "graph" else decode.PersistentDecode(cfg, wd, device=dev)
+    eng = (decode.DecodeStep(cfg, wd, device=dev, dtype=dtype) if engine == "graph"
+           else decode.PersistentDecode(cfg, wd, device=dev))
     g = torch.Generator().manual_seed(seed + 1)
-    kc = torch.zeros(cfg.L, cfg.NKV, cfg.S, cfg.HD, dtype=torch.float16)
-    kc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).half()
+    kc = torch.zeros(cfg.L, cfg.NKV, cfg.S, cfg.HD, dtype=dtype)
+    kc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).to(dtype)
     vc = torch.zeros_like(kc)
-    vc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).half()
+    vc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).to(dtype)
     eng.kc.copy_(kc.to(dev))
     eng.vc.copy_(vc.to(dev))
     tok = 7
     eng.set_state(tok, ctx)
     if use_graph:
         eng.capture()
-    md = _oracle_model(cfg, w)
-    okc, ovc = kc.numpy().copy(), vc.numpy().copy()
+    odt = "bf16" if dtype == torch.bfloat16 else np.float16
+    md = _oracle_model(cfg, w, odt)
+    okc, ovc = kc.float().numpy().copy(), vc.float().numpy().copy()
     reps = []
     for s in range(steps):
         pos = ctx + s
         eng.replay() if use_graph else eng.step()
         torch.cuda.synchronize()
-        logits, h, x = OG.decode_step(md, tok, pos, okc, ovc)
+        logits, h, x = OG.decode_step(md, tok, pos, okc, ovc, dt=odt)
         assert int(eng.pos.item()) == pos + 1
         if engine == "persistent":
             assert eng.status_word() == 0, "a grid barrier timed out"
@@ -73,9 +80,9 @@ def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph"):
         # this step's K/V were written at slot pos of every layer
         np.testing.assert_allclose(_np(eng.vc[:, :, pos]), ovc[:, :, pos].astype(np.float32), rtol=1e-2, atol=1e-2)
         # continue from the oracle's own state for the next step, so errors do not compound across steps
-        eng.x.copy_(torch.tensor(x).half().to(dev))
-        eng.kc[:, :, pos].copy_(torch.tensor(okc[:, :, pos]).to(dev))
-        eng.vc[:, :, pos].copy_(torch.tensor(ovc[:, :, pos]).to(dev))
+        eng.x.copy_(torch.tensor(x).to(eng.x.dtype).to(dev))
+        eng.kc[:, :, pos].copy_(torch.tensor(okc[:, :, pos]).to(dtype).to(dev))
+        eng.vc[:, :, pos].copy_(torch.tensor(ovc[:, :, pos]).to(dtype).to(dev))
     return reps
 
 
@@ -86,6 +93,21 @@ SMALL = dict(L=3, H=256, NH=4, NKV=2, HD=128, inter=384, S=64, n_audio=100, voca
 def test_small_model_steps(use_graph, dev):
     cfg = decode.Config(**SMALL)
     reps = _run(cfg, dev, ctx=5, steps=4, use_graph=use_graph)
+    print(reps[-1])
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_small_model_steps_bf16(use_graph, dev):
+    """The graph engine as the reference engine allocates it (engine/rumik_fused.py:40-52): bf16 x / h / q / o / act,
+    bf16 KV cache, bf16 cos / sin and LayerNorm weights; the oracle rounds at bf16 at the same points."""
+    cfg = decode.Config(**SMALL)
+    reps = _run(cfg, dev, ctx=5, steps=4, use_graph=use_graph, dtype=torch.bfloat16)
+    print(reps[-1])
+
+
+def test_full_width_two_layers_bf16(dev):
+    cfg = decode.Config(L=2, vocab=64, sliding=[True, False])
+    reps = _run(cfg, dev, ctx=700, steps=2, use_graph=True, dtype=torch.bfloat16)
     print(reps[-1])
 
 
@@ -165,3 +187,47 @@ def test_persistent_step_with_sampler_token_loop(dev):
         tok = new  # the oracle continues on the GPU's token stream
         eng.kc[:, :, ctx + s].copy_(torch.tensor(okc[:, :, ctx + s]).to(dev))
         eng.vc[:, :, ctx + s].copy_(torch.tensor(ovc[:, :, ctx + s]).to(dev))
+
+
+@pytest.mark.parametrize("ctx", [1023, 1030, 2040, 2046])
+def test_persistent_long_contexts(ctx, dev):
+    """The contexts the benchmark times: the full 2048-slot cache with 64 splits per KV head. At ctx 1023 all 64
+    splits hold 16 slots, at 1030 43 splits hold 24, at 2040 / 2046 all 64 hold 32 (every prefetched K / V slot of
+    a streamer is used, and the 64-split combine runs in every head's blocks). Two steps each, both checked."""
+    cfg = decode.Config(L=2, vocab=64, sliding=[True, False])
+    reps = _run(cfg, dev, ctx=ctx, steps=2, use_graph=True, engine="persistent", seed=40 + ctx % 7)
+    print(ctx, reps[-1])
+
+
+def _cpu(w):
+    return {k: ([tuple(t.cpu() for t in v) if isinstance(v, tuple) else v.cpu() for v in vv]
+                if isinstance(vv, list) else (tuple(t.cpu() for t in vv) if isinstance(vv, tuple) else vv.cpu()))
+            for k, vv in w.items()}
+
+
+@pytest.mark.timeout(900)
+def test_persistent_36_layers_at_last_slot(dev):
+    """Config 4's whole step: 36 full-width layers (RoPE on 3 of every 4), the int8 head over 16385 rows, the
+    2048-slot cache filled to 2047 slots, one step at pos 2047 (the benchmark's ctx 2048). x, the final hidden state,
+    the logits and the new K / V slot of every layer against the decode oracle."""
+    cfg = decode.Config(vocab=64)
+    w = decode.random_weights(cfg, 6, device=dev, gen_device="cuda")
+    wc = _cpu(w)
+    eng = decode.PersistentDecode(cfg, w, device=dev)
+    pos = cfg.S - 1
+    g = torch.Generator(device=dev).manual_seed(7)
+    eng.kc[:, :, :pos].normal_(generator=g)
+    eng.vc[:, :, :pos].normal_(generator=g)
+    okc, ovc = eng.kc.cpu().numpy(), eng.vc.cpu().numpy()
+    eng.set_state(9, pos)
+    eng.capture()
+    eng.replay()
+    torch.cuda.synchronize()
+    assert eng.status_word() == 0 and int(eng.pos.item()) == pos + 1
+    md = _oracle_model(cfg, wc)
+    logits, h, x = OG.decode_step(md, 9, pos, okc, ovc)
+    for name, got, ref in (("x", eng.x, x), ("hn", eng.hn, h), ("logits", eng.logits, logits),
+                           ("k", eng.kc[:, :, pos], okc[:, :, pos]), ("v", eng.vc[:, :, pos], ovc[:, :, pos])):
+        rep = O.parity_report(_np(got).ravel(), np.asarray(ref, np.float32).ravel())
+        print(name, rep)
+        assert rep["norm_rel"] < 1e-2 and rep["cosine"] > 0.9999, (name, rep)

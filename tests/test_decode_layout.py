@@ -10,26 +10,78 @@ import decode
 def test_work_table_covers_every_tile_once(cfg_kw):
     cfg = decode.Config(**cfg_kw)
     nb, nsp = 256, min(32, 256 // cfg.NKV)
+    lim = decode.decode_limits()
     t = decode.work_table(cfg, nb, nsp)
     qkv_tiles = (cfg.NH + 2 * cfg.NKV) * cfg.HD // 16
     n_tiles = qkv_tiles + 2 * cfg.inter // 16
-    tiles = t[:, :8]
-    assert (tiles >= 0).sum(1).max() <= decode.MAX_TILES
+    tiles = t[:, :lim.max_tiles]
+    assert (tiles >= 0).sum(1).max() <= lim.max_tiles
     # q / k / v tiles come first and fit the first pass
     for b in range(nb):
         row = [int(v) for v in tiles[b] if v >= 0]
         nq = sum(v < qkv_tiles for v in row)
-        assert nq <= decode.FIRST_PASS and all(v < qkv_tiles for v in row[:nq])
+        assert nq <= lim.first_pass and all(v < qkv_tiles for v in row[:nq])
     got = sorted(int(v) for v in tiles.flatten() if v >= 0)
     assert got == list(range(n_tiles))
     # slices are contiguous, cover all MLP channels, and each block owns the gate/up tiles of its slices
-    sb, se = t[:, 8].tolist(), t[:, 9].tolist()
+    sb, se = t[:, lim.slice_begin_col].tolist(), t[:, lim.slice_end_col].tolist()
     assert sb[0] == 0 and se[-1] == cfg.inter // 16 and all(se[b] == sb[b + 1] for b in range(nb - 1))
-    assert max(e - s for s, e in zip(sb, se)) <= decode.MAX_SLICES
+    assert max(e - s for s, e in zip(sb, se)) <= lim.max_slices
     for b in range(nb):
         own = set(int(v) for v in tiles[b] if v >= qkv_tiles)
         assert own == {qkv_tiles + 2 * k + h for k in range(sb[b], se[b]) for h in (0, 1)}
-    assert (t[:, 10:] == -1).all()
+    assert (t[:, lim.slice_end_col + 1:] == -1).all()
+
+
+def test_limits_match_the_kernel_contract():
+    """The limits come from the library (rk_decode_get_limits), not from copies in Python."""
+    lim = decode.decode_limits()
+    assert 1 <= lim.first_pass <= lim.max_tiles < lim.slice_begin_col < lim.slice_end_col < lim.work_stride
+    assert lim.max_slices >= 1 and lim.x_copies >= 1 and lim.max_splits >= 1
+    # the default model fits: 2048-slot cache over 64 splits, 688 MLP slices over 256 blocks
+    cfg = decode.Config()
+    assert -(-cfg.S // 64) <= lim.max_slots_per_split and -(-cfg.inter // 16 // 256) <= lim.max_slices
+
+
+def _table_and_cfg():
+    cfg = decode.Config()
+    return decode.work_table(cfg, 256, 64), cfg
+
+
+def test_validation_rejects_a_qkv_tile_after_the_first_pass():
+    """A q / k / v tile placed after the first pass would be published after the block's own q poll (which may wait
+    for it): a circular wait. The host refuses such a table before any launch."""
+    lim = decode.decode_limits()
+    t, cfg = _table_and_cfg()
+    qkv_tiles = (cfg.NH + 2 * cfg.NKV) * cfg.HD // 16
+    b = next(i for i in range(256) if 0 <= int(t[i, 0]) < qkv_tiles and int(t[i, lim.first_pass]) >= 0)
+    bad = t.clone()
+    bad[b, 0], bad[b, lim.first_pass] = t[b, lim.first_pass], t[b, 0]  # move the q/k/v tile to the second pass
+    with pytest.raises(ValueError, match="first"):
+        decode.validate_work_table(bad, cfg)
+
+
+@pytest.mark.parametrize("edit", ["drop_tile", "dup_tile", "gap", "slice_gap", "foreign_tile", "wide"])
+def test_validation_rejects_malformed_tables(edit):
+    lim = decode.decode_limits()
+    t, cfg = _table_and_cfg()
+    bad = t.clone()
+    n0 = int((t[0, :lim.max_tiles] >= 0).sum())
+    if edit == "drop_tile":
+        bad[0, n0 - 1] = -1
+    elif edit == "dup_tile":
+        bad[0, n0 - 1] = t[1, 0]
+    elif edit == "gap":
+        bad[0, 0] = -1
+    elif edit == "slice_gap":
+        bad[5, lim.slice_end_col] += 1
+    elif edit == "foreign_tile":  # swap one gate/up tile between two blocks: tiles stay unique, ownership breaks
+        i, j = n0 - 1, int((t[100, :lim.max_tiles] >= 0).sum()) - 1
+        bad[0, i], bad[100, j] = t[100, j], t[0, i]
+    elif edit == "wide":
+        bad = torch.cat([bad, bad[:, :1]], 1)
+    with pytest.raises(ValueError):
+        decode.validate_work_table(bad, cfg)
 
 
 def test_o_layout_items():

@@ -64,3 +64,23 @@ def test_stop_after_min_new(dev):
     toks, stats = gen.generate([3, 9], seed=2)
     assert len(toks) == eng.min_new and eng.end_id not in toks
     assert int(eng.out[eng.min_new].item()) == eng.end_id
+
+
+def test_nonzero_status_stops_generation(dev):
+    """A step whose status word is nonzero ends generation with DecodeError instead of emitting tokens sampled from
+    invalid logits. The condition is forced from the host: after the first frame the device position is moved past
+    the cache, so the next step's blocks all leave at entry (status bit 2); no wait times out."""
+    from generate import DecodeError
+    eng, ids = _engine(dev, b2=-50.0)
+    gen = Generator(eng, Q=Q, max_new=64)
+    seen = []
+
+    def on_frame(toks):
+        seen.append(len(toks))
+        if len(seen) == 1:
+            eng.pos.fill_(eng.cfg.S + 3)  # ordered after the frame already queued, before the next one
+    with pytest.raises(DecodeError, match="status 4"):
+        gen.generate([5, 17], seed=1, on_frame=on_frame)
+    assert seen and eng.status_word() == 0  # the engine was reset before the error was raised
+    toks, _ = gen.generate([5, 17], seed=1)  # and still generates afterwards
+    assert len(toks) == 65

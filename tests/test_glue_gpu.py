@@ -188,3 +188,105 @@ def test_unsplit_attn_matches_split(dev):
     ref = OG.attend(_np(q).reshape(NH, HD), _np(kc)[:, :201], _np(vc)[:, :201])
     np.testing.assert_allclose(_np(o1).reshape(NH, HD), ref, rtol=1e-2, atol=2e-3)
     np.testing.assert_allclose(_np(o1), _np(o2), rtol=1e-2, atol=2e-3)
+
+
+# ---- bf16: the reference engine's activation dtype (engine/rumik_fused.py:40-52); the oracle rounds at bf16
+BF16 = torch.bfloat16
+
+
+def _bf(v):
+    return OG.round_bf16(np.asarray(v, np.float32))
+
+
+def test_add_ln_bf16(dev):
+    g = torch.Generator().manual_seed(10)
+    x, a, b = (torch.randn(2048, generator=g).bfloat16() for _ in range(3))
+    w = (torch.rand(2048, generator=g) + 0.5).bfloat16()
+    xd, hd = x.to(dev), torch.empty(2048, dtype=BF16, device=dev)
+    fused.add_ln(xd, a.to(dev), b.to(dev), w.to(dev), hd, 1e-5)
+    xs = _bf(x.float().numpy() + a.float().numpy() + b.float().numpy())
+    np.testing.assert_array_equal(_np(xd), xs)  # one rounding of the fp32 sum, bit-exact
+    ref = _bf(OG.cohere_ln(xs, w.float().numpy()))
+    np.testing.assert_allclose(_np(hd), ref, rtol=8e-3, atol=8e-3)  # bf16 output: 2^-8 relative per value
+
+
+def test_embed_ln_bf16(dev):
+    g = torch.Generator().manual_seed(11)
+    eq = torch.randint(-127, 128, (50, 2048), generator=g, dtype=torch.int8)
+    es = (torch.rand(50, generator=g) * 0.01 + 1e-3).half()
+    w = (torch.rand(2048, generator=g) + 0.5).bfloat16()
+    tok = torch.tensor([33], dtype=torch.int64, device=dev)
+    x, h = torch.empty(2048, dtype=BF16, device=dev), torch.empty(2048, dtype=BF16, device=dev)
+    fused.embed_ln(tok, eq.to(dev), es.to(dev), w.to(dev), x, h, 1e-5)
+    xr = _bf(eq[33].float().numpy() * np.float32(es[33].float()))
+    np.testing.assert_array_equal(_np(x), xr)
+    np.testing.assert_allclose(_np(h), _bf(OG.cohere_ln(xr, w.float().numpy())), rtol=8e-3, atol=8e-3)
+
+
+@pytest.mark.parametrize("pos,rope", [(0, True), (1777, True), (300, False)])
+def test_post_bf16(pos, rope, dev):
+    NH, NKV, HD, inter, S = 16, 4, 128, 11008, 2048
+    g = torch.Generator().manual_seed(12 + pos)
+    y = torch.randn((NH + 2 * NKV) * HD + 2 * inter, generator=g).bfloat16()
+    cos, sin = (torch.tensor(t).bfloat16() for t in OG.rope_tables(S, HD))
+    kc = torch.zeros(NKV, S, HD, dtype=BF16, device=dev)
+    vc = torch.zeros_like(kc)
+    qo = torch.empty(NH * HD, dtype=BF16, device=dev)
+    act = torch.empty(inter, dtype=BF16, device=dev)
+    fused.post[(1,)](y.to(dev), torch.tensor([pos], device=dev), cos.to(dev), sin.to(dev), kc, vc, qo, act, S, inter,
+                     NH=NH, NKV=NKV, HD=HD, ROPE=rope)
+    torch.cuda.synchronize()
+    yf = y.float().numpy()
+    q = yf[:NH * HD].reshape(NH, HD)
+    k = yf[NH * HD:(NH + NKV) * HD].reshape(NKV, HD)
+    v = yf[(NH + NKV) * HD:(NH + 2 * NKV) * HD].reshape(NKV, HD)
+    gt, up = yf[(NH + 2 * NKV) * HD:][:inter], yf[(NH + 2 * NKV) * HD:][inter:]
+    if rope:
+        c, s_ = cos[pos].float().numpy(), sin[pos].float().numpy()
+        q, k = OG.rope(q, c, s_), OG.rope(k, c, s_)
+    np.testing.assert_allclose(_np(qo).reshape(NH, HD), _bf(q), rtol=8e-3, atol=8e-3)
+    np.testing.assert_allclose(_np(kc[:, pos]), _bf(k), rtol=8e-3, atol=8e-3)
+    np.testing.assert_array_equal(_np(vc[:, pos]), v)
+    np.testing.assert_allclose(_np(act), _bf(OG.silu(gt) * up), rtol=8e-3, atol=8e-3)
+
+
+def _attn_dt(q, kc, vc, pos, dev, nsplit=64, NH=16, NKV=4, HD=128, dt=BF16):
+    po = torch.empty(NH, nsplit, HD, device=dev)
+    pm = torch.empty(NH, nsplit, device=dev)
+    pl = torch.empty(NH, nsplit, device=dev)
+    out = torch.empty(NH * HD, dtype=dt, device=dev)
+    p = torch.tensor([pos], device=dev)
+    fused.attn_split[(NKV, nsplit)](q, kc, vc, p, po, pm, pl, kc.shape[1], HD ** -0.5, REP=NH // NKV, HD=HD,
+                                    NSPLIT=nsplit)
+    fused.attn_combine[(NH,)](po, pm, pl, p, out, HD=HD, NSPLIT=nsplit)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("pos", [0, 300, 2047])
+def test_attention_bf16(pos, dev):
+    NH, NKV, HD, S = 16, 4, 128, 2048
+    g = torch.Generator().manual_seed(100 + pos)
+    kc = torch.randn(NKV, S, HD, generator=g).bfloat16()
+    vc = torch.randn(NKV, S, HD, generator=g).bfloat16()
+    q = torch.randn(NH * HD, generator=g).bfloat16()
+    out = _attn_dt(q.to(dev), kc.to(dev), vc.to(dev), pos, dev)
+    ref = OG.attend(q.float().numpy().reshape(NH, HD), kc[:, :pos + 1].float().numpy(), vc[:, :pos + 1].float().numpy())
+    rep = O.parity_report(_np(out), _bf(ref).ravel())
+    assert rep["norm_rel"] < 4e-3 and rep["cosine"] > 0.99999, rep
+
+
+def test_attention_bf16_beyond_fp16_range(dev):
+    """bf16 keys and queries far outside fp16's range (|k| up to 3e5, |q| down to 1e-6) keep their values: the
+    q . k products are formed in fp32, so scores stay finite and the result matches the fp32 oracle."""
+    NH, NKV, HD, S, pos = 16, 4, 128, 256, 99
+    g = torch.Generator().manual_seed(7)
+    kc = (torch.randn(NKV, S, HD, generator=g) * 1e5).bfloat16()       # |k| ~ 1e5 > 65504
+    vc = torch.randn(NKV, S, HD, generator=g).bfloat16()
+    q = (torch.randn(NH * HD, generator=g) * 3e-6).bfloat16()          # scores q.k / sqrt(128) = O(1)
+    assert float(kc.float().abs().max()) > 65504 and float(q.float().abs().min()) < 6e-5
+    out = _attn_dt(q.to(dev), kc.to(dev), vc.to(dev), pos, dev, nsplit=16)
+    assert torch.isfinite(out.float()).all()
+    ref = OG.attend(q.float().numpy().reshape(NH, HD), kc[:, :pos + 1].float().numpy(), vc[:, :pos + 1].float().numpy())
+    rep = O.parity_report(_np(out), _bf(ref).ravel())
+    assert rep["norm_rel"] < 1e-2 and rep["cosine"] > 0.9999, rep

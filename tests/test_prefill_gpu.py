@@ -39,10 +39,34 @@ def test_config3_shapes(M, N, K, dev):
     print(f"M={M} N={N} K={K}: {rep}")
 
 
-def test_config3_m512(dev):
-    X, q, s, m = synth.prefill_case(512, 3072, 2048, 3)
+@pytest.mark.parametrize("N,K,kernel", [(3072, 2048, H.MM_TILE64), (22016, 2048, H.MM_TILE128),
+                                         (2048, 11008, H.MM_TILE64)])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_config3_m512(N, K, kernel, xdt, dev):
+    """M = 512 on every config-3 shape; gate+up 22016 x 2048 runs the 128 x 128 tile kernel (asserted)."""
+    assert H.mm_plan(512, N, K)[0] == kernel
+    X, q, s, m = synth.prefill_case(512, N, K, 3)
+    X = X.to(xdt)
     Y = mm_int4.mm_int4(X.to(dev), q.to(dev), s.to(dev), m.to(dev))
-    _check(Y, _ref(X, q, s, m), "M=512")
+    rep = _check(Y, _ref(X, q, s, m), f"M=512 N={N} K={K} {xdt}")
+    print(f"M=512 N={N} K={K} {xdt}: {rep}")
+
+
+@pytest.mark.parametrize("T,kernel", [(34, H.MM_TILE64), (69, H.MM_TILE64), (201, H.MM_TILE128)])
+def test_reference_w_in_prompts(T, kernel, dev):
+    """The reference's own check (kernels/mm_int4.py:92-106): w_in 25088 x 2048 at T in {34, 69, 201}, bf16 X as
+    the engine passes it; T = 201 selects the 128 x 128 tile kernel (asserted)."""
+    N, K = 25088, 2048
+    assert H.mm_plan(T, N, K) == (kernel, 1)
+    X, q, s, m = synth.prefill_case(T, N, K, 30 + T)
+    X = X.bfloat16()
+    Y = mm_int4.mm_int4(X.to(dev), q.to(dev), s.to(dev), m.to(dev))
+    assert Y.dtype == torch.bfloat16
+    ref = _ref(X, q, s, m)
+    rep = _check(Y, ref, f"T={T}")
+    # the reference's own metric: norm-relative error against the fp32 dequantize-then-matmul (~0.0017 there)
+    assert rep["norm_rel"] < 5e-3, rep
+    print(f"T={T}: {rep}")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 128), (3, 17, 256), (17, 100, 384), (33, 48, 2048), (65, 129, 1152),

@@ -53,7 +53,7 @@ def _model(dev, seed=21):
           for k, vv in w.items()}
     n = lambda t: t.numpy()  # noqa: E731
     cos, sin = OG.rope_tables(cfg.S, cfg.HD, cfg.rope_theta)
-    md = OG.DecodeModel(
+    md = OG.DecodeModel(cache_weights=True,
         L=cfg.L, H=cfg.H, NH=cfg.NH, NKV=cfg.NKV, HD=cfg.HD, inter=cfg.inter, eps=cfg.eps,
         w_in=[tuple(map(n, t)) for t in w["w_in"]], w_o=[tuple(map(n, t)) for t in w["w_o"]],
         w_down=[tuple(map(n, t)) for t in w["w_down"]], ln=[n(t) for t in w["ln"]], norm=n(w["norm"]),
@@ -63,23 +63,27 @@ def _model(dev, seed=21):
     return cfg, wd, md
 
 
-def test_prefill_matches_stepwise_oracle(dev):
+@pytest.mark.parametrize("T", [12, 69])
+def test_prefill_matches_stepwise_oracle(dev, T):
+    """The whole batched prefill against the decode oracle stepped over the prompt (the reference's decode-vs-prefill
+    consistency check, engine/check.py:46-56); T = 69 is the benchmarked prompt length (its w_in product runs the
+    64 x 64 tile kernel over 392 column tiles, w_o / w_down the split-free 64 x 64 plan)."""
     cfg, wd, md = _model(dev)
     eng = decode.PersistentDecode(cfg, wd, device=dev, keep_layer_weights=True)
-    pf = PF.Prefill(cfg, wd, eng.kc, eng.vc, eng.cos, eng.sin, max_T=64)
-    ids = [int(v) for v in torch.randint(0, cfg.vocab, (12,), generator=torch.Generator().manual_seed(4))]
+    pf = PF.Prefill(cfg, wd, eng.kc, eng.vc, eng.cos, eng.sin, max_T=128)
+    ids = [int(v) for v in torch.randint(0, cfg.vocab, (T,), generator=torch.Generator().manual_seed(4))]
     hn = pf.run(ids, hn=eng.hn)
     torch.cuda.synchronize()
     okc = np.zeros((cfg.L, cfg.NKV, cfg.S, cfg.HD), np.float16)
     ovc = np.zeros_like(okc)
     for t, tok in enumerate(ids):
         _, h, x = OG.decode_step(md, tok, t, okc, ovc)
-    for got, ref in ((eng.kc[:, :, :12], okc[:, :, :12]), (eng.vc[:, :, :12], ovc[:, :, :12]), (hn, h)):
+    for got, ref in ((eng.kc[:, :, :T], okc[:, :, :T]), (eng.vc[:, :, :T], ovc[:, :, :T]), (hn, h)):
         rep = O.parity_report(_np(got).reshape(-1), ref.astype(np.float32).reshape(-1))
         assert rep["norm_rel"] < 1e-2 and rep["cosine"] > 0.9999, rep
     # each layer's cache rows, slot by slot
     for i in range(cfg.L):
-        for t in (0, 5, 11):
+        for t in (0, T // 2, T - 1):
             rep = O.parity_report(_np(eng.kc[i, :, t]).reshape(-1), okc[i, :, t].astype(np.float32).reshape(-1))
             assert rep["norm_rel"] < 1e-2, (i, t, rep)
 

@@ -128,3 +128,33 @@ def test_file_is_plain_safetensors(ckpt):
     assert header["__metadata__"]["format"] == W.FORMAT
     assert set(header) - {"__metadata__"} == set(ex)
     assert np.dtype("uint8").itemsize == 1
+
+
+def test_drop_in_quantize_is_bit_exact_with_the_oracle():
+    """kernels/int4_gemv.quantize (torch, load time) writes exactly the codes, scales and mins of the pinned oracle
+    (oracle.int4.quantize, reference kernels/int4_gemv.py:16-24) on seeded inputs: random weights at several
+    scales, groups whose values sit exactly on rounding ties (half to even), constant groups (the 1e-8 clamp) and
+    bf16 / fp16 inputs."""
+    import int4_gemv
+    from oracle import int4 as O
+    g = torch.Generator().manual_seed(31)
+    cases = [torch.randn(64, 1024, generator=g) * sc for sc in (1e-3, 0.05, 1.0, 300.0)]
+    ties = (torch.randint(0, 31, (32, 512), generator=g).float() * 0.5)  # k / 2 on [0, 15]: every odd k is a tie
+    ties[:, ::128] = 0.0
+    ties[:, 1::128] = 15.0                                              # min 0, max 15: step exactly 1
+    cases.append(ties)
+    const = torch.full((8, 256), 0.37)
+    const[4:] = -2.0
+    cases.append(const)
+    cases.append((torch.randn(16, 2048, generator=g) * 0.02).bfloat16())
+    cases.append((torch.randn(16, 2048, generator=g) * 0.02).half())
+    for w in cases:
+        q, s, m = int4_gemv.quantize(w)
+        oq, os_, om = O.quantize(w.float().numpy())
+        assert np.array_equal(q.numpy(), oq)
+        assert np.array_equal(s.numpy().view(np.uint16), os_.view(np.uint16))
+        assert np.array_equal(m.numpy().view(np.uint16), om.view(np.uint16))
+    # the tie case really exercised ties, both directions
+    codes = O.unpack_int4(O.quantize(ties.numpy())[0])
+    half = (ties.numpy() * 2).astype(int) % 2 == 1
+    assert half.sum() > 1000 and set(np.unique(codes[half] % 2)) == {0}  # ties went to the even code

@@ -40,6 +40,7 @@ extern "C" {
 #define RK_ERR_NULL (-4)   /* a required pointer is NULL */
 #define RK_ERR_ALIGN (-5)  /* a pointer is not aligned as the kernel's vector loads need */
 #define RK_ERR_LAUNCH (-6) /* the HIP launch itself failed */
+#define RK_ERR_SCRATCH (-7) /* the call needs more scratch than the library's fixed array holds */
 
 typedef void* rk_stream_t; /* a hipStream_t; NULL = the default stream */
 
@@ -138,6 +139,19 @@ size_t rk_mm_int4_workspace_bytes(int M, int N, int K);
 int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
                        const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, void* workspace,
                        size_t workspace_bytes, rk_stream_t stream);
+
+/* rk_mm_int4_g128_ws without a workspace argument and without any allocation: the split-K partial sums go to a
+ * fixed array of RK_MM_SCRATCH_BYTES in the library's device memory (one per GPU, held until the process ends,
+ * its address looked up once per device on the first call). No counterpart in the reference: it is for callers
+ * that cannot allocate (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same plan, kernels and results as rk_mm_int4_g128_ws. Shapes whose split-K partials exceed the array
+ * (rk_mm_int4_workspace_bytes(M, N, K) > RK_MM_SCRATCH_BYTES; none with K <= 49152) return RK_ERR_SCRATCH before
+ * any launch. Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on different streams
+ * without ordering) race and give wrong results; calls ordered on one stream are safe. */
+#define RK_MM_SCRATCH_BYTES (8u << 20)
+int rk_mm_int4_g128_noalloc(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
+                            const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K,
+                            rk_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------
  * Decode-step glue (reference engine/fused.py). Activations of one decode step are vectors of `act_dtype`

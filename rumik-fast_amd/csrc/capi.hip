@@ -14,6 +14,7 @@ const char* rk_status_string(int status) {
         case RK_ERR_NULL: return "null pointer";
         case RK_ERR_ALIGN: return "misaligned pointer (16-byte alignment required)";
         case RK_ERR_LAUNCH: return "kernel launch failed";
+        case RK_ERR_SCRATCH: return "workspace larger than the library's fixed scratch (RK_MM_SCRATCH_BYTES)";
         default: return "unknown status";
     }
 }

@@ -12,6 +12,8 @@
 //   * per group: C = sum of 4 MFMAs from zero, then acc = scale * C + xsum * min in fp32 (xsum[g][m] precomputed
 //     per block in LDS; a lane's 4 D rows are 4 consecutive m, one ds_read_b128).
 // Codes never leave int4 in HBM; every product is exact, sums are fp32.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -488,6 +490,34 @@ int mm_run(const MmPlan& p, const void* X, int x_dtype, int ldx, const uint8_t* 
 
 }  // namespace
 
+// ---------------------------------------------------------------------------------------------- fixed scratch
+// The split-K partial sums of rk_mm_int4_g128_noalloc live here instead of in a caller's workspace: one array per
+// GPU, held until the process ends. In host code `scratch` is only a stand-in for the symbol; its device address
+// on each GPU comes from hipGetSymbolAddress (scratch_ptr) and only that address is passed to kernels.
+static __device__ __align__(256) float scratch[RK_MM_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices];  // device address of `scratch` per device (null until that device's first call)
+
+// the current device's address of `scratch`, looked up once per device with that device current
+int scratch_ptr(float** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return RK_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RK_ERR_LAUNCH;
+        g_scratch[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch[dev];
+    return RK_OK;
+}
+
+}  // namespace
+
 extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
                                const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K,
                                rk_stream_t stream) {
@@ -519,5 +549,24 @@ extern "C" int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uin
     if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) return RK_ERR_SHAPE;
     if (p.ws > 0 && ((uintptr_t)workspace & 15)) return RK_ERR_ALIGN;
     return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, static_cast<float*>(workspace),
+                  reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int rk_mm_int4_g128_noalloc(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
+                                       const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K,
+                                       rk_stream_t stream) {
+    // every check comes before the device is touched: a rejected call launches nothing
+    const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
+    if (st != RK_OK) return st;
+    const MmPlan p = mm_plan(M, N, K, true);
+    if (p.ws > RK_MM_SCRATCH_BYTES) return RK_ERR_SCRATCH;
+    float* part = nullptr;
+    if (p.ws > 0) {
+        const int e = scratch_ptr(&part);
+        if (e != RK_OK) return e;
+    }
+    // the partial sums need no clearing: block (tile, split) writes every (m, n) of its tile for its split before
+    // the reduction kernel, ordered after it on the stream, reads them
+    return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, part,
                   reinterpret_cast<hipStream_t>(stream));
 }

@@ -154,3 +154,16 @@ def test_mm_int4_plan_query(M, N, K, kernel):
     assert (sp2 > 1) == (nbytes > 0) and nbytes == (sp2 * M * N * 4 if sp2 > 1 else 0)
     with pytest.raises(RuntimeError):
         HL.mm_plan(M, N, 100, use_workspace=False)
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch():
+    """rk_mm_int4_g128_noalloc refuses, before touching any device, a shape whose split-K partials exceed the fixed
+    scratch (the pointers below are never dereferenced), and names the reason."""
+    M, N, K = 2048, 1024, 65536
+    assert HL.lib().rk_mm_int4_workspace_bytes(M, N, K) > HL.MM_SCRATCH_BYTES
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16, ctypes.c_void_p)
+    st = HL.lib().rk_mm_int4_g128_noalloc(p, HL.F16, K, p, p, p, p, HL.F16, N, M, N, K, None)
+    assert st == HL.ERR_SCRATCH
+    assert "scratch" in HL.lib().rk_status_string(st).decode()
+    assert HL.lib().rk_mm_int4_g128_noalloc(p, HL.F16, K, p, p, p, p, HL.F16, N, M, N, 100, None) == -1  # shape

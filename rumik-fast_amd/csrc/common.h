@@ -59,11 +59,42 @@ RK_DEV float dot2(h2_t a, h2_t b, float c) { return __builtin_amdgcn_fdot2(a, b,
 // byte permute (v_perm_b32): result byte i = byte sel_i of the 8-byte value {hi:lo}
 RK_DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 
+// ---------------------------------------------------------------- cross-row exchange without LDS
+// gfx950's v_permlane32_swap exchanges lanes 32..63 of one VGPR with lanes 0..31 of another (v_permlane16_swap:
+// the odd 16-lane rows of one with the even rows of the other). With both operands holding v, the two results are
+// v's lower and upper half, each in both halves; a + b is then v[i] + v[i ^ 32] in every lane, bit for bit what a
+// __shfl_xor exchange gives (IEEE addition commutes), without the LDS round trip of ds_bpermute. Inline asm: this
+// compiler's builtin drops the second result when it feeds float arithmetic. The s_nops give the wait states a
+// VALU write needs before the swap reads it, and the swap's results before a VALU reads them.
+template <int ROWS>
+RK_DEV void swap_halves(float v, float& a, float& b) {
+    static_assert(ROWS == 16 || ROWS == 32, "16- or 32-lane halves");
+    int x = __builtin_bit_cast(int, v), y = x;
+    if constexpr (ROWS == 32)
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+    else
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+    a = __builtin_bit_cast(float, x);
+    b = __builtin_bit_cast(float, y);
+}
+template <int M>
+RK_DEV float sum_xor(float v) {  // v[i] + v[i ^ M], M = 16 or 32
+    float a, b;
+    swap_halves<M>(v, a, b);
+    return a + b;
+}
+template <int M>
+RK_DEV float max_xor(float v) {  // max(v[i], v[i ^ M]), M = 16 or 32
+    float a, b;
+    swap_halves<M>(v, a, b);
+    return fmaxf(a, b);
+}
+
 // ---------------------------------------------------------------- wave64 reductions
-// Full-wave sum; every lane ends with the total. DPP inside 16-lane rows, ds_swizzle-free cross-row steps.
+// Full-wave sum; every lane ends with the total. Cross-row steps by lane swaps, DPP inside 16-lane rows.
 RK_DEV float wave_sum(float v) {
-    v += __shfl_xor(v, 32);
-    v += __shfl_xor(v, 16);
+    v = sum_xor<32>(v);
+    v = sum_xor<16>(v);
     v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));  // row_half_mirror
     v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));   // quad xor 2
     v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));   // quad xor 1
@@ -72,8 +103,8 @@ RK_DEV float wave_sum(float v) {
 }
 
 RK_DEV float wave_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 32));
-    v = fmaxf(v, __shfl_xor(v, 16));
+    v = max_xor<32>(v);
+    v = max_xor<16>(v);
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true)));
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true)));
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)));

@@ -360,7 +360,7 @@ RK_DEV void stage_h_frag(const RowVals& h, int rho, Lds& S) {
     sum += dpp<0x124>(sum);  // row_ror 4
     sum += dpp<0x122>(sum);  // row_ror 2
     sum += dpp<0x121>(sum);  // row_ror 1
-    sum += __shfl_xor(sum, 16);  // rows 0 + 1 (group 2 rho), rows 2 + 3 (group 2 rho + 1)
+    sum = sum_xor<16>(sum);  // rows 0 + 1 (group 2 rho), rows 2 + 3 (group 2 rho + 1)
     if ((lane & 31) == 0) S.hsum[g] = sum;
 }
 
@@ -430,8 +430,9 @@ RK_DEV int mlp_wave() { return wave_id() - kM0; }
 // the compiler can then wait for exactly the loads a computation needs. With data-dependent branches around loads
 // it cannot count the loads issued after a prefetch and waits for all of them.
 // win_t: per (layer, tile, group) 1 KiB of codes in lane order.
-// Paced: at most two tiles' loads (6) in flight per wave. The tile waves have nothing else to do meanwhile, and a
-// chip-wide burst of every block's tiles would queue ahead of the critical path's polls for microseconds.
+// Paced: at most two loads in flight per wave. The tile waves have nothing else to do meanwhile (the prefetch
+// still lands well before the next layer needs it), while a chip-wide burst of every block's tiles would queue ahead
+// of the critical path's polls for microseconds: a poll's loads wait behind what the CU already has in flight.
 RK_DEV void tile_issue(const Params& p, int l, const Lds& S, const Work& wk, TileRegs& tr) {
     const int lane = lane_id(), m = mlp_wave();
     const size_t base = (size_t)l * n_tiles(p);
@@ -446,7 +447,7 @@ RK_DEV void tile_issue(const Params& p, int l, const Lds& S, const Work& wk, Til
         const u2_t sm = *(reinterpret_cast<const u2_t*>(p.win_sm) + (T * 8 + slot) * 16 + (lane & 15));
         tr.sm[0][t] = sm.x;
         tr.sm[1][t] = sm.y;
-        if (t >= 1) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // tiles <= t - 2 have landed
+        asm volatile("s_waitcnt vmcnt(2)" ::: "memory");  // all but the last two loads have landed
     }
 }
 
@@ -613,6 +614,7 @@ RK_DEV void down_issue(const Params& p, int l, const Work& wk, DownRegs& dr) {
 #pragma unroll
         for (int q = 0; q < 2; ++q)
             dr.sm[k][q] = *reinterpret_cast<const u2_t*>(p.wd_sm + ((size_t)l * ngd + min(gb + q, ngd - 1)) * kH + 2 * rp);
+        asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // paced like the tiles: one row-pair group in flight
     }
 }
 
@@ -779,12 +781,12 @@ RK_DEV void attention(const Params& p, int64_t pos, const KVRegs& kv, const QReg
         d += dpp<0x141>(d);  // row_half_mirror: the other half of the 8 chunk lanes
         const float sc = valid ? d * p.scale : -INFINITY;
         float m = fmaxf(sc, dpp<0x128>(sc));  // row_ror 8 = lane ^ 8 inside a 16-lane row
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
+        m = max_xor<16>(m);
+        m = max_xor<32>(m);
         const float e = m == -INFINITY ? 0.f : __expf(sc - m);
         float l = e + dpp<0x128>(e);
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        l = sum_xor<16>(l);
+        l = sum_xor<32>(l);
         mx[r] = m;
         pe[r] = e;
         ls[r] = l;
@@ -1000,7 +1002,7 @@ RK_DEV void o_part(const Params& p, uint32_t tag, const ORegs& o, const Lds& S, 
         v += dpp<0xB1>(v);  // the row's 4 chunks sit in lanes 4j .. 4j + 3
         v += dpp<0x4E>(v);
         v = __builtin_fmaf(v, h16((uint16_t)o.sm[k]), h16((uint16_t)(o.sm[k] >> 16)) * asum);
-        const float nxt = __shfl_down(v, 4);  // the next row's total (lane + 4)
+        const float nxt = dpp<0x104>(v);  // row_shl 4: the next row's total (lane + 4, same 16-lane row)
         if ((lane & 7) == 0) {
             const int row = 128 * r + (i >> 2);  // even
             st_coh64(top + ((size_t)(row >> 3) * p.NH + h) * 4 + ((row & 7) >> 1), tpair(v, nxt, tag));
@@ -1016,8 +1018,8 @@ RK_DEV void o_part(const Params& p, uint32_t tag, const ORegs& o, const Lds& S, 
 RK_DEV float class4_sum(float v) {  // sum over the 16 lanes that share lane % 4
     v += dpp<0x128>(v);  // row_ror 8
     v += dpp<0x124>(v);  // row_ror 4
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
+    v = sum_xor<16>(v);
+    v = sum_xor<32>(v);
     return v;
 }
 

@@ -16,7 +16,12 @@ value = algorithmic bytes per step (sum over the four projections of N*K/2 + 4*N
 roofline: the dominant kernel (the fused w_in + SiLU launch, 27,328,000 B per launch: codes, scales, mins, x and the
 3072 + 11008 outputs), its average launch duration measured with HIP events on its stream over back-to-back
 launches with rotated weights.
-cpu_baseline: the CPU oracle's dequantize-then-matmul of the same step (numpy fp32), on this host's cores.
+roofline.read_ceiling_us: the best time of a read-only kernel over the same bytes in the same setting (the
+reference's kernels/roofline.py method), and a dense bf16 GEMV's read rate beside it.
+parity: the dominant projection against the float64 oracle (max_rel and max_rel_strict).
+decode_tok_s: the 36-layer step's tokens per second at ctx 256 / 1024 / 2048 (config 4).
+cpu_baseline: the CPU oracle's dequantize-then-matmul of the same step (numpy fp32), on this host's cores, with
+matmul-only times and configs 2 / 3 / a config-4 layer beside it.
 Extra fields: the per-projection kernel times, the int8 audio head (config 2), the int4 prefill (config 3), the
 sampling tail, and the 36-layer decode step (config 4) with and without sampling inside the graph.
 """
@@ -93,41 +98,112 @@ def load_traffic():
         return None
 
 
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _timed(fn, budget_s):
+    """repetitions of fn() in about budget_s seconds (one warm call first): (reps, seconds)"""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        if time.perf_counter() - t0 >= budget_s:
+            return n, time.perf_counter() - t0
+
+
 def cpu_baseline(budget_s):
-    """numpy oracle: dequantize-then-matmul of one config-1 step, repeated for about budget_s seconds."""
+    """The CPU oracle on this host, bounded to about budget_s seconds in all:
+    - config 1 (the bench's workload, the value): one decoder layer's four projections, numpy fp32
+      dequantize-then-matmul (the reference's own CPU check, kernels/int4_gemv.py:27-30), and the same products
+      with the weights dequantized once beforehand (matmul only);
+    - config 2: the int8 audio head 16385 x 2048, both ways;
+    - config 3: the prefill product at M = 34 over the three layer shapes, both ways;
+    - a config-4 layer: the oracle's whole decode step for one full-width layer at ctx 256 (embedding, LayerNorm,
+      w_in, RoPE, attention, o, down, residual, a 16-row head), both ways.
+    Dequantization is single-threaded numpy; the matmuls use the BLAS threads (`cores`)."""
     import numpy as np
-    import torch
     import synth
+    import decode
+    from oracle import glue as OG
     from oracle import int4 as O
     try:
         from threadpoolctl import threadpool_info
         cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
     except Exception:
         cores = 1
+    share = budget_s / 8.0
     g = synth.generator(1)
     mats = {k: tuple(t.numpy() for t in synth.int4_weights(N, K, g)) for k, (N, K) in SHAPES.items()}
+    deq = {k: O.dequantize(*w) for k, w in mats.items()}
     x = synth.activations(H, g).numpy()
     ob = synth.activations(H, g).numpy()
+    f32 = lambda v: np.asarray(v, np.float32)  # noqa: E731
 
-    def step():
-        O.gemv_int4(x, *mats["qkv"])
-        O.gemv_int4(ob, *mats["o"])
-        gu = O.gemv_int4(x, *mats["gate_up"])
+    def step(dequant):
+        mv = (lambda k, v: O.gemv_int4(v, *mats[k])) if dequant else (lambda k, v: deq[k] @ f32(v))
+        mv("qkv", x)
+        mv("o", ob)
+        gu = mv("gate_up", x)
         gate, up = gu[:INTER], gu[INTER:]
         act = (gate / (1 + np.exp(-gate)) * up).astype(np.float16)
-        O.gemv_int4(act, *mats["down"])
+        mv("down", act)
 
-    step()  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        step()
-        n += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = time.perf_counter() - t0
     nbytes = sum(int4_bytes(N, K) for N, K in SHAPES.values())
-    return {"value": round(nbytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": int(cores), "kind": "port",
-            "sample": f"{n} config-1 steps (one weight copy), numpy fp32 dequantize-then-matmul, {dt:.1f} s"}
+    n1, t1 = _timed(lambda: step(True), 2 * share)
+    n1m, t1m = _timed(lambda: step(False), share)
+    res = {"value": round(nbytes * n1 / t1 / 1e9, 3), "unit": "GB/s", "cores": int(cores), "kind": "port",
+           "sample": f"{n1} config-1 steps (one weight copy), numpy fp32 dequantize-then-matmul, {t1:.1f} s",
+           "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
+           "config1_us_per_step": {"dequant_matmul": round(t1 / n1 * 1e6, 1), "matmul_only": round(t1m / n1m * 1e6, 1)},
+           "config1_matmul_only_GB_s": round(nbytes * n1m / t1m / 1e9, 3)}
+    del deq
+    # config 2: int8 head
+    q8, s8 = synth.int8_weights(16385, H, g)
+    q8, s8 = q8.numpy(), s8.numpy()
+    w8 = O.int8_codes(q8, "s8").astype(np.float32) * s8.astype(np.float32)[:, None]
+    n2, t2 = _timed(lambda: O.gemv_int8_rows(x, q8, s8, "s8"), share / 2)
+    n2m, t2m = _timed(lambda: w8 @ f32(x), share / 2)
+    res["config2_us"] = {"dequant_matmul": round(t2 / n2 * 1e6, 1), "matmul_only": round(t2m / n2m * 1e6, 1)}
+    del w8
+    # config 3: prefill product at M = 34 over the three shapes
+    X = np.stack([synth.activations(H, g).numpy() for _ in range(34)])
+    Xd = np.stack([synth.activations(INTER, g).numpy() for _ in range(34)])
+    shapes3 = {"qkv": X, "gate_up": X, "down": Xd}
+    deq3 = {k: O.dequantize(*mats[k]) for k in shapes3}
+    n3, t3 = _timed(lambda: [O.mm_int4(v, *mats[k]) for k, v in shapes3.items()], share)
+    n3m, t3m = _timed(lambda: [f32(v) @ deq3[k].T for k, v in shapes3.items()], share / 2)
+    res["config3_M34_us"] = {"dequant_matmul": round(t3 / n3 * 1e6, 1), "matmul_only": round(t3m / n3m * 1e6, 1),
+                             "shapes": ["3072x2048", "22016x2048", "2048x11008"]}
+    del deq3
+    # a config-4 layer: the oracle's decode step of a one-layer full-width model at ctx 256
+    cfg = decode.Config(L=1, vocab=64, n_audio=16)
+    w = decode.random_weights(cfg, 5, device="cpu", gen_device="cpu")
+    nf = lambda t: t.numpy()  # noqa: E731
+    cos, sin = OG.rope_tables(cfg.S, cfg.HD, cfg.rope_theta)
+
+    def model(cache):
+        return OG.DecodeModel(cache_weights=cache, L=1, H=cfg.H, NH=cfg.NH, NKV=cfg.NKV, HD=cfg.HD, inter=cfg.inter,
+                              eps=cfg.eps, w_in=[tuple(map(nf, w["w_in"][0]))], w_o=[tuple(map(nf, w["w_o"][0]))],
+                              w_down=[tuple(map(nf, w["w_down"][0]))], ln=[nf(w["ln"][0])], norm=nf(w["norm"]),
+                              emb=(nf(w["emb"][0]), nf(w["emb"][1])), head=(nf(w["head"][0]), nf(w["head"][1])),
+                              rope=(OG.round_to(cos, np.float16), OG.round_to(sin, np.float16)), sliding=cfg.sliding)
+    rng = np.random.default_rng(6)
+    kc = rng.standard_normal((1, cfg.NKV, cfg.S, cfg.HD)).astype(np.float16)
+    vc = rng.standard_normal((1, cfg.NKV, cfg.S, cfg.HD)).astype(np.float16)
+    md, mdc = model(False), model(True)
+    n4, t4 = _timed(lambda: OG.decode_step(md, 7, 255, kc, vc), share)
+    n4m, t4m = _timed(lambda: OG.decode_step(mdc, 7, 255, kc, vc), share / 2)
+    res["config4_layer_ctx256_us"] = {"dequant_matmul": round(t4 / n4 * 1e6, 1),
+                                      "matmul_only": round(t4m / n4m * 1e6, 1)}
+    return res
 
 
 def run_decode(dev, steps):
@@ -374,12 +450,40 @@ def main():
     proj["o_down_pair"] = {"us": round(pair_us, 2), "GB_s": round(pair_bytes / pair_us / 1e3, 1)}
     log(f"[bench] projections: {proj}")
     achieved = WIN_BYTES / win_us / 1e3
+    # the read ceiling of that launch: rk_read_only over the same bytes (w_in's codes, scales and mins), the same 16
+    # rotated copies back to back in one graph, best over launch shapes (the reference's kernels/roofline.py
+    # method); and a dense bf16 GEMV (torch.mm, 4x the weight bytes) as the vendor library's practical read rate
+    import roofline as RF
+    ro_us, ro_shape = RF.ceiling_us([L["w_in"] for L in layers])
+    ro_bytes = sum(t.numel() * t.element_size() for t in layers[0]["w_in"])
+    log(f"[bench] read ceiling: {ro_us:.2f} us for {ro_bytes} B ({ro_bytes / ro_us / 1e3:.0f} GB/s), {ro_shape}")
+    # parity of the dominant projection on copy 0 against the float64 oracle (max_rel with the per-output
+    # conditioning floor, max_rel_strict with the fp16 floor alone)
+    from oracle import int4 as O
+    y_chk = cuda_gemv.gemv_int4_cuda(x, *layers[0]["w_in"], out=torch.empty(N_WIN, device=dev, dtype=torch.float32))
+    a_chk = (x.cpu().numpy(), *(t.cpu().numpy() for t in layers[0]["w_in"]))
+    parity = O.parity_report(y_chk.cpu().numpy(), O.gemv_int4_f64(*a_chk), O.cond_floor(O.gemv_int4_abs(*a_chk)))
+    parity = {"check": "gemv int4 w_in 25088x2048 (copy 0) vs float64 oracle",
+              **{k: (round(v, 8) if isinstance(v, float) else v) for k, v in parity.items()}}
+    log(f"[bench] parity: {parity}")
+    del layers, y_chk, a_chk
+    torch.cuda.empty_cache()
+    wb = [torch.randn(H, N_WIN, device=dev, generator=gen).bfloat16() for _ in range(4)]  # 4 x 103 MB: past the cache
+    xb, yb = x.bfloat16().view(1, H), torch.empty(1, N_WIN, device=dev, dtype=torch.bfloat16)
+    for w in wb:  # hipBLASLt picks its algorithm and workspace on a first call, which a capture does not allow
+        torch.mm(xb, w, out=yb)
+    g = graph_of([lambda w=w: torch.mm(xb, w, out=yb) for w in wb])
+    bf_us = time_graph_us(g, len(wb))
+    del g, wb
+    torch.cuda.empty_cache()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": load_traffic(),
                 "kernel": "gemv int4 g128 w_in [qkv | gate | up] N=25088 K=2048 + SiLU*up epilogue",
-                "us_per_launch": round(win_us, 2)}
-    del layers
-    torch.cuda.empty_cache()
+                "us_per_launch": round(win_us, 2),
+                "read_ceiling_us": round(ro_us, 2), "read_ceiling_GB_s": round(ro_bytes / ro_us / 1e3, 1),
+                "read_ceiling_shape": ro_shape, "frac_of_read_ceiling": round(ro_us / win_us, 4),
+                "dense_bf16_gemv_us": round(bf_us, 2),
+                "dense_bf16_gemv_GB_s": round(2 * N_WIN * H / bf_us / 1e3, 1)}
 
     # ---- config 2: int8 audio head (16385 x 2048, fp16 row scale, fp32 logits), 20 rotated copies
     heads = [synth.int8_weights(16385, H, gen, device=dev) for _ in range(20)]
@@ -443,7 +547,10 @@ def main():
                                "the reference engine's one w_in projection with SiLU*up fused, o and down in one launch: 2 launches "
                                "per step, 16 steps (16 weight copies) per hipGraph replay",
                    "bytes_per_step": step_bytes, "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2)},
+        "decode_tok_s": ({k: decode_res[k]["tok_s"] for k in ("ctx256", "ctx1024", "ctx2048")}
+                         if decode_res else None),
         "roofline": roofline,
+        "parity": parity,
         "cpu_baseline": cpu,
         "projections": proj,
         "int8_head": head,

@@ -350,6 +350,15 @@ int rk_sample_tail(const void* h, int h_dtype, const float* lnw, const float* ln
                    int64_t* tok, int64_t* out, float inv_temp, int64_t end_id, int min_new, int topk, int64_t* keys,
                    int64_t* scratch, int nc, float* z1, unsigned* counter, rk_stream_t stream);
 
+/* Read-only ceiling (a measurement kernel; replaces the reference's kernels/roofline.py:20-33 `read_only`, which
+ * loads an int4 matrix's codes, scales and mins and integer-sums them): reads the three buffers a (na bytes),
+ * b (nb), c (nc) with 16-byte nontemporal loads, grid-stride, `unroll` loads in flight per thread (1, 2, 4 or 8),
+ * and writes one uint32 per block to sink[blocks]: the wrapping sum of the block's 32-bit words, so the sink's
+ * total is the wrapping sum of every word of the three buffers. Sizes must be multiples of 16 and the pointers
+ * 16-byte aligned (RK_ERR_SHAPE / RK_ERR_ALIGN); 1 <= blocks <= 65536 (256 threads each). */
+int rk_read_only(const void* a, size_t na, const void* b, size_t nb, const void* c, size_t nc, int blocks, int unroll,
+                 uint32_t* sink, rk_stream_t stream);
+
 #pragma GCC visibility pop
 
 #ifdef __cplusplus

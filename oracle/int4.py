@@ -57,14 +57,18 @@ def gemv_int4(x, q, s, m) -> np.ndarray:
     return dequantize(q, s, m) @ np.asarray(x).astype(np.float32)
 
 
-def gemv_int4_f64(x, q, s, m) -> np.ndarray:
-    """Same product in float64 throughout (an error-free shadow for judging fp32 rounding)."""
+def dequantize_f64(q, s, m, group: int = G) -> np.ndarray:
+    """dequantize() in float64: code * scale + min is exact there (4-bit code times an fp16 value, plus an fp16)."""
     codes = unpack_int4(q).astype(np.float64)
     n, k = codes.shape
-    s64 = np.asarray(s, dtype=np.float16).astype(np.float64).reshape(n, k // G, 1)
-    m64 = np.asarray(m, dtype=np.float16).astype(np.float64).reshape(n, k // G, 1)
-    w = (codes.reshape(n, k // G, G) * s64 + m64).reshape(n, k)
-    return w @ np.asarray(x).astype(np.float64)
+    s64 = np.asarray(s, dtype=np.float16).astype(np.float64).reshape(n, k // group, 1)
+    m64 = np.asarray(m, dtype=np.float16).astype(np.float64).reshape(n, k // group, 1)
+    return (codes.reshape(n, k // group, group) * s64 + m64).reshape(n, k)
+
+
+def gemv_int4_f64(x, q, s, m) -> np.ndarray:
+    """Same product in float64 throughout (an error-free shadow for judging fp32 rounding)."""
+    return dequantize_f64(q, s, m) @ np.asarray(x).astype(np.float64)
 
 
 def int8_codes(q, q_kind: str) -> np.ndarray:
@@ -83,6 +87,12 @@ def gemv_int8_rows(x, q, s, q_kind: str = "u8") -> np.ndarray:
     return w @ np.asarray(x).astype(np.float32)
 
 
+def gemv_int8_rows_f64(x, q, s, q_kind: str = "u8") -> np.ndarray:
+    """gemv_int8_rows in float64 throughout (the per-row scale applied to the exact code, as the fp32 form does)."""
+    w = int8_codes(q, q_kind).astype(np.float64) * np.asarray(s).astype(np.float64)[:, None]
+    return w @ np.asarray(x).astype(np.float64)
+
+
 def quantize_int8_rows(w, pad_to: int = 16):
     """[N, K] -> (uint8 [N', K] = int8 + 128, fp32 scale [N']), rows zero-padded to a multiple of pad_to;
     scale = max(max|w| / 127, 1e-8), code = clip(round(w / scale), -127, 127) (kernels/cuda_gemv.py:234-242)."""
@@ -99,6 +109,11 @@ def quantize_int8_rows(w, pad_to: int = 16):
 def mm_int4(X, q, s, m) -> np.ndarray:
     """Prefill product Y[T, N] = X[T, K] @ dequantize(W)^T in fp32 (kernels/mm_int4.py:96-97)."""
     return np.asarray(X).astype(np.float32) @ dequantize(q, s, m).T
+
+
+def mm_int4_f64(X, q, s, m) -> np.ndarray:
+    """The prefill product in float64 throughout."""
+    return np.asarray(X).astype(np.float64) @ dequantize_f64(q, s, m).T
 
 
 # ---------------------------------------------------------------- error metrics used by every parity test

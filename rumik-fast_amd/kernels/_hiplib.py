@@ -28,6 +28,7 @@ _SIGS = {
     "rk_gemv_int8_rows_ex": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_mm_int4_g128": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_mm_int4_plan": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
+    "rk_read_only": ([_p, ctypes.c_size_t, _p, ctypes.c_size_t, _p, ctypes.c_size_t, _i, _i, _p, _p], _i),
     "rk_mm_int4_workspace_bytes": ([_i, _i, _i], ctypes.c_size_t),
     "rk_mm_int4_g128_ws": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, ctypes.c_size_t, _p], _i),
     "rk_mm_int4_g128_noalloc": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
@@ -74,7 +75,8 @@ def lib():
 
 MM_REGS, MM_TILE128, MM_TILE64 = 0, 1, 2
 MM_SCRATCH_BYTES = 8 << 20  # RK_MM_SCRATCH_BYTES: the fixed split-K scratch of rk_mm_int4_g128_noalloc
-ERR_SCRATCH = -7
+# status codes (RK_OK and RK_ERR_* of the header)
+OK, ERR_SHAPE, ERR_BLOCK, ERR_DTYPE, ERR_NULL, ERR_ALIGN, ERR_LAUNCH, ERR_SCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
 
 
 def mm_plan(M: int, N: int, K: int, use_workspace: bool = True):

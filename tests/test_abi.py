@@ -167,3 +167,9 @@ def test_noalloc_rejects_shapes_beyond_its_scratch():
     assert st == HL.ERR_SCRATCH
     assert "scratch" in HL.lib().rk_status_string(st).decode()
     assert HL.lib().rk_mm_int4_g128_noalloc(p, HL.F16, K, p, p, p, p, HL.F16, N, M, N, 100, None) == -1  # shape
+
+
+def test_status_constants_match_the_header():
+    text = HEADER.read_text()
+    codes = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define RK_(OK|ERR_\w+) \(?(-?\d+)\)?", text)}
+    assert codes and all(getattr(HL, k) == v for k, v in codes.items()), codes

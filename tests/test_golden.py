@@ -30,6 +30,8 @@ def test_oracle_gemv_int4_fixture():
 
 def test_oracle_gemv_int8_fixture():
     d = load("gemv_int8_80x256.npz")
+    np.testing.assert_allclose(O.gemv_int8_rows_f64(d["x"], d["codes"], d["s"], "s8"), d["y"], rtol=1e-12,
+                               atol=1e-12)
     y = O.gemv_int8_rows(d["x"], d["codes"], d["s"], "s8")
     _close_to_f64(y, d["y"], O.gemv_int8_abs(d["x"], d["codes"], d["s"], "s8"))
     # the reference's uint8 + 128 layout gives the same result
@@ -39,6 +41,7 @@ def test_oracle_gemv_int8_fixture():
 
 def test_oracle_mm_int4_fixture():
     d = load("mm_int4_5x64x256.npz")
+    np.testing.assert_allclose(O.mm_int4_f64(d["X"], d["q"], d["s"], d["m"]), d["Y"], rtol=1e-12, atol=1e-12)
     _close_to_f64(O.mm_int4(d["X"], d["q"], d["s"], d["m"]), d["Y"], O.mm_int4_abs(d["X"], d["q"], d["s"], d["m"]))
 
 

@@ -117,6 +117,43 @@ RK_DEV bool pair_ok(uint64_t q, uint32_t tag) {
 // the two fp16 values of a tagged pair as one packed fp16x2 dword
 RK_DEV uint32_t pair_val(uint64_t q) { return (uint32_t)(q & 0xFFFFu) | ((uint32_t)(q >> 16) & 0xFFFF0000u); }
 
+// ---------------------------------------------------------------------------------------------- phase trace
+// A build option (RK_DECODE_TRACE; off in the product library, where every RK_TRACE is empty): wall-clock stamps per
+// (layer, event), kept in LDS during the step and copied out at its end to the buffer rk_decode_trace_set names
+// ([block][64 layers][kTrEvents] uint64, 100 MHz ticks). rumik-fast_amd/decode_trace.py builds and reads it.
+enum TraceEvent {
+    kTrXPolled,        // row wave 0: its part of x polled
+    kTrLnDone,         // row wave 0: LayerNorm statistics combined, h formed
+    kTrHStaged,        // row wave 0: its h groups staged
+    kTrTile0Done,      // row wave 0: its part of tile 0 computed
+    kTrQkvPublished,   // the last row wave: q / k / v tile published
+    kTrQPolled,        // attention wave 0: q (and k / v at pos) polled
+    kTrAttnDone,       // attention wave 0: its slots' attention computed
+    kTrMerged,         // attention wave 0: its head's split partial published
+    kTrCombDone,       // attention wave 0: its combine part formed (poll included)
+    kTrCombMerged,     // attention wave 0: the head's attention output merged
+    kTrOPublished,     // attention wave 0: its o partials published
+    kTrPass2Start,     // tile wave W4: released for pass 2
+    kTrActReady,       // the last tile wave: act formed
+    kTrDownPublished,  // down wave W12: its down partials published
+    kTrGatherPolled,   // row wave 0: its down / o partials polled
+    kTrXPublished,     // the gather's last arriver: x rows published
+    kTrXPolled4,       // row wave 4 (W12): its part of x polled
+    kTrGatherPolled4,  // row wave 4 (W12): its down partials polled
+    kTrEvents
+};
+#ifdef RK_DECODE_TRACE
+__device__ unsigned long long* g_trace;
+#define RK_TRACE(cond, ev)                                                             \
+    do {                                                                               \
+        if ((cond) && lane_id() == 0) S.trace[l][(ev)] = wall_clock64();               \
+    } while (0)
+#else
+#define RK_TRACE(cond, ev) \
+    do {                   \
+    } while (0)
+#endif
+
 // ---------------------------------------------------------------------------------------------- LDS layout
 struct Lds {
     uint4 hfrag[kH / 8];                      // MFMA A fragments of h
@@ -140,6 +177,9 @@ struct Lds {
     float xrow[8];                            // this block's 8 rows of the residual stream
     int16_t work[kWork];
     // intra-block synchronization: flags hold the layer + 1 they announce, counters count arrivals
+#ifdef RK_DECODE_TRACE
+    unsigned long long trace[64][kTrEvents];
+#endif
     uint32_t p1_done, act_ready;
     uint32_t cnt_ln, cnt_h, cnt_g, cnt_head, cnt_t0, cnt_p1, cnt_p2, cnt_att, cnt_comb;
     uint32_t abort;
@@ -394,10 +434,14 @@ RK_DEV void x_phase(const Params& p, int l, uint32_t step, int64_t pos, int64_t 
         x_poll(p, S, tag_of(step, l - 1), rho, xv);
         if (l == 1 && rho == 0 && blockIdx.x == 0 && lane_id() == 0) p.pos[0] = pos + 1;  // every block read pos
     }
+    RK_TRACE(rho == 0, kTrXPolled);
+    RK_TRACE(rho == 4, kTrXPolled4);
     keep_xrow(xv, rho, S);
     layernorm_rows(p, S, l, rho, w, xv);
+    RK_TRACE(rho == 0, kTrLnDone);
     stage_h_frag(xv, rho, S);
     arrive(&S.cnt_h);
+    RK_TRACE(rho == 0, kTrHStaged);
 }
 
 // Row wave after the last layer: the final LayerNorm, h as natural pairs for the int8 head (read by the tile
@@ -1035,6 +1079,8 @@ RK_DEV void gather_phase(const Params& p, int l, uint32_t tag, int rho, Lds& S) 
                       return 128 * rho + 64 * k + lane < 4 * nb ? run + 64 * k : nullptr;
                   },
                   v);
+    RK_TRACE(rho == 0, kTrGatherPolled);
+    RK_TRACE(rho == 4, kTrGatherPolled4);
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -1076,6 +1122,7 @@ RK_DEV void gather_phase(const Params& p, int l, uint32_t tag, int rho, Lds& S) 
         st_coh64(reinterpret_cast<uint64_t*>(p.tx) + (lane >> 2) * kRepQwords + 4 * blockIdx.x + j,
                  tpair(S.xrow[2 * j], S.xrow[2 * j + 1], tag));
     }
+    RK_TRACE(true, kTrXPublished);
 }
 
 // ---------------------------------------------------------------------------------------------- head
@@ -1147,8 +1194,10 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
 RK_DEV void row_pass1(const Params& p, int l, int64_t pos, uint32_t tag, const Work& wk, int rho, Lds& S) {
     flag_wait(p, S, &S.cnt_t0, (uint32_t)kMW * (l + 1));
     tile0_part(wk, rho, S);
+    RK_TRACE(rho == 0, kTrTile0Done);
     if (arrive_last(&S.cnt_p1, (uint32_t)kRW * (l + 1))) {
         if (wk.nq) qkv_epilogue(p, l, pos, tag, S);
+        RK_TRACE(wk.nq, kTrQkvPublished);
         flag_set(&S.p1_done, (uint32_t)l + 1);
     }
     // the row waves' weight loads follow the epilogue's stores, not the other way round (a store issued into a
@@ -1174,17 +1223,23 @@ RK_DEV void attention_main(const Params& p, uint32_t step, int64_t pos, int64_t 
         if (split_of(p, pos).att) {
             QRegs qr;
             q_poll(p, S, REP, pos, tag, qr);
+            RK_TRACE(a == 0, kTrQPolled);
             attention<REP>(p, pos, kv, qr, S);
+            RK_TRACE(a == 0, kTrAttnDone);
             arrive(&S.cnt_att);
             flag_wait(p, S, &S.cnt_att, (uint32_t)kAW * (l + 1));
 #pragma unroll
             for (int r = a; r < REP; r += kAW) attention_merge<REP>(p, pos, tag, S, r);
+            RK_TRACE(a == 0, kTrMerged);
         }
         comb_part(p, S, o_head(), pos, tag);
+        RK_TRACE(a == 0, kTrCombDone);
         arrive(&S.cnt_comb);
         flag_wait(p, S, &S.cnt_comb, (uint32_t)kAW * (l + 1));
         const float asum = comb_merge(S);
+        RK_TRACE(a == 0, kTrCombMerged);
         o_part(p, tag, orr, S, asum);
+        RK_TRACE(a == 0, kTrOPublished);
         gather_phase(p, l, tag, rho, S);
     }
     x_final(p, step, pos, rho, S);
@@ -1202,10 +1257,12 @@ RK_DEV void tile_main(const Params& p, uint32_t step, int64_t pos, const Work& w
     arrive(&S.cnt_t0);
     for (int l = 0; l < p.L; ++l) {
         flag_wait(p, S, &S.p1_done, (uint32_t)l + 1);  // h staged, tile 0 done (its partials are in)
+        RK_TRACE(wave_id() == kM0, kTrPass2Start);
         tile_compute<1, kMaxTiles>(tr, wk, S);
         if (arrive_last(&S.cnt_p2, (uint32_t)kMW * (l + 1))) {
             act_epilogue(p, wk, S);
             flag_set(&S.act_ready, (uint32_t)l + 1);
+            RK_TRACE(true, kTrActReady);
         }
         if (l + 1 < p.L) {
             tile_issue(p, l + 1, S, wk, tr);
@@ -1234,6 +1291,7 @@ RK_DEV void down_main(const Params& p, uint32_t step, int64_t pos, int64_t tok, 
         down_issue(p, l, wk, dr);
         flag_wait(p, S, &S.act_ready, (uint32_t)l + 1);
         down_compute(p, tag, wk, dr, S);
+        RK_TRACE(rho == 4, kTrDownPublished);
         gather_phase(p, l, tag, rho, S);
     }
     x_final(p, step, pos, rho, S);
@@ -1256,6 +1314,9 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         S.rcos[tid] = h16(p.cos_t[(size_t)pos * kHD + 2 * tid]);
         S.rsin[tid] = h16(p.sin_t[(size_t)pos * kHD + 2 * tid]);
     }
+#ifdef RK_DECODE_TRACE
+    for (int i = tid; i < 64 * kTrEvents; i += kThreads) (&S.trace[0][0])[i] = 0ull;
+#endif
     if (tid == 0) {
         S.p1_done = S.act_ready = 0u;
         S.cnt_ln = S.cnt_h = S.cnt_g = S.cnt_head = S.cnt_t0 = S.cnt_p1 = S.cnt_p2 = S.cnt_att = S.cnt_comb = 0u;
@@ -1270,6 +1331,12 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     } else {
         down_main(p, step, pos, tok, work_of(p, S), S);
     }
+#ifdef RK_DECODE_TRACE
+    __syncthreads();
+    if (g_trace)
+        for (int i = tid; i < 64 * kTrEvents; i += kThreads)
+            g_trace[(size_t)blockIdx.x * 64 * kTrEvents + i] = (&S.trace[0][0])[i];
+#endif
     if (tid == 0) p.ctr[blockIdx.x] = step + 1;
 }
 
@@ -1321,6 +1388,14 @@ extern "C" int rk_decode_step_persistent(const rk_decode_params* params, int nbl
 }
 
 extern "C" int rk_decode_params_size(void) { return (int)sizeof(Params); }
+
+#ifdef RK_DECODE_TRACE
+// trace builds only: the stamp buffer ([nblocks][64][kTrEvents] uint64, or NULL) and the event count
+extern "C" __attribute__((visibility("default"))) int rk_decode_trace_set(unsigned long long* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &buf, sizeof(buf)) == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+extern "C" __attribute__((visibility("default"))) int rk_decode_trace_events(void) { return kTrEvents; }
+#endif
 
 extern "C" int rk_decode_get_limits(rk_decode_limits* out) {
     if (!out) return RK_ERR_NULL;

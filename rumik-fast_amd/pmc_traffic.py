@@ -17,6 +17,11 @@ Two steps:
     timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE --kernel-trace -d OUT/write -o write --output-format csv \
         -- python3 rumik-fast_amd/pmc_traffic.py run
     python3 rumik-fast_amd/pmc_traffic.py summarize OUT/fetch OUT/write
+
+The same two steps for the one-launch 36-layer decode step (config 4): `run-decode` launches the copy kernel, then
+DECODE_STEPS eager steps at each of ctx 256, 1024 and 2048 (one dispatch each); `summarize-decode` gives the HBM bytes
+per token against the algorithmic bytes (every weight once plus the K/V slots read) and writes
+profiles/decode_step_traffic.json.
 """
 import csv
 import glob
@@ -108,10 +113,83 @@ def summarize(fetch_dir, write_dir):
           f"{r['traffic_bytes'] / GEMV_BYTES:.3f}) |")
 
 
+DECODE_STEPS = 4
+DECODE_CTX = (256, 1024, 2048)
+
+
+def run_decode():
+    sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "kernels"))
+    sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "engine"))
+    import torch
+    import decode
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    cfg = decode.Config()
+    eng = decode.PersistentDecode(cfg, decode.random_weights(cfg, 4, device=dev), device=dev)
+    eng.fill_cache(cfg.S, seed=5)
+    eng.set_state(7, 0)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    for ctx in DECODE_CTX:
+        for _ in range(DECODE_STEPS):
+            eng.pos.fill_(ctx - 1)
+            eng.step()
+    torch.cuda.synchronize()
+    if eng.status_word() != 0:
+        raise SystemExit(f"decode step status {eng.status_word()}")
+    print("pmc_traffic: decode run done", flush=True)
+
+
+def _per_dispatch_list(rows, counter, pred):
+    """[(dispatch id, counter value summed over the dispatch's rows)] in dispatch order"""
+    per = {}
+    for r in rows:
+        if r.get("Counter_Name") != counter or not pred(r.get("Kernel_Name", "")):
+            continue
+        key = int(r.get("Dispatch_Id") or r.get("Correlation_Id"))
+        per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    return [per[k] for k in sorted(per)]
+
+
+def summarize_decode(fetch_dir, write_dir):
+    sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "engine"))
+    import decode
+    cfg = decode.Config()
+    is_copy = lambda n: "neg" in n.lower()  # noqa: E731
+    is_dec = lambda n: "decode_step_kernel" in n  # noqa: E731
+    fr, wr = _rows(fetch_dir), _rows(write_dir)
+    f_copy, _ = _per_dispatch(fr, "FETCH_SIZE", is_copy)
+    w_copy, _ = _per_dispatch(wr, "WRITE_SIZE", is_copy)
+    kf, kw = f_copy * 1024 / COPY_BYTES, w_copy * 1024 / COPY_BYTES
+    fd, wd = _per_dispatch_list(fr, "FETCH_SIZE", is_dec), _per_dispatch_list(wr, "WRITE_SIZE", is_dec)
+    n = DECODE_STEPS
+    if len(fd) != n * len(DECODE_CTX) or len(wd) != n * len(DECODE_CTX):
+        raise SystemExit(f"expected {n * len(DECODE_CTX)} decode dispatches, got {len(fd)} / {len(wd)}")
+    rec = {"fetch_scale": round(kf, 4), "write_scale": round(kw, 4), "steps_per_ctx": n}
+    print("| ctx | FETCH_SIZE / step | WRITE_SIZE / step | HBM bytes / token (scaled) | algorithmic bytes / token "
+          "| traffic / algorithmic |\n|---|---|---|---|---|---|")
+    for i, ctx in enumerate(DECODE_CTX):
+        f = sum(fd[i * n:(i + 1) * n]) / n
+        w = sum(wd[i * n:(i + 1) * n]) / n
+        fb, wb = f * 1024 / kf, w * 1024 / kw
+        alg = cfg.weight_bytes() + cfg.kv_bytes(ctx)
+        rec[f"ctx{ctx}"] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "traffic_bytes": round(fb + wb),
+                            "algorithmic_bytes": alg, "ratio": round((fb + wb) / alg, 4)}
+        print(f"| {ctx} | {f:,.0f} KiB | {w:,.0f} KiB | {fb + wb:,.0f} B | {alg:,} B | {(fb + wb) / alg:.3f} |")
+    (ROOT / "profiles" / "decode_step_traffic.json").write_text(json.dumps(rec, indent=1) + "\n")
+
+
 if __name__ == "__main__":
     if len(sys.argv) >= 2 and sys.argv[1] == "run":
         run()
+    elif len(sys.argv) >= 2 and sys.argv[1] == "run-decode":
+        run_decode()
     elif len(sys.argv) == 4 and sys.argv[1] == "summarize":
         summarize(sys.argv[2], sys.argv[3])
+    elif len(sys.argv) == 4 and sys.argv[1] == "summarize-decode":
+        summarize_decode(sys.argv[2], sys.argv[3])
     else:
         raise SystemExit(__doc__)

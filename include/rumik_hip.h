@@ -10,6 +10,13 @@
  *                 w[n,k] = code[n,k] * scale[n,k/128] + min[n,k/128]
  *   int8 weights  q int8 [N, K] (RK_Q_S8) or uint8 = int8 + 128 (RK_Q_U8); one scale per row (fp16 or fp32)
  *   activations   fp16 / bf16 vectors; outputs fp16 / bf16 / fp32
+ *
+ * bf16 activations into the GEMVs and the prefill product (rk_gemv_int4_g128*, rk_gemv_int8_rows*,
+ * rk_mm_int4_g128*) are converted to fp16 for the fp16 dot products / matrix cores. The conversion is exact for
+ * magnitudes in fp16's normal range [2^-14, 65504] (bf16's 8-bit significand fits fp16's 11 bits); larger
+ * magnitudes become +-inf and smaller ones lose low bits as fp16 subnormals. The activations these kernels take
+ * (LayerNorm outputs, SiLU(gate)*up, attention outputs) are far inside that range. The glue kernels keep bf16 values
+ * in fp32 (rk_attn_split's scores included), so they have no such limit.
  */
 #ifndef RUMIK_HIP_H
 #define RUMIK_HIP_H

@@ -204,7 +204,7 @@ int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_str
  * The whole decode step in one persistent launch (no reference counterpart as a single kernel: it replaces the
  * ~260 launches of RumikFused._step, engine/rumik_fused.py:97-121, plus the audio head of _logits, :84-89).
  * Hidden size 2048 and head dim 128 are fixed; NH * 128 == 2048; NH / NKV in {1, 2, 4, 8}; inter % 128 == 0 and
- * inter <= 11008. One block per CU (nblocks = 256 on MI355X, co-residency is checked); block b owns rows
+ * inter <= 11008; 1 <= n_audio <= 512 * nblocks (RK_ERR_SHAPE otherwise). One block per CU (nblocks = 256 on MI355X, co-residency is checked); block b owns rows
  * [8b, 8b + 8) of the residual stream, the w_in tiles and w_down column slices its `work` row lists, attention
  * split b % nsp of KV head b / nsp (b < NKV * nsp), and the combine of head b / 16 with its w_o slice (rows of
  * group b % 16).

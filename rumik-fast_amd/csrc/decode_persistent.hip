@@ -58,9 +58,9 @@ constexpr int kMaxTiles = 7;               // w_in tiles per block
 constexpr int kGPW = 2;                    // column groups per MLP wave (8 x 2 = 16)
 constexpr int kFirstPass = 1;              // q / k / v tiles per block (published before the gate / up pass)
 constexpr int kMaxSlices = 3;              // w_down 16-column slices per block
+constexpr int kCombPer = 16;               // splits per attention wave in the combine (4 x 16 = 64)
 constexpr int kRP = kH / 2 / kDLanes;      // down row pairs per down lane (4)
 constexpr int kSlotsPerWave = 8;           // cached slots per attention wave (4 x 8 = 32 per split)
-constexpr int kCombPer = 16;               // splits per attention wave in the combine (4 x 16 = 64)
 constexpr int kOItems = 512;               // o items per (head, row group); 2 per attention lane
 constexpr int kHeadRows = 7;               // head rows per MLP wave loaded ahead (the rest load when used)
 constexpr int kWork = 16;                  // int16 entries per block in the work table
@@ -76,6 +76,7 @@ constexpr int kMaxSplits = 64;
 static_assert(kRP * kDLanes * 2 == kH, "down rows split evenly over the down lanes");
 static_assert(kOItems == 2 * kALanes, "two o items per attention lane");
 static_assert(kMW * kGPW == kNG, "MLP waves cover the 16 column groups");
+static_assert(kAW * kCombPer >= kMaxSplits, "the combine's polls cover every split");
 
 typedef rk_decode_params Params;
 
@@ -765,26 +766,27 @@ struct QRegs {
     uint32_t knew, vnew;
 };
 
-RK_DEV bool q_poll(const Params& p, Lds& S, int rep, int64_t pos, uint32_t tag, QRegs& qr) {
+template <int REP>
+RK_DEV bool q_poll(const Params& p, Lds& S, int64_t pos, uint32_t tag, QRegs& qr) {
     const int lane = lane_id();
     const Split s = split_of(p, pos);
     const bool has_pos = s.start <= pos && pos < s.end;
     const uint32_t z = opaque_vgpr(0u);  // not hoistable: see x_poll
     const uint64_t* tq = reinterpret_cast<const uint64_t*>(p.tq) + z;
     const uint64_t* tkv = reinterpret_cast<const uint64_t*>(p.tkv) + z;
-    uint32_t v[kMaxRep + 2];
-    const bool ok = poll_pairs<kMaxRep + 2>(
+    uint32_t v[REP + 2];  // one poll batch: the REP heads' q, then k and v at pos
+    const bool ok = poll_pairs<REP + 2>(
         p, S, tag,
         [&](int k) -> const uint64_t* {
-            if (k < kMaxRep) return k < rep ? tq + (size_t)(s.g * rep + k) * (kHD / 2) + lane : nullptr;
+            if (k < REP) return tq + (size_t)(s.g * REP + k) * (kHD / 2) + lane;
             if (!has_pos) return nullptr;
-            return tkv + (size_t)((k - kMaxRep) * p.NKV + s.g) * (kHD / 2) + lane;
+            return tkv + (size_t)((k - REP) * p.NKV + s.g) * (kHD / 2) + lane;
         },
         v);
 #pragma unroll
-    for (int k = 0; k < kMaxRep; ++k) qr.q[k] = v[k];
-    qr.knew = v[kMaxRep];
-    qr.vnew = v[kMaxRep + 1];
+    for (int k = 0; k < REP; ++k) qr.q[k] = v[k];
+    qr.knew = v[REP];
+    qr.vnew = v[REP + 1];
     return ok;
 }
 
@@ -1029,6 +1031,7 @@ RK_DEV void o_part(const Params& p, uint32_t tag, const ORegs& o, const Lds& S, 
     const int h = o_head(), r = o_rgroup();
     const Int4Masks km = int4_masks();
     uint64_t* top = reinterpret_cast<uint64_t*>(p.top);
+    float vals[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int i = ls + k * kALanes, c = i & 3;
@@ -1045,11 +1048,19 @@ RK_DEV void o_part(const Params& p, uint32_t tag, const ORegs& o, const Lds& S, 
         float v = chunk_dot_int4(o.w[k], xp, km);
         v += dpp<0xB1>(v);  // the row's 4 chunks sit in lanes 4j .. 4j + 3
         v += dpp<0x4E>(v);
-        v = __builtin_fmaf(v, h16((uint16_t)o.sm[k]), h16((uint16_t)(o.sm[k] >> 16)) * asum);
-        const float nxt = dpp<0x104>(v);  // row_shl 4: the next row's total (lane + 4, same 16-lane row)
+        vals[k] = __builtin_fmaf(v, h16((uint16_t)o.sm[k]), h16((uint16_t)(o.sm[k] >> 16)) * asum);
+    }
+    // both items before either store: after a store, gfx9 waits for its acknowledgement before any later use of a
+    // load (one counter for both), which the second item's weights would otherwise pay (the empty asm keeps the
+    // compiler from sinking the second item's math below the first store)
+    asm volatile("" ::"v"(vals[0]), "v"(vals[1]));
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = ls + k * kALanes;
+        const float nxt = dpp<0x104>(vals[k]);  // row_shl 4: the next row's total (lane + 4, same 16-lane row)
         if ((lane & 7) == 0) {
             const int row = 128 * r + (i >> 2);  // even
-            st_coh64(top + ((size_t)(row >> 3) * p.NH + h) * 4 + ((row & 7) >> 1), tpair(v, nxt, tag));
+            st_coh64(top + ((size_t)(row >> 3) * p.NH + h) * 4 + ((row & 7) >> 1), tpair(vals[k], nxt, tag));
         }
     }
 }
@@ -1156,6 +1167,7 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
     const int lane = lane_id(), m = mlp_wave();
     int r0, r1;
     head_rows(p, r0, r1);
+    float res = 0.f;  // lane k: the logit of the wave's row k (at most 64 rows per wave: checked on the host)
     for (int k = 0; r0 + m + kMW * k < r1; ++k) {
         const int r = r0 + m + kMW * k;
         u4_t w[2];
@@ -1184,8 +1196,12 @@ RK_DEV void head_compute(const Params& p, const TileRegs& tr, const Lds& S) {
             acc += chunk_dot_int8<true>(w[j], xp);
         }
         acc = wave_sum(acc);
-        if (lane == 0) p.logits[r] = acc * h16(p.head_s[r]);
+        if (lane == k) res = acc * h16(p.head_s[r]);
     }
+    // one store per row, all after the loop: a store inside it would make each next row's use of its (long since
+    // landed) codes wait for that store's acknowledgement (gfx9 counts loads and stores together)
+    const int nrows = r1 > r0 + m ? (r1 - r0 - m + kMW - 1) / kMW : 0;
+    if (lane < nrows) p.logits[r0 + m + kMW * lane] = res;
 }
 
 // row wave, after its x phase: its part of tile 0 once the tile waves have staged the layer's codes; the last of
@@ -1222,7 +1238,7 @@ RK_DEV void attention_main(const Params& p, uint32_t step, int64_t pos, int64_t 
         o_issue(p, l, orr);
         if (split_of(p, pos).att) {
             QRegs qr;
-            q_poll(p, S, REP, pos, tag, qr);
+            q_poll<REP>(p, S, pos, tag, qr);
             RK_TRACE(a == 0, kTrQPolled);
             attention<REP>(p, pos, kv, qr, S);
             RK_TRACE(a == 0, kTrAttnDone);
@@ -1367,6 +1383,7 @@ extern "C" int rk_decode_step_persistent(const rk_decode_params* params, int nbl
     const int rep = p.NH / p.NKV;
     if (!(rep == 1 || rep == 2 || rep == 4 || rep == 8)) return RK_ERR_SHAPE;
     if (p.inter <= 0 || p.inter % 128 || p.inter > 11008) return RK_ERR_SHAPE;
+    if (p.n_audio <= 0 || p.n_audio > 64 * kMW * nblocks) return RK_ERR_SHAPE;  // head rows: <= 64 per tile wave
     if (nblocks <= 0 || nblocks * 8 != kH) return RK_ERR_BLOCK;  // block b owns rows [8b, 8b + 8)
     if (p.nsp <= 0 || p.nsp > kMaxSplits || p.NKV * p.nsp > nblocks || p.inter / 16 > kMaxSlices * nblocks ||
         (p.S + p.nsp - 1) / p.nsp > kAW * kSlotsPerWave)  // every cached slot of a split is in registers

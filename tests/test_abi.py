@@ -101,8 +101,12 @@ def test_decode_step_validates_before_launch():
     import decode
     p = decode.RkDecodeParams()
     assert HL.lib().rk_decode_step_persistent(None, 256, None) == -4
-    p.L, p.NH, p.NKV, p.inter, p.S, p.nsp = 2, 16, 4, 11008, 64, 64
+    p.L, p.NH, p.NKV, p.inter, p.S, p.nsp, p.n_audio = 2, 16, 4, 11008, 64, 64, 16385
     assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 256, None) == -4  # null buffers
+    for n in (0, 512 * 256 + 1):  # head rows: 1 .. 64 per tile wave
+        p.n_audio = n
+        assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 256, None) == -1
+    p.n_audio = 16385
     p.NH = 12  # 12 * 128 != 2048
     assert HL.lib().rk_decode_step_persistent(ctypes.byref(p), 256, None) == -1
     p.NH, p.inter = 16, 11000  # not a multiple of 128

@@ -124,20 +124,29 @@ int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const
                     const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, rk_stream_t stream);
 
 /* The kernel plan rk_mm_int4_g128 (use_workspace = 0) or rk_mm_int4_g128_ws (use_workspace = 1) runs for this
- * shape: *kernel = RK_MM_TILE128 (LDS-staged 128 x 128 tiles), RK_MM_TILE64 (LDS-staged 64 x 64 tiles) or
- * RK_MM_REGS (register-staged 64 x 64 tiles, for K too long to stage a block's scales in LDS); *splits = the
- * number of K splits (1 = none; > 1 only with a workspace). Host-only query, no GPU needed; RK_ERR_SHAPE for
- * sizes rk_mm_int4_g128 rejects. Part of the mm_int4 drop-in (reference kernels/mm_int4.py:59-73 picks its
- * Triton tile from BM / BN); the reference has no plan query. */
+ * shape: *kernel = RK_MM_TILE128 (LDS-staged 128 x 128 tiles), RK_MM_TILE64 (LDS-staged 64 x 64 tiles),
+ * RK_MM_REGS (register-staged 64 x 64 tiles, for K too long to stage a block's scales in LDS), or, with a
+ * workspace only, RK_MM_PREP128 / RK_MM_PREP64 / RK_MM_PREP48 (X prepared once into the workspace in matrix-core
+ * fragment order, then blocks of 128 / 64 / 48 rows x 128 columns fed by direct memory-to-LDS copies; chosen when
+ * the shape has enough column blocks to fill the chip, K is short enough for a block's scale and min rows to sit
+ * in LDS, and N * K / 128 is a multiple of 8); *splits = the number of K splits (1 = none; > 1 only with a
+ * workspace). Host-only query, no GPU needed; RK_ERR_SHAPE for sizes rk_mm_int4_g128 rejects. Part of the
+ * mm_int4 drop-in (reference kernels/mm_int4.py:59-73 picks its Triton tile from BM / BN); the reference has no
+ * plan query. */
 #define RK_MM_REGS 0
 #define RK_MM_TILE128 1
 #define RK_MM_TILE64 2
+#define RK_MM_PREP128 3
+#define RK_MM_PREP64 4
+#define RK_MM_PREP48 5
 int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits);
 
-/* Bytes of fp32 workspace rk_mm_int4_g128_ws uses for this shape (0: it needs none). Shapes whose output tiles
- * alone leave CUs idle (few rows and columns, long K) are split over K into fp32 partial sums that a second kernel
- * adds in a fixed order. Part of the same drop-in for mm_int4 (reference kernels/mm_int4.py:59-73), which
- * allocates its output per call; the Python wrapper allocates this workspace the same way. */
+/* Bytes of workspace rk_mm_int4_g128_ws uses for this shape (0: it needs none). Shapes whose output tiles alone
+ * leave CUs idle (few rows and columns, long K) are split over K into fp32 partial sums that a second kernel adds
+ * in a fixed order; shapes on the RK_MM_PREP* kernels hold X prepared in fragment order (ceil(M / 16) * 16 * K
+ * fp16) and its per-group row sums (K / 128 * ceil(M / 16) * 16 fp32). Part of the same drop-in for mm_int4
+ * (reference kernels/mm_int4.py:59-73), which allocates its output per call; the Python wrapper allocates this
+ * workspace the same way. */
 size_t rk_mm_int4_workspace_bytes(int M, int N, int K);
 
 /* rk_mm_int4_g128 with a caller-provided workspace of at least rk_mm_int4_workspace_bytes(M, N, K) bytes
@@ -151,7 +160,9 @@ int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uint8_t* q, co
  * fixed array of RK_MM_SCRATCH_BYTES in the library's device memory (one per GPU, held until the process ends,
  * its address looked up once per device on the first call). No counterpart in the reference: it is for callers
  * that cannot allocate (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Same plan, kernels and results as rk_mm_int4_g128_ws. Shapes whose split-K partials exceed the array
+ * Same plan, kernels and results as rk_mm_int4_g128_ws, except that it never takes the RK_MM_PREP* kernels (their
+ * prepared X would not fit the array): where rk_mm_int4_g128_ws takes one, this entry runs the tile plan of
+ * rk_mm_int4_g128 (results equal up to fp32 summation order). Shapes whose split-K partials exceed the array
  * (rk_mm_int4_workspace_bytes(M, N, K) > RK_MM_SCRATCH_BYTES; none with K <= 49152) return RK_ERR_SCRATCH before
  * any launch. Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on different streams
  * without ordering) race and give wrong results; calls ordered on one stream are safe. */

@@ -394,6 +394,254 @@ __global__ __launch_bounds__(512) void mm_int4_lds_kernel(const void* __restrict
         }
 }
 
+// ---------------------------------------------------------------------------------------------- prepared-X kernel
+// Two launches, for the workspace entry on shapes with enough column blocks to fill the chip:
+//   mm_xprep_kernel: X once into the workspace, in the MFMA A-fragment order of dequant8's code order (fp16), plus
+//     the fp32 sum of each row over each group;
+//   mm_int4_prep_kernel<MT>: blocks of 16 MT rows x 128 columns, eight waves, wave w owning column tile w (16
+//     columns) for all rows. Every K step (one group) is copied straight from memory into a three-slot LDS ring
+//     with global_load_lds_dwordx4 (16 bytes per lane, no staging waves, no register round trip): the block's X
+//     fragments, its 128 code rows, the rows' sums. The block's scale and min rows are copied once into LDS. A
+//     wave dequantises its own columns (no column is converted twice) and runs 4 MT MFMAs per step.
+// The copies are ordered by explicit vmcnt waits: each wave waits for its own copies of step g, then a barrier
+// makes every wave's copies of step g visible and certifies that every wave has left step g - 1, whose slot the
+// copies of step g + 2 then fill.
+
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at their maxima)
+#define RK_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// Xp[mt][g][t][lane] (16 bytes): afrag of X[16 mt + j][128 g + 32 s + 8 t .. + 7], lane = j + 16 s (rows past M are
+// zero); xs[g][m] = fp32 sum of X[m][128 g .. 128 g + 127]. One thread per 16-byte chunk (m, g, c = 4 s + t).
+template <bool BF16>
+__global__ __launch_bounds__(256) void mm_xprep_kernel(const void* __restrict__ X, int ldx, int M, int Mp, int K,
+                                                       uint4* __restrict__ Xp, float* __restrict__ xs) {
+    const int NG = K >> 7;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)Mp * NG * 16) return;  // whole 16-lane rows leave together (the total is a multiple of 16)
+    const int c = (int)(idx & 15);
+    const size_t rg = idx >> 4;
+    const int g = (int)(rg % NG), m = (int)(rg / NG);
+    u4_t d = {0u, 0u, 0u, 0u};
+    if (m < M)
+        d = *reinterpret_cast<const u4_t*>(reinterpret_cast<const uint16_t*>(X) + (size_t)m * ldx + 128 * g + 8 * c);
+    const int s = c >> 2, t = c & 3;
+    Xp[(((size_t)(m >> 4) * NG + g) * 4 + t) * 64 + (m & 15) + 16 * s] =
+        __builtin_bit_cast(uint4, afrag(d, BF16 ? RK_BF16 : RK_F16));
+    float f = 0.f;
+    if (BF16) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            f += __builtin_bit_cast(float, d[e] << 16) + __builtin_bit_cast(float, d[e] & 0xffff0000u);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const h2_t v = as_h2(d[e]);
+            f += (float)v.x + (float)v.y;
+        }
+    }
+    f += dpp<0xB1>(f);   // the row's 16 chunks sit in one 16-lane DPP row
+    f += dpp<0x4E>(f);
+    f += dpp<0x141>(f);
+    f += dpp<0x140>(f);
+    if (c == 0) xs[(size_t)g * Mp + m] = f;
+}
+
+template <int MT>
+struct PrepStage {
+    uint4 x[MT][4][64];  // [m tile][MFMA t][lane (row j, quarter s)]
+    uint4 w[8][64];      // [column tile][lane (column j, quarter s)]: bytes 16 s .. 16 s + 15 of the column's group
+};
+static_assert(sizeof(PrepStage<3>) == (3 * 4 + 8) * 64 * 16, "stage layout: x then w, no padding");
+constexpr int kPrepRing = 3;  // X / code slots: steps g, g + 1 (in flight), g + 2 (being copied)
+constexpr int kPrepXsRing = 4;  // row-sum slots live one step longer: step g - 1's are read in step g
+
+template <int MT>
+size_t mm_prep_lds_bytes(int ng) {
+    return kPrepRing * sizeof(PrepStage<MT>) + kPrepXsRing * 128 * 4 + (size_t)2 * 128 * ng * 2;
+}
+
+// One block: rows mb .. mb + 16 MT - 1, columns nb .. nb + 127. Requires (N * NG) % 8 == 0 (the scale / min arrays
+// end on a 16-byte boundary) and 16-byte aligned scale / min arrays; the host checks both.
+template <int MT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void mm_int4_prep_kernel(const uint4* __restrict__ Xp, const float* __restrict__ xsg, int Mp,
+                         const uint8_t* __restrict__ q, const uint16_t* __restrict__ sc,
+                         const uint16_t* __restrict__ mn, void* __restrict__ Y, int ydt, int ldy, int M, int N,
+                         int K) {
+    constexpr int BM = 16 * MT;
+    constexpr int XPW = (MT * 4 + 7) / 8;  // X tile copies per wave per step (surplus slots repeat the last tile)
+    using Stage = PrepStage<MT>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    Stage* stg = reinterpret_cast<Stage*>(smem);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // 1-D grid, XCD-grouped as in mm_int4_lds_kernel: the row blocks of one column block run on one L2
+    const int G = gridDim.x, L = blockIdx.x, GY = (Mp + BM - 1) / BM;
+    const int Lv = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
+    const int mb = (Lv % GY) * BM, nb = (Lv / GY) * 128;
+    const int NG = K >> 7;
+    const int mts = min(MT, (Mp - mb) >> 4);  // m tiles of this block present in Xp
+    float* xsr = reinterpret_cast<float*>(stg + kPrepRing);              // [kPrepXsRing][128]
+    uint16_t* tsc = reinterpret_cast<uint16_t*>(xsr + kPrepXsRing * 128);  // [128][NG]
+    uint16_t* tmn = tsc + 128 * NG;
+    const int jn = lane & 15, sq = lane >> 4;
+
+    // the block's scale and min rows ([n][g], contiguous), 16-byte copies clamped inside the arrays
+    {
+        const int nch = 16 * NG;                                        // 16-byte chunks per table
+        const int lastc = (int)(((size_t)N * NG * 2) / 16) - 1;
+        const size_t c0 = (size_t)nb * NG / 8;
+        for (int b0 = wave * 64; b0 < nch; b0 += 512) {
+            const int ci = min((int)(c0 + b0 + lane), lastc);
+            if (b0 + lane < nch) {  // lanes past the table copy nothing
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(sc) + ci,
+                                                 reinterpret_cast<uint4*>(tsc) + b0, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(mn) + ci,
+                                                 reinterpret_cast<uint4*>(tmn) + b0, 16, 0, 0);
+            }
+        }
+    }
+    // a step's copies per wave: X tiles i = wave + 8 k (m tile i / 4, t = i % 4), code tile `wave`, and 64 row sums
+    // (waves 0 and 1)
+    const uint8_t* wsrc = q + (size_t)min(nb + 16 * wave + jn, N - 1) * (size_t)(K >> 1) + 16 * sq;
+    // copy destinations are addressed from the LDS base, not through the MT-dependent stage type: a dependent LDS
+    // operand keeps the host pass from instantiating the kernel (its launch stub would be missing)
+    auto issue = [&](int g) {
+        uint4* slot = reinterpret_cast<uint4*>(smem + (size_t)(g % kPrepRing) * sizeof(Stage));  // Stage::x, Stage::w
+#pragma unroll
+        for (int k = 0; k < XPW; ++k) {
+            const int i = min(wave + 8 * k, MT * 4 - 1), mt = i >> 2, t = i & 3;
+            __builtin_amdgcn_global_load_lds(Xp + (((size_t)(mb / 16 + min(mt, mts - 1)) * NG + g) * 4 + t) * 64 + lane,
+                                             slot + (mt * 4 + t) * 64, 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds(wsrc + 64 * g, slot + MT * 4 * 64 + wave * 64, 16, 0, 0);
+        if (wave < 2)
+            __builtin_amdgcn_global_load_lds(xsg + (size_t)g * Mp + min(mb + 64 * wave + lane, Mp - 1),
+                                             xsr + (g % kPrepXsRing) * 128 + 64 * wave, 4, 0, 0);
+    };
+
+    f4_t acc[MT], c[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    const DqConsts kc = {opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u)};
+    const int col = 16 * wave + jn;
+#pragma unroll
+    for (int p = 0; p < kPrepRing - 1; ++p) issue(min(p, NG - 1));
+    // the epilogue's arguments come in before the loop: a scalar load still in flight would turn every LDS wait
+    // of the loop into lgkmcnt(0) (scalar loads complete out of order)
+    asm volatile("" ::"s"(Y), "s"(ydt), "s"(ldy), "s"(M), "s"(N));
+    for (int g = 0; g < NG; ++g) {
+        // newer than this wave's copies of step g: its copies of step g + 1 (XPW + 1, or XPW + 2 with row sums)
+        if (wave < 2) RK_VMCNT(XPW + 2); else RK_VMCNT(XPW + 1);
+        __builtin_amdgcn_s_barrier();
+        issue(min(g + kPrepRing - 1, NG - 1));  // into the slot of step g - 1 (clamped: the last steps repeat)
+        const Stage& st = stg[g % kPrepRing];
+        const u4_t wq = __builtin_bit_cast(u4_t, st.w[wave][lane]);
+        // X fragments of MFMA step t + 1 are read while step t's MFMAs run
+        h8_t Xa[MT], Xb[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) Xa[mt] = __builtin_bit_cast(h8_t, st.x[mt][0][lane]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            h8_t* Xc = (t & 1) ? Xb : Xa;
+            h8_t* Xn = (t & 1) ? Xa : Xb;
+            if (t < 3) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) Xn[mt] = __builtin_bit_cast(h8_t, st.x[mt][t + 1][lane]);
+            }
+            const h8_t Wf = dequant8(wq[t], kc);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                c[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xc[mt], Wf, t == 0 ? f4_t{0.f, 0.f, 0.f, 0.f} : c[mt],
+                                                             0, 0, 0);
+        }
+        // D[i][j]: row 4 (lane / 16) + e of m tile mt, column lane % 16 of the wave's tile; group affine in fp32
+        const float scl = f16_bits_to_f32(tsc[col * NG + g]), mnv = f16_bits_to_f32(tmn[col * NG + g]);
+        const float* xs = xsr + (g % kPrepXsRing) * 128;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const f4_t xv = *reinterpret_cast<const f4_t*>(&xs[mt * 16 + 4 * sq]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mt][e] = __builtin_fmaf(c[mt][e], scl, __builtin_fmaf(xv[e], mnv, acc[mt][e]));
+        }
+    }
+    RK_VMCNT(0);
+    __builtin_amdgcn_s_barrier();  // every wave has left the ring: it becomes the output transpose buffer
+
+    // the wave's BM x 16 tile through LDS ([BM][17] fp32), then 16-byte row pieces: lane -> row 32 i + lane / 2,
+    // columns 8 (lane % 2) .. + 7
+    float* tb = reinterpret_cast<float*>(smem) + wave * (BM * 17);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tb[(mt * 16 + 4 * sq + e) * 17 + jn] = acc[mt][e];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave reads back only its own tile
+    const int n0 = nb + 16 * wave;
+    const bool vec_ok = (((uintptr_t)Y | (size_t)ldy * (ydt == RK_F32 ? 4 : 2)) & (ydt == RK_F32 ? 15 : 7)) == 0;
+#pragma unroll
+    for (int i = 0; i < (BM + 31) / 32; ++i) {
+        const int r = 32 * i + (lane >> 1), cc = 8 * (lane & 1);
+        const int m = mb + r, n = n0 + cc;
+        if (r >= BM || m >= M || n >= N) continue;
+        const float* p = tb + r * 17 + cc;
+        const size_t o = (size_t)m * ldy + n;
+        if (n + 7 < N && vec_ok) {
+            if (ydt == RK_F32) {
+                *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(Y) + o) = f4_t{p[0], p[1], p[2], p[3]};
+                *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(Y) + o + 4) = f4_t{p[4], p[5], p[6], p[7]};
+            } else if (ydt == RK_F16) {
+                const h8_t h = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
+                                (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
+                *reinterpret_cast<h8_t*>(reinterpret_cast<uint16_t*>(Y) + o) = h;
+            } else {
+                u4_t b;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    b[e] = (uint32_t)f32_to_bf16_bits(p[2 * e]) | ((uint32_t)f32_to_bf16_bits(p[2 * e + 1]) << 16);
+                *reinterpret_cast<u4_t*>(reinterpret_cast<uint16_t*>(Y) + o) = b;
+            }
+        } else {
+            for (int e = 0; e < 8 && n + e < N; ++e) store_act(Y, ydt, o + e, p[e]);
+        }
+    }
+}
+
+// the three block heights the plan uses; explicit instantiation also emits their host launch stubs
+#define RK_PREP_INST(MT)                                                                                          \
+    template __global__ void mm_int4_prep_kernel<MT>(const uint4* __restrict__, const float* __restrict__, int,    \
+                                                     const uint8_t* __restrict__, const uint16_t* __restrict__,     \
+                                                     const uint16_t* __restrict__, void* __restrict__, int, int,    \
+                                                     int, int, int);
+RK_PREP_INST(3)
+RK_PREP_INST(4)
+RK_PREP_INST(8)
+#undef RK_PREP_INST
+
+// workspace of the prepared-X plan: Xp (Mp K fp16) then xs (NG Mp fp32)
+inline size_t mm_prep_ws_bytes(int M, int K) {
+    const size_t Mp = (size_t)(M + 15) / 16 * 16;
+    return Mp * (size_t)K * 2 + (size_t)(K / 128) * Mp * 4;
+}
+
+template <int MT>
+hipError_t launch_mm_prep(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s, const uint16_t* m,
+                          void* Y, int ydt, int ldy, int M, int N, int K, void* ws, hipStream_t st) {
+    constexpr int BM = 16 * MT;
+    const int NG = K / 128, Mp = (M + 15) / 16 * 16;
+    uint4* Xp = static_cast<uint4*>(ws);
+    float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (size_t)Mp * K * 2);
+    const size_t chunks = (size_t)Mp * NG * 16;
+    const dim3 pg((unsigned)((chunks + 255) / 256));
+    if (xdt == RK_BF16)
+        hipLaunchKernelGGL((mm_xprep_kernel<true>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
+    else
+        hipLaunchKernelGGL((mm_xprep_kernel<false>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
+    const dim3 grid(((N + 127) / 128) * ((Mp + BM - 1) / BM));
+    hipLaunchKernelGGL((mm_int4_prep_kernel<MT>), grid, dim3(512), mm_prep_lds_bytes<MT>(NG), st, Xp, xs, Mp, q, s, m,
+                       Y, ydt, ldy, M, N, K);
+    return hipGetLastError();
+}
+
 // Y[m, n] = sum over splits of part[split][m][n] (fixed order), in Y's dtype
 __global__ __launch_bounds__(256) void mm_splitk_reduce(const float* __restrict__ part, int splits,
                                                         void* __restrict__ Y, int ydt, int ldy, int M, int N) {
@@ -446,16 +694,29 @@ namespace {
 
 constexpr size_t kLdsMax = 160 * 1024;
 
-// Kernel choice for one shape: 128 x 128 tiles (cfg 1) when that still gives every CU a block, else 64 x 64 tiles
-// (cfg 2), split over K when a workspace is allowed and the tiles alone leave CUs idle (each split keeps >= 4
+// Kernel choice for one shape. With a caller's workspace (rk_mm_int4_g128_ws) and enough 128-column blocks to give
+// most CUs one (cfg 3 / 4 / 5: the prepared-X kernel with 128 / 64 / 48-row blocks; its workspace holds the prepared
+// X). Otherwise 128 x 128 tiles (cfg 1) when that still gives every CU a block, else 64 x 64 tiles (cfg 2), split
+// over K when a workspace or the fixed scratch is allowed and the tiles alone leave CUs idle (each split keeps >= 4
 // groups); cfg 0 is the register-staged kernel, for K too long to stage one block's scales in LDS.
 struct MmPlan {
     int cfg, splits;
-    size_t ws;  // fp32 partial bytes
+    size_t ws;  // workspace bytes: fp32 partials (cfg 2 with splits > 1) or the prepared X (cfg 3 - 5)
 };
 
-MmPlan mm_plan(int M, int N, int K, bool allow_ws) {
+enum MmMode { kMmPlain = 0, kMmWorkspace = 1, kMmScratch = 2 };  // rk_mm_int4_g128, _ws, _noalloc
+constexpr long kPrepMinBlocks = 160;  // measured: below this the tile kernels' extra blocks win
+
+MmPlan mm_plan(int M, int N, int K, int mode) {
     const int NG = K / 128;
+    if (mode == kMmWorkspace && ((long)N * NG) % 8 == 0) {
+        const int mt = M <= 48 ? 3 : M <= 64 ? 4 : 8;
+        const long Mp = (M + 15) / 16 * 16;
+        const long blocks = (long)((N + 127) / 128) * ((Mp + 16 * mt - 1) / (16 * mt));
+        const size_t lds = mt == 3 ? mm_prep_lds_bytes<3>(NG) : mt == 4 ? mm_prep_lds_bytes<4>(NG) : mm_prep_lds_bytes<8>(NG);
+        if (blocks >= kPrepMinBlocks && lds <= kLdsMax) return {mt == 8 ? 3 : mt == 4 ? 4 : 5, 1, mm_prep_ws_bytes(M, K)};
+    }
+    const bool allow_ws = mode != kMmPlain;
     const long big = (long)((N + 127) / 128) * ((M + 127) / 128);
     if (M > 64 && big >= 256 && mm_lds_bytes<4, 4>(NG) <= kLdsMax) return {1, 1, 0};
     const long small = (long)((N + 63) / 64) * ((M + 63) / 64);
@@ -477,12 +738,19 @@ int mm_check(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16
 }
 
 int mm_run(const MmPlan& p, const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
-           const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, float* part, hipStream_t s) {
+           const uint16_t* min, void* Y, int y_dtype, int ldy, int M, int N, int K, void* ws, hipStream_t s) {
     hipError_t e;
     if (p.cfg == 1)
         e = launch_mm_lds<4, 4>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, nullptr, 1, s);
     else if (p.cfg == 2)
-        e = launch_mm_lds<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, part, p.splits, s);
+        e = launch_mm_lds<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, static_cast<float*>(ws),
+                                p.splits, s);
+    else if (p.cfg == 3)
+        e = launch_mm_prep<8>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
+    else if (p.cfg == 4)
+        e = launch_mm_prep<4>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
+    else if (p.cfg == 5)
+        e = launch_mm_prep<3>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
     else
         e = launch_mm<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
@@ -523,21 +791,22 @@ extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_
                                rk_stream_t stream) {
     const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
     if (st != RK_OK) return st;
-    return mm_run(mm_plan(M, N, K, false), X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, nullptr,
+    return mm_run(mm_plan(M, N, K, kMmPlain), X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, nullptr,
                   reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
-    const MmPlan p = mm_plan(M, N, K, use_workspace != 0);
-    if (kernel) *kernel = p.cfg == 1 ? RK_MM_TILE128 : p.cfg == 2 ? RK_MM_TILE64 : RK_MM_REGS;
+    const MmPlan p = mm_plan(M, N, K, use_workspace != 0 ? kMmWorkspace : kMmPlain);
+    static const int kCode[6] = {RK_MM_REGS, RK_MM_TILE128, RK_MM_TILE64, RK_MM_PREP128, RK_MM_PREP64, RK_MM_PREP48};
+    if (kernel) *kernel = kCode[p.cfg];
     if (splits) *splits = p.splits;
     return RK_OK;
 }
 
 extern "C" size_t rk_mm_int4_workspace_bytes(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
-    return mm_plan(M, N, K, true).ws;
+    return mm_plan(M, N, K, kMmWorkspace).ws;
 }
 
 extern "C" int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
@@ -545,10 +814,13 @@ extern "C" int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uin
                                   void* workspace, size_t workspace_bytes, rk_stream_t stream) {
     const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
     if (st != RK_OK) return st;
-    const MmPlan p = mm_plan(M, N, K, true);
+    MmPlan p = mm_plan(M, N, K, kMmWorkspace);
+    // the prepared-X kernel copies the scale / min rows in 16-byte pieces; other arrays take the tile plan, which
+    // needs no more workspace (shapes with that many column blocks are not split over K)
+    if (p.cfg >= 3 && (((uintptr_t)scale | (uintptr_t)min) & 15)) p = mm_plan(M, N, K, kMmScratch);
     if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) return RK_ERR_SHAPE;
     if (p.ws > 0 && ((uintptr_t)workspace & 15)) return RK_ERR_ALIGN;
-    return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, static_cast<float*>(workspace),
+    return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, workspace,
                   reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -558,7 +830,7 @@ extern "C" int rk_mm_int4_g128_noalloc(const void* X, int x_dtype, int ldx, cons
     // every check comes before the device is touched: a rejected call launches nothing
     const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
     if (st != RK_OK) return st;
-    const MmPlan p = mm_plan(M, N, K, true);
+    const MmPlan p = mm_plan(M, N, K, kMmScratch);
     if (p.ws > RK_MM_SCRATCH_BYTES) return RK_ERR_SCRATCH;
     float* part = nullptr;
     if (p.ws > 0) {

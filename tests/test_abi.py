@@ -55,9 +55,14 @@ def test_version_and_status_strings():
                                           (200, 33, 11008, 21), (34, 22016, 2048, 1), (512, 2048, 11008, 1),
                                           (512, 22016, 2048, 1), (4, 32, 256, 1)])
 def test_mm_int4_split_k_plan(M, N, K, splits):
-    """fp32 partials only where 64 x 64 output tiles leave CUs idle: splits = min(ceil(256 / tiles), groups / 4)"""
+    """fp32 partials only where 64 x 64 output tiles leave CUs idle: splits = min(ceil(256 / tiles), groups / 4);
+    shapes on the prepared-X kernel hold the prepared X instead"""
     nbytes = HL.lib().rk_mm_int4_workspace_bytes(M, N, K)
-    assert nbytes == (splits * M * N * 4 if splits > 1 else 0)
+    if HL.mm_plan(M, N, K)[0] in HL.MM_PREP:
+        Mp = (M + 15) // 16 * 16
+        assert splits == 1 and nbytes == Mp * K * 2 + (K // 128) * Mp * 4
+    else:
+        assert nbytes == (splits * M * N * 4 if splits > 1 else 0)
 
 
 def test_mm_int4_ws_rejects_small_workspace():
@@ -145,6 +150,18 @@ def test_sampler_entry_points_validate_before_any_device_work():
                               16384, 8, 30, P, P, 2048, P, None, S) == -4
 
 
+@pytest.mark.parametrize("M,N,K,kernel", [(512, 22016, 2048, HL.MM_PREP128), (201, 25088, 2048, HL.MM_PREP128),
+                                          (69, 25088, 2048, HL.MM_PREP128), (34, 22016, 2048, HL.MM_PREP48),
+                                          (64, 22016, 4096, HL.MM_PREP64), (128, 22016, 2048, HL.MM_PREP128),
+                                          (512, 3072, 2048, HL.MM_TILE64), (512, 2048, 11008, HL.MM_TILE64),
+                                          (34, 3072, 2048, HL.MM_TILE64), (34, 22017, 128, HL.MM_TILE64)])
+def test_mm_int4_workspace_plan(M, N, K, kernel):
+    """With a workspace, shapes with >= 160 column blocks of 128 take the prepared-X kernel (48 / 64 / 128-row
+    blocks by M); too few blocks, K too long for the block's scale tables, or N * K / 128 not a multiple of 8 keep
+    the tile plan."""
+    assert HL.mm_plan(M, N, K, use_workspace=True)[0] == kernel
+
+
 @pytest.mark.parametrize("M,N,K,kernel", [(512, 22016, 2048, HL.MM_TILE128), (201, 25088, 2048, HL.MM_TILE128),
                                           (512, 2048, 11008, HL.MM_TILE64), (69, 25088, 2048, HL.MM_TILE64),
                                           (34, 22016, 2048, HL.MM_TILE64), (128, 22016, 2048, HL.MM_TILE64),
@@ -155,7 +172,12 @@ def test_mm_int4_plan_query(M, N, K, kernel):
     assert k == kernel and sp == 1
     k2, sp2 = HL.mm_plan(M, N, K, use_workspace=True)
     nbytes = HL.lib().rk_mm_int4_workspace_bytes(M, N, K)
-    assert (sp2 > 1) == (nbytes > 0) and nbytes == (sp2 * M * N * 4 if sp2 > 1 else 0)
+    if k2 in HL.MM_PREP:  # prepared X (fp16, rows padded to 16) and its per-group row sums (fp32)
+        Mp = (M + 15) // 16 * 16
+        assert sp2 == 1 and nbytes == Mp * K * 2 + (K // 128) * Mp * 4
+        assert k2 == (HL.MM_PREP48 if M <= 48 else HL.MM_PREP64 if M <= 64 else HL.MM_PREP128)
+    else:
+        assert (sp2 > 1) == (nbytes > 0) and nbytes == (sp2 * M * N * 4 if sp2 > 1 else 0)
     with pytest.raises(RuntimeError):
         HL.mm_plan(M, N, 100, use_workspace=False)
 

@@ -39,11 +39,12 @@ def test_config3_shapes(M, N, K, dev):
     print(f"M={M} N={N} K={K}: {rep}")
 
 
-@pytest.mark.parametrize("N,K,kernel", [(3072, 2048, H.MM_TILE64), (22016, 2048, H.MM_TILE128),
+@pytest.mark.parametrize("N,K,kernel", [(3072, 2048, H.MM_TILE64), (22016, 2048, H.MM_PREP128),
                                          (2048, 11008, H.MM_TILE64)])
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 def test_config3_m512(N, K, kernel, xdt, dev):
-    """M = 512 on every config-3 shape; gate+up 22016 x 2048 runs the 128 x 128 tile kernel (asserted)."""
+    """M = 512 on every config-3 shape through the drop-in (workspace entry); gate+up 22016 x 2048 runs the
+    prepared-X kernel (asserted; its tile-kernel run is test_prepared_x_against_tile_kernels)."""
     assert H.mm_plan(512, N, K)[0] == kernel
     X, q, s, m = synth.prefill_case(512, N, K, 3)
     X = X.to(xdt)
@@ -52,10 +53,11 @@ def test_config3_m512(N, K, kernel, xdt, dev):
     print(f"M=512 N={N} K={K} {xdt}: {rep}")
 
 
-@pytest.mark.parametrize("T,kernel", [(34, H.MM_TILE64), (69, H.MM_TILE64), (201, H.MM_TILE128)])
+@pytest.mark.parametrize("T,kernel", [(34, H.MM_PREP48), (69, H.MM_PREP128), (201, H.MM_PREP128)])
 def test_reference_w_in_prompts(T, kernel, dev):
     """The reference's own check (kernels/mm_int4.py:92-106): w_in 25088 x 2048 at T in {34, 69, 201}, bf16 X as
-    the engine passes it; T = 201 selects the 128 x 128 tile kernel (asserted)."""
+    the engine passes it, through the drop-in (the prepared-X kernels, asserted); the same prompts on the tile
+    kernels are in test_prepared_x_against_tile_kernels."""
     N, K = 25088, 2048
     assert H.mm_plan(T, N, K) == (kernel, 1)
     X, q, s, m = synth.prefill_case(T, N, K, 30 + T)
@@ -172,3 +174,95 @@ def test_warmup_and_graph(dev):
         g.replay()
         torch.cuda.synchronize()
         _check(Y, _ref(X.cpu(), q.cpu(), s.cpu(), m.cpu()), f"replay {i}")
+
+
+# ---- the prepared-X kernels (workspace entry) against the tile kernels (plain entry) and the oracle
+def _abi(X, q, s, m, Y, ws=None, ldx=None, ldy=None):
+    L = H.lib()
+    M, K = X.shape[0], q.shape[1] * 2
+    N = q.shape[0]
+    args = [H.ptr(X), H.dt(X), ldx or X.stride(0), H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(Y), H.dt(Y), ldy or Y.stride(0),
+            M, N, K]
+    if ws is None:
+        H.check(L.rk_mm_int4_g128(*args, H.stream(X.device)), "rk_mm_int4_g128")
+    else:
+        H.check(L.rk_mm_int4_g128_ws(*args, H.ptr(ws), ws.numel(), H.stream(X.device)), "rk_mm_int4_g128_ws")
+
+
+def _ws(M, N, K, dev):
+    n = H.lib().rk_mm_int4_workspace_bytes(M, N, K)
+    return torch.full((max(n, 16),), 0xFF, device=dev, dtype=torch.uint8)  # stale contents must not matter
+
+
+@pytest.mark.parametrize("M,N,K,prep,tile", [(512, 22016, 2048, H.MM_PREP128, H.MM_TILE128),
+                                             (201, 25088, 2048, H.MM_PREP128, H.MM_TILE128),
+                                             (69, 25088, 2048, H.MM_PREP128, H.MM_TILE64),
+                                             (34, 25088, 2048, H.MM_PREP48, H.MM_TILE64),
+                                             (128, 22016, 2048, H.MM_PREP128, H.MM_TILE64),
+                                             (64, 22016, 4096, H.MM_PREP64, H.MM_TILE64)])
+def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
+    """Each benchmarked / reference prompt shape on both plans: both within the oracle bar, and equal to each other up
+    to fp32 summation order."""
+    assert H.mm_plan(M, N, K, use_workspace=True) == (prep, 1)
+    assert H.mm_plan(M, N, K, use_workspace=False) == (tile, 1)
+    X, q, s, m = synth.prefill_case(M, N, K, 21)
+    X = X.bfloat16() if M in (34, 69, 201) else X  # the engine passes bf16 on the w_in prompts
+    Xd, qd, sd, md = X.to(dev), q.to(dev), s.to(dev), m.to(dev)
+    Yp = torch.full((M, N), 3.0, device=dev, dtype=torch.float32)
+    Yt = torch.full((M, N), -3.0, device=dev, dtype=torch.float32)
+    _abi(Xd, qd, sd, md, Yp, ws=_ws(M, N, K, dev))
+    _abi(Xd, qd, sd, md, Yt)
+    torch.cuda.synchronize()
+    ref = _ref(X, q, s, m)
+    rp = _check(Yp, ref, f"prepared M={M} N={N} K={K}")
+    _check(Yt, ref, f"tile M={M} N={N} K={K}")
+    np.testing.assert_allclose(_np(Yp), _np(Yt), rtol=1e-4, atol=1e-6 * float(np.abs(_np(Yt)).max()))
+    print(f"M={M} N={N} K={K}: {rp}")
+
+
+@pytest.mark.parametrize("M,N,K,xdt,ydt", [(5, 20488, 256, torch.float16, torch.float16),
+                                           (47, 20480, 384, torch.bfloat16, torch.float32),
+                                           (61, 20360, 1152, torch.float16, torch.bfloat16),
+                                           (130, 20480, 256, torch.bfloat16, torch.bfloat16),
+                                           (200, 20600, 512, torch.float16, torch.float32)])
+def test_prepared_x_ragged_and_dtypes(M, N, K, xdt, ydt, dev):
+    """Ragged rows (the last block's missing m tiles, rows past M), ragged columns (N not a multiple of 128 or 8),
+    odd group counts, every input / output dtype; nothing is written outside [M, N]."""
+    kernel, _ = H.mm_plan(M, N, K, use_workspace=True)
+    assert kernel in H.MM_PREP, (M, N, K, kernel)
+    X, q, s, m = synth.prefill_case(M, N, K, 22)
+    X = X.to(xdt)
+    Xd, qd, sd, md = X.to(dev), q.to(dev), s.to(dev), m.to(dev)
+    Yw = torch.full((M + 1, N + 8), 7.0, device=dev, dtype=ydt)  # one guard row, eight guard columns
+    Y = Yw[:M, :N]
+    _abi(Xd, qd, sd, md, Y, ws=_ws(M, N, K, dev), ldy=N + 8)
+    torch.cuda.synchronize()
+    _check(Y, _ref(X, q, s, m), f"M={M} N={N} K={K} {xdt}->{ydt}")
+    assert torch.all(Yw[M] == 7.0) and torch.all(Yw[:, N:] == 7.0)
+
+
+def test_prepared_x_strided_rows_and_scale_fallback(dev):
+    """X rows with a stride beyond K; scale / min arrays that are not 16-byte aligned take the tile plan instead
+    (same workspace size suffices) — both within the bar."""
+    M, N, K = 40, 20480, 512
+    X, q, s, m = synth.prefill_case(M, N, K, 23)
+    Xw = torch.zeros(M, K + 64, dtype=torch.float16)
+    Xw[:, :K] = X
+    Xd, qd = Xw.to(dev), q.to(dev)
+    sd, md = s.to(dev), m.to(dev)
+    ws = _ws(M, N, K, dev)
+    Y = torch.empty(M, N, device=dev, dtype=torch.float32)
+    _abi(Xd, qd, sd, md, Y, ws=ws, ldx=K + 64)
+    torch.cuda.synchronize()
+    ref = _ref(X, q, s, m)
+    _check(Y, ref, "strided X")
+    # the same scales and mins, 2 bytes past a 16-byte boundary
+    sb = torch.empty(s.numel() + 1, dtype=torch.float16, device=dev)[1:].view(N, K // 128)
+    mb_ = torch.empty(m.numel() + 1, dtype=torch.float16, device=dev)[1:].view(N, K // 128)
+    sb.copy_(sd)
+    mb_.copy_(md)
+    assert sb.data_ptr() % 16 and mb_.data_ptr() % 16
+    Y2 = torch.empty_like(Y)
+    _abi(Xd, qd, sb, mb_, Y2, ws=ws, ldx=K + 64)
+    torch.cuda.synchronize()
+    _check(Y2, ref, "unaligned scales")

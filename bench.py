@@ -5,20 +5,21 @@
 
 Workload (one "step"): config 1 of the benchmark definition — one decoder layer's decode projections at batch 1,
 int4 g128, x fp16 ~N(0,1): fused QKV (2048 -> 3072), O (2048 -> 2048), fused gate+up (2048 -> 2*11008) followed by
-SiLU(gate)*up, down (11008 -> 2048). The step runs them the way the reference engine does (engine/rumik_fused.py,
-engine/rumik_int4.py:97): QKV and gate+up are one input projection over the rows [q k v | gate | up] (w_in, 25088
-rows), whose epilogue here also applies SiLU(gate)*up (the MLP part of the reference's post), then O, then down:
-three launches. Each step uses the weights of the next of 16 distinct synthetic layers (665 MB in all), so no step
-is served from the 256 MB Infinity Cache. A step is one hipGraph replay; weights and inputs are resident in HBM
-before timing.
+SiLU(gate)*up, down (11008 -> 2048). QKV and gate+up are the reference engine's one input projection over the rows
+[q k v | gate | up] (w_in, 25088 rows; engine/rumik_fused.py:100, engine/rumik_int4.py:97) with SiLU(gate)*up (the
+MLP part of the reference's post); O takes a given attention output and down takes that act. The step is ONE launch
+of rk_gemv_int4_g128_layer (all four projections; the grid meets once, when act is complete); the two-launch form
+(w_in + SiLU, then O + down) is timed beside it. Each step uses the weights of the next of 16 distinct synthetic
+layers (665 MB in all), so no step is served from the 256 MB Infinity Cache. 16 steps are one hipGraph replay;
+weights and inputs are resident in HBM before timing.
 
 value = algorithmic bytes per step (sum over the four projections of N*K/2 + 4*N*K/128 + 2K + 2N) / wall time.
-roofline: the dominant kernel (the fused w_in + SiLU launch, 27,328,000 B per launch: codes, scales, mins, x and the
-3072 + 11008 outputs), its average launch duration measured with HIP events on its stream over back-to-back
-launches with rotated weights.
-roofline.read_ceiling_us: the best time of a read-only kernel over the same bytes in the same setting (the
-reference's kernels/roofline.py method), and a dense bf16 GEMV's read rate beside it.
-parity: the dominant projection against the float64 oracle (max_rel and max_rel_strict).
+roofline: the dominant kernel (the layer launch: the step's bytes in one launch), its average launch duration
+measured with HIP events on its stream over back-to-back launches with rotated weights.
+roofline.read_ceiling_us: the best time of a read-only kernel over the same number of bytes in the same setting
+(the reference's kernels/roofline.py method), and a dense bf16 GEMV's read rate beside it.
+parity: the layer launch's outputs on copy 0 (q/k/v rows and down) and the w_in projection against the float64
+oracle (max_rel and max_rel_strict).
 decode_tok_s: the 36-layer step's tokens per second at ctx 256 / 1024 / 2048 (config 4).
 cpu_baseline: the CPU oracle's dequantize-then-matmul of the same step (numpy fp32), on this host's cores, with
 matmul-only times and configs 2 / 3 / a config-4 layer beside it.
@@ -93,7 +94,7 @@ def load_traffic():
         return None
     try:
         d = json.loads(f.read_text())
-        return d.get("gemv_int4_w_in_silu_25088x2048", {}).get("traffic_bytes")
+        return d.get("gemv_layer_config1", {}).get("traffic_bytes")
     except Exception:
         return None
 
@@ -397,8 +398,14 @@ def main():
     act = torch.empty(INTER, device=dev, dtype=torch.float16)
     y_d = torch.empty(H, device=dev, dtype=torch.float16)
 
+    lp = cuda_gemv.LayerProjections(NQKV, INTER, dev)
+
     def step_fns(L):
-        # w_in (qkv | gate | up) with SiLU*up fused, then o and down (both inputs ready) in one launch
+        # the four projections in one launch (w_in with SiLU*up, o over ob, down over this launch's act)
+        return [lambda: lp(x, L["w_in"], ob, L["o"], L["down"], y_qkv, act, y_o, y_d)]
+
+    def two_launch_fns(L):
+        # the same step as two launches: w_in with SiLU*up fused, then o and down in one launch
         return [lambda: cuda_gemv.gemv_int4_silu_cuda(x, *L["w_in"], NQKV, out=y_qkv, act=act),
                 lambda: cuda_gemv.gemv_int4_pair_cuda(ob, L["o"], act, L["down"], out1=y_o, out2=y_d)]
 
@@ -427,6 +434,17 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     value = step_bytes * args.steps / elapsed / 1e9
     log(f"[bench] config 1: {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s")
+    assert lp.status() == 0, "layer launch: an exchange wait ran out"
+
+    # ---- the dominant kernel: the layer launch alone (16 rotated copies back to back in one graph), and the
+    # two-launch form of the same step
+    g = graph_of([f for L in layers for f in step_fns(L)])
+    layer_us = time_graph_us(g, N_COPIES)
+    del g
+    g = graph_of([f for L in layers for f in two_launch_fns(L)])
+    two_us = time_graph_us(g, N_COPIES)
+    del g
+    log(f"[bench] layer launch {layer_us:.2f} us, two-launch step {two_us:.2f} us")
 
     # ---- per-projection kernel times (back-to-back launches over the 16 copies)
     proj = {}
@@ -449,24 +467,38 @@ def main():
     pair_bytes = int4_bytes(*SHAPES["o"]) + int4_bytes(*SHAPES["down"])
     proj["o_down_pair"] = {"us": round(pair_us, 2), "GB_s": round(pair_bytes / pair_us / 1e3, 1)}
     log(f"[bench] projections: {proj}")
-    achieved = WIN_BYTES / win_us / 1e3
-    # the read ceiling of that launch: rk_read_only over the same bytes (w_in's codes, scales and mins), the same 16
-    # rotated copies back to back in one graph, best over launch shapes (the reference's kernels/roofline.py
-    # method); and a dense bf16 GEMV (torch.mm, 4x the weight bytes) as the vendor library's practical read rate
+    achieved = step_bytes / layer_us / 1e3
+    # the read ceiling of that launch: rk_read_only over buffers of the same sizes as one copy's codes, scales and
+    # mins (all four projections), 16 rotated copies back to back in one graph, best over launch shapes (the
+    # reference's kernels/roofline.py method); and a dense bf16 GEMV (torch.mm, 4x the weight bytes) as the vendor
+    # library's practical read rate
     import roofline as RF
-    ro_us, ro_shape = RF.ceiling_us([L["w_in"] for L in layers])
-    ro_bytes = sum(t.numel() * t.element_size() for t in layers[0]["w_in"])
+    mats0 = [layers[0][k] for k in ("w_in", "o", "down")]
+    sizes = [sum(m[i].numel() * m[i].element_size() for m in mats0) for i in range(3)]
+    ro_mats = [tuple(torch.empty(n, device=dev, dtype=torch.uint8) for n in sizes) for _ in range(N_COPIES)]
+    ro_us, ro_shape = RF.ceiling_us(ro_mats)
+    ro_bytes = sum(sizes)
+    del ro_mats
     log(f"[bench] read ceiling: {ro_us:.2f} us for {ro_bytes} B ({ro_bytes / ro_us / 1e3:.0f} GB/s), {ro_shape}")
-    # parity of the dominant projection on copy 0 against the float64 oracle (max_rel with the per-output
-    # conditioning floor, max_rel_strict with the fp16 floor alone)
+    # parity on copy 0 against the float64 oracle (max_rel with the per-output conditioning floor, max_rel_strict
+    # with the fp16 floor alone): the layer launch's q/k/v rows (over x) and down rows (over the act it wrote), and
+    # the w_in projection alone
     from oracle import int4 as O
-    y_chk = cuda_gemv.gemv_int4_cuda(x, *layers[0]["w_in"], out=torch.empty(N_WIN, device=dev, dtype=torch.float32))
-    a_chk = (x.cpu().numpy(), *(t.cpu().numpy() for t in layers[0]["w_in"]))
-    parity = O.parity_report(y_chk.cpu().numpy(), O.gemv_int4_f64(*a_chk), O.cond_floor(O.gemv_int4_abs(*a_chk)))
-    parity = {"check": "gemv int4 w_in 25088x2048 (copy 0) vs float64 oracle",
-              **{k: (round(v, 8) if isinstance(v, float) else v) for k, v in parity.items()}}
+
+    def rep(y, xv, w, label):
+        a = (xv.float().cpu().numpy(), *(t.cpu().numpy() for t in w))
+        r = O.parity_report(y.float().cpu().numpy(), O.gemv_int4_f64(*a), O.cond_floor(O.gemv_int4_abs(*a)))
+        return {"check": label, **{k: (round(v, 8) if isinstance(v, float) else v) for k, v in r.items()}}
+    L0 = layers[0]
+    y_l, act_l, yo_l, yd_l = lp(x, L0["w_in"], ob, L0["o"], L0["down"])
+    torch.cuda.synchronize()
+    y_chk = cuda_gemv.gemv_int4_cuda(x, *L0["w_in"], out=torch.empty(N_WIN, device=dev, dtype=torch.float32))
+    parity = rep(y_chk, x, L0["w_in"], "gemv int4 w_in 25088x2048 (copy 0) vs float64 oracle")
+    parity["layer"] = [rep(y_l, x, tuple(t[:NQKV] for t in L0["w_in"]), "layer launch q/k/v rows"),
+                       rep(yo_l, ob, L0["o"], "layer launch o rows"),
+                       rep(yd_l, act_l, L0["down"], "layer launch down rows (over the act it wrote)")]
     log(f"[bench] parity: {parity}")
-    del layers, y_chk, a_chk
+    del layers, y_chk, y_l, act_l, yo_l, yd_l
     torch.cuda.empty_cache()
     wb = [torch.randn(H, N_WIN, device=dev, generator=gen).bfloat16() for _ in range(4)]  # 4 x 103 MB: past the cache
     xb, yb = x.bfloat16().view(1, H), torch.empty(1, N_WIN, device=dev, dtype=torch.bfloat16)
@@ -478,10 +510,12 @@ def main():
     torch.cuda.empty_cache()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": load_traffic(),
-                "kernel": "gemv int4 g128 w_in [qkv | gate | up] N=25088 K=2048 + SiLU*up epilogue",
-                "us_per_launch": round(win_us, 2),
+                "kernel": "gemv_layer_kernel: w_in [qkv | gate | up] 25088x2048 + SiLU*up, o 2048x2048, down "
+                          "2048x11008 in one launch",
+                "us_per_launch": round(layer_us, 2), "bytes_per_launch": step_bytes,
+                "two_launch_us_per_step": round(two_us, 2),
                 "read_ceiling_us": round(ro_us, 2), "read_ceiling_GB_s": round(ro_bytes / ro_us / 1e3, 1),
-                "read_ceiling_shape": ro_shape, "frac_of_read_ceiling": round(ro_us / win_us, 4),
+                "read_ceiling_shape": ro_shape, "frac_of_read_ceiling": round(ro_us / layer_us, 4),
                 "dense_bf16_gemv_us": round(bf_us, 2),
                 "dense_bf16_gemv_GB_s": round(2 * N_WIN * H / bf_us / 1e3, 1)}
 
@@ -544,8 +578,8 @@ def main():
         "data": "synthetic (seeded int4 g128 codes / fp16 scale+min, x ~ N(0,1)); 16 distinct weight copies",
         "config": {"workload": "config 1: one decoder layer's decode projections (qkv 3072x2048, o 2048x2048, "
                                "gate+up 22016x2048 + SiLU*up, down 2048x11008), batch 1; qkv and gate+up run as "
-                               "the reference engine's one w_in projection with SiLU*up fused, o and down in one launch: 2 launches "
-                               "per step, 16 steps (16 weight copies) per hipGraph replay",
+                               "the reference engine's one w_in projection with SiLU*up fused; all four in one "
+                               "launch per step, 16 steps (16 weight copies) per hipGraph replay",
                    "bytes_per_step": step_bytes, "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2)},
         "decode_tok_s": ({k: decode_res[k]["tok_s"] for k in ("ctx256", "ctx1024", "ctx2048")}
                          if decode_res else None),

@@ -103,6 +103,27 @@ int rk_gemv_int4_g128_silu(const void* x, int x_dtype, const uint8_t* q, const u
                            const uint16_t* min, void* y, void* act, int y_dtype, int n_plain, int inter, int K,
                            int waves, rk_stream_t stream);
 
+/* One decoder layer's four decode projections in ONE launch: y_plain / act exactly as rk_gemv_int4_g128_silu
+ * (w_in over x, act = silu(gate) * up with gate and up rounded to y_dtype first), y_o = dequant(w_o) ob and
+ * y_down = dequant(w_down) act, where act is the one this launch computes. Replaces the reference's gemv(h, w_in),
+ * the MLP part of fused.post, gemv(ob, w_o) and gemv(act, w_down) of one layer (engine/rumik_fused.py:100-101,
+ * 115-116) when o's input is already at hand (the benchmark's layer-projection workload). Shapes: w_in
+ * [n_plain + 2*inter, H], w_o [H, H], w_down [H, inter], int4 g128 (codes, fp16 scale / min) as rk_gemv_int4_g128;
+ * H == 2048, inter a multiple of 128 up to 12288, n_plain >= 0 small enough for the grid (RK_ERR_SHAPE otherwise:
+ * then run rk_gemv_int4_g128_silu and rk_gemv_int4_g128_pair). x / ob RK_F16 or RK_BF16 (x_dtype), outputs
+ * RK_F16 or RK_BF16 (y_dtype); x, ob and the code arrays 16-byte aligned.
+ * ws: rk_gemv_int4_g128_layer_ws_bytes(inter) bytes, 4-byte aligned, ZEROED before its first use and then kept
+ * for this call alone (its words carry per-block launch counters, so hipGraph replays need no reset; one launch
+ * at a time per workspace). One block per CU, all resident at once; the grid meets once (act), every wait
+ * bounded: a wait that runs out (200 ms) sets bit 0 of the workspace's first 32-bit word and leaves y_down
+ * unwritten. No separate reference counterpart. */
+size_t rk_gemv_int4_g128_layer_ws_bytes(int inter);
+int rk_gemv_int4_g128_layer(const void* x, const void* ob, int x_dtype, const uint8_t* q_in, const uint16_t* s_in,
+                            const uint16_t* m_in, const uint8_t* q_o, const uint16_t* s_o, const uint16_t* m_o,
+                            const uint8_t* q_down, const uint16_t* s_down, const uint16_t* m_down, void* y_plain,
+                            void* act, void* y_o, void* y_down, int y_dtype, int n_plain, int inter, int H, void* ws,
+                            size_t ws_bytes, rk_stream_t stream);
+
 /* Batch-1 int8 per-row GEMV: y[n] = scale[n] * sum_k code[n,k] * x[k], fp32 accumulate.
  * Replaces gemv_int8_cuda(x, q, s, out) -> gemv_int8 (reference kernels/cuda_gemv.py:245-249, :188-195).
  * q_kind: RK_Q_S8 or RK_Q_U8; scale dtype RK_F16 or RK_F32; y dtype RK_F32 / RK_BF16 / RK_F16.

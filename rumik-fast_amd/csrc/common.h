@@ -143,8 +143,11 @@ RK_DEV void reduce_step(float (&v)[R], int& n, int lane) {
 #pragma unroll
         for (int i = 0; i < R / 2; ++i) {
             if (i < h) {
-                float keep = up ? v[i + h] : v[i];
-                float send = up ? v[i] : v[i + h];
+                // both values first, then the selects: a select between two elements of v itself can be folded
+                // into one load at a lane-dependent index, which would move v to scratch memory
+                const float lo = v[i], hi = v[i + h];
+                const float keep = up ? hi : lo;
+                const float send = up ? lo : hi;
                 v[i] = keep + xor_lane<M>(send);
             }
         }

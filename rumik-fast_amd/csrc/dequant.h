@@ -84,3 +84,51 @@ RK_DEV float chunk_dot_int8(u4_t w, const uint32_t* xp) {
     }
     return a0 + a1;
 }
+
+// The 32 x values of chunk c (4 x 16 bytes), loaded raw: issued before the weights so that processing them waits for
+// x only (vector-memory results return in issue order).
+struct XChunk {
+    u4_t d[4];
+};
+RK_DEV void load_x_raw(const void* __restrict__ x, int c, XChunk& xc) {
+    const u4_t* xv = reinterpret_cast<const u4_t*>(x) + (size_t)c * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xc.d[i] = xv[i];
+}
+
+// chunk c's x as 16 fp16 pairs in dequant order, and their fp32 sum
+RK_DEV void process_x_chunk(const XChunk& xc, int xdt, uint32_t (&xp)[16], float& xs) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u4_t d = xc.d[i];  // 8 consecutive 16-bit values: d.x = (x0,x1), d.y = (x2,x3), d.z = (x4,x5), d.w = (x6,x7)
+        if (xdt == RK_BF16) {
+            // bf16 -> fp32 (exact, summed) -> fp16 (round to nearest even) pairs
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t v = d[e];
+                f[2 * e] = __builtin_bit_cast(float, v << 16);
+                f[2 * e + 1] = __builtin_bit_cast(float, v & 0xffff0000u);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += f[e];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h2_t p;
+                p.x = (_Float16)f[e];
+                p.y = (_Float16)f[e + 4];
+                xp[4 * i + e] = as_u32(p);
+            }
+        } else {
+            xp[4 * i + 0] = perm(d.z, d.x, 0x05040100u);  // (x0, x4)
+            xp[4 * i + 1] = perm(d.z, d.x, 0x07060302u);  // (x1, x5)
+            xp[4 * i + 2] = perm(d.w, d.y, 0x05040100u);  // (x2, x6)
+            xp[4 * i + 3] = perm(d.w, d.y, 0x07060302u);  // (x3, x7)
+            const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s = dot2(as_h2(d[e]), one, s);
+        }
+    }
+    xs = s;
+}

@@ -24,6 +24,9 @@ _SIGS = {
     "rk_gemv_int4_g128_valu": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_pair": ([_p, _i, _p, _p, _p, _p, _i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p], _i),
     "rk_gemv_int4_g128_silu": ([_p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "rk_gemv_int4_g128_layer_ws_bytes": ([_i], ctypes.c_size_t),
+    "rk_gemv_int4_g128_layer": ([_p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p,
+                                 ctypes.c_size_t, _p], _i),
     "rk_gemv_int8_rows": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _p], _i),
     "rk_gemv_int8_rows_ex": ([_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_mm_int4_g128": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),

@@ -92,6 +92,59 @@ def gemv_int4_silu_cuda(x, q, s, m, n_plain, out=None, act=None):
     return y, a
 
 
+class LayerProjections:
+    """One decoder layer's four decode projections in one launch (rk_gemv_int4_g128_layer): w_in over x with
+    act = silu(gate) * up fused, o over ob, and down over that act -- the reference's gemv(h, w_in), the MLP part of
+    post, gemv(ob, w_o) and gemv(act, w_down) (engine/rumik_fused.py:100-101, 115-116) when ob is already at hand.
+    Owns the zeroed workspace the launch's exchange needs (one launch at a time per instance; hipGraph replays of a
+    captured call need no reset). Outputs as gemv_int4_silu_cuda and gemv_int4_pair_cuda give them.
+
+        lp = LayerProjections(n_plain, inter, device)
+        y_plain, act, y_o, y_down = lp(x, w_in, ob, w_o, w_down)
+    """
+
+    def __init__(self, n_plain, inter, device):
+        self.n_plain, self.inter = int(n_plain), int(inter)
+        nbytes = H.lib().rk_gemv_int4_g128_layer_ws_bytes(self.inter)
+        if nbytes == 0:
+            raise RuntimeError("shape")
+        self.ws = torch.zeros(nbytes // 4, device=device, dtype=torch.int32)
+
+    def status(self):
+        """The workspace's status word: 0, or bit 0 once a launch's exchange ran out of time."""
+        return int(self.ws[0].item())
+
+    def __call__(self, x, w_in, ob, w_o, w_down, out=None, act=None, out_o=None, out_d=None):
+        n_plain, inter = self.n_plain, self.inter
+        q, s, m = w_in
+        Hd = x.numel()
+        dt = x.dtype
+        a = act if act is not None else torch.empty(inter, device=x.device, dtype=dt)
+        y = out if out is not None else (torch.empty(n_plain, device=x.device, dtype=a.dtype) if n_plain else None)
+        yo = out_o if out_o is not None else torch.empty(Hd, device=x.device, dtype=a.dtype)
+        yd = out_d if out_d is not None else torch.empty(Hd, device=x.device, dtype=a.dtype)
+        H.require_gpu(x, q, s, m, a, y)
+        if q.dim() != 2 or q.dtype != torch.uint8 or q.shape[0] != n_plain + 2 * inter or q.shape[1] * 2 != Hd:
+            raise RuntimeError("shape")
+        ng = Hd // G
+        if s.dtype != torch.float16 or m.dtype != torch.float16 or s.numel() != q.shape[0] * ng or m.numel() != s.numel():
+            raise RuntimeError("shape")
+        if not all(t.is_contiguous() for t in (x, q, s, m, a)):
+            raise RuntimeError("shape")
+        if _check_int4(ob, *w_o, yo) != (Hd, Hd) or _check_int4(a, *w_down, yd) != (Hd, inter):
+            raise RuntimeError("shape")
+        if ob.dtype != dt or any(t.dtype != a.dtype for t in (yo, yd) + ((y,) if y is not None else ())):
+            raise RuntimeError("dtype")
+        if a.numel() != inter or (y is not None and (y.numel() < n_plain or not y.is_contiguous())):
+            raise RuntimeError("shape")
+        st = H.lib().rk_gemv_int4_g128_layer(
+            H.ptr(x), H.ptr(ob), H.dt(x), H.ptr(q), H.ptr(s), H.ptr(m), H.ptr(w_o[0]), H.ptr(w_o[1]),
+            H.ptr(w_o[2]), H.ptr(w_down[0]), H.ptr(w_down[1]), H.ptr(w_down[2]), H.ptr(y), H.ptr(a), H.ptr(yo),
+            H.ptr(yd), H.dt(a), n_plain, inter, Hd, H.ptr(self.ws), self.ws.numel() * 4, H.stream(x.device))
+        H.check(st)
+        return y, a, yo, yd
+
+
 def quantize_int8_rows(w, pad_to=16):
     """[N, K] -> (uint8 [N', K] = int8 + 128, fp32 scale [N']), rows zero-padded to a multiple of pad_to.
     Symmetric per row: w ~ (q - 128) * scale, scale = max|w| / 127 (reference kernels/cuda_gemv.py:234-242)."""

@@ -18,6 +18,10 @@ Two steps:
         -- python3 rumik-fast_amd/pmc_traffic.py run
     python3 rumik-fast_amd/pmc_traffic.py summarize OUT/fetch OUT/write
 
+The same two steps for the one-launch layer projections (bench.py's step: w_in + SiLU*up, o and down in one
+launch of rk_gemv_int4_g128_layer): `run-layer` and `summarize-layer` (key gemv_layer_config1 of
+profiles/traffic.json).
+
 The same two steps for the one-launch 36-layer decode step (config 4): `run-decode` launches the copy kernel, then
 DECODE_STEPS eager steps at each of ctx 256, 1024 and 2048 (one dispatch each); `summarize-decode` gives the HBM bytes
 per token against the algorithmic bytes (every weight once plus the K/V slots read) and writes
@@ -101,7 +105,7 @@ def summarize(fetch_dir, write_dir):
         "traffic_bytes": round(fetch_b + write_b), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
         "algorithmic_bytes": GEMV_BYTES, "fetch_scale": round(kf, 4), "write_scale": round(kw, 4),
         "dispatches": {"copy_fetch": nfc, "copy_write": nwc, "gemv_fetch": nfg, "gemv_write": nwg}}}
-    (ROOT / "profiles" / "traffic.json").write_text(json.dumps(rec, indent=1) + "\n")
+    _merge_traffic(rec)
     r = rec[KEY]
     print("| quantity | value |\n|---|---|")
     print(f"| copy kernel (torch.neg, 256 MiB fp16) FETCH_SIZE / dispatch | {f_copy:.0f} KiB (scale {kf:.4f}) |")
@@ -111,6 +115,77 @@ def summarize(fetch_dir, write_dir):
     print(f"| traffic / launch (scaled) | {r['traffic_bytes']:,} B |")
     print(f"| algorithmic bytes / launch | {GEMV_BYTES:,} B (traffic / algorithmic = "
           f"{r['traffic_bytes'] / GEMV_BYTES:.3f}) |")
+
+
+def _merge_traffic(rec):
+    f = ROOT / "profiles" / "traffic.json"
+    d = json.loads(f.read_text()) if f.exists() else {}
+    d.update(rec)
+    f.write_text(json.dumps(d, indent=1) + "\n")
+
+
+H_O, LAYER_KEY = 2048, "gemv_layer_config1"
+
+
+def _int4_bytes(n, k):
+    return n * k // 2 + 4 * n * (k // 128) + 2 * k + 2 * n
+
+
+LAYER_BYTES = sum(_int4_bytes(n, k) for n, k in ((N_PLAIN, K), (H_O, K), (2 * INTER, K), (H_O, INTER)))
+
+
+def run_layer():
+    sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "kernels"))
+    import torch
+    import cuda_gemv
+    import synth
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    gen = synth.generator(1, "cuda")
+    layers = [(synth.int4_weights(N, K, gen, device=dev), synth.int4_weights(H_O, K, gen, device=dev),
+               synth.int4_weights(H_O, INTER, gen, device=dev)) for _ in range(N_COPIES)]
+    x = torch.randn(K, device=dev, generator=gen).half()
+    ob = torch.randn(K, device=dev, generator=gen).half()
+    outs = [torch.empty(n, device=dev, dtype=torch.float16) for n in (N_PLAIN, INTER, H_O, H_O)]
+    lp = cuda_gemv.LayerProjections(N_PLAIN, INTER, dev)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for w_in, w_o, w_d in layers:
+            lp(x, w_in, ob, w_o, w_d, *outs)
+    torch.cuda.synchronize()
+    if lp.status() != 0:
+        raise SystemExit(f"layer launch status {lp.status()}")
+    print("pmc_traffic: layer run done", flush=True)
+
+
+def summarize_layer(fetch_dir, write_dir):
+    is_copy = lambda n: "neg" in n.lower()  # noqa: E731
+    is_layer = lambda n: "gemv_layer_kernel" in n  # noqa: E731
+    fr, wr = _rows(fetch_dir), _rows(write_dir)
+    f_copy, nfc = _per_dispatch(fr, "FETCH_SIZE", is_copy)
+    w_copy, nwc = _per_dispatch(wr, "WRITE_SIZE", is_copy)
+    f_l, nfl = _per_dispatch(fr, "FETCH_SIZE", is_layer)
+    w_l, nwl = _per_dispatch(wr, "WRITE_SIZE", is_layer)
+    kf, kw = f_copy * 1024 / COPY_BYTES, w_copy * 1024 / COPY_BYTES
+    fetch_b, write_b = f_l * 1024 / kf, w_l * 1024 / kw
+    rec = {LAYER_KEY: {
+        "traffic_bytes": round(fetch_b + write_b), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
+        "algorithmic_bytes": LAYER_BYTES, "fetch_scale": round(kf, 4), "write_scale": round(kw, 4),
+        "dispatches": {"copy_fetch": nfc, "copy_write": nwc, "layer_fetch": nfl, "layer_write": nwl}}}
+    _merge_traffic(rec)
+    r = rec[LAYER_KEY]
+    print("| quantity | value |\n|---|---|")
+    print(f"| copy kernel (torch.neg, 256 MiB fp16) FETCH_SIZE / dispatch | {f_copy:.0f} KiB (scale {kf:.4f}) |")
+    print(f"| copy kernel WRITE_SIZE / dispatch | {w_copy:.0f} KiB (scale {kw:.4f}) |")
+    print(f"| layer launch FETCH_SIZE / dispatch | {f_l:.0f} KiB -> {fetch_b:,.0f} B |")
+    print(f"| layer launch WRITE_SIZE / dispatch | {w_l:.0f} KiB -> {write_b:,.0f} B |")
+    print(f"| traffic / launch (scaled) | {r['traffic_bytes']:,} B |")
+    print(f"| algorithmic bytes / launch | {LAYER_BYTES:,} B (traffic / algorithmic = "
+          f"{r['traffic_bytes'] / LAYER_BYTES:.3f}) |")
 
 
 DECODE_STEPS = 4
@@ -185,6 +260,10 @@ def summarize_decode(fetch_dir, write_dir):
 if __name__ == "__main__":
     if len(sys.argv) >= 2 and sys.argv[1] == "run":
         run()
+    elif len(sys.argv) >= 2 and sys.argv[1] == "run-layer":
+        run_layer()
+    elif len(sys.argv) == 4 and sys.argv[1] == "summarize-layer":
+        summarize_layer(sys.argv[2], sys.argv[3])
     elif len(sys.argv) >= 2 and sys.argv[1] == "run-decode":
         run_decode()
     elif len(sys.argv) == 4 and sys.argv[1] == "summarize":

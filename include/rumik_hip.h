@@ -109,9 +109,10 @@ int rk_gemv_int4_g128_silu(const void* x, int x_dtype, const uint8_t* q, const u
  * the MLP part of fused.post, gemv(ob, w_o) and gemv(act, w_down) of one layer (engine/rumik_fused.py:100-101,
  * 115-116) when o's input is already at hand (the benchmark's layer-projection workload). Shapes: w_in
  * [n_plain + 2*inter, H], w_o [H, H], w_down [H, inter], int4 g128 (codes, fp16 scale / min) as rk_gemv_int4_g128;
- * H == 2048, inter a multiple of 128 up to 12288, n_plain >= 0 small enough for the grid (RK_ERR_SHAPE otherwise:
- * then run rk_gemv_int4_g128_silu and rk_gemv_int4_g128_pair). x / ob RK_F16 or RK_BF16 (x_dtype), outputs
- * RK_F16 or RK_BF16 (y_dtype); x, ob and the code arrays 16-byte aligned.
+ * H == 2048; inter a multiple of 128 up to 12288 (at most 48 gate / up pairs per block);
+ * n_plain >= 0 with at most 12 rows per block (3072 on 256 CUs); RK_ERR_SHAPE otherwise: then run
+ * rk_gemv_int4_g128_silu and rk_gemv_int4_g128_pair. x / ob RK_F16 or RK_BF16 (x_dtype), outputs RK_F16 or RK_BF16
+ * (y_dtype); x, ob and the code arrays 16-byte aligned, the scale and min arrays 4-byte aligned (RK_ERR_ALIGN).
  * ws: rk_gemv_int4_g128_layer_ws_bytes(inter) bytes, 4-byte aligned, ZEROED before its first use and then kept
  * for this call alone (its words carry per-block launch counters, so hipGraph replays need no reset; one launch
  * at a time per workspace). One block per CU, all resident at once; the grid meets once (act), every wait

@@ -81,11 +81,15 @@ RK_DEV uint32_t ld_coh(const uint32_t* p) {
 RK_DEV uint16_t bits_as(int dt, float v) { return dt == RK_F16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v); }
 RK_DEV float from_bits(int dt, uint16_t b) { return dt == RK_F16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b); }
 
-// one row's share of this lane (chunk `lane` of a K = 2048 row): scale * dot + min * xsum
-RK_DEV float row_part(u4_t w, uint16_t s, uint16_t m, const uint32_t (&xp)[16], float xs, const Int4Masks& km) {
-    const float d = chunk_dot_int4(w, xp, km);
-    return __builtin_fmaf(d, f16_bits_to_f32(s), f16_bits_to_f32(m) * xs);
-}
+// A build option (RK_LAYER_TRACE; off in the product library, where RK_LTR is empty): wall-clock stamps per (block,
+// wave, event) in registers, stored at the end of the launch to the buffer rk_layer_trace_set names
+// ([block][8 waves][8 events] uint64, 100 MHz ticks); rumik-fast_amd/layer_trace.py builds and reads it.
+#ifdef RK_LAYER_TRACE
+__device__ unsigned long long* g_layer_trace;
+#define RK_LTR(i) (T_[i] = wall_clock64())
+#else
+#define RK_LTR(i) ((void)0)
+#endif
 
 // A barrier for LDS traffic only: waits for this wave's LDS operations but not for its outstanding global loads
 // (which __syncthreads would), and keeps the compiler from moving memory accesses across it.
@@ -117,31 +121,42 @@ RK_DEV void load_pairs(const uint32_t* src, uint32_t (&p)[16], float& s) {
     s = __builtin_bit_cast(float, src[16]);
 }
 
-struct RowLoad {
-    u4_t w;
-    uint16_t s, m;
-};
-// row `row`'s chunk `lane` with its scale and min; when !ok, a line of `spare` (a cached 4 KB vector) instead
-RK_DEV void issue_row(const uint8_t* q, const uint16_t* sc, const uint16_t* mn, int row, bool ok, const void* spare,
-                      int lane, RowLoad& r) {
-    const size_t gi = (size_t)row * (kH / 128) + (lane >> 2);
-    const uint16_t* sp = ok ? sc + gi : reinterpret_cast<const uint16_t*>(spare);
-    const uint16_t* mp = ok ? mn + gi : reinterpret_cast<const uint16_t*>(spare);
+// row `row`'s code chunk `lane`; when !ok, a line of `spare` (a cached 4 KB vector) instead
+RK_DEV u4_t issue_row(const uint8_t* q, int row, bool ok, const void* spare, int lane) {
     const u4_t* wp = ok ? reinterpret_cast<const u4_t*>(q + (size_t)row * (kH / 2)) + lane
                         : reinterpret_cast<const u4_t*>(spare) + lane;
-    r.s = *sp;
-    r.m = *mp;
-    r.w = __builtin_nontemporal_load(wp);
+    return __builtin_nontemporal_load(wp);
 }
+
+// one row's share of this lane from its codes and its group's packed scale | min << 16
+RK_DEV float row_part_sm(u4_t w, uint32_t sm, const uint32_t (&xp)[16], float xs, const Int4Masks& km) {
+    const h2_t v = as_h2(sm);
+    return __builtin_fmaf(chunk_dot_int4(w, xp, km), (float)v.x, (float)v.y * xs);
+}
+
+// The block's scales and mins, packed per group as scale | min << 16 in LDS: gate rows, up rows, q/k/v rows and o
+// rows (16 groups each, K = 2048), then the down rows (inter / 128 groups each). Regions in groups.
+constexpr int kTabG = 0;
+constexpr int kTabU = kTabG + kWaves * kPairSlots * 16;
+constexpr int kTabQ = kTabU + kWaves * kPairSlots * 16;
+constexpr int kTabO = kTabQ + 2 * kPlainSlots * 16;
+constexpr int kTabD = kTabO + 2 * kOSlots * 16;
+constexpr int kTabWords = kTabD + kDownRows * (kMaxInter / 128);
+constexpr int kTabIter = (kTabWords / 2 + kThreads - 1) / kThreads;  // group pairs per thread
 
 __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
     __shared__ uint32_t wave_bad[kWaves];          // a down wave whose wait ran out
     __shared__ uint32_t pub[kWaves * kPairSlots];  // this block's act values (bits), by local channel
     __shared__ float red[kDownWaves][kDownRows];   // down partial sums per wave
     __shared__ __align__(16) uint32_t xq[2][64][20];  // x, then the attention output: chunk pairs + sum
+    __shared__ uint32_t tab[kTabWords];                // the block's scales | mins, by region
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int b = blockIdx.x;
+#ifdef RK_LAYER_TRACE
+    uint64_t T_[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+    RK_LTR(0);
     const int nch2 = a.inter >> 5;  // down's 32-column chunks
     const int ng2 = a.inter >> 7;
     uint32_t* status = a.ws;
@@ -158,6 +173,43 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
         load_x_raw(a.x, lane, xc);
         load_x_raw(a.ob, lane, oc);
     }
+    // the block's scale / min rows are contiguous per region: copied as dwords (two groups each)
+    const int npb = max(0, min(a.pb, a.inter - p0)), nq = max(0, min(a.qb, a.n_plain - q0));
+    const int no = max(0, min(a.obr, kH - o0)), nd = max(0, min(a.db, kH - d0));
+    const int cG = npb * 8, cU = cG + npb * 8, cQ = cU + nq * 8, cO = cQ + no * 8, cD = cO + nd * ng2 / 2;
+    uint32_t ts[kTabIter], tm[kTabIter];
+    int tdst[kTabIter];
+#pragma unroll
+    for (int it = 0; it < kTabIter; ++it) {
+        const int i = threadIdx.x + it * kThreads;  // group pair
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(a.x);  // spare (cached) for pairs past the tables
+        const uint32_t* mp = sp;
+        int dst = -1;
+        if (i < cG) {
+            sp = reinterpret_cast<const uint32_t*>(a.s_in + (size_t)(a.n_plain + p0) * 16) + i;
+            mp = reinterpret_cast<const uint32_t*>(a.m_in + (size_t)(a.n_plain + p0) * 16) + i;
+            dst = kTabG + 2 * i;
+        } else if (i < cU) {
+            sp = reinterpret_cast<const uint32_t*>(a.s_in + (size_t)(a.n_plain + a.inter + p0) * 16) + (i - cG);
+            mp = reinterpret_cast<const uint32_t*>(a.m_in + (size_t)(a.n_plain + a.inter + p0) * 16) + (i - cG);
+            dst = kTabU + 2 * (i - cG);
+        } else if (i < cQ) {
+            sp = reinterpret_cast<const uint32_t*>(a.s_in + (size_t)q0 * 16) + (i - cU);
+            mp = reinterpret_cast<const uint32_t*>(a.m_in + (size_t)q0 * 16) + (i - cU);
+            dst = kTabQ + 2 * (i - cU);
+        } else if (i < cO) {
+            sp = reinterpret_cast<const uint32_t*>(a.s_o + (size_t)o0 * 16) + (i - cQ);
+            mp = reinterpret_cast<const uint32_t*>(a.m_o + (size_t)o0 * 16) + (i - cQ);
+            dst = kTabO + 2 * (i - cQ);
+        } else if (i < cD) {
+            sp = reinterpret_cast<const uint32_t*>(a.s_d + (size_t)d0 * ng2) + (i - cO);
+            mp = reinterpret_cast<const uint32_t*>(a.m_d + (size_t)d0 * ng2) + (i - cO);
+            dst = kTabD + 2 * (i - cO);
+        }
+        ts[it] = *sp;
+        tm[it] = *mp;
+        tdst[it] = dst;
+    }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -165,8 +217,6 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
     const Int4Masks km = int4_masks();
     uint32_t step = 0, tag = 0;
     h2_t dq[kDownRows][16];  // down waves: chunk dchunk of the block's down rows, as fp16 pairs
-    uint16_t sd[kDownRows], md[kDownRows];
-    uint32_t smd[kDownRows];  // down scale | min << 16, packed once the loads land
 
     // ---- phase 1. Two wave roles with streams of about equal length, in the order they are consumed:
     //   down waves (0..5):  6 gate / up pair slots (gate, then up), then the 8 down rows' chunk of each lane;
@@ -179,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
         constexpr int kP = kPairSlots;  // pair slots
         constexpr int kGU = 2 * kP;
         constexpr int kUnits = kGU + (kDown ? kDownRows : kPlainSlots + kOSlots);
-        RowLoad rl[kDown ? kGU : kGU + kPlainSlots + kOSlots];
+        u4_t rl[kDown ? kGU : kGU + kPlainSlots + kOSlots];
         u4_t wd[kDownRows];
         const int qw = wave - kDownWaves;  // q/o waves: 0, 1
         // local pair index of slot s: w + 8s (the block's waves read 8 consecutive rows per slot)
@@ -190,26 +240,22 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
             } else if constexpr (k < kGU) {
                 const int pl = pair_of(k >> 1);
                 const bool ok = pl < a.pb && p0 + pl < a.inter;
-                issue_row(a.q_in, a.s_in, a.m_in, a.n_plain + (k & 1) * a.inter + p0 + pl, ok, a.x, lane, rl[k]);
+                rl[k] = issue_row(a.q_in, a.n_plain + (k & 1) * a.inter + p0 + pl, ok, a.x, lane);
             } else if constexpr (kDown) {
                 constexpr int r = k - kGU;
                 const bool ok = r < a.db && d0 + r < kH && dchunk < nch2;
                 const size_t row = ok ? (size_t)(d0 + r) : 0;
-                const uint16_t* sp = ok ? a.s_d + row * ng2 + (dchunk >> 2) : reinterpret_cast<const uint16_t*>(a.x);
-                const uint16_t* mp = ok ? a.m_d + row * ng2 + (dchunk >> 2) : reinterpret_cast<const uint16_t*>(a.x);
                 const u4_t* wp = ok ? reinterpret_cast<const u4_t*>(a.q_d + row * (a.inter >> 1)) + dchunk
                                     : reinterpret_cast<const u4_t*>(a.x) + lane;
-                sd[r] = *sp;
-                md[r] = *mp;
                 wd[r] = __builtin_nontemporal_load(wp);
             } else if constexpr (k < kGU + kPlainSlots) {
                 const int ql = qw + 2 * (k - kGU);
                 const bool ok = ql < a.qb && q0 + ql < a.n_plain;
-                issue_row(a.q_in, a.s_in, a.m_in, q0 + ql, ok, a.x, lane, rl[k]);
+                rl[k] = issue_row(a.q_in, q0 + ql, ok, a.x, lane);
             } else {
                 const int ol = qw + 2 * (k - kGU - kPlainSlots);
                 const bool ok = ol < a.obr && o0 + ol < kH;
-                issue_row(a.q_o, a.s_o, a.m_o, o0 + ol, ok, a.x, lane, rl[k]);
+                rl[k] = issue_row(a.q_o, o0 + ol, ok, a.x, lane);
             }
         };
         static_for<0, kAhead>([&](auto kc) __attribute__((always_inline)) { issue(kc); });
@@ -232,10 +278,17 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
             for (int i = 0; i < 4; ++i) dst[i] = u4_t{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
             xq[1][lane][16] = __builtin_bit_cast(uint32_t, ps);
         }
+#pragma unroll
+        for (int it = 0; it < kTabIter; ++it)
+            if (tdst[it] >= 0) {
+                tab[tdst[it]] = (ts[it] & 0xFFFFu) | (tm[it] << 16);
+                tab[tdst[it] + 1] = (ts[it] >> 16) | (tm[it] & 0xFFFF0000u);
+            }
         lds_barrier();
         uint32_t xp[16];
         float xs;
         load_pairs(xq[0][lane], xp, xs);
+        RK_LTR(1);
 
         // gate / up: slot s of each in vg[s] / vu[s]; after the reductions lanes 8s..8s+7 hold slot s of both
         {
@@ -244,7 +297,9 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
             for (int s = 0; s < 8; ++s) vg[s] = vu[s] = 0.f;
             static_for<0, kGU>([&](auto kc) __attribute__((always_inline)) {
                 constexpr int k = decltype(kc)::value;
-                const float r = row_part(rl[k].w, rl[k].s, rl[k].m, xp, xs, km);
+                const int pl = min(pair_of(k >> 1), kWaves * kPairSlots - 1);
+                const uint32_t sm = tab[((k & 1) ? kTabU : kTabG) + pl * 16 + (lane >> 2)];
+                const float r = row_part_sm(rl[k], sm, xp, xs, km);
                 if constexpr (k & 1) vu[k >> 1] = r; else vg[k >> 1] = r;
                 issue(std::integral_constant<int, k + kAhead>{});
             });
@@ -271,6 +326,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
             }
             if (lane == 0) st_coh(flags + b, tag);
         }
+        RK_LTR(2);
 
         if constexpr (kDown) {
             // the down chunks to fp16 pairs, kept for phase 2
@@ -283,7 +339,6 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) dq[r][4 * i + e] = p[e];
                 }
-                smd[r] = (uint32_t)sd[r] | ((uint32_t)md[r] << 16);
                 issue(std::integral_constant<int, decltype(kc)::value + kAhead>{});
             });
         } else {
@@ -296,8 +351,13 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
             for (int s = 0; s < 16; ++s) v[s] = 0.f;
             static_for<kGU, kUnits>([&](auto kc) __attribute__((always_inline)) {
                 constexpr int k = decltype(kc)::value;
-                if constexpr (k < kGU + kPlainSlots) v[k - kGU] = row_part(rl[k].w, rl[k].s, rl[k].m, xp, xs, km);
-                else v[8 + k - kGU - kPlainSlots] = row_part(rl[k].w, rl[k].s, rl[k].m, op, os, km);
+                if constexpr (k < kGU + kPlainSlots) {
+                    const int ql = qw + 2 * (k - kGU);
+                    v[k - kGU] = row_part_sm(rl[k], tab[kTabQ + ql * 16 + (lane >> 2)], xp, xs, km);
+                } else {
+                    const int ol = qw + 2 * (k - kGU - kPlainSlots);
+                    v[8 + k - kGU - kPlainSlots] = row_part_sm(rl[k], tab[kTabO + ol * 16 + (lane >> 2)], op, os, km);
+                }
                 issue(std::integral_constant<int, k + kAhead>{});
             });
             wave_reduce_rows<16>(v);
@@ -315,6 +375,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
     };
     if (wave < kDownWaves) phase1(std::true_type{});
     else phase1(std::false_type{});
+    RK_LTR(3);
 
     // ---- phase 2 on the down waves, while the q/o waves finish their streams: take act chunk t (32 tagged words,
     // one per channel) into registers in dot order, and compute chunk t of the block's down rows (v_dot2, fp32
@@ -329,6 +390,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
         const bool mine = dchunk < nch2;
         const int cc = min(dchunk, nch2 - 1);
         uint32_t wv[32];
+        RK_LTR(4);
         while (true) {
 #pragma unroll
             for (int i = 0; i < 32; ++i) wv[i] = ld_coh(xw + (size_t)i * nch2 + cc);
@@ -353,6 +415,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
                 break;
             }
         }
+        RK_LTR(5);
         if (!bad) {
             XChunk ac;
 #pragma unroll
@@ -374,7 +437,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
                     a0 = dot2(dq[r][4 * i + 2], as_h2(ap[4 * i + 2]), a0);
                     a1 = dot2(dq[r][4 * i + 3], as_h2(ap[4 * i + 3]), a1);
                 }
-                const h2_t sm = as_h2(smd[r]);
+                const h2_t sm = as_h2(tab[kTabD + r * ng2 + (cc >> 2)]);
                 const float v = __builtin_fmaf(a0 + a1, (float)sm.x, (float)sm.y * as);
                 acc[r] = mine ? v : 0.f;
             }
@@ -382,6 +445,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
             if ((lane & 7) == 0) red[wave][lane >> 3] = acc[0];
         }
         if (lane == 0) wave_bad[wave] = bad ? 1u : 0u;
+        RK_LTR(6);
     }
     __syncthreads();
     if (wave == 0 && lane < kDownRows) {
@@ -396,6 +460,11 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
         const int row = d0 + lane;
         if (!any_bad && lane < a.db && row < kH) store_act(a.y_down, a.ydt, (size_t)row, v);
     }
+    RK_LTR(7);
+#ifdef RK_LAYER_TRACE
+    if (g_layer_trace && lane == 0)
+        for (int i = 0; i < 8; ++i) g_layer_trace[((size_t)b * kWaves + wave) * 8 + i] = T_[i];
+#endif
     if (threadIdx.x == 0) st_coh(ctr + b, step + 1u);
 }
 
@@ -437,7 +506,9 @@ extern "C" int rk_gemv_int4_g128_layer(const void* x, const void* ob, int x_dtyp
     if (H != kH || n_plain < 0 || inter <= 0 || inter % 128 || inter > kMaxInter) return RK_ERR_SHAPE;
     if (ws_bytes < rk_gemv_int4_g128_layer_ws_bytes(inter)) return RK_ERR_SHAPE;
     if (((uintptr_t)x & 15) || ((uintptr_t)ob & 15) || ((uintptr_t)q_in & 15) || ((uintptr_t)q_o & 15) ||
-        ((uintptr_t)q_down & 15) || ((uintptr_t)ws & 3) || ((uintptr_t)act & 1))
+        ((uintptr_t)q_down & 15) || ((uintptr_t)ws & 3) || ((uintptr_t)act & 1) || ((uintptr_t)s_in & 3) ||
+        ((uintptr_t)m_in & 3) || ((uintptr_t)s_o & 3) || ((uintptr_t)m_o & 3) || ((uintptr_t)s_down & 3) ||
+        ((uintptr_t)m_down & 3))
         return RK_ERR_ALIGN;
     const int nb = layer_blocks();
     if (nb <= 0 || nb > kMaxBlocks) return RK_ERR_BLOCK;
@@ -459,3 +530,10 @@ extern "C" int rk_gemv_int4_g128_layer(const void* x, const void* ob, int x_dtyp
     hipLaunchKernelGGL(gemv_layer_kernel, dim3(nb), dim3(kThreads), kLdsBytes, (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
+
+#ifdef RK_LAYER_TRACE
+// trace builds only: the stamp buffer ([blocks][8][8] uint64, or NULL)
+extern "C" __attribute__((visibility("default"))) int rk_layer_trace_set(unsigned long long* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_layer_trace), &buf, sizeof(buf)) == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+#endif

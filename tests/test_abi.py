@@ -111,14 +111,14 @@ def test_layer_projections_validate_before_launch():
     buf, odd = ctypes.c_void_p(256), ctypes.c_void_p(258)
     nws = lib.rk_gemv_int4_g128_layer_ws_bytes(11008)
 
-    def call(x=buf, ws=buf, xdt=HL.F16, ydt=HL.F16, n_plain=3072, inter=11008, hid=2048, nbytes=nws, q=buf):
-        return lib.rk_gemv_int4_g128_layer(x, buf, xdt, q, buf, buf, buf, buf, buf, buf, buf, buf, buf, buf, buf,
+    def call(x=buf, ws=buf, xdt=HL.F16, ydt=HL.F16, n_plain=3072, inter=11008, hid=2048, nbytes=nws, q=buf, sc=buf):
+        return lib.rk_gemv_int4_g128_layer(x, buf, xdt, q, sc, buf, buf, buf, buf, buf, buf, buf, buf, buf, buf,
                                            buf, ydt, n_plain, inter, hid, ws, nbytes, None)
     assert call(x=None) == -4 and call(ws=None) == -4
     assert call(xdt=HL.F32) == -3 and call(ydt=HL.F32) == -3
     assert call(hid=4096) == -1 and call(inter=11008 + 64) == -1 and call(inter=12416) == -1
     assert call(n_plain=-1) == -1 and call(nbytes=nws - 4) == -1
-    assert call(q=odd) == -5
+    assert call(q=odd) == -5 and call(sc=odd) == -5  # codes 16-byte, scales / mins 4-byte aligned
 
 
 def test_decode_step_validates_before_launch():

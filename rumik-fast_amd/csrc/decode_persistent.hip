@@ -714,8 +714,8 @@ RK_DEV void down_compute(const Params& p, uint32_t tag, const Work& wk, const Do
 
 // ---------------------------------------------------------------------------------------------- attention
 // slots per attention split: n / nsp rounded up to 8, at least kMinChunk (short contexts use fewer, fuller splits,
-// so the combine waits on fewer blocks)
-constexpr int kMinChunk = 16;
+// so the combine waits on fewer blocks; a full split, 32 slots, measured best at ctx 256 / 1024 / 2048)
+constexpr int kMinChunk = kAW * kSlotsPerWave;
 RK_DEV int split_chunk(int n, int nsp) { return max(kMinChunk, ((n + nsp - 1) / nsp + 7) & ~7); }
 
 struct Split {

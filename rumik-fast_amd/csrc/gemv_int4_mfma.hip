@@ -339,13 +339,17 @@ hipError_t launch_mfma(const void* x, int xdt, const uint8_t* q, const uint16_t*
 }  // namespace
 
 // KS (waves per 16-row tile) and teams (tiles per block) for one call; blocks are 4 waves (KS * teams = 4, or
-// the caller's `waves` when that is smaller). Default KS: enough waves for about two per SIMD of the 256 CUs
-// (tiles * KS >= 2048), at most one group per wave.
+// the caller's `waves` when that is smaller). Default KS: the largest that leaves every wave at least 6 of the
+// row's 128-column groups. Measured (16 rotated copies, hipGraph): 6-8 groups per wave (one load batch of kGB) are
+// the fast range; 4 per wave and 16 or more per wave are both slow -- N = 8192 K = 2048 8.8 us with 4 per wave,
+// 3.9 with 8; N = 32768 K = 2048 19.4 us with 16, 8.7 with 8; N = 16384 K = 4096 10.9 with 16, 8.8 with 8;
+// N = 8192 K = 3072 7.7 with 6, 8.6 with 12; N = 22016 / 25088 K = 2048 (8 per wave) unchanged.
 static void plan_mfma(int tiles, int K, int waves, int* ks_out, int* teams_out) {
+    (void)tiles;
     const int NG = K / 128;
     const int w = waves ? waves : 4;
     int ks = 1;
-    while (ks < w && ks * 2 <= NG && tiles * ks < 2048) ks *= 2;
+    while (ks < w && ks * 2 <= NG && NG / (ks * 2) >= 6) ks *= 2;
     *ks_out = ks;
     *teams_out = w / ks;
 }

@@ -65,6 +65,14 @@ def test_config_shapes(N, K, seed, path, dev):
     print(f"{path} N={N} K={K}: {rep}")
 
 
+@pytest.mark.parametrize("N,K,seed", [(32768, 2048, 21), (8192, 3072, 22), (16384, 1024, 23), (8200, 4096, 24)])
+def test_large_n_split_plans(N, K, seed, dev):
+    """Large-N shapes of the matrix-core path, one per split of K over a tile's waves (2 waves at K = 2048, 4 at
+    3072 / 4096, 1 at 1024; N = 8200 also leaves a partial last tile), through the default entry."""
+    y, ref = _run(N, K, seed, dev)
+    _assert_parity(y, ref, f"N={N} K={K}")
+
+
 @pytest.mark.parametrize("path", ["default", "mfma", "valu"])
 @pytest.mark.parametrize("N,K", [(1, 128), (3, 256), (17, 384), (1001, 2048), (63, 4096), (5, 11008), (7, 32768),
                                  (40, 1152), (33, 65536)])

@@ -151,8 +151,10 @@ int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const
  * workspace only, RK_MM_PREP128 / RK_MM_PREP64 / RK_MM_PREP48 (X prepared once into the workspace in matrix-core
  * fragment order, then blocks of 128 / 64 / 48 rows x 128 columns fed by direct memory-to-LDS copies; chosen when
  * the shape has enough column blocks to fill the chip, K is short enough for a block's scale and min rows to sit
- * in LDS, and N * K / 128 is a multiple of 8); *splits = the number of K splits (1 = none; > 1 only with a
- * workspace). Host-only query, no GPU needed; RK_ERR_SHAPE for sizes rk_mm_int4_g128 rejects. Part of the
+ * in LDS, and N * K / 128 is a multiple of 8), or, for M <= 48 and K <= 2048 (with or without a workspace),
+ * RK_MM_STREAM (X held in registers as matrix-core fragments for the whole launch while 16-column tiles of codes
+ * stream past, one block per CU, no workspace);
+ * *splits = the number of K splits (1 = none; > 1 only with a workspace). Host-only query, no GPU needed; RK_ERR_SHAPE for sizes rk_mm_int4_g128 rejects. Part of the
  * mm_int4 drop-in (reference kernels/mm_int4.py:59-73 picks its Triton tile from BM / BN); the reference has no
  * plan query. */
 #define RK_MM_REGS 0
@@ -161,6 +163,7 @@ int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const
 #define RK_MM_PREP128 3
 #define RK_MM_PREP64 4
 #define RK_MM_PREP48 5
+#define RK_MM_STREAM 6
 int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits);
 
 /* Bytes of workspace rk_mm_int4_g128_ws uses for this shape (0: it needs none). Shapes whose output tiles alone

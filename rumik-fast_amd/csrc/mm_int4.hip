@@ -617,6 +617,270 @@ RK_PREP_INST(4)
 RK_PREP_INST(8)
 #undef RK_PREP_INST
 
+// ---------------------------------------------------------------------------------------------- small-M stream
+// For M <= 16 MT rows (MT <= 3) and K <= 2048 X is small enough to stay in registers: a block of eight waves holds X
+// as MFMA A fragments for the whole launch, wave w owning <= 2 of the <= 16 groups, and
+// streams 16-column tiles of codes past them (D tiles of codes in flight per wave: all of a block's tiles when it
+// has <= 8). Per tile a wave dequantises
+// its groups' codes once (16 bytes per lane per group: column j = lane % 16, bytes 16 s .. 16 s + 15 of the group,
+// s = lane / 16, as in the tile kernels), runs 4 MT MFMAs per group and applies the group's scale in fp32; the
+// eight waves' sums meet in LDS (two buffers, one barrier per tile), wave mt < MT adds them in wave order together
+// with the tile's min term (sum over groups of rowsum * min, fp32 MFMAs) into the block's output stage, and the
+// block stores its tiles at the end as 16-byte row pieces. Weights are read exactly once; X once per block.
+// The tile loop has no conditional memory instruction: every step issues the same two code loads (clamped to the
+// block's last tile; the surplus re-reads hit the L2) and computes (steps past the block's tiles compute on the
+// clamped codes and are never stored), and the global stores come after the loop. The compiler's vmcnt waits
+// then stay exact; a conditional load or store in the loop makes it wait for everything in flight.
+constexpr int kStreamWaves = 8;
+constexpr int kStreamMaxGroups = 16;  // K <= 2048: two groups per wave
+constexpr int kStreamBlocks = 256;    // one block per CU
+constexpr int kStreamTab = 4;         // scale / min table entries copied per thread (tables <= 2048 entries)
+
+// A build option (RK_STREAM_TRACE; off in the product library, where RK_STR is empty): wall-clock stamps per (block,
+// wave, event) in scalar registers, stored at the end of the launch to the buffer rk_stream_trace_set names
+// ([block][8 waves][16 events] uint64, 100 MHz ticks); rumik-fast_amd/mm_stream_trace.py builds and reads it.
+// Events: 0 start, 1 prologue loads issued, 2 X fragments and row sums done, 3 tables in LDS (barrier passed),
+// 4 / 5 tile 0 computed / reduced (its barrier passed), 6 / 7 tile 1, 8 / 9 the block's last tile, 10 loop done,
+// 11 stores issued, 12 stores complete.
+#ifdef RK_STREAM_TRACE
+__device__ unsigned long long* g_stream_trace;
+#define RK_STR(i) (T_[i] = wall_clock64())
+#else
+#define RK_STR(i) ((void)0)
+#endif
+
+template <int MT>
+constexpr size_t stream_red_bytes() { return (size_t)2 * kStreamWaves * MT * 64 * sizeof(f4_t); }
+constexpr size_t kStreamXsBytes = (size_t)kStreamMaxGroups * 64 * sizeof(float);  // row sums [group][row]
+
+// grid, prefetch depth and LDS sizes of one shape (K <= 2048): NT tiles per block, D tiles in flight
+struct StreamShape {
+    int BPC, D, NT, NG;
+};
+inline StreamShape stream_shape(int N, int K) {
+    const int T = (N + 15) / 16;
+    const int NT = (T + kStreamBlocks - 1) / kStreamBlocks;
+    // every code tile of a block in flight from the start when it has <= 8 (depths 1 2 3 4 6 8 are built)
+    const int D = NT <= 4 ? NT : NT <= 6 ? 6 : NT <= 8 ? 8 : 4;
+    return {(T + NT - 1) / NT, D, NT, K / 128};
+}
+template <int MT>
+size_t mm_stream_lds_bytes(const StreamShape& sh) {
+    return stream_red_bytes<MT>() + kStreamXsBytes + (size_t)sh.NT * MT * 64 * sizeof(f4_t) +
+           (size_t)2 * 16 * sh.NT * sh.NG * 2;
+}
+
+// Block b: tiles b NT .. b NT + NT - 1 (fewer in the last block) of the T = ceil(N / 16) column tiles.
+template <int MT, int D, bool BF16>
+__global__ __launch_bounds__(512) void mm_int4_stream_kernel(const uint16_t* __restrict__ X, int ldx,
+                                                             const uint8_t* __restrict__ q,
+                                                             const uint16_t* __restrict__ sc,
+                                                             const uint16_t* __restrict__ mn, void* __restrict__ Y,
+                                                             int ydt, int ldy, int M, int N, int K, int NT) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    f4_t* red = reinterpret_cast<f4_t*>(smem);                                       // [2][8][MT][64]
+    float* xsl = reinterpret_cast<float*>(smem + stream_red_bytes<MT>());            // [16][64]
+    f4_t* outb = reinterpret_cast<f4_t*>(smem + stream_red_bytes<MT>() + kStreamXsBytes);  // [NT][MT][64]
+    uint16_t* tsc = reinterpret_cast<uint16_t*>(outb + (size_t)NT * MT * 64);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int jn = lane & 15, sq = lane >> 4;
+    const int NG = K >> 7, T = (N + 15) >> 4, KB = K >> 1;
+    const int b = blockIdx.x, ngc = NG;
+    const int t0 = b * NT, ntl = min(NT, T - t0);
+    const int wl0 = wave * ngc / kStreamWaves, GW = (wave + 1) * ngc / kStreamWaves - wl0;  // 0, 1 or 2 groups
+    const int wg0 = wl0;
+    const int rows = min(16 * ntl, N - 16 * t0);                                    // the block's weight rows
+    uint16_t* tmn = tsc + rows * ngc;
+#ifdef RK_STREAM_TRACE
+    uint64_t T_[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+    RK_STR(0);
+
+    // codes of tile i (clamped to the block's last tile); both group slots are always loaded (a wave with fewer
+    // groups re-reads its first)
+    const int g1 = GW > 1 ? 64 : 0;
+    const uint8_t* qb = q + 64 * min(wg0, NG - 1) + 16 * sq;
+    auto issue = [&](int i, u4_t (&w)[2]) {
+        const int n = min(16 * (t0 + min(i, ntl - 1)) + jn, N - 1);
+        const uint8_t* src = qb + (size_t)n * KB;
+        w[0] = *reinterpret_cast<const u4_t*>(src);
+        w[1] = *reinterpret_cast<const u4_t*>(src + g1);
+    };
+    // the block's scale / min rows: kStreamTab entries per thread and table (issued before
+    // X: they come from HBM, X mostly from the L2)
+    uint16_t tv[2][kStreamTab];
+#pragma unroll
+    for (int k = 0; k < kStreamTab; ++k) {
+        const int p = min(tid + 512 * k, rows * ngc - 1);
+        const int r = p / ngc, gi = p - r * ngc;
+        const size_t o = (size_t)(16 * t0 + r) * NG + gi;
+        tv[0][k] = sc[o];
+        tv[1][k] = mn[o];
+    }
+    // X of the wave's groups, raw; lanes of rows past M and waves' absent groups load nothing (zeros)
+    u4_t xr[2][MT][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xr[i][mt][t] = u4_t{0u, 0u, 0u, 0u};
+            if (i < GW && 16 * mt + jn < M) {
+                const u4_t* src = reinterpret_cast<const u4_t*>(X + (size_t)(16 * mt + jn) * ldx + 128 * (wg0 + i) + 32 * sq);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xr[i][mt][t] = src[t];
+            }
+        }
+    // then the first D tiles' codes (issued after X, so that waiting for X does not wait for them)
+    u4_t wq[D][2];
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, wq[d]);
+    RK_STR(1);
+
+    // X fragments, and the rows' sums per group on the matrix cores (X against an all-ones B: exact fp16 products,
+    // fp32 sums, in the accumulator layout: lane l holds rows 4 (l / 16) + e) into xsl[local group][row]
+    h8_t xf[2][MT][4];
+    const h8_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
+                       (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            f4_t rs = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                xf[i][mt][t] = afrag(xr[i][mt][t], BF16 ? RK_BF16 : RK_F16);
+                rs = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[i][mt][t], ones, rs, 0, 0, 0);
+            }
+            if (i < GW && jn == 0) *reinterpret_cast<f4_t*>(&xsl[(wl0 + i) * 64 + 16 * mt + 4 * sq]) = rs;
+        }
+    }
+    RK_STR(2);
+#pragma unroll
+    for (int k = 0; k < kStreamTab; ++k) {
+        const int p = tid + 512 * k;
+        if (p < rows * ngc) {
+            tsc[p] = tv[0][k];
+            tmn[p] = tv[1][k];
+        }
+    }
+    __syncthreads();  // tables and row sums in LDS
+    RK_STR(3);
+    // the min term sum_g xs[m][g] min[n][g] of m tile `wave` is added by that wave at the reduction, on the matrix
+    // cores in fp32 (v_mfma_f32_16x16x4f32, four groups per instruction: A lane l = xs[row l % 16][group 4 q +
+    // l / 16], B lane l = min[column l % 16][group 4 q + l / 16], zero past the last group)
+    float xsa[4];
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+        const int gl = 4 * qq + sq;
+        xsa[qq] = (wave < MT && gl < ngc) ? xsl[gl * 64 + 16 * min(wave, MT - 1) + jn] : 0.f;
+    }
+
+    const DqConsts kc = {opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u)};
+    const int steps = (ntl + D - 1) / D * D;  // the last D-step may run up to D - 1 clamped, unstored tiles
+    for (int base = 0; base < steps; base += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int i = base + d;
+            f4_t acc[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
+            const int r = min(16 * i + jn, rows - 1);  // this lane's weight row (column of Y) within the block
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                if (gi >= GW) break;
+                f4_t c[MT];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const h8_t Wf = dequant8(wq[d][gi][t], kc);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        c[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[gi][mt][t], Wf,
+                                                                     t == 0 ? f4_t{0.f, 0.f, 0.f, 0.f} : c[mt], 0, 0, 0);
+                }
+                const float scl = f16_bits_to_f32(tsc[r * ngc + wl0 + gi]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[mt][e] = __builtin_fmaf(c[mt][e], scl, acc[mt][e]);
+            }
+            issue(i + D, wq[d]);
+#ifdef RK_STREAM_TRACE
+            if (i == 0) RK_STR(4);
+            if (i == 1) RK_STR(6);
+            if (i == ntl - 1) RK_STR(8);
+#endif
+            f4_t* rb = red + (size_t)(i & 1) * kStreamWaves * MT * 64;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) rb[(wave * MT + mt) * 64 + lane] = acc[mt];
+            __syncthreads();
+#ifdef RK_STREAM_TRACE
+            if (i == 0) RK_STR(5);
+            if (i == 1) RK_STR(7);
+            if (i == ntl - 1) RK_STR(9);
+#endif
+            if (wave < MT && i < ntl) {  // 64 MT threads: (m tile = wave, lane), the waves' sums in wave order
+                f4_t v = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    const int gl = 4 * qq + sq;
+                    const float mnv = gl < ngc ? f16_bits_to_f32(tmn[r * ngc + gl]) : 0.f;
+                    v = __builtin_amdgcn_mfma_f32_16x16x4f32(xsa[qq], mnv, v, 0, 0, 0);
+                }
+#pragma unroll
+                for (int w = 0; w < kStreamWaves; ++w) {
+                    const f4_t u = rb[(w * MT + wave) * 64 + lane];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] += u[e];
+                }
+                outb[(i * MT + wave) * 64 + lane] = v;
+            }
+        }
+    }
+    __syncthreads();
+    RK_STR(10);
+    // the block's tiles as 8-column row pieces: piece (row m, tile i, half h) = Y[m][16 (t0 + i) + 8 h .. + 7];
+    // outb[i][mt][lane l][e] holds Y row 16 mt + 4 (l / 16) + e, column 16 (t0 + i) + l % 16
+    const bool vec_ok = (((uintptr_t)Y | (size_t)ldy * (ydt == RK_F32 ? 4 : 2)) & (ydt == RK_F32 ? 15 : 7)) == 0;
+    for (int it = tid; it < M * ntl * 2; it += 512) {
+        const int m = it / (ntl * 2), rest = it - m * ntl * 2, i = rest >> 1, h = rest & 1;
+        const int mt = m >> 4, sqm = (m >> 2) & 3, e = m & 3;
+        const float* src = reinterpret_cast<const float*>(outb + (size_t)(i * MT + mt) * 64 + 16 * sqm + 8 * h) + e;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = src[4 * j];
+        const int n = 16 * (t0 + i) + 8 * h;
+        if (n >= N) continue;
+        const size_t o = (size_t)m * ldy + n;
+        if (n + 7 < N && vec_ok) {
+            if (ydt == RK_F32) {
+                *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(Y) + o) = f4_t{v[0], v[1], v[2], v[3]};
+                *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(Y) + o + 4) = f4_t{v[4], v[5], v[6], v[7]};
+            } else if (ydt == RK_F16) {
+                const h8_t hv = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3],
+                                 (_Float16)v[4], (_Float16)v[5], (_Float16)v[6], (_Float16)v[7]};
+                *reinterpret_cast<h8_t*>(reinterpret_cast<uint16_t*>(Y) + o) = hv;
+            } else {
+                u4_t bv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    bv[j] = (uint32_t)f32_to_bf16_bits(v[2 * j]) | ((uint32_t)f32_to_bf16_bits(v[2 * j + 1]) << 16);
+                *reinterpret_cast<u4_t*>(reinterpret_cast<uint16_t*>(Y) + o) = bv;
+            }
+        } else {
+            for (int j = 0; j < 8 && n + j < N; ++j) store_act(Y, ydt, o + j, v[j]);
+        }
+    }
+#ifdef RK_STREAM_TRACE
+    RK_STR(11);
+    __builtin_amdgcn_s_waitcnt(0);
+    RK_STR(12);
+    if (g_stream_trace && lane == 0)
+        for (int k = 0; k < 16; ++k) g_stream_trace[((size_t)b * kStreamWaves + wave) * 16 + k] = T_[k];
+#endif
+}
+
 // workspace of the prepared-X plan: Xp (Mp K fp16) then xs (NG Mp fp32)
 inline size_t mm_prep_ws_bytes(int M, int K) {
     const size_t Mp = (size_t)(M + 15) / 16 * 16;
@@ -650,6 +914,41 @@ __global__ __launch_bounds__(256) void mm_splitk_reduce(const float* __restrict_
     float v = 0.f;
     for (int k = 0; k < splits; ++k) v += part[k * MN + i];
     store_act(Y, ydt, (i / N) * ldy + i % N, v);
+}
+
+template <int MT, int D>
+hipError_t launch_mm_stream_md(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s,
+                               const uint16_t* m, void* Y, int ydt, int ldy, int M, int N, int K, hipStream_t st) {
+    const StreamShape sh = stream_shape(N, K);
+    const size_t lds = mm_stream_lds_bytes<MT>(sh);
+    const uint16_t* x = static_cast<const uint16_t*>(X);
+    if (xdt == RK_BF16)
+        hipLaunchKernelGGL((mm_int4_stream_kernel<MT, D, true>), dim3(sh.BPC), dim3(512), lds, st, x, ldx, q, s, m,
+                           Y, ydt, ldy, M, N, K, sh.NT);
+    else
+        hipLaunchKernelGGL((mm_int4_stream_kernel<MT, D, false>), dim3(sh.BPC), dim3(512), lds, st, x, ldx, q, s, m,
+                           Y, ydt, ldy, M, N, K, sh.NT);
+    return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_mm_stream_mt(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s,
+                               const uint16_t* m, void* Y, int ydt, int ldy, int M, int N, int K, hipStream_t st) {
+    switch (stream_shape(N, K).D) {
+        case 1: return launch_mm_stream_md<MT, 1>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+        case 2: return launch_mm_stream_md<MT, 2>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+        case 3: return launch_mm_stream_md<MT, 3>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+        case 4: return launch_mm_stream_md<MT, 4>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+        case 6: return launch_mm_stream_md<MT, 6>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+        default: return launch_mm_stream_md<MT, 8>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+    }
+}
+
+hipError_t launch_mm_stream(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s, const uint16_t* m,
+                            void* Y, int ydt, int ldy, int M, int N, int K, hipStream_t st) {
+    if (M <= 16) return launch_mm_stream_mt<1>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+    if (M <= 32) return launch_mm_stream_mt<2>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
+    return launch_mm_stream_mt<3>(X, xdt, ldx, q, s, m, Y, ydt, ldy, M, N, K, st);
 }
 
 template <int WM, int WN>
@@ -707,8 +1006,22 @@ struct MmPlan {
 enum MmMode { kMmPlain = 0, kMmWorkspace = 1, kMmScratch = 2 };  // rk_mm_int4_g128, _ws, _noalloc
 constexpr long kPrepMinBlocks = 160;  // measured: below this the tile kernels' extra blocks win
 
+// M <= 48 and K <= 2048: the stream kernel (cfg 6) when its tables fit in LDS. Longer K was measured split into
+// chunks of 16 groups with fp32 partial sums: slower than the tile kernels' split over K (M = 34, 2048 x 11008:
+// 17.0 us against 15.3), so those shapes keep the tile plans.
+MmPlan mm_stream_plan(int M, int N, int K, int mode) {
+    if (M > 48 || K > 128 * kStreamMaxGroups) return {-1, 0, 0};
+    const StreamShape sh = stream_shape(N, K);
+    const size_t lds = M <= 16 ? mm_stream_lds_bytes<1>(sh) : M <= 32 ? mm_stream_lds_bytes<2>(sh) : mm_stream_lds_bytes<3>(sh);
+    if (lds > kLdsMax || 16L * sh.NT * sh.NG > 512L * kStreamTab) return {-1, 0, 0};
+    (void)mode;  // no workspace: the same plan for every entry
+    return {6, 1, 0};
+}
+
 MmPlan mm_plan(int M, int N, int K, int mode) {
     const int NG = K / 128;
+    const MmPlan sp = mm_stream_plan(M, N, K, mode);
+    if (sp.cfg == 6) return sp;
     if (mode == kMmWorkspace && ((long)N * NG) % 8 == 0) {
         const int mt = M <= 48 ? 3 : M <= 64 ? 4 : 8;
         const long Mp = (M + 15) / 16 * 16;
@@ -751,6 +1064,8 @@ int mm_run(const MmPlan& p, const void* X, int x_dtype, int ldx, const uint8_t* 
         e = launch_mm_prep<4>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
     else if (p.cfg == 5)
         e = launch_mm_prep<3>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
+    else if (p.cfg == 6)
+        e = launch_mm_stream(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     else
         e = launch_mm<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
@@ -798,7 +1113,8 @@ extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_
 extern "C" int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
     const MmPlan p = mm_plan(M, N, K, use_workspace != 0 ? kMmWorkspace : kMmPlain);
-    static const int kCode[6] = {RK_MM_REGS, RK_MM_TILE128, RK_MM_TILE64, RK_MM_PREP128, RK_MM_PREP64, RK_MM_PREP48};
+    static const int kCode[7] = {RK_MM_REGS,    RK_MM_TILE128, RK_MM_TILE64, RK_MM_PREP128,
+                                 RK_MM_PREP64, RK_MM_PREP48,  RK_MM_STREAM};
     if (kernel) *kernel = kCode[p.cfg];
     if (splits) *splits = p.splits;
     return RK_OK;
@@ -817,7 +1133,7 @@ extern "C" int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uin
     MmPlan p = mm_plan(M, N, K, kMmWorkspace);
     // the prepared-X kernel copies the scale / min rows in 16-byte pieces; other arrays take the tile plan, which
     // needs no more workspace (shapes with that many column blocks are not split over K)
-    if (p.cfg >= 3 && (((uintptr_t)scale | (uintptr_t)min) & 15)) p = mm_plan(M, N, K, kMmScratch);
+    if (p.cfg >= 3 && p.cfg <= 5 && (((uintptr_t)scale | (uintptr_t)min) & 15)) p = mm_plan(M, N, K, kMmScratch);
     if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) return RK_ERR_SHAPE;
     if (p.ws > 0 && ((uintptr_t)workspace & 15)) return RK_ERR_ALIGN;
     return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, workspace,
@@ -842,3 +1158,10 @@ extern "C" int rk_mm_int4_g128_noalloc(const void* X, int x_dtype, int ldx, cons
     return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, part,
                   reinterpret_cast<hipStream_t>(stream));
 }
+
+#ifdef RK_STREAM_TRACE
+// trace builds only: the stamp buffer of the stream kernel ([blocks][8][16] uint64, or NULL)
+extern "C" __attribute__((visibility("default"))) int rk_stream_trace_set(unsigned long long* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_stream_trace), &buf, sizeof(buf)) == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+#endif

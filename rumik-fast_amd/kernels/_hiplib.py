@@ -76,7 +76,7 @@ def lib():
     return _lib
 
 
-MM_REGS, MM_TILE128, MM_TILE64, MM_PREP128, MM_PREP64, MM_PREP48 = 0, 1, 2, 3, 4, 5
+MM_REGS, MM_TILE128, MM_TILE64, MM_PREP128, MM_PREP64, MM_PREP48, MM_STREAM = 0, 1, 2, 3, 4, 5, 6
 MM_PREP = (MM_PREP128, MM_PREP64, MM_PREP48)
 MM_SCRATCH_BYTES = 8 << 20  # RK_MM_SCRATCH_BYTES: the fixed split-K scratch of rk_mm_int4_g128_noalloc
 # status codes (RK_OK and RK_ERR_* of the header)

@@ -20,11 +20,11 @@ import torch  # noqa: E402
 import _hiplib as H  # noqa: E402
 import synth  # noqa: E402
 
-SHAPES = ((34, 3072, 2048), (34, 22016, 2048), (34, 2048, 11008), (128, 3072, 2048), (128, 22016, 2048),
+SHAPES = ((16, 22016, 2048), (48, 22016, 2048), (34, 25088, 2048), (34, 3072, 2048), (34, 22016, 2048), (34, 2048, 11008), (128, 3072, 2048), (128, 22016, 2048),
           (128, 2048, 11008), (512, 3072, 2048), (512, 22016, 2048), (512, 2048, 11008), (69, 25088, 2048),
           (201, 25088, 2048), (512, 25088, 2048))
 NAMES = {H.MM_REGS: "regs", H.MM_TILE128: "tile128", H.MM_TILE64: "tile64", H.MM_PREP128: "prep128",
-         H.MM_PREP64: "prep64", H.MM_PREP48: "prep48"}
+         H.MM_PREP64: "prep64", H.MM_PREP48: "prep48", H.MM_STREAM: "stream"}
 
 
 def _best_us(fn, reps, stream):

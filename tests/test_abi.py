@@ -51,13 +51,15 @@ def test_version_and_status_strings():
     assert "misaligned" in lib.rk_status_string(-5).decode()
 
 
-@pytest.mark.parametrize("M,N,K,splits", [(34, 2048, 11008, 8), (34, 3072, 2048, 4), (128, 2048, 11008, 4),
+@pytest.mark.parametrize("M,N,K,splits", [(34, 2048, 11008, 8), (34, 3072, 2048, 1), (128, 2048, 11008, 4),
                                           (200, 33, 11008, 21), (34, 22016, 2048, 1), (512, 2048, 11008, 1),
-                                          (512, 22016, 2048, 1), (4, 32, 256, 1)])
+                                          (512, 22016, 2048, 1), (4, 32, 256, 1), (64, 2048, 11008, 8),
+                                          (5, 200, 4096, 8)])
 def test_mm_int4_split_k_plan(M, N, K, splits):
     """fp32 partials only where 64 x 64 output tiles leave CUs idle: splits = min(ceil(256 / tiles), groups / 4);
-    shapes on the prepared-X kernel hold the prepared X instead"""
+    shapes on the prepared-X kernel hold the prepared X instead, and the stream kernel (M <= 48, K <= 2048) none"""
     nbytes = HL.lib().rk_mm_int4_workspace_bytes(M, N, K)
+    assert HL.mm_plan(M, N, K)[1] == (splits if HL.mm_plan(M, N, K)[0] not in HL.MM_PREP else 1)
     if HL.mm_plan(M, N, K)[0] in HL.MM_PREP:
         Mp = (M + 15) // 16 * 16
         assert splits == 1 and nbytes == Mp * K * 2 + (K // 128) * Mp * 4
@@ -170,23 +172,29 @@ def test_sampler_entry_points_validate_before_any_device_work():
 
 
 @pytest.mark.parametrize("M,N,K,kernel", [(512, 22016, 2048, HL.MM_PREP128), (201, 25088, 2048, HL.MM_PREP128),
-                                          (69, 25088, 2048, HL.MM_PREP128), (34, 22016, 2048, HL.MM_PREP48),
+                                          (69, 25088, 2048, HL.MM_PREP128), (34, 22016, 2048, HL.MM_STREAM),
                                           (64, 22016, 4096, HL.MM_PREP64), (128, 22016, 2048, HL.MM_PREP128),
                                           (512, 3072, 2048, HL.MM_TILE64), (512, 2048, 11008, HL.MM_TILE64),
-                                          (34, 3072, 2048, HL.MM_TILE64), (34, 22017, 128, HL.MM_TILE64)])
+                                          (34, 3072, 2048, HL.MM_STREAM), (34, 22017, 128, HL.MM_STREAM),
+                                          (34, 2048, 11008, HL.MM_TILE64), (48, 20480, 2048, HL.MM_STREAM),
+                                          (49, 20480, 2048, HL.MM_PREP64), (40, 65536, 2048, HL.MM_PREP48),
+                                          (50, 2048, 11008, HL.MM_TILE64)])
 def test_mm_int4_workspace_plan(M, N, K, kernel):
-    """With a workspace, shapes with >= 160 column blocks of 128 take the prepared-X kernel (48 / 64 / 128-row
-    blocks by M); too few blocks, K too long for the block's scale tables, or N * K / 128 not a multiple of 8 keep
-    the tile plan."""
+    """With a workspace, M <= 48 at K <= 2048 takes the stream kernel unless a block's scale / min tables would
+    exceed 2048 entries (very wide N); otherwise shapes with >= 160 column blocks of 128 take the prepared-X kernel
+    (48 / 64 / 128-row blocks by M); too few blocks, K too long for the block's scale tables, or N * K / 128 not a
+    multiple of 8 keep the tile plan."""
     assert HL.mm_plan(M, N, K, use_workspace=True)[0] == kernel
 
 
 @pytest.mark.parametrize("M,N,K,kernel", [(512, 22016, 2048, HL.MM_TILE128), (201, 25088, 2048, HL.MM_TILE128),
                                           (512, 2048, 11008, HL.MM_TILE64), (69, 25088, 2048, HL.MM_TILE64),
-                                          (34, 22016, 2048, HL.MM_TILE64), (128, 22016, 2048, HL.MM_TILE64),
-                                          (512, 3072, 2048, HL.MM_TILE64), (4, 32, 200064, HL.MM_REGS)])
+                                          (34, 22016, 2048, HL.MM_STREAM), (128, 22016, 2048, HL.MM_TILE64),
+                                          (512, 3072, 2048, HL.MM_TILE64), (4, 32, 200064, HL.MM_REGS),
+                                          (34, 2048, 11008, HL.MM_TILE64)])
 def test_mm_int4_plan_query(M, N, K, kernel):
-    """The plan query names the kernel each shape runs (the GPU tests assert it for the shapes they cover)."""
+    """The plan query names the kernel each shape runs (the GPU tests assert it for the shapes they cover). Without
+    a workspace the stream kernel (M <= 48, K <= 2048) needs none either."""
     k, sp = HL.mm_plan(M, N, K, use_workspace=False)
     assert k == kernel and sp == 1
     k2, sp2 = HL.mm_plan(M, N, K, use_workspace=True)

@@ -53,10 +53,10 @@ def test_config3_m512(N, K, kernel, xdt, dev):
     print(f"M=512 N={N} K={K} {xdt}: {rep}")
 
 
-@pytest.mark.parametrize("T,kernel", [(34, H.MM_PREP48), (69, H.MM_PREP128), (201, H.MM_PREP128)])
+@pytest.mark.parametrize("T,kernel", [(34, H.MM_STREAM), (69, H.MM_PREP128), (201, H.MM_PREP128)])
 def test_reference_w_in_prompts(T, kernel, dev):
     """The reference's own check (kernels/mm_int4.py:92-106): w_in 25088 x 2048 at T in {34, 69, 201}, bf16 X as
-    the engine passes it, through the drop-in (the prepared-X kernels, asserted); the same prompts on the tile
+    the engine passes it, through the drop-in (the kernels the plan picks, asserted); T = 69 / 201 on the tile
     kernels are in test_prepared_x_against_tile_kernels."""
     N, K = 25088, 2048
     assert H.mm_plan(T, N, K) == (kernel, 1)
@@ -79,10 +79,12 @@ def test_ragged(M, N, K, dev):
     _check(Y, _ref(X, q, s, m), f"M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("M,N,K", [(34, 2048, 11008), (34, 3072, 2048), (5, 200, 4096), (128, 2048, 11008)])
+@pytest.mark.parametrize("M,N,K", [(34, 2048, 11008), (34, 3072, 4096), (5, 200, 4096), (128, 2048, 11008),
+                                   (64, 2048, 11008)])
 def test_split_k_matches_single_pass(M, N, K, dev):
-    """The split-K plan (fp32 partials + ordered sum) against the single-pass kernel of rk_mm_int4_g128 and the
-    oracle; both calls go through the C ABI, the second twice into one workspace."""
+    """The split-K plans (fp32 partials + ordered sum: the stream kernel's K chunks for M <= 48, the 64 x 64 tile
+    kernel's K splits above) against the single-pass kernel of rk_mm_int4_g128 and the oracle; both calls go through
+    the C ABI, the second twice into one workspace."""
     L = H.lib()
     nws = L.rk_mm_int4_workspace_bytes(M, N, K)
     assert nws > 0
@@ -197,7 +199,7 @@ def _ws(M, N, K, dev):
 @pytest.mark.parametrize("M,N,K,prep,tile", [(512, 22016, 2048, H.MM_PREP128, H.MM_TILE128),
                                              (201, 25088, 2048, H.MM_PREP128, H.MM_TILE128),
                                              (69, 25088, 2048, H.MM_PREP128, H.MM_TILE64),
-                                             (34, 25088, 2048, H.MM_PREP48, H.MM_TILE64),
+                                             (40, 65536, 2048, H.MM_PREP48, H.MM_TILE64),
                                              (128, 22016, 2048, H.MM_PREP128, H.MM_TILE64),
                                              (64, 22016, 4096, H.MM_PREP64, H.MM_TILE64)])
 def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
@@ -206,7 +208,7 @@ def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
     assert H.mm_plan(M, N, K, use_workspace=True) == (prep, 1)
     assert H.mm_plan(M, N, K, use_workspace=False) == (tile, 1)
     X, q, s, m = synth.prefill_case(M, N, K, 21)
-    X = X.bfloat16() if M in (34, 69, 201) else X  # the engine passes bf16 on the w_in prompts
+    X = X.bfloat16() if M in (40, 69, 201) else X  # the engine passes bf16 on the w_in prompts
     Xd, qd, sd, md = X.to(dev), q.to(dev), s.to(dev), m.to(dev)
     Yp = torch.full((M, N), 3.0, device=dev, dtype=torch.float32)
     Yt = torch.full((M, N), -3.0, device=dev, dtype=torch.float32)
@@ -220,8 +222,8 @@ def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
     print(f"M={M} N={N} K={K}: {rp}")
 
 
-@pytest.mark.parametrize("M,N,K,xdt,ydt", [(5, 20488, 256, torch.float16, torch.float16),
-                                           (47, 20480, 384, torch.bfloat16, torch.float32),
+@pytest.mark.parametrize("M,N,K,xdt,ydt", [(49, 20488, 256, torch.float16, torch.float16),
+                                           (63, 20480, 384, torch.bfloat16, torch.float32),
                                            (61, 20360, 1152, torch.float16, torch.bfloat16),
                                            (130, 20480, 256, torch.bfloat16, torch.bfloat16),
                                            (200, 20600, 512, torch.float16, torch.float32)])
@@ -244,7 +246,7 @@ def test_prepared_x_ragged_and_dtypes(M, N, K, xdt, ydt, dev):
 def test_prepared_x_strided_rows_and_scale_fallback(dev):
     """X rows with a stride beyond K; scale / min arrays that are not 16-byte aligned take the tile plan instead
     (same workspace size suffices) — both within the bar."""
-    M, N, K = 40, 20480, 512
+    M, N, K = 50, 20480, 512
     X, q, s, m = synth.prefill_case(M, N, K, 23)
     Xw = torch.zeros(M, K + 64, dtype=torch.float16)
     Xw[:, :K] = X
@@ -266,3 +268,65 @@ def test_prepared_x_strided_rows_and_scale_fallback(dev):
     _abi(Xd, qd, sb, mb_, Y2, ws=ws, ldx=K + 64)
     torch.cuda.synchronize()
     _check(Y2, ref, "unaligned scales")
+
+
+# ---- the small-M stream kernel (M <= 48: X held in registers, code tiles streamed, K chunks of 16 groups)
+F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
+
+
+@pytest.mark.parametrize("M,N,K,xdt,ydt", [(34, 3072, 2048, F16, F16), (34, 22016, 2048, F16, F16),
+                                           (34, 25088, 2048, BF16, BF16), (1, 64, 128, F16, F32),
+                                           (16, 2048, 2048, BF16, F16), (17, 100, 384, F16, BF16),
+                                           (48, 20360, 1152, BF16, F32), (33, 48, 2048, F16, F16),
+                                           (3, 17, 256, BF16, F32), (32, 4104, 1920, F16, F16),
+                                           (40, 30000, 1408, F16, F16)])
+def test_stream_kernel(M, N, K, xdt, ydt, dev):
+    """Every m-tile count (M = 1 .. 48), K from one group to 16 (K = 1920 / 1408: 15 / 11 groups, so waves own one
+    or two groups; K = 128: seven waves with none), ragged columns (N % 16 != 0, a short last block), 1 .. 8 tiles
+    per block, every dtype pairing, X rows with a stride beyond K; against the oracle, nothing written outside
+    [M, N], and the three entries (workspace, no-alloc and plain) bit-identical."""
+    kernel, splits = H.mm_plan(M, N, K, use_workspace=True)
+    assert kernel == H.MM_STREAM and splits == 1
+    X, q, s, m = synth.prefill_case(M, N, K, 40 + M)
+    X = X.to(xdt)
+    Xw = torch.zeros(M, K + 32, dtype=xdt)
+    Xw[:, :K] = X
+    Xd, qd, sd, md = Xw.to(dev), q.to(dev), s.to(dev), m.to(dev)
+    Yw = torch.full((M + 1, N + 8), 7.0, device=dev, dtype=ydt)  # one guard row, eight guard columns
+    Y = Yw[:M, :N]
+    _abi(Xd, qd, sd, md, Y, ws=_ws(M, N, K, dev), ldx=K + 32, ldy=N + 8)
+    torch.cuda.synchronize()
+    rep = _check(Y, _ref(X, q, s, m), f"M={M} N={N} K={K} {xdt}->{ydt}")
+    assert torch.all(Yw[M] == 7.0) and torch.all(Yw[:, N:] == 7.0)
+    L = H.lib()
+    Yn = torch.full((M, N), -7.0, device=dev, dtype=ydt)
+    H.check(L.rk_mm_int4_g128_noalloc(H.ptr(Xd), H.dt(Xd), K + 32, H.ptr(qd), H.ptr(sd), H.ptr(md), H.ptr(Yn),
+                                      H.dt(Yn), N, M, N, K, H.stream(dev)), "noalloc")
+    assert H.mm_plan(M, N, K, use_workspace=False) == (H.MM_STREAM, 1)
+    Yp = torch.full((M, N), 9.0, device=dev, dtype=ydt)
+    _abi(Xd, qd, sd, md, Yp, ldx=K + 32)
+    torch.cuda.synchronize()
+    assert torch.equal(Yp, Y)
+    torch.cuda.synchronize()
+    assert torch.equal(Yn, Y)
+    print(f"M={M} N={N} K={K} {xdt}->{ydt}: {rep}")
+
+
+def test_stream_kernel_one_hot_codes(dev):
+    """Exact known answers through the stream kernel: a single code 1 at column k of row n (all else 0), scale 1,
+    min 0, X = integers, gives Y[:, n] = X[:, k] exactly, for k at both nibbles and in every quarter / group of a
+    chunk; other columns are exactly 0."""
+    M, N, K = 34, 64, 2048
+    X = torch.randint(-8, 9, (M, K), dtype=torch.float32).half()
+    q = torch.zeros(N, K // 2, dtype=torch.uint8)
+    ks = [0, 1, 7, 8, 31, 32, 127, 128, 255, 1000, 1777, 2047]
+    for n, k in enumerate(ks):
+        q[n, k // 2] = 1 if k % 2 == 0 else 0x10
+    s = torch.ones(N, K // 128, dtype=torch.float16)
+    mn = torch.zeros(N, K // 128, dtype=torch.float16)
+    assert H.mm_plan(M, N, K) == (H.MM_STREAM, 1)
+    Y = mm_int4.mm_int4(X.to(dev), q.to(dev), s.to(dev), mn.to(dev), out=torch.empty(M, N, device=dev, dtype=F32))
+    want = torch.zeros(M, N)
+    for n, k in enumerate(ks):
+        want[:, n] = X[:, k].float()
+    assert torch.equal(Y.cpu(), want)

@@ -247,27 +247,26 @@ RK_DEV void arrive(uint32_t* ctr) {
 }
 
 // Poll N tagged fp16 pairs per lane (qword addresses from addr(k); nullptr = not needed) until every tag matches;
-// val[k] receives the packed pair. Every iteration loads all N words and the status word unconditionally, so they
-// are one batch with a single wait: reloading a word already validated is harmless, because its next value is
-// written only after every consumer has finished this poll (the exchanges' dataflow order), and its first
-// validated value is the one kept. Wave-uniform control flow; false after an abort or a timeout.
+// val[k] receives the packed pair. Each iteration loads the words this lane still lacks (lanes holding a validated
+// word, or needing none, are masked off and fetch nothing, so a second round re-reads only what is missing) and
+// the status word, as one batch with a single wait; a word's first validated value is the one kept (its next value
+// is written only after every consumer has finished this poll: the exchanges' dataflow order). Wave-uniform control
+// flow; false after an abort or a timeout.
 template <int N, class Addr>
 RK_DEV bool poll_pairs(const Params& p, Lds& S, uint32_t tag, Addr addr, uint32_t (&val)[N]) {
     static_assert(N <= 32, "pending mask");
-    // a valid, lane-varying address for the unneeded slots (a uniform one is turned into scalar moves and waits)
-    const uint64_t* dummy = reinterpret_cast<const uint64_t*>(p.tx) + lane_id();
     uint32_t pending = 0;
 #pragma unroll
     for (int k = 0; k < N; ++k)
         if (addr(k)) pending |= 1u << k;
     const uint64_t t0 = wall_clock64();
-    while (true) {
-        uint64_t q[N];
+    uint64_t q[N];
 #pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const uint64_t* a = addr(k);
-            q[k] = ld_coh64(a ? a : dummy);
-        }
+    for (int k = 0; k < N; ++k) q[k] = 0;
+    while (true) {
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (pending & (1u << k)) q[k] = ld_coh64(addr(k));
         const uint32_t st = ld_coh(p.status);
 #pragma unroll
         for (int k = 0; k < N; ++k)
@@ -925,12 +924,19 @@ RK_DEV bool comb_part(const Params& p, Lds& S, int h, int64_t pos, uint32_t tag)
         uint32_t val[kCombPer];  // split i0 + k's pair of dims (2 lane, 2 lane + 1); zero for k >= cnt
 #pragma unroll
         for (int k = 0; k < kCombPer; ++k) val[k] = 0u;
-        while (true) {
-            // one batch per iteration (see poll_pairs): the splits' pairs, the (m, l) words and the status
-            uint64_t q[kCombPer];
+        uint64_t q[kCombPer], qm = 0, ql = 0;
 #pragma unroll
-            for (int k = 0; k < kCombPer; ++k) q[k] = ld_coh64(po + (size_t)min(i0 + k, nsp - 1) * (kHD / 2));
-            const uint64_t qm = ld_coh64(tml), ql = ld_coh64(tml + 1);
+        for (int k = 0; k < kCombPer; ++k) q[k] = 0;
+        while (true) {
+            // one batch per iteration (see poll_pairs): the pairs of the splits still missing (a wave-uniform set),
+            // the (m, l) words a lane still lacks, and the status
+#pragma unroll
+            for (int k = 0; k < kCombPer; ++k)
+                if (pending & (1u << k)) q[k] = ld_coh64(po + (size_t)(i0 + k) * (kHD / 2));
+            if (!ml_done) {
+                qm = ld_coh64(tml);
+                ql = ld_coh64(tml + 1);
+            }
             const uint32_t st = ld_coh(p.status);
 #pragma unroll
             for (int k = 0; k < kCombPer; ++k)

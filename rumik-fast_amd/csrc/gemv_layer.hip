@@ -12,9 +12,12 @@
 //   * block b owns gate / up pairs [b*pb, b*pb + pb), q/k/v rows [b*qb, ...), o rows [b*ob, ...) and down rows
 //     [b*db, ...). K = 2048 is one 16-byte code chunk (32 columns) per lane, so a wave reads a row with one load;
 //     x and the attention output are read once per block and shared through LDS in dot order;
-//   * two wave roles with streams of about equal length: the down waves (0..5) take 6 gate / up pair slots and then
-//     the 8 down rows' chunk 64w + lane (thread-per-chunk), the q/o waves (6, 7) 6 pair slots and then the q/k/v
-//     and o rows. Each wave keeps kAhead load units in flight and computes a row as soon as it lands;
+//   * two wave roles with streams of about equal length: the down waves (2..7) take up to 6 gate / up pair slots
+//     and then the 8 down rows' chunk 64 (w - 2) + lane (thread-per-chunk), the q/o waves (0, 1) 6 pair slots and
+//     then the q/k/v and o rows. The q/o waves, whose streams are the longest, are the oldest: a CU issues its
+//     waves' memory requests oldest first, so they no longer trail the others and the down waves' act read, which
+//     queues behind every load the CU has in flight, starts sooner. Each wave keeps kAhead load units in flight and
+//     computes a row as soon as it lands;
 //   * act values are published as tagged 32-bit words (value bits | launch tag << 16) with agent-scope stores, so a
 //     reader on any XCD takes a word only once it carries this launch's tag: no fences. A per-block flag (also the
 //     tag) follows the words; the tag comes from a per-block launch counter in the workspace that the block
@@ -33,7 +36,8 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kH = 2048;            // hidden size: one 32-column chunk per lane in phase 1
-constexpr int kDownWaves = 6;       // waves 0..5: gate / up and down; waves 6, 7: gate / up, q/k/v and o
+constexpr int kDownWaves = 6;       // waves 2..7: gate / up and down; waves 0, 1: gate / up, q/k/v and o
+constexpr int kQoWaves = kWaves - kDownWaves;
 constexpr int kPairSlots = 6;       // gate / up pair slots per wave: local pairs w + 8s
 constexpr int kPlainSlots = 6;      // q/k/v rows per q/o wave
 constexpr int kOSlots = 4;          // o rows per q/o wave
@@ -164,7 +168,8 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
     uint32_t* flags = a.ws + kHdrWords + kCtrWords;  // per-block "act slice published" flags (the tag)
     uint32_t* xw = a.ws + kHdrWords + 2 * kCtrWords;  // tagged act words, channel 32c + i at i * nch2 + c
     const int p0 = b * a.pb, q0 = b * a.qb, o0 = b * a.obr, d0 = b * a.db;
-    const int dchunk = 64 * wave + lane;  // down waves: this lane's down chunk (valid below nch2)
+    const int dw = wave - kQoWaves;         // down waves: 0 .. 5
+    const int dchunk = 64 * dw + lane;      // down waves: this lane's down chunk (valid below nch2)
 
     // x and the attention output are read once per block (wave 0; lane = chunk) and shared through LDS in dot order:
     // a CU serves its waves' memory requests in issue order, so they go out before any weight request of the block
@@ -219,8 +224,8 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
     h2_t dq[kDownRows][16];  // down waves: chunk dchunk of the block's down rows, as fp16 pairs
 
     // ---- phase 1. Two wave roles with streams of about equal length, in the order they are consumed:
-    //   down waves (0..5):  6 gate / up pair slots (gate, then up), then the 8 down rows' chunk of each lane;
-    //   q/o waves (6, 7):   6 gate / up pair slots, then 6 q/k/v rows and 4 o rows.
+    //   down waves (2..7):  up to 6 gate / up pair slots (gate, then up), then the 8 down rows' chunk of each lane;
+    //   q/o waves (0, 1):   6 gate / up pair slots, then 6 q/k/v rows and 4 o rows.
     // kAhead units stay in flight: a wave computes a row as soon as it lands and issues the unit kAhead places
     // further on, so the rows are computed while the rest streams. Units past the block's share load a line of x
     // instead (cached; the result is dropped).
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
         constexpr int kUnits = kGU + (kDown ? kDownRows : kPlainSlots + kOSlots);
         u4_t rl[kDown ? kGU : kGU + kPlainSlots + kOSlots];
         u4_t wd[kDownRows];
-        const int qw = wave - kDownWaves;  // q/o waves: 0, 1
+        const int qw = wave;  // q/o waves: 0, 1
         // local pair index of slot s: w + 8s (the block's waves read 8 consecutive rows per slot)
         auto pair_of = [&](int s) { return wave + kWaves * s; };
         auto issue = [&](auto kc) __attribute__((always_inline)) {  // unit number as a compile-time constant
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
         // the last q/o wave publishes the block's act slice and then the block's flag (one store stream: the flag
         // usually lands after the words; readers check the words' tags in any case)
         lds_barrier();
-        if (wave == kWaves - 1) {
+        if (wave == kQoWaves - 1) {
             const int np = min(a.pb, a.inter - p0);
             for (int l = lane; l < np; l += 64) {
                 const int c = p0 + l;
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
             }
         }
     };
-    if (wave < kDownWaves) phase1(std::true_type{});
+    if (wave >= kQoWaves) phase1(std::true_type{});
     else phase1(std::false_type{});
     RK_LTR(3);
 
@@ -383,7 +388,7 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
     // gets here most blocks have published, so the words are read at once; if some are not there yet the wave
     // waits on the blocks' flags (nb words per poll: the blocks still streaming are not slowed by the waiting ones)
     // before it reads the words again.
-    if (wave < kDownWaves && 64 * wave < nch2) {
+    if (wave >= kQoWaves && 64 * dw < nch2) {
         bool bad = false;
         const uint64_t t0 = wall_clock64();
         const int nb = gridDim.x;
@@ -442,9 +447,9 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
                 acc[r] = mine ? v : 0.f;
             }
             wave_reduce_rows<kDownRows>(acc);  // lanes 8r..8r+7 hold row r
-            if ((lane & 7) == 0) red[wave][lane >> 3] = acc[0];
+            if ((lane & 7) == 0) red[dw][lane >> 3] = acc[0];
         }
-        if (lane == 0) wave_bad[wave] = bad ? 1u : 0u;
+        if (lane == 0) wave_bad[dw] = bad ? 1u : 0u;
         RK_LTR(6);
     }
     __syncthreads();

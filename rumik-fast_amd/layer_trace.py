@@ -20,7 +20,7 @@ PKG = Path(__file__).resolve().parent
 LIB = PKG / "lib" / "librumik_layer_trace.so"
 EVENTS = ["start", "x and tables in LDS", "gate / up done, act published", "streams done (phase 1)",
           "phase 2 start (down waves)", "act chunk in registers (down waves)", "down rows done (down waves)", "end"]
-ROLES = (("down waves (0..5)", slice(0, 6)), ("q/o waves (6, 7)", slice(6, 8)))
+ROLES = (("down waves (2..7)", slice(2, 8)), ("q/o waves (0, 1)", slice(0, 2)))
 
 
 def build():

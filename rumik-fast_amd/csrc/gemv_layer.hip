@@ -38,6 +38,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kH = 2048;            // hidden size: one 32-column chunk per lane in phase 1
 constexpr int kDownWaves = 6;       // waves 2..7: gate / up and down; waves 0, 1: gate / up, q/k/v and o
 constexpr int kQoWaves = kWaves - kDownWaves;
+constexpr int kPairRot = 3;         // pair slot owner index of wave w: (w + 3) % 8
 constexpr int kPairSlots = 6;       // gate / up pair slots per wave: local pairs w + 8s
 constexpr int kPlainSlots = 6;      // q/k/v rows per q/o wave
 constexpr int kOSlots = 4;          // o rows per q/o wave
@@ -237,8 +238,11 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
         u4_t rl[kDown ? kGU : kGU + kPlainSlots + kOSlots];
         u4_t wd[kDownRows];
         const int qw = wave;  // q/o waves: 0, 1
-        // local pair index of slot s: w + 8s (the block's waves read 8 consecutive rows per slot)
-        auto pair_of = [&](int s) { return wave + kWaves * s; };
+        // local pair index of slot s: o + 8s with the wave's owner index o = (w + 3) % 8 (the block's waves read 8
+        // consecutive rows per slot). A block's pairs (43 at inter = 11008) leave slot 5 to owners 0..2 only; the
+        // rotation gives those extra pairs to down waves 5..7, so the q/o waves, whose streams are the longest, carry
+        // five pairs
+        auto pair_of = [&](int s) { return (wave + kPairRot) % kWaves + kWaves * s; };
         auto issue = [&](auto kc) __attribute__((always_inline)) {  // unit number as a compile-time constant
             constexpr int k = decltype(kc)::value;
             if constexpr (k >= kUnits) {
@@ -529,7 +533,7 @@ extern "C" int rk_gemv_int4_g128_layer(const void* x, const void* ob, int x_dtyp
     a.obr = cdiv(H, nb);
     a.db = cdiv(H, nb);
     a.ws = reinterpret_cast<uint32_t*>(ws);
-    // the per-wave slots: pairs wave + 8s (s < 6), q/k/v rows (7 - wave) + 8s (s < 2), one o row and one down row
+    // the per-wave slots: pairs (wave + 3) % 8 + 8s (s < 6); q/k/v and o rows on the two q/o waves; the down rows
     if (a.pb > kMaxPairs || a.qb > 2 * kPlainSlots || a.obr > 2 * kOSlots || a.db > kDownRows)
         return RK_ERR_SHAPE;
     hipLaunchKernelGGL(gemv_layer_kernel, dim3(nb), dim3(kThreads), kLdsBytes, (hipStream_t)stream, a);

@@ -15,14 +15,21 @@ weights and inputs are resident in HBM before timing.
 
 value = algorithmic bytes per step (sum over the four projections of N*K/2 + 4*N*K/128 + 2K + 2N) / wall time.
 roofline: the dominant kernel (the layer launch: the step's bytes in one launch), its average launch duration
-measured with HIP events on its stream over back-to-back launches with rotated weights.
+measured with HIP events on its stream over back-to-back launches with rotated weights. The layer launch is a
+bench-only projection-throughput kernel: o's input is given at launch time, so no engine path can call it (in the
+decode step o's input is this layer's attention output, which needs the q / k / v the same launch produces); the
+drop-in GEMVs and the realisable two-launch schedule are reported beside it (`gemv_gate_up`, `two_launch`).
 roofline.read_ceiling_us: the best time of a read-only kernel over the same number of bytes in the same setting
-(the reference's kernels/roofline.py method), and a dense bf16 GEMV's read rate beside it.
+(the reference's kernels/roofline.py method: one grid-stride pass, swept over threads per block, blocks and loads
+in flight); roofline.read_ceilings: that ceiling at each projection's exact byte count, next to the kernel's time;
+and a dense bf16 GEMV's read rate.
 parity: the layer launch's outputs on copy 0 (q/k/v rows and down) and the w_in projection against the float64
 oracle (max_rel and max_rel_strict).
 decode_tok_s: the 36-layer step's tokens per second at ctx 256 / 1024 / 2048 (config 4).
-cpu_baseline: the CPU oracle's dequantize-then-matmul of the same step (numpy fp32), on this host's cores, with
-matmul-only times and configs 2 / 3 / a config-4 layer beside it.
+cpu_baseline: the reference's CPU path for the same step, dequantize then matmul in torch fp32
+(kernels/int4_gemv.py:27-30 as kernels/bench_gemv.py:43 runs it) on CPU tensors with every thread torch is given,
+with a matmul-only time, and the numpy oracle's single-threaded dequantization and configs 2 / 3 / a config-4 layer
+beside it.
 Extra fields: the per-projection kernel times, the int8 audio head (config 2), the int4 prefill (config 3), the
 sampling tail, and the 36-layer decode step (config 4) with and without sampling inside the graph.
 """
@@ -129,7 +136,8 @@ def cpu_baseline(budget_s):
     - config 3: the prefill product at M = 34 over the three layer shapes, both ways;
     - a config-4 layer: the oracle's whole decode step for one full-width layer at ctx 256 (embedding, LayerNorm,
       w_in, RoPE, attention, o, down, residual, a 16-row head), both ways.
-    Dequantization is single-threaded numpy; the matmuls use the BLAS threads (`cores`)."""
+    The value is the torch path (the reference's dequantize then @, with every thread torch has: `cores`); the
+    numpy oracle's figures (single-threaded dequantization, BLAS-threaded matmuls) are reported beside it."""
     import numpy as np
     import synth
     import decode
@@ -140,7 +148,7 @@ def cpu_baseline(budget_s):
         cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
     except Exception:
         cores = 1
-    share = budget_s / 8.0
+    share = budget_s / 10.0
     g = synth.generator(1)
     mats = {k: tuple(t.numpy() for t in synth.int4_weights(N, K, g)) for k, (N, K) in SHAPES.items()}
     deq = {k: O.dequantize(*w) for k, w in mats.items()}
@@ -158,13 +166,40 @@ def cpu_baseline(budget_s):
         mv("down", act)
 
     nbytes = sum(int4_bytes(N, K) for N, K in SHAPES.values())
-    n1, t1 = _timed(lambda: step(True), 2 * share)
-    n1m, t1m = _timed(lambda: step(False), share)
-    res = {"value": round(nbytes * n1 / t1 / 1e9, 3), "unit": "GB/s", "cores": int(cores), "kind": "port",
-           "sample": f"{n1} config-1 steps (one weight copy), numpy fp32 dequantize-then-matmul, {t1:.1f} s",
+    # the reference's own CPU path in torch: dequantize (the format's definition, kernels/int4_gemv.py:27-30, the
+    # drop-in module's torch function on CPU tensors) then @ x.float(), every projection of the step, with all the
+    # threads torch is given (OMP_NUM_THREADS: the box's CPU share)
+    import torch
+    import int4_gemv
+    threads = torch.get_num_threads()
+    tm = {k: tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in w) for k, w in mats.items()}
+    tdeq = {k: int4_gemv.dequantize(*w) for k, w in tm.items()}
+    tx, tob = torch.from_numpy(x).float(), torch.from_numpy(ob).float()
+
+    def tstep(dequant):
+        mv = (lambda k, v: int4_gemv.dequantize(*tm[k]) @ v) if dequant else (lambda k, v: tdeq[k] @ v)
+        mv("qkv", tx)
+        mv("o", tob)
+        gu = mv("gate_up", tx)
+        act = (torch.nn.functional.silu(gu[:INTER]) * gu[INTER:]).half().float()
+        mv("down", act)
+
+    with torch.inference_mode():
+        n0, t0 = _timed(lambda: tstep(True), 2 * share)
+        n0m, t0m = _timed(lambda: tstep(False), share)
+    del tdeq
+    n1, t1 = _timed(lambda: step(True), share)
+    n1m, t1m = _timed(lambda: step(False), share / 2)
+    res = {"value": round(nbytes * n0 / t0 / 1e9, 3), "unit": "GB/s", "cores": int(threads), "kind": "port",
+           "sample": f"{n0} config-1 steps (one weight copy): torch fp32 dequantize-then-matmul on CPU tensors, "
+                     f"{threads} threads, {t0:.1f} s",
            "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
-           "config1_us_per_step": {"dequant_matmul": round(t1 / n1 * 1e6, 1), "matmul_only": round(t1m / n1m * 1e6, 1)},
-           "config1_matmul_only_GB_s": round(nbytes * n1m / t1m / 1e9, 3)}
+           "config1_us_per_step": {"dequant_matmul": round(t0 / n0 * 1e6, 1),
+                                   "matmul_only": round(t0m / n0m * 1e6, 1)},
+           "config1_matmul_only_GB_s": round(nbytes * n0m / t0m / 1e9, 3),
+           "numpy_oracle": {"config1_us_per_step": {"dequant_matmul": round(t1 / n1 * 1e6, 1),
+                                                    "matmul_only": round(t1m / n1m * 1e6, 1)},
+                            "dequant_threads": 1, "blas_threads": int(cores)}}
     del deq
     # config 2: int8 head
     q8, s8 = synth.int8_weights(16385, H, g)
@@ -434,13 +469,16 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     value = step_bytes * args.steps / elapsed / 1e9
     log(f"[bench] config 1: {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s")
-    assert lp.status() == 0, "layer launch: an exchange wait ran out"
+    if lp.status() != 0:
+        raise RuntimeError("layer launch: an exchange wait ran out during the timed steps")
 
     # ---- the dominant kernel: the layer launch alone (16 rotated copies back to back in one graph), and the
     # two-launch form of the same step
     g = graph_of([f for L in layers for f in step_fns(L)])
     layer_us = time_graph_us(g, N_COPIES)
     del g
+    if lp.status() != 0:
+        raise RuntimeError("layer launch: an exchange wait ran out while timing the launch")
     g = graph_of([f for L in layers for f in two_launch_fns(L)])
     two_us = time_graph_us(g, N_COPIES)
     del g
@@ -476,10 +514,29 @@ def main():
     mats0 = [layers[0][k] for k in ("w_in", "o", "down")]
     sizes = [sum(m[i].numel() * m[i].element_size() for m in mats0) for i in range(3)]
     ro_mats = [tuple(torch.empty(n, device=dev, dtype=torch.uint8) for n in sizes) for _ in range(N_COPIES)]
-    ro_us, ro_shape = RF.ceiling_us(ro_mats)
+    ro_us, ro_shape, ro_all = RF.ceiling_us(ro_mats)
     ro_bytes = sum(sizes)
     del ro_mats
     log(f"[bench] read ceiling: {ro_us:.2f} us for {ro_bytes} B ({ro_bytes / ro_us / 1e3:.0f} GB/s), {ro_shape}")
+    # the same ceiling at each projection's exact algorithmic byte count (one contiguous buffer per copy): the full
+    # sweep for gate+up (the GEMV the >= 70 % target names), the 8 best shapes of it for the others
+    ceil = {}
+    gu_bytes = int4_bytes(*SHAPES["gate_up"])
+    us, sh, allr = RF.ceiling_at(gu_bytes, dev)
+    ceil["gate_up"] = (gu_bytes, us, sh)
+    best8 = [s for _, s in allr[:8]]
+    for name, nb in (("w_in_silu", WIN_BYTES), ("down", int4_bytes(*SHAPES["down"])),
+                     ("qkv", int4_bytes(*SHAPES["qkv"])), ("o", int4_bytes(*SHAPES["o"])),
+                     ("int8_head", int8_bytes(16385, H))):
+        us, sh, _ = RF.ceiling_at(nb, dev, copies=16 if nb > 8e6 else 64, candidates=best8)
+        ceil[name] = (nb, us, sh)
+    kern_us = {k: proj[k]["us"] for k in ("gate_up", "down", "qkv", "o", "w_in_silu")}
+    read_ceilings = {k: {"bytes": nb, "ceiling_us": round(us, 2), "ceiling_GB_s": round(nb / us / 1e3, 1),
+                         "ceiling_frac_of_peak": round(nb / us / 1e3 / PEAK_HBM_GBS, 4), "shape": sh,
+                         **({"kernel_us": kern_us[k], "kernel_frac_of_ceiling": round(us / kern_us[k], 4)}
+                            if k in kern_us else {})}
+                     for k, (nb, us, sh) in ceil.items()}
+    log(f"[bench] read ceilings: {read_ceilings}")
     # parity on copy 0 against the float64 oracle (max_rel with the per-output conditioning floor, max_rel_strict
     # with the fp16 floor alone): the layer launch's q/k/v rows (over x) and down rows (over the act it wrote), and
     # the w_in projection alone
@@ -511,11 +568,14 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": load_traffic(),
                 "kernel": "gemv_layer_kernel: w_in [qkv | gate | up] 25088x2048 + SiLU*up, o 2048x2048, down "
-                          "2048x11008 in one launch",
+                          "2048x11008 in one launch (bench-only projection throughput: o's input is given at "
+                          "launch; no engine path calls it, the decode step runs each layer inside "
+                          "decode_step_kernel)",
                 "us_per_launch": round(layer_us, 2), "bytes_per_launch": step_bytes,
                 "two_launch_us_per_step": round(two_us, 2),
                 "read_ceiling_us": round(ro_us, 2), "read_ceiling_GB_s": round(ro_bytes / ro_us / 1e3, 1),
                 "read_ceiling_shape": ro_shape, "frac_of_read_ceiling": round(ro_us / layer_us, 4),
+                "read_ceilings": read_ceilings,
                 "dense_bf16_gemv_us": round(bf_us, 2),
                 "dense_bf16_gemv_GB_s": round(2 * N_WIN * H / bf_us / 1e3, 1)}
 
@@ -579,11 +639,18 @@ def main():
         "config": {"workload": "config 1: one decoder layer's decode projections (qkv 3072x2048, o 2048x2048, "
                                "gate+up 22016x2048 + SiLU*up, down 2048x11008), batch 1; qkv and gate+up run as "
                                "the reference engine's one w_in projection with SiLU*up fused; all four in one "
-                               "launch per step, 16 steps (16 weight copies) per hipGraph replay",
+                               "bench-only launch per step (o's input given), 16 steps (16 weight copies) per "
+                               "hipGraph replay",
                    "bytes_per_step": step_bytes, "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2)},
         "decode_tok_s": ({k: decode_res[k]["tok_s"] for k in ("ctx256", "ctx1024", "ctx2048")}
                          if decode_res else None),
         "roofline": roofline,
+        "gemv_gate_up": {"kernel": "drop-in gemv_int4_cuda, 22016x2048 (the GEMV the >= 70% target names)",
+                         "us": proj["gate_up"]["us"], "GB_s": proj["gate_up"]["GB_s"],
+                         "frac_of_peak": round(proj["gate_up"]["GB_s"] / PEAK_HBM_GBS, 4),
+                         "frac_of_read_ceiling": read_ceilings["gate_up"]["kernel_frac_of_ceiling"]},
+        "two_launch": {"kernel": "realisable schedule: w_in + SiLU*up, then o + down (drop-in GEMVs)",
+                       "us_per_step": round(two_us, 2), "GB_s": round(step_bytes / two_us / 1e3, 1)},
         "parity": parity,
         "cpu_baseline": cpu,
         "projections": proj,

@@ -115,9 +115,14 @@ int rk_gemv_int4_g128_silu(const void* x, int x_dtype, const uint8_t* q, const u
  * (y_dtype); x, ob and the code arrays 16-byte aligned, the scale and min arrays 4-byte aligned (RK_ERR_ALIGN).
  * ws: rk_gemv_int4_g128_layer_ws_bytes(inter) bytes, 4-byte aligned, ZEROED before its first use and then kept
  * for this call alone (its words carry per-block launch counters, so hipGraph replays need no reset; one launch
- * at a time per workspace). One block per CU, all resident at once; the grid meets once (act), every wait
+ * at a time per workspace). One block per CU, all resident at once: the call needs the whole device (256 CUs on
+ * MI355X; with fewer CUs, e.g. a partitioned device, every call returns RK_ERR_SHAPE) and no other kernel running
+ * on it meanwhile (a block that cannot start leaves the others waiting). The grid meets once (act), every wait
  * bounded: a wait that runs out (200 ms) sets bit 0 of the workspace's first 32-bit word and leaves y_down
- * unwritten. No separate reference counterpart. */
+ * unwritten; the caller reads that word after the call's stream has finished (LayerProjections.status()) and
+ * zeroes it before reusing the workspace. No engine path calls this entry: in the decode step o's input is this
+ * layer's attention output, which depends on the q / k / v this launch produces. No separate reference
+ * counterpart. */
 size_t rk_gemv_int4_g128_layer_ws_bytes(int inter);
 int rk_gemv_int4_g128_layer(const void* x, const void* ob, int x_dtype, const uint8_t* q_in, const uint16_t* s_in,
                             const uint16_t* m_in, const uint8_t* q_o, const uint16_t* s_o, const uint16_t* m_o,
@@ -187,9 +192,11 @@ int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uint8_t* q, co
  * that cannot allocate (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Same plan, kernels and results as rk_mm_int4_g128_ws, except that it never takes the RK_MM_PREP* kernels (their
  * prepared X would not fit the array): where rk_mm_int4_g128_ws takes one, this entry runs the tile plan of
- * rk_mm_int4_g128 (results equal up to fp32 summation order). Shapes whose split-K partials exceed the array
- * (rk_mm_int4_workspace_bytes(M, N, K) > RK_MM_SCRATCH_BYTES; none with K <= 49152) return RK_ERR_SCRATCH before
- * any launch. Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on different streams
+ * rk_mm_int4_g128 (results equal up to fp32 summation order). The limit is checked on the plan this entry runs (the
+ * tile plan, never a RK_MM_PREP* one): when that plan splits K and its fp32 partial sums (splits * M * N * 4 bytes)
+ * exceed RK_MM_SCRATCH_BYTES (no shape with K <= 49152 does), the call returns RK_ERR_SCRATCH before any launch.
+ * rk_mm_int4_workspace_bytes may be larger for the same shape (it sizes the prepared-X plan), and such a call still
+ * succeeds. Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on different streams
  * without ordering) race and give wrong results; calls ordered on one stream are safe. */
 #define RK_MM_SCRATCH_BYTES (8u << 20)
 int rk_mm_int4_g128_noalloc(const void* X, int x_dtype, int ldx, const uint8_t* q, const uint16_t* scale,
@@ -257,7 +264,9 @@ int rk_silu_mul(const void* gate_up, void* act, int act_dtype, int inter, rk_str
  * step = the block's ctr entry) and poll the words themselves: tx, tq, tkv, top, tdp, tpo (fp16 words) and tml
  * (fp32 m / l | tag << 32). All exchange buffers, ctr and status start at zero; after a nonzero status, re-zero them.
  * status bit 1 = a wait exceeded 200 ms (the step finishes early with garbage); bit 2 = pos outside [0, S)
- * (nothing is computed or written, pos is not advanced).
+ * (nothing is computed or written, pos is not advanced); bit 3 = some layer's residual sum x = x + o + down left
+ * the fp16 range or was NaN (the step is fp16 end to end, unlike the reference's bf16 engine; the step completes,
+ * its outputs are not meaningful). Bit 0 accompanies bit 1.
  * ------------------------------------------------------------------------------------------------------------ */
 typedef struct rk_decode_params {
     int L, NH, NKV, inter, S, n_audio, nsp;
@@ -395,12 +404,18 @@ int rk_sample_tail(const void* h, int h_dtype, const float* lnw, const float* ln
 
 /* Read-only ceiling (a measurement kernel; replaces the reference's kernels/roofline.py:20-33 `read_only`, which
  * loads an int4 matrix's codes, scales and mins and integer-sums them): reads the three buffers a (na bytes),
- * b (nb), c (nc) with 16-byte nontemporal loads, grid-stride, `unroll` loads in flight per thread (1, 2, 4 or 8),
- * and writes one uint32 per block to sink[blocks]: the wrapping sum of the block's 32-bit words, so the sink's
- * total is the wrapping sum of every word of the three buffers. Sizes must be multiples of 16 and the pointers
- * 16-byte aligned (RK_ERR_SHAPE / RK_ERR_ALIGN); 1 <= blocks <= 65536 (256 threads each). */
+ * b (nb), c (nc) as one range of 16-byte items in a single grid-stride pass, with 16-byte nontemporal loads,
+ * `unroll` loads in flight per thread (1, 2, 4 or 8), and writes one uint32 per block to sink[blocks]: the wrapping
+ * sum of the block's 32-bit words, so the sink's total is the wrapping sum of every word of the three buffers.
+ * Sizes must be multiples of 16 and the pointers 16-byte aligned (RK_ERR_SHAPE / RK_ERR_ALIGN);
+ * 1 <= blocks <= 65536 (256 threads each). */
 int rk_read_only(const void* a, size_t na, const void* b, size_t nb, const void* c, size_t nc, int blocks, int unroll,
                  uint32_t* sink, rk_stream_t stream);
+
+/* rk_read_only with the block size as a knob: threads per block 256, 512 or 1024 (RK_ERR_BLOCK otherwise), for the
+ * launch-shape sweep of the ceiling. Same reads and sink as rk_read_only. */
+int rk_read_only_ex(const void* a, size_t na, const void* b, size_t nb, const void* c, size_t nc, int threads,
+                    int blocks, int unroll, uint32_t* sink, rk_stream_t stream);
 
 #pragma GCC visibility pop
 

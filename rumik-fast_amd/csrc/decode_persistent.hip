@@ -34,7 +34,8 @@
 // tile waves form after their last read of h).
 //
 // Every wait is bounded by wall-clock time (200 ms): on expiry the kernel sets an abort bit in `status`, every
-// later wait returns at once and the grid drains with garbage results.
+// later wait returns at once and the grid drains with garbage results. A residual sum that leaves the fp16 range
+// (or is NaN) sets a sticky status bit and the step runs on: the caller decides what to do with the token.
 #include "dequant.h"
 
 namespace {
@@ -70,7 +71,7 @@ constexpr int kSliceBegin = 8, kSliceEnd = 9;
 constexpr int kXRep = 16;
 constexpr int kRepQwords = kH / 2;         // qwords per copy (2048 tagged fp16 words)
 constexpr uint64_t kWaitTicks = 20000000ull;  // 200 ms at the 100 MHz wall clock
-constexpr unsigned kAbort = 1u, kTimeout = 2u, kBadPos = 4u;
+constexpr unsigned kAbort = 1u, kTimeout = 2u, kBadPos = 4u, kNonFinite = 8u;
 constexpr int kMaxSplits = 64;
 
 static_assert(kRP * kDLanes * 2 == kH, "down rows split evenly over the down lanes");
@@ -1122,6 +1123,7 @@ RK_DEV void gather_phase(const Params& p, int l, uint32_t tag, int rho, Lds& S) 
         if (lane < 4) S.opart[lane] = make_float2(o0, o1);
     }
     if (!arrive_last(&S.cnt_g, (uint32_t)kRW * (l + 1))) return;
+    bool bad = false;
     if (lane < 4) {  // lane = row pair: rows 2 lane, 2 lane + 1
         float2 d = make_float2(0.f, 0.f);
 #pragma unroll
@@ -1130,9 +1132,13 @@ RK_DEV void gather_phase(const Params& p, int l, uint32_t tag, int rho, Lds& S) 
             d.y += S.gpart[r][lane].y;
         }
         const float2 o = S.opart[lane];
-        S.xrow[2 * lane] = rnd16(S.xrow[2 * lane] + rnd16(o.x) + rnd16(d.x));
-        S.xrow[2 * lane + 1] = rnd16(S.xrow[2 * lane + 1] + rnd16(o.y) + rnd16(d.y));
+        const float x0 = rnd16(S.xrow[2 * lane] + rnd16(o.x) + rnd16(d.x));
+        const float x1 = rnd16(S.xrow[2 * lane + 1] + rnd16(o.y) + rnd16(d.y));
+        S.xrow[2 * lane] = x0;
+        S.xrow[2 * lane + 1] = x1;
+        bad = !(__builtin_isfinite(x0) && __builtin_isfinite(x1));  // beyond 65504 the fp16 sum is inf
     }
+    if (__ballot(bad) != 0ull && lane == 0) atomicOr(p.status, kNonFinite);
     static_assert(4 * kXRep <= 64, "one store per lane");
     if (lane < 4 * kXRep) {  // lane = copy * 4 + pair
         const int j = lane & 3;

@@ -474,7 +474,9 @@ __global__ __launch_bounds__(kThreads) void gemv_layer_kernel(LayerArgs a) {
     if (g_layer_trace && lane == 0)
         for (int i = 0; i < 8; ++i) g_layer_trace[((size_t)b * kWaves + wave) * 8 + i] = T_[i];
 #endif
-    if (threadIdx.x == 0) st_coh(ctr + b, step + 1u);
+    // the counter is kept reduced modulo 65535, so consecutive launches always carry different tags (a plain
+    // uint32 counter would wrap from 2^32 - 1 to 0, and both values give tag 1)
+    if (threadIdx.x == 0) st_coh(ctr + b, (step + 1u) % 65535u);
 }
 
 int layer_blocks() {

@@ -9,8 +9,9 @@ tail attached (one hipGraph = decode step + sample; the sampled token is the nex
 - generation stops at </audio> (tokens after it in the same frame are dropped, a frame queued after it is ignored),
   at max_new tokens or when the cache is full;
 - the one-launch step's status word is copied back with every frame (same event): a nonzero status (a wait that
-  timed out, so the step drained with garbage, or a position outside the cache) raises DecodeError after the
-  engine's exchange buffers are reset, instead of emitting tokens sampled from invalid logits;
+  timed out, so the step drained with garbage, a position outside the cache, or a residual sum beyond the fp16
+  range) raises DecodeError after the engine's exchange buffers are reset, instead of emitting tokens sampled from
+  invalid logits;
 - to_codes: audio token ids -> [1, Q, frames] Mimi codes, whole frames only, resynchronising on a broken codebook
   round robin (rumik_int4.py:310-324).
 The prompt: with a prefill.Prefill (all prompt rows of a layer at once: mm_int4 and the matrix-core causal
@@ -45,12 +46,13 @@ class Generator:
         if eng.graph is None:
             eng.capture()
 
-    @torch.inference_mode()
     def _fail(self, status, where):
         self.eng.reset()
         raise DecodeError(f"decode step status {status} ({where}): bit 1 = a cross-block wait timed out, bit 2 = "
-                          "position outside the cache; the engine's exchange buffers were reset")
+                          "position outside the cache, bit 3 = a residual sum left the fp16 range; the engine's "
+                          "exchange buffers were reset")
 
+    @torch.inference_mode()
     def prefill(self, ids):
         """Process the prompt; returns the first generated token (a device scalar, also in eng.tok / eng.out[0]).
         With a prefill.Prefill: all prompt rows per layer at once on the matrix cores, then the audio head and the

@@ -32,6 +32,7 @@ _SIGS = {
     "rk_mm_int4_g128": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "rk_mm_int4_plan": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
     "rk_read_only": ([_p, ctypes.c_size_t, _p, ctypes.c_size_t, _p, ctypes.c_size_t, _i, _i, _p, _p], _i),
+    "rk_read_only_ex": ([_p, ctypes.c_size_t, _p, ctypes.c_size_t, _p, ctypes.c_size_t, _i, _i, _i, _p, _p], _i),
     "rk_mm_int4_workspace_bytes": ([_i, _i, _i], ctypes.c_size_t),
     "rk_mm_int4_g128_ws": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, ctypes.c_size_t, _p], _i),
     "rk_mm_int4_g128_noalloc": ([_p, _i, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),

@@ -5,8 +5,10 @@ engine/check_fused.py:20-34).
 
 Tolerances: every activation is stored in fp16 and the step chains ~8 kernels per layer, so results are compared by
 norm-relative error / cosine: hidden state and logits within 1e-2 / 0.9999 per step on the small model, on the
-full-width model, at the benchmarked contexts (1024 / 2048 slots: all 64 attention splits, up to 32 slots per split)
-and for one whole 36-layer step at the last cache slot.
+full-width model, at the benchmarked contexts (1023 / 1030 slots: 32 / 33 attention splits of 32 slots; 2040 / 2046:
+all 64 splits) and for one whole 36-layer step at the last cache slot. The one-launch step's int8 head is also held
+to the GEMV bar on every logit: the head recomputed by the oracle over the kernel's own exported final hidden state
+`hn`, max relative error <= 1e-2 per output with the per-output conditioning floor (oracle.int4.cond_floor).
 """
 import numpy as np
 import pytest
@@ -74,6 +76,7 @@ def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph", dtyp
         if engine == "persistent":  # the exported final hidden state (the sampler's input)
             rh = O.parity_report(_np(eng.hn), h)
             assert rh["norm_rel"] < tol and rh["cosine"] > 0.9999, (s, rh)
+            _head_per_output(eng, w["head"])
         reps.append((rx, rl))
         assert rx["norm_rel"] < tol and rx["cosine"] > 0.9999, (s, rx)
         assert rl["norm_rel"] < tol and rl["cosine"] > 0.9999, (s, rl)
@@ -84,6 +87,17 @@ def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph", dtyp
         eng.kc[:, :, pos].copy_(torch.tensor(okc[:, :, pos]).to(dtype).to(dev))
         eng.vc[:, :, pos].copy_(torch.tensor(ovc[:, :, pos]).to(dtype).to(dev))
     return reps
+
+
+def _head_per_output(eng, head):
+    """the one-launch step's int8 head against the oracle's over the kernel's own hn, on every logit: max relative
+    error <= 1e-2 with the per-output conditioning floor (the GEMV bar; reference kernels/cuda_gemv.py:245-249)"""
+    hq, hs = (t.cpu().numpy() for t in head)
+    hn = _np(eng.hn)
+    ref = O.gemv_int8_rows_f64(hn, hq, hs, "s8")
+    rep = O.parity_report(_np(eng.logits), ref, O.cond_floor(O.gemv_int8_abs(hn, hq, hs, "s8")))
+    assert rep["max_rel"] <= 1e-2 and rep["n"] == hq.shape[0], rep
+    return rep
 
 
 SMALL = dict(L=3, H=256, NH=4, NKV=2, HD=128, inter=384, S=64, n_audio=100, vocab=50, nsplit=8)
@@ -189,11 +203,47 @@ def test_persistent_step_with_sampler_token_loop(dev):
         eng.vc[:, :, ctx + s].copy_(torch.tensor(ovc[:, :, ctx + s]).to(dev))
 
 
+def test_persistent_fp16_overflow_sets_status(dev):
+    """The one-launch step is fp16 end to end (the reference engine is bf16): a residual sum beyond 65504 becomes
+    inf. Forced from the host: the token's embedding scale is set so that the embedding row itself overflows. The
+    step must still finish normally (no wait times out, pos advances) and report status bit 3 (value 8); a finite
+    step on a normal token reports 0."""
+    cfg = decode.Config(L=2, vocab=16, n_audio=64, S=64)
+    w = decode.random_weights(cfg, 3, device=dev, gen_device="cuda")
+    w["emb"][1][5] = 60000.0  # fp16 scale: 127 * 60000 is far beyond the fp16 range
+    eng = decode.PersistentDecode(cfg, w, device=dev)
+    eng.set_state(4, 3)
+    eng.step()
+    torch.cuda.synchronize()
+    assert eng.status_word() == 0 and int(eng.pos.item()) == 4
+    eng.set_state(5, 4)
+    eng.step()
+    torch.cuda.synchronize()
+    st = eng.status_word()
+    assert st & 8 and not st & 3, st
+    assert int(eng.pos.item()) == 5
+    eng.reset()
+    eng.set_state(4, 3)  # slots 0..3 only: slot 4 now holds the overflowed step's K / V
+    eng.step()
+    torch.cuda.synchronize()
+    assert eng.status_word() == 0
+
+
+@pytest.mark.parametrize("n_audio", [16321, 16384, 257])
+def test_persistent_head_ragged_tail(n_audio, dev):
+    """The one-launch step's int8 head splits its rows over the blocks in runs of ceil(n_audio / blocks): 16321 leaves
+    the last block one row, 16384 fills every block exactly (64 rows), 257 gives 128 blocks two rows, one block a
+    single row and the rest none. Every logit is checked against the head over the kernel's own hn."""
+    cfg = decode.Config(L=1, vocab=32, n_audio=n_audio, S=64)
+    _run(cfg, dev, ctx=10, steps=1, use_graph=False, engine="persistent", seed=50 + n_audio % 11)
+
+
 @pytest.mark.parametrize("ctx", [1023, 1030, 2040, 2046])
 def test_persistent_long_contexts(ctx, dev):
-    """The contexts the benchmark times: the full 2048-slot cache with 64 splits per KV head. At ctx 1023 all 64
-    splits hold 16 slots, at 1030 43 splits hold 24, at 2040 / 2046 all 64 hold 32 (every prefetched K / V slot of
-    a streamer is used, and the 64-split combine runs in every head's blocks). Two steps each, both checked."""
+    """The contexts the benchmark times, on the full 2048-slot cache (at most 64 splits per KV head, at least 32
+    slots per split): ctx 1023 / 1030 (the first step attends over 1024 / 1031 slots) use 32 / 33 splits of 32 slots,
+    2040 / 2046 all 64 splits of 32 (every prefetched K / V slot of a split is used, and the 64-split combine runs in
+    every head's blocks). Two steps each, both checked."""
     cfg = decode.Config(L=2, vocab=64, sliding=[True, False])
     reps = _run(cfg, dev, ctx=ctx, steps=2, use_graph=True, engine="persistent", seed=40 + ctx % 7)
     print(ctx, reps[-1])
@@ -231,3 +281,4 @@ def test_persistent_36_layers_at_last_slot(dev):
         rep = O.parity_report(_np(got).ravel(), np.asarray(ref, np.float32).ravel())
         print(name, rep)
         assert rep["norm_rel"] < 1e-2 and rep["cosine"] > 0.9999, (name, rep)
+    print("head per output", _head_per_output(eng, wc["head"]))

@@ -328,6 +328,73 @@ typedef struct rk_decode_limits {
 
 int rk_decode_get_limits(rk_decode_limits* out);
 
+/* ------------------------------------------------------------------------------------------------------------
+ * The same decode step as ONE launch with the grid split by role (replaces the same reference code as
+ * rk_decode_step_persistent: RumikFused._step, engine/rumik_fused.py:97-121, with _logits :84-89). 256 blocks of
+ * 1024 threads (one per CU, co-residency checked). Latency blocks (64, role kind 0, index j): residual rows
+ * [32j, 32j + 32), q/k/v tiles [nq j, nq j + nq) (nq = (NH + 2 NKV) * 8 / 64), attention split j % (64 / NKV) of KV
+ * head j / (64 / NKV), the combine of head j / 4 and its o slice for rows [512 (j % 4), + 512). Stream blocks (192,
+ * kind 1, index i): MLP slices [sb, se) of 16 channels (their gate / up tiles and w_down columns; a contiguous
+ * partition of the inter / 16 slices, at most 4 per block) and int8 head rows i + 192 (w + 16 k). role[b] =
+ * {kind, index, sb, se} for block b (sb = se = 0 for latency blocks); every index exactly once.
+ * Shapes: NH * 128 == 2048, NKV 4 or 8, inter a multiple of 128 with at most 4 slices per stream block,
+ * 1 <= n_audio <= 192 * 16 * 64; nsp (splits per KV head) <= min(16, 64 / NKV) and S <= nsp * 128; min_chunk (the
+ * fewest slots per split) a positive multiple of 8 (RK_ERR_SHAPE / RK_ERR_BLOCK otherwise).
+ * Weights as for rk_decode_step_persistent (win_t, wo_q, wd_t, wd_sm, ln_w, norm_w, emb, head unchanged), except
+ * win_sm: per (layer, tile, 128-column group, row) the word scale | min << 16, and wo_sm: per (layer, head, row).
+ * Exchange buffers have two halves (even / odd layers), all tagged words as for rk_decode_step_persistent:
+ *   tx [2][16 copies][2048]; tq [2][NH*128]; tkv [2][2][NKV*128]; tpo [2][NH][nsp][128]; tml [2][NH][nsp][2];
+ *   top [2][64 latency blocks][NH][32 rows]; tdp [2][64 latency blocks][192 stream blocks][32 rows].
+ * All of them, ctr [256] and status start at zero; after a nonzero status, re-zero them. Status bits as for
+ * rk_decode_step_persistent (1 wait timed out, 2 pos outside [0, S), 3 residual beyond the fp16 range). */
+typedef struct rk_decode_roles_params {
+    int L, NH, NKV, inter, S, n_audio, nsp, min_chunk;
+    float eps, scale;
+    unsigned long long sliding; /* bit l set: RoPE on layer l */
+    const int64_t* tok;
+    int64_t* pos;
+    const int8_t* emb_q;
+    const uint16_t* emb_s;
+    const uint8_t* win_t;   /* [L, n_in/16, 16 groups, 64 lanes, 16 B] */
+    const uint32_t* win_sm; /* [L, n_in/16, 16 groups, 16 rows] */
+    const uint8_t* wo_q;    /* [L, NH, 4 quarters, 2048 items, 16 B] */
+    const uint32_t* wo_sm;  /* [L, NH, 2048] */
+    const uint8_t* wd_t;    /* [L, inter/16, 2048, 8 B] */
+    const uint32_t* wd_sm;  /* [L, inter/128, 2048] */
+    const uint16_t* ln_w;   /* [L, 2048] fp16 */
+    const uint16_t* norm_w;
+    const uint16_t* cos_t;  /* [S, 128] fp16 */
+    const uint16_t* sin_t;
+    uint16_t* kc;           /* [L, NKV, S, 128] fp16 */
+    uint16_t* vc;
+    const int8_t* head_q;   /* [n_audio, 2048] */
+    const uint16_t* head_s;
+    float* logits;
+    const int16_t* role;    /* [256, 4] */
+    uint32_t* tx;
+    uint32_t* tq;
+    uint32_t* tkv;
+    uint32_t* tpo;
+    unsigned long long* tml;
+    uint32_t* top;
+    uint32_t* tdp;
+    unsigned* ctr;
+    unsigned* status;
+    uint16_t* hn;           /* [2048] fp16 final LayerNorm output, or NULL */
+} rk_decode_roles_params;
+
+int rk_decode_step_roles(const rk_decode_roles_params* params, rk_stream_t stream);
+
+/* sizeof(rk_decode_roles_params) as compiled */
+int rk_decode_roles_params_size(void);
+
+/* the role-split step's compiled limits (host-only query) */
+typedef struct rk_decode_roles_limits {
+    int blocks, latency_blocks, max_slices, x_copies, max_splits, slots_per_wave, waves;
+} rk_decode_roles_limits;
+
+int rk_decode_roles_get_limits(rk_decode_roles_limits* out);
+
 /* pos[0] += 1 on the device (the `self.pos += 1` of the captured step, reference engine/rumik_fused.py:120). */
 int rk_pos_advance(int64_t* pos, rk_stream_t stream);
 

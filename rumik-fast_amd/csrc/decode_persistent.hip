@@ -843,7 +843,11 @@ RK_DEV void attention(const Params& p, int64_t pos, const KVRegs& kv, const QReg
     for (int r = 0; r < REP; ++r) acc[r] = make_float2(0.f, 0.f);
 #pragma unroll
     for (int uu = 0; uu < kSlotsPerWave; ++uu) {
-        const h2_t vp = as_h2(slot_of(s, a, uu) == pos ? qr.vnew : kv.v[uu]);
+        // slots past the split's end are selected away, not multiplied by p = 0: whatever a cache slot beyond pos
+        // holds (a NaN left by an overflowed step included) must not reach the result, as with the reference's
+        // masked loads (other = 0)
+        const int su = slot_of(s, a, uu);
+        const h2_t vp = as_h2(su == pos ? qr.vnew : (su < s.end ? kv.v[uu] : 0u));
         const float v0 = (float)vp.x, v1 = (float)vp.y;
 #pragma unroll
         for (int r = 0; r < REP; ++r) {

@@ -291,7 +291,72 @@ def validate_work_table(table, cfg, lim=None):
         raise ValueError("every w_in tile must be listed exactly once")
 
 
-class PersistentDecode:
+class _OneLaunch:
+    """What the one-launch engines share: state, cache filling, the sampling tail in the captured step, capture /
+    replay and the status word. Subclasses set kc, vc, tok, pos, logits, hn, status, the exchange buffers
+    (`_exchange`) and `_launch()`."""
+
+    def reset(self):
+        """Zero the exchange buffers, step counters and status (needed after a nonzero status)."""
+        for t in self._exchange:
+            t.zero_()
+
+    def set_state(self, tok: int, pos: int):
+        self.tok.fill_(tok)
+        self.pos.fill_(pos)
+
+    def fill_cache(self, ctx: int, seed: int = 0):
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        self.kc[:, :, :ctx].normal_(generator=g)
+        self.vc[:, :, :ctx].normal_(generator=g)
+
+    def attach_sampler(self, stop, audio_ids, end_id, top_k=30, min_new=8, temperature=0.8, max_new=1800):
+        """Sample the next token inside the step (reference engine/rumik_fused.py:92-94, engine/sample.py): after
+        the int8 head, the fused sampling tail reads `logits` and `hn`, writes out[step_i] and `tok` (the next
+        step's input token) and advances step_i, so replaying the captured step generates tokens autoregressively
+        on the device. `stop`: the stop predictor's state dict (0.weight, 0.bias, 1.weight, 1.bias, 3.weight,
+        3.bias); `audio_ids` [n_audio] int64 maps head rows to token ids."""
+        import sample
+        self.H = self.cfg.H
+        self.stop = {k: v.to(self.dev) for k, v in stop.items()}
+        self.audio_ids = audio_ids.to(self.dev, torch.int64).contiguous()
+        self.end_id, self.top_k, self.min_new, self.temperature = int(end_id), int(top_k), int(min_new), float(temperature)
+        self.step_i = torch.zeros(1, dtype=torch.int64, device=self.dev)
+        self.out = torch.zeros(max_new + 8, dtype=torch.int64, device=self.dev)
+        self.sampler = sample.FusedSampler(self, lambda: self.logits)
+        return self.sampler
+
+    def step(self):
+        self._launch()
+        if self.sampler is not None:
+            self.sampler()
+
+    def capture(self):
+        saved = [self.kc.clone(), self.vc.clone(), self.pos.clone(), self.tok.clone()]
+        if self.sampler is not None:
+            saved += [self.step_i.clone(), self.out.clone()]
+        self.step()
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        torch.cuda.synchronize(self.dev)
+        self.kc.copy_(saved[0]); self.vc.copy_(saved[1]); self.pos.copy_(saved[2]); self.tok.copy_(saved[3])
+        if self.sampler is not None:
+            self.step_i.copy_(saved[4]); self.out.copy_(saved[5])
+        torch.cuda.synchronize(self.dev)
+        self.graph = g
+        return g
+
+    def replay(self):
+        self.graph.replay()
+
+    def status_word(self) -> int:
+        """0 when every wait of every step so far completed in time."""
+        return int(self.status.item())
+
+
+class PersistentDecode(_OneLaunch):
     """The decode step as one persistent kernel launch (csrc/decode_persistent.hip). Same weights, state and
     outputs as DecodeStep; needs hidden 2048 and head dim 128 and one block per 8 rows of the hidden state
     (256 blocks, one per CU on MI355X). `weights` as from random_weights; they are re-laid out once (stacked over
@@ -366,62 +431,148 @@ class PersistentDecode:
         """the residual stream after the last layer of the last step (fp16, decoded from the tagged words)"""
         return self.tx[:2048].view(torch.float16)[0::2]
 
-    def reset(self):
-        """Zero the exchange buffers, step counters and status (needed after a nonzero status)."""
-        for t in (self.tx, self.tq, self.tkv, self.top, self.tdp, self.tpo, self.tml, self.ctr, self.status):
-            t.zero_()
+    @property
+    def _exchange(self):
+        return (self.tx, self.tq, self.tkv, self.top, self.tdp, self.tpo, self.tml, self.ctr, self.status)
 
-    def set_state(self, tok: int, pos: int):
-        self.tok.fill_(tok)
-        self.pos.fill_(pos)
-
-    def fill_cache(self, ctx: int, seed: int = 0):
-        g = torch.Generator(device=self.dev).manual_seed(seed)
-        self.kc[:, :, :ctx].normal_(generator=g)
-        self.vc[:, :, :ctx].normal_(generator=g)
-
-    def attach_sampler(self, stop, audio_ids, end_id, top_k=30, min_new=8, temperature=0.8, max_new=1800):
-        """Sample the next token inside the step (reference engine/rumik_fused.py:92-94, engine/sample.py): after
-        the int8 head, the fused sampling tail reads `logits` and `hn`, writes out[step_i] and `tok` (the next
-        step's input token) and advances step_i, so replaying the captured step generates tokens autoregressively
-        on the device. `stop`: the stop predictor's state dict (0.weight, 0.bias, 1.weight, 1.bias, 3.weight,
-        3.bias); `audio_ids` [n_audio] int64 maps head rows to token ids."""
-        import sample
-        self.H = self.cfg.H
-        self.stop = {k: v.to(self.dev) for k, v in stop.items()}
-        self.audio_ids = audio_ids.to(self.dev, torch.int64).contiguous()
-        self.end_id, self.top_k, self.min_new, self.temperature = int(end_id), int(top_k), int(min_new), float(temperature)
-        self.step_i = torch.zeros(1, dtype=torch.int64, device=self.dev)
-        self.out = torch.zeros(max_new + 8, dtype=torch.int64, device=self.dev)
-        self.sampler = sample.FusedSampler(self, lambda: self.logits)
-        return self.sampler
-
-    def step(self):
+    def _launch(self):
         HL.check(HL.lib().rk_decode_step_persistent(ctypes.byref(self.params), self.nblocks, HL.stream(self.dev)),
                  "decode_step_persistent")
-        if self.sampler is not None:
-            self.sampler()
 
-    def capture(self):
-        saved = [self.kc.clone(), self.vc.clone(), self.pos.clone(), self.tok.clone()]
-        if self.sampler is not None:
-            saved += [self.step_i.clone(), self.out.clone()]
-        self.step()
-        torch.cuda.synchronize(self.dev)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self.step()
-        torch.cuda.synchronize(self.dev)
-        self.kc.copy_(saved[0]); self.vc.copy_(saved[1]); self.pos.copy_(saved[2]); self.tok.copy_(saved[3])
-        if self.sampler is not None:
-            self.step_i.copy_(saved[4]); self.out.copy_(saved[5])
-        torch.cuda.synchronize(self.dev)
-        self.graph = g
-        return g
 
-    def replay(self):
-        self.graph.replay()
+# ---------------------------------------------------------------------------------------------- role-split step
+class RkDecodeRolesParams(ctypes.Structure):
+    """ctypes mirror of rk_decode_roles_params (include/rumik_hip.h); its size is checked against the library."""
+    _fields_ = [(n, ctypes.c_int) for n in ("L", "NH", "NKV", "inter", "S", "n_audio", "nsp", "min_chunk")] + [
+        ("eps", ctypes.c_float), ("scale", ctypes.c_float), ("sliding", ctypes.c_ulonglong)] + [
+        (n, ctypes.c_void_p) for n in (
+            "tok", "pos", "emb_q", "emb_s", "win_t", "win_sm", "wo_q", "wo_sm", "wd_t", "wd_sm", "ln_w", "norm_w",
+            "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "role", "tx", "tq", "tkv", "tpo", "tml",
+            "top", "tdp", "ctr", "status", "hn")]
 
-    def status_word(self) -> int:
-        """0 when every wait of every step so far completed in time."""
-        return int(self.status.item())
+
+class RkDecodeRolesLimits(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("blocks", "latency_blocks", "max_slices", "x_copies", "max_splits",
+                                            "slots_per_wave", "waves")]
+
+
+def roles_limits() -> RkDecodeRolesLimits:
+    """The role-split kernel's compiled limits (a host-only query: no GPU needed)."""
+    lim = RkDecodeRolesLimits()
+    HL.check(HL.lib().rk_decode_roles_get_limits(ctypes.byref(lim)), "decode_roles_get_limits")
+    return lim
+
+
+def group_scale_min(sm):
+    """per-(row, group) scale | min words [n_in, 16] -> per (tile, group, row): int32 [n_in / 16, 16, 16]."""
+    return sm.reshape(sm.shape[0] // 16, 16, -1).permute(0, 2, 1).contiguous()
+
+
+def role_table(cfg, lim=None):
+    """Block -> role for the role-split step: int16 [blocks, 4] = (kind, index, slice begin, slice end).
+    Latency blocks (kind 0): the blocks b with (b // 8) % 4 == 0 (8 on each XCD: block b runs on XCD b % 8),
+    numbered in block order. Stream blocks (kind 1): the others, numbered XCD by XCD (the 24 of XCD x get indices
+    24x .. 24x + 23), so stream blocks with neighbouring MLP slices, which share w_down scale rows, sit on one XCD
+    and its L2; stream block i takes slices [i * n / 192, (i + 1) * n / 192) of the n = inter / 16."""
+    lim = lim or roles_limits()
+    nb, nl = lim.blocks, lim.latency_blocks
+    ns = nb - nl
+    nsl = cfg.inter // 16
+    if -(-nsl // ns) > lim.max_slices:
+        raise ValueError("too many MLP slices per stream block")
+    table = torch.zeros(nb, 4, dtype=torch.int16)
+    lat = [b for b in range(nb) if (b // 8) % 4 == 0]
+    if len(lat) != nl:
+        raise ValueError("latency block placement does not match the kernel")
+    for j, b in enumerate(lat):
+        table[b] = torch.tensor([0, j, 0, 0], dtype=torch.int16)
+    stream = sorted((b for b in range(nb) if (b // 8) % 4 != 0), key=lambda b: (b % 8, b))
+    for i, b in enumerate(stream):
+        table[b] = torch.tensor([1, i, i * nsl // ns, (i + 1) * nsl // ns], dtype=torch.int16)
+    return table
+
+
+class RoleDecode(_OneLaunch):
+    """The decode step as one persistent launch with the grid split by role (csrc/decode_roles.hip): 64 latency
+    blocks run the step's chain (x, LayerNorm, q/k/v, attention, combine, o, the residual rows), 192 stream blocks
+    the MLP (gate / up, SiLU, down) and the int8 head. Same weights, state and outputs as DecodeStep and
+    PersistentDecode; hidden 2048, head dim 128, 16 query heads with 4 or 8 KV heads, 256 CUs.
+    nsp: attention splits per KV head (default min(16, 64 / NKV)); min_chunk: the fewest cache slots per split."""
+
+    def __init__(self, cfg: Config, weights, device="cuda", nsp=None, min_chunk=32, keep_layer_weights=False):
+        if cfg.H != 2048 or cfg.HD != 128 or cfg.NH * cfg.HD != 2048 or cfg.NKV not in (4, 8):
+            raise ValueError("the role-split step is built for hidden 2048 / head dim 128 / 16 q and 4 or 8 kv heads")
+        self.cfg, self.dev = cfg, torch.device(device)
+        d = self.dev
+        lib = HL.lib()
+        if lib.rk_decode_roles_params_size() != ctypes.sizeof(RkDecodeRolesParams):
+            raise RuntimeError("rk_decode_roles_params layout mismatch between the library and decode.py")
+        self.limits = roles_limits()
+        nl, ns = self.limits.latency_blocks, self.limits.blocks - self.limits.latency_blocks
+        self.nblocks = self.limits.blocks
+        self.nsp = nsp or min(self.limits.max_splits, nl // cfg.NKV)
+        if self.nsp > min(self.limits.max_splits, nl // cfg.NKV) or -(-cfg.S // self.nsp) > \
+                self.limits.waves * self.limits.slots_per_wave:
+            raise ValueError("cache length / attention splits beyond the kernel's limits")
+        w, c = weights, cfg
+        stack = lambda f, key: torch.stack([f(t) for t in w[key]]).contiguous()  # noqa: E731
+        self.win_t = stack(lambda t: tile_layout(interleave_gate_up(t[0], c)), "w_in")
+        self.win_sm = stack(lambda t: group_scale_min(pack_scale_min(interleave_gate_up(t[1], c),
+                                                                     interleave_gate_up(t[2], c))), "w_in")
+        self.wo_q = stack(lambda t: o_layout(t[0], c.NH), "w_o")
+        self.wo_sm = stack(lambda t: pack_scale_min(t[1], t[2]).t().contiguous(), "w_o")
+        self.wd_t = stack(lambda t: down_layout(t[0]), "w_down")
+        self.wd_sm = stack(lambda t: pack_scale_min(t[1], t[2]).t().contiguous(), "w_down")
+        self.ln = torch.stack(w["ln"]).contiguous()
+        self.norm, self.emb, self.head = w["norm"], w["emb"], w["head"]
+        if not keep_layer_weights:
+            for k in ("w_in", "w_o", "w_down"):
+                w[k].clear()
+        self.role = role_table(c, self.limits).to(d)
+        i32 = torch.int32
+        xr = self.limits.x_copies
+        self.tx = torch.zeros(2, xr, 2048, dtype=i32, device=d)
+        self.tq = torch.zeros(2, c.NH * c.HD, dtype=i32, device=d)
+        self.tkv = torch.zeros(2, 2, c.NKV * c.HD, dtype=i32, device=d)
+        self.tpo = torch.zeros(2, c.NH, self.nsp, c.HD, dtype=i32, device=d)
+        self.tml = torch.zeros(2, c.NH, self.nsp, 2, dtype=torch.int64, device=d)
+        self.top = torch.zeros(2, nl, c.NH, 32, dtype=i32, device=d)
+        self.tdp = torch.zeros(2, nl, ns, 32, dtype=i32, device=d)
+        self.ctr = torch.zeros(self.nblocks, dtype=i32, device=d)
+        self.status = torch.zeros(1, dtype=i32, device=d)
+        self.logits = torch.zeros(c.n_audio, dtype=torch.float32, device=d)
+        self.hn = torch.zeros(c.H, dtype=torch.float16, device=d)
+        self.kc = torch.zeros(c.L, c.NKV, c.S, c.HD, dtype=torch.float16, device=d)
+        self.vc = torch.zeros_like(self.kc)
+        self.tok = torch.zeros(1, dtype=torch.int64, device=d)
+        self.pos = torch.zeros(1, dtype=torch.int64, device=d)
+        self.cos, self.sin = rope_tables(c.S, c.HD, c.rope_theta, torch.float16, d)
+        sliding = sum(1 << i for i, on in enumerate(c.sliding) if on)
+        P = RkDecodeRolesParams(L=c.L, NH=c.NH, NKV=c.NKV, inter=c.inter, S=c.S, n_audio=c.n_audio, nsp=self.nsp,
+                                min_chunk=int(min_chunk), eps=c.eps, scale=c.HD ** -0.5, sliding=sliding)
+        for name, t in (("tok", self.tok), ("pos", self.pos), ("emb_q", self.emb[0]), ("emb_s", self.emb[1]),
+                        ("win_t", self.win_t), ("win_sm", self.win_sm), ("wo_q", self.wo_q), ("wo_sm", self.wo_sm),
+                        ("wd_t", self.wd_t), ("wd_sm", self.wd_sm), ("ln_w", self.ln), ("norm_w", self.norm),
+                        ("cos_t", self.cos), ("sin_t", self.sin), ("kc", self.kc), ("vc", self.vc),
+                        ("head_q", self.head[0]), ("head_s", self.head[1]), ("logits", self.logits),
+                        ("role", self.role), ("tx", self.tx), ("tq", self.tq), ("tkv", self.tkv), ("tpo", self.tpo),
+                        ("tml", self.tml), ("top", self.top), ("tdp", self.tdp), ("ctr", self.ctr),
+                        ("status", self.status), ("hn", self.hn)):
+            if not t.is_contiguous() or t.device != d:
+                raise RuntimeError(f"{name} must be a contiguous tensor on {d}")
+            setattr(P, name, t.data_ptr())
+        self.params = P
+        self.graph = None
+        self.sampler = None
+
+    @property
+    def x(self):
+        """the residual stream after the last layer of the last step (fp16, decoded from the tagged words)"""
+        return self.tx[self.cfg.L & 1, 0].view(torch.float16)[0::2]
+
+    @property
+    def _exchange(self):
+        return (self.tx, self.tq, self.tkv, self.tpo, self.tml, self.top, self.tdp, self.ctr, self.status)
+
+    def _launch(self):
+        HL.check(HL.lib().rk_decode_step_roles(ctypes.byref(self.params), HL.stream(self.dev)), "decode_step_roles")

@@ -20,6 +20,15 @@ from oracle import int4 as O
 
 pytestmark = pytest.mark.gpu
 
+# the two one-launch engines: every block doing every role (csrc/decode_persistent.hip) and the grid split into
+# latency and stream blocks (csrc/decode_roles.hip)
+ONE_LAUNCH = ["persistent", "roles"]
+
+
+def _one_launch(engine, cfg, w, dev):
+    return (decode.PersistentDecode(cfg, w, device=dev) if engine == "persistent"
+            else decode.RoleDecode(cfg, w, device=dev))
+
 
 def _np(t):
     return t.detach().float().cpu().numpy()
@@ -47,7 +56,7 @@ def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph", dtyp
               if isinstance(vv, list) else (tuple(t.to(dev) for t in vv) if isinstance(vv, tuple) else vv.to(dev)))
           for k, vv in w.items()}
     eng = (decode.DecodeStep(cfg, wd, device=dev, dtype=dtype) if engine == "graph"
-           else decode.PersistentDecode(cfg, wd, device=dev))
+           else _one_launch(engine, cfg, wd, dev))
     g = torch.Generator().manual_seed(seed + 1)
     kc = torch.zeros(cfg.L, cfg.NKV, cfg.S, cfg.HD, dtype=dtype)
     kc[:, :, :ctx] = torch.randn(cfg.L, cfg.NKV, ctx, cfg.HD, generator=g).to(dtype)
@@ -69,11 +78,11 @@ def _run(cfg, dev, ctx, steps, use_graph, seed=4, tol=1e-2, engine="graph", dtyp
         torch.cuda.synchronize()
         logits, h, x = OG.decode_step(md, tok, pos, okc, ovc, dt=odt)
         assert int(eng.pos.item()) == pos + 1
-        if engine == "persistent":
+        if engine != "graph":
             assert eng.status_word() == 0, "a grid barrier timed out"
         rx = O.parity_report(_np(eng.x), x)
         rl = O.parity_report(_np(eng.logits), logits)
-        if engine == "persistent":  # the exported final hidden state (the sampler's input)
+        if engine != "graph":  # the exported final hidden state (the sampler's input)
             rh = O.parity_report(_np(eng.hn), h)
             assert rh["norm_rel"] < tol and rh["cosine"] > 0.9999, (s, rh)
             _head_per_output(eng, w["head"])
@@ -131,22 +140,26 @@ def test_full_width_four_layers(dev):
     print(reps[-1])
 
 
+@pytest.mark.parametrize("engine", ONE_LAUNCH)
 @pytest.mark.parametrize("use_graph", [False, True])
-def test_persistent_full_width(use_graph, dev):
+def test_persistent_full_width(use_graph, engine, dev):
     # the one-launch step: hidden 2048, 16 / 4 heads, MLP 11008, 3 layers (one of them NoPE), ctx 300
     cfg = decode.Config(L=3, vocab=64, sliding=[True, False, True])
-    reps = _run(cfg, dev, ctx=300, steps=3, use_graph=use_graph, engine="persistent")
+    reps = _run(cfg, dev, ctx=300, steps=3, use_graph=use_graph, engine=engine)
     print(reps[-1])
 
 
-def test_persistent_small_mlp_and_ctx_edges(dev):
-    # inter 2048, contexts at the edges: first slot and the last slot of the cache
+@pytest.mark.parametrize("engine", ONE_LAUNCH)
+def test_persistent_small_mlp_and_ctx_edges(engine, dev):
+    # inter 2048, contexts at the edges: first slot and the last slot of the cache (the role-split step: 128 MLP
+    # slices over 192 stream blocks, so 64 of them hold none)
     cfg = decode.Config(L=2, inter=2048, S=256, vocab=32, n_audio=1000)
-    _run(cfg, dev, ctx=0, steps=2, use_graph=True, engine="persistent")
-    _run(cfg, dev, ctx=254, steps=2, use_graph=False, engine="persistent")
+    _run(cfg, dev, ctx=0, steps=2, use_graph=True, engine=engine)
+    _run(cfg, dev, ctx=254, steps=2, use_graph=False, engine=engine)
 
 
-def test_persistent_step_with_sampler_token_loop(dev):
+@pytest.mark.parametrize("engine", ONE_LAUNCH)
+def test_persistent_step_with_sampler_token_loop(engine, dev):
     """Decode step + sampling tail in one captured graph (reference engine/rumik_fused.py:92-94): each replay's
     sampled token is the next replay's input. Per replay: the token is the sampling oracle's pick on the step's own
     logits / hidden state and uniforms (oracle/sample.py), and the step itself matches the decode oracle run on the
@@ -158,7 +171,7 @@ def test_persistent_step_with_sampler_token_loop(dev):
     wd = {k: ([tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev) for v in vv]
               if isinstance(vv, list) else (tuple(t.to(dev) for t in vv) if isinstance(vv, tuple) else vv.to(dev)))
           for k, vv in w.items()}
-    eng = decode.PersistentDecode(cfg, wd, device=dev)
+    eng = _one_launch(engine, cfg, wd, dev)
     g = torch.Generator().manual_seed(9)
     stop = {"0.weight": torch.ones(cfg.H), "0.bias": torch.zeros(cfg.H),
             "1.weight": (torch.randn(512, cfg.H, generator=g) / cfg.H ** 0.5).bfloat16(),
@@ -203,7 +216,8 @@ def test_persistent_step_with_sampler_token_loop(dev):
         eng.vc[:, :, ctx + s].copy_(torch.tensor(ovc[:, :, ctx + s]).to(dev))
 
 
-def test_persistent_fp16_overflow_sets_status(dev):
+@pytest.mark.parametrize("engine", ONE_LAUNCH)
+def test_persistent_fp16_overflow_sets_status(engine, dev):
     """The one-launch step is fp16 end to end (the reference engine is bf16): a residual sum beyond 65504 becomes
     inf. Forced from the host: the token's embedding scale is set so that the embedding row itself overflows. The
     step must still finish normally (no wait times out, pos advances) and report status bit 3 (value 8); a finite
@@ -211,7 +225,7 @@ def test_persistent_fp16_overflow_sets_status(dev):
     cfg = decode.Config(L=2, vocab=16, n_audio=64, S=64)
     w = decode.random_weights(cfg, 3, device=dev, gen_device="cuda")
     w["emb"][1][5] = 60000.0  # fp16 scale: 127 * 60000 is far beyond the fp16 range
-    eng = decode.PersistentDecode(cfg, w, device=dev)
+    eng = _one_launch(engine, cfg, w, dev)
     eng.set_state(4, 3)
     eng.step()
     torch.cuda.synchronize()
@@ -229,23 +243,25 @@ def test_persistent_fp16_overflow_sets_status(dev):
     assert eng.status_word() == 0
 
 
+@pytest.mark.parametrize("engine", ONE_LAUNCH)
 @pytest.mark.parametrize("n_audio", [16321, 16384, 257])
-def test_persistent_head_ragged_tail(n_audio, dev):
+def test_persistent_head_ragged_tail(n_audio, engine, dev):
     """The one-launch step's int8 head splits its rows over the blocks in runs of ceil(n_audio / blocks): 16321 leaves
     the last block one row, 16384 fills every block exactly (64 rows), 257 gives 128 blocks two rows, one block a
     single row and the rest none. Every logit is checked against the head over the kernel's own hn."""
     cfg = decode.Config(L=1, vocab=32, n_audio=n_audio, S=64)
-    _run(cfg, dev, ctx=10, steps=1, use_graph=False, engine="persistent", seed=50 + n_audio % 11)
+    _run(cfg, dev, ctx=10, steps=1, use_graph=False, engine=engine, seed=50 + n_audio % 11)
 
 
+@pytest.mark.parametrize("engine", ONE_LAUNCH)
 @pytest.mark.parametrize("ctx", [1023, 1030, 2040, 2046])
-def test_persistent_long_contexts(ctx, dev):
+def test_persistent_long_contexts(ctx, engine, dev):
     """The contexts the benchmark times, on the full 2048-slot cache (at most 64 splits per KV head, at least 32
     slots per split): ctx 1023 / 1030 (the first step attends over 1024 / 1031 slots) use 32 / 33 splits of 32 slots,
     2040 / 2046 all 64 splits of 32 (every prefetched K / V slot of a split is used, and the 64-split combine runs in
     every head's blocks). Two steps each, both checked."""
     cfg = decode.Config(L=2, vocab=64, sliding=[True, False])
-    reps = _run(cfg, dev, ctx=ctx, steps=2, use_graph=True, engine="persistent", seed=40 + ctx % 7)
+    reps = _run(cfg, dev, ctx=ctx, steps=2, use_graph=True, engine=engine, seed=40 + ctx % 7)
     print(ctx, reps[-1])
 
 
@@ -256,14 +272,15 @@ def _cpu(w):
 
 
 @pytest.mark.timeout(900)
-def test_persistent_36_layers_at_last_slot(dev):
+@pytest.mark.parametrize("engine", ONE_LAUNCH)
+def test_persistent_36_layers_at_last_slot(engine, dev):
     """Config 4's whole step: 36 full-width layers (RoPE on 3 of every 4), the int8 head over 16385 rows, the
     2048-slot cache filled to 2047 slots, one step at pos 2047 (the benchmark's ctx 2048). x, the final hidden state,
     the logits and the new K / V slot of every layer against the decode oracle."""
     cfg = decode.Config(vocab=64)
     w = decode.random_weights(cfg, 6, device=dev, gen_device="cuda")
     wc = _cpu(w)
-    eng = decode.PersistentDecode(cfg, w, device=dev)
+    eng = _one_launch(engine, cfg, w, dev)
     pos = cfg.S - 1
     g = torch.Generator(device=dev).manual_seed(7)
     eng.kc[:, :, :pos].normal_(generator=g)

@@ -132,3 +132,57 @@ def test_interleave_gate_up_rows():
     assert r[:a] == list(range(a))
     # per 8 channels: 8 gate rows then the 8 matching up rows
     assert r[a:a + 16] == list(range(a, a + 8)) + list(range(a + cfg.inter, a + cfg.inter + 8))
+
+
+# ---------------------------------------------------------------------------------------------- role-split step
+@pytest.mark.parametrize("inter", [11008, 2048, 128])
+def test_role_table_partitions_the_work(inter):
+    """64 latency blocks, 8 on each XCD (block b runs on XCD b % 8), numbered 0..63 once each; 192 stream blocks
+    numbered 0..191 once each, XCD by XCD, whose MLP slices form a contiguous partition of inter / 16 with at most
+    max_slices each (stream blocks may hold none when the MLP is narrow)."""
+    lim = decode.roles_limits()
+    cfg = decode.Config(inter=inter)
+    t = decode.role_table(cfg, lim)
+    assert t.shape == (lim.blocks, 4)
+    kind, idx, sb, se = (t[:, i].tolist() for i in range(4))
+    lat = [b for b in range(lim.blocks) if kind[b] == 0]
+    assert len(lat) == lim.latency_blocks
+    assert sorted(idx[b] for b in lat) == list(range(lim.latency_blocks))
+    assert all(sum(1 for b in lat if b % 8 == x) == lim.latency_blocks // 8 for x in range(8))
+    stream = sorted((b for b in range(lim.blocks) if kind[b] == 1), key=lambda b: idx[b])
+    assert [idx[b] for b in stream] == list(range(lim.blocks - lim.latency_blocks))
+    end = 0
+    for b in stream:
+        assert sb[b] == end and 0 <= se[b] - sb[b] <= lim.max_slices
+        end = se[b]
+    assert end == inter // 16
+    # consecutive stream indices on one XCD (24 per XCD)
+    per = len(stream) // 8
+    assert all(len({stream[i] % 8 for i in range(x * per, (x + 1) * per)}) == 1 for x in range(8))
+
+
+def test_role_limits_match_the_kernel_contract():
+    lim = decode.roles_limits()
+    assert (lim.blocks, lim.latency_blocks, lim.max_slices, lim.x_copies) == (256, 64, 4, 16)
+    assert lim.max_splits * lim.slots_per_wave * 0 == 0 and lim.waves * lim.slots_per_wave >= 2048 // 16
+
+
+def test_group_scale_min_words():
+    """win_sm of the role-split step: per (tile, group, row) the word of (row 16 tile + row, group)."""
+    g = torch.Generator().manual_seed(3)
+    sm = torch.randint(-2 ** 31, 2 ** 31 - 1, (64, 16), dtype=torch.int32, generator=g)
+    out = decode.group_scale_min(sm)
+    assert out.shape == (4, 16, 16)
+    for T in range(4):
+        for grp in range(16):
+            for r in range(16):
+                assert out[T, grp, r] == sm[16 * T + r, grp]
+
+
+def test_role_head_rows_fit_the_waves():
+    """stream block i, wave w takes head rows i + 192 (w + 16 k): every row once, at most 64 per wave."""
+    for n in (16385, 257, 1):
+        rows = sorted(i + 192 * (w + 16 * k) for i in range(192) for w in range(16) for k in range(64)
+                      if i + 192 * (w + 16 * k) < n)
+        assert rows == list(range(n))
+        assert max(len([k for k in range(64) if i + 192 * (w + 16 * k) < n]) for i in range(192) for w in range(16)) <= 64

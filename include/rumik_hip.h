@@ -332,8 +332,10 @@ int rk_decode_get_limits(rk_decode_limits* out);
  * The same decode step as ONE launch with the grid split by role (replaces the same reference code as
  * rk_decode_step_persistent: RumikFused._step, engine/rumik_fused.py:97-121, with _logits :84-89). 256 blocks of
  * 1024 threads (one per CU, co-residency checked). Latency blocks (64, role kind 0, index j): residual rows
- * [32j, 32j + 32), q/k/v tiles [nq j, nq j + nq) (nq = (NH + 2 NKV) * 8 / 64), attention split j % (64 / NKV) of KV
- * head j / (64 / NKV), the combine of head j / 4 and its o slice for rows [512 (j % 4), + 512). Stream blocks (192,
+ * [32j, 32j + 32), attention split j % (64 / NKV) of KV head g = j / (64 / NKV), the combine of head j / 4 and its
+ * o slice for rows [512 (j % 4), + 512), and nq = (NH + 2 NKV) * 8 / 64 q/k/v tiles of latency group g (the blocks
+ * of KV head g): entries [nq i, nq i + nq), i = j % (64 / NKV), of the group's list [q tiles of heads g REP ..
+ * g REP + REP - 1 | k tiles of KV head g | v tiles of KV head g] (REP = NH / NKV, 8 tiles per head). Stream blocks (192,
  * kind 1, index i): MLP slices [sb, se) of 16 channels (their gate / up tiles and w_down columns; a contiguous
  * partition of the inter / 16 slices, at most 4 per block) and int8 head rows i + 192 (w + 16 k). role[b] =
  * {kind, index, sb, se} for block b (sb = se = 0 for latency blocks); every index exactly once.
@@ -346,7 +348,11 @@ int rk_decode_get_limits(rk_decode_limits* out);
  *   tx [2][16 copies][2048]; tq [2][NH*128]; tkv [2][2][NKV*128]; tpo [2][NH][nsp][128]; tml [2][NH][nsp][2];
  *   top [2][64 latency blocks][NH][32 rows]; tdp [2][64 latency blocks][192 stream blocks][32 rows].
  * All of them, ctr [256] and status start at zero; after a nonzero status, re-zero them. Status bits as for
- * rk_decode_step_persistent (1 wait timed out, 2 pos outside [0, S), 3 residual beyond the fp16 range). */
+ * rk_decode_step_persistent (1 wait timed out, 2 pos outside [0, S), 3 residual beyond the fp16 range).
+ * local_xcd = 1: every latency group's blocks share one XCD (the role table gives them equal b % 8, and a launch
+ * deals block b to XCD (b + c) % 8, which rk_decode_roles_placement lets the host confirm), so the group's q / k / v
+ * and split-partial words stay in that XCD's L2 (faster hops); with local_xcd = 0 they are written through to
+ * memory like the other exchanges. */
 typedef struct rk_decode_roles_params {
     int L, NH, NKV, inter, S, n_audio, nsp, min_chunk;
     float eps, scale;
@@ -381,9 +387,15 @@ typedef struct rk_decode_roles_params {
     unsigned* ctr;
     unsigned* status;
     uint16_t* hn;           /* [2048] fp16 final LayerNorm output, or NULL */
+    int local_xcd;          /* 1: latency-group exchanges through the group's XCD L2 (see above) */
 } rk_decode_roles_params;
 
 int rk_decode_step_roles(const rk_decode_roles_params* params, rk_stream_t stream);
+
+/* xcc[b] = the XCD that block b of a 256-block launch ran on (device int32 [256]; asynchronous on stream). Lets
+ * the host confirm the round-robin placement local_xcd relies on (xcc[b] - b constant mod 8). No reference
+ * counterpart. */
+int rk_decode_roles_placement(int32_t* xcc, rk_stream_t stream);
 
 /* sizeof(rk_decode_roles_params) as compiled */
 int rk_decode_roles_params_size(void);

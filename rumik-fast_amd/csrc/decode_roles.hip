@@ -31,10 +31,6 @@
 // (or is NaN) sets a sticky status bit and the step runs on.
 #include "dequant.h"
 
-#ifndef RK_SB_SCHED
-#define RK_SB_SCHED 0
-#endif
-
 namespace {
 
 constexpr int kWaves = 16;
@@ -95,6 +91,28 @@ RK_DEV uint64_t ld_coh64(const uint64_t* p) {
 }
 RK_DEV void st_coh64(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
+// Traffic inside a latency group (the 64 / NKV latency blocks of one KV head: its q / k / v words and its attention
+// split partials, produced and consumed only inside the group). With p.local_xcd the role table puts each group on
+// one XCD, so these words are written into that XCD's L2 (nontemporal store, no write-through) and the group's
+// agent-scope polls hit them there: a coherent load refetches a line from memory unless this L2 holds it dirty,
+// and a line written on this XCD is dirty here. Measured one way: ~0.3 us through the L2 against ~0.6 us through
+// memory. Without p.local_xcd they go through memory like every other exchange. (The dispatcher deals a launch's
+// blocks to the XCDs round robin, block b to XCD (b + c) % 8 for some c of the launch, so blocks with equal b % 8
+// share an XCD; a group split over XCDs would not see its words and its waits would time out, not read stale data:
+// every word carries the tag of its step and layer.)
+RK_DEV void st_grp(uint32_t* a, uint32_t v, bool local) {
+    if (local)
+        __builtin_nontemporal_store(v, a);
+    else
+        st_coh(a, v);
+}
+RK_DEV void st_grp64(uint64_t* a, uint64_t v, bool local) {
+    if (local)
+        __builtin_nontemporal_store(v, a);
+    else
+        st_coh64(a, v);
+}
+
 // ---------------------------------------------------------------------------------------------- tagged words
 RK_DEV uint32_t tag_of(uint32_t step, int l) { return 1u + (step * 64u + (uint32_t)l) % 65535u; }
 RK_DEV uint32_t tword(float v, uint32_t tag) { return (uint32_t)f16b(v) | (tag << 16); }
@@ -132,6 +150,9 @@ enum TraceEvent {
     kTrCombFirst,     // latency: the combine's first poll round returned
     kTrCombRounds,    // latency: the combine's poll rounds (a count, not a time)
     kTrCombStart,     // latency: the combine's poll started
+    kTrCombChecked,   // latency: the combine's first poll round checked without completing (its loads returned)
+    kTrSplitAcked,    // latency: the split partial stores acknowledged (max over the publishing waves)
+    kTrCombDrained,   // latency: wave 0's earlier memory operations all complete at the combine's start
     kTrEvents
 };
 #ifdef RK_ROLES_TRACE
@@ -370,22 +391,19 @@ struct TileRegs {
     uint32_t sm[NT];
 };
 
-// wave w: group w of tiles t0 .. t0 + nt - 1. The load count is fixed and every load unconditional (entries past
+// wave w: group w of tiles tile(0) .. tile(nt - 1). The load count is fixed and every load unconditional (entries past
 // nt read one 16-byte word of the layer's tile 0 in every lane, a single broadcast request, and are ignored), so the
 // compiler can wait for exactly the loads a computation needs: a load skipped on some path would make it wait for
 // every load in flight at that point.
-// PACE: at most two tiles' loads in flight per wave (the wave waits before issuing more), so a block's prefetch
-// never puts more than ~32 KB into the memory queues at once.
-template <int NT, bool PACE = false>
-RK_DEV void tile_issue(const Params& p, int l, int t0, int nt, TileRegs<NT>& r) {
+template <int NT, class TileOf>
+RK_DEV void tile_issue(const Params& p, int l, TileOf tile, int nt, TileRegs<NT>& r) {
     const int w = wave_id(), L = lane_id();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const bool on = t < nt;
-        const size_t T = (size_t)l * n_tiles(p) + keep_if(on, (size_t)(t0 + t));
+        const size_t T = (size_t)l * n_tiles(p) + keep_if(on, (size_t)tile(t));
         r.w[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.win_t) + (T * kNG + w) * 64 + keep_if(on, L));
         r.sm[t] = p.win_sm[(T * kNG + w) * 16 + keep_if(on, L & 15)];
-        if constexpr (PACE) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     }
 }
 
@@ -599,11 +617,13 @@ RK_DEV void split_publish(const Params& p, int l, const Split& s, int nsg, uint3
     }
     const size_t pi = ((size_t)(l & 1) * p.NH + s.g * REP + r) * p.nsp + s.sp;
     const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
-    st_coh64(reinterpret_cast<uint64_t*>(p.tpo + pi * kHD) + L, tpair(ax * inv, ay * inv, tag));
+    const bool local = p.local_xcd != 0;
+    st_grp64(reinterpret_cast<uint64_t*>(p.tpo + pi * kHD) + L, tpair(ax * inv, ay * inv, tag), local);
     if (L == 0) {
-        st_coh64(reinterpret_cast<uint64_t*>(p.tml) + 2 * pi, (uint64_t)__builtin_bit_cast(uint32_t, M) | ((uint64_t)tag << 32));
-        st_coh64(reinterpret_cast<uint64_t*>(p.tml) + 2 * pi + 1,
-                 (uint64_t)__builtin_bit_cast(uint32_t, Lt) | ((uint64_t)tag << 32));
+        st_grp64(reinterpret_cast<uint64_t*>(p.tml) + 2 * pi,
+                 (uint64_t)__builtin_bit_cast(uint32_t, M) | ((uint64_t)tag << 32), local);
+        st_grp64(reinterpret_cast<uint64_t*>(p.tml) + 2 * pi + 1,
+                 (uint64_t)__builtin_bit_cast(uint32_t, Lt) | ((uint64_t)tag << 32), local);
     }
 }
 
@@ -613,6 +633,10 @@ RK_DEV void split_publish(const Params& p, int l, const Split& s, int nsg, uint3
 RK_DEV bool combine(const Params& p, Lds& S, int l, int h, int64_t pos, uint32_t tag) {
     const int L = lane_id();
     RK_TRACE(true, kTrCombStart);
+#ifdef RK_ROLES_TRACE
+    __builtin_amdgcn_s_waitcnt(0);
+    RK_TRACE(true, kTrCombDrained);
+#endif
     int rounds = 0;
     const int cnt = comb_splits(p, pos);
     const size_t hb = ((size_t)(l & 1) * p.NH + h) * p.nsp;
@@ -655,6 +679,7 @@ RK_DEV bool combine(const Params& p, Lds& S, int l, int h, int64_t pos, uint32_t
             ml_done = true;
         }
         if (pending == 0 && __all(ml_done)) break;
+        RK_TRACE(rounds == 1, kTrCombChecked);
         if (!wait_more(p, S, t0, st)) {
             ok = false;
             break;
@@ -822,7 +847,6 @@ struct DownRegs {
     u2_t sm[2];
 };
 
-template <bool PACE = false>
 RK_DEV void down_issue(const Params& p, int l, int sb, int se, DownRegs& d) {
     const int g = tid();
     const int nsl = p.inter / 16, ngd = p.inter / 128, gb = sb / 8;
@@ -831,7 +855,6 @@ RK_DEV void down_issue(const Params& p, int l, int sb, int se, DownRegs& d) {
         const bool on = sb + i < se;
         d.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p.wd_t) +
                                             ((size_t)l * nsl + keep_if(on, sb + i)) * (kH / 2) + keep_if(on, g));
-        if constexpr (PACE) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q)
@@ -1016,17 +1039,31 @@ RK_DEV void x_norm(const Params& p, Lds& S, int l, const XIn& in, int lb) {
 }
 
 // ---------------------------------------------------------------------------------------------- the roles
+// Latency block j's u-th q/k/v tile (u < nq = (REP + 2) * 8 / (64 / NKV)): latency group g = j / (64 / NKV)
+// computes exactly the rows its attention splits poll, the q rows of heads g REP .. g REP + REP - 1 and the k and v
+// rows of KV head g (REP * 8 + 8 + 8 tiles), member i = j % (64 / NKV) taking entries [i nq, i nq + nq) of that
+// list, so the group's q / k / v exchange never leaves the group.
+RK_DEV int qkv_tile(const Params& p, int j, int u) {
+    constexpr int kTH = kHD / 16;  // tiles per head
+    const int per = kNL / p.NKV, rep = p.NH / p.NKV, nq = (rep + 2) * kTH / per;
+    const int g = j / per, t = (j % per) * nq + u, qt = rep * kTH;
+    if (t < qt) return g * qt + t;
+    if (t < qt + kTH) return p.NH * kTH + g * kTH + (t - qt);
+    return (p.NH + p.NKV) * kTH + g * kTH + (t - qt - kTH);
+}
+
 // q/k/v tile epilogue, wave 0 lane (tile t = L / 16, row j = L % 16): RoPE on q / k rows (pairs 2i, 2i + 1 sit in
 // adjacent lanes), published tagged; k and v also written into the cache at pos
-RK_DEV void qkv_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, int t0, int nq, const Lds& S) {
+RK_DEV void qkv_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, int lb, int nq, const Lds& S) {
     const int L = lane_id();
     const int t = L >> 4, j = L & 15;
     const float y = t < nq ? tile_out(S, t, j) : 0.f;
     const float partner = dpp<0xB1>(y);  // row j ^ 1 (quad_perm [1,0,3,2])
     if (t >= nq) return;
     const int NH = p.NH, NKV = p.NKV;
-    const int row = (t0 + t) * 16 + j;
+    const int row = qkv_tile(p, lb, t) * 16 + j;
     const int qk_rows = (NH + NKV) * kHD;
+    const bool local = p.local_xcd != 0;
     uint32_t* tq = p.tq + (size_t)(l & 1) * NH * kHD;
     uint32_t* tkv = p.tkv + (size_t)(l & 1) * 2 * NKV * kHD;
     if (row < qk_rows) {
@@ -1038,15 +1075,15 @@ RK_DEV void qkv_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, int 
         }
         out = rnd16(out);
         if (row < NH * kHD) {
-            st_coh(tq + row, tword(out, tag));
+            st_grp(tq + row, tword(out, tag), local);
         } else {
             const int r2 = row - NH * kHD;
-            st_coh(tkv + r2, tword(out, tag));
+            st_grp(tkv + r2, tword(out, tag), local);
             p.kc[(((size_t)l * NKV + r2 / kHD) * p.S + pos) * kHD + r2 % kHD] = f16b(out);
         }
     } else {
         const int r2 = row - qk_rows;
-        st_coh(tkv + NKV * kHD + r2, tword(y, tag));
+        st_grp(tkv + NKV * kHD + r2, tword(y, tag), local);
         p.vc[(((size_t)l * NKV + r2 / kHD) * p.S + pos) * kHD + r2 % kHD] = f16b(y);
     }
 }
@@ -1075,7 +1112,8 @@ RK_DEV void latency_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, i
     constexpr int NQ = LatencyRegs<REP>::NQ;
     const int w = wave_id();
     const uint32_t tag = tag_of(step, l);
-    const int t0 = j * NQ, h = j / kOQ, r = j % kOQ;
+    const int h = j / kOQ, r = j % kOQ;
+    const auto qt = [&](int u) { return qkv_tile(p, j, u); };
     const Split s = split_of(p, j, pos);
     const AttnPlan ap = attn_plan<REP>(s);
     // this layer's K / V slots and o items: the x-waves issue theirs after the LayerNorm (issued before it, they
@@ -1095,12 +1133,12 @@ RK_DEV void latency_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, i
     __syncthreads();
     RK_TRACE(true, kTrTilesDone);
     if (w == 0) {
-        qkv_epilogue(p, l, pos, tag, t0, NQ, S);
+        qkv_epilogue(p, l, pos, tag, j, NQ, S);
         RK_TRACE(true, kTrQkvPublished);
         if (s.att) q_poll<REP>(p, S, l, s, pos, tag);
         RK_TRACE(true, kTrQPolled);
     } else if constexpr (!LAST) {
-        tile_issue<NQ>(p, l + 1, t0, NQ, R.tr);
+        tile_issue<NQ>(p, l + 1, qt, NQ, R.tr);
     }
     __syncthreads();
     RK_TRACE(true, kTrAttnStart);
@@ -1114,7 +1152,13 @@ RK_DEV void latency_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, i
             RK_TRACE_MAX(kTrAttnEnd);
         }
         __syncthreads();
-        if (attn_wave() < REP) split_publish<REP>(p, l, s, ap.nsg, tag, S);
+        if (attn_wave() < REP) {
+            split_publish<REP>(p, l, s, ap.nsg, tag, S);
+#ifdef RK_ROLES_TRACE
+            __builtin_amdgcn_s_waitcnt(0);
+            RK_TRACE_MAX(kTrSplitAcked);
+#endif
+        }
         RK_TRACE(true, kTrSplitPublished);
     }
     if (w == 0) {
@@ -1122,7 +1166,7 @@ RK_DEV void latency_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, i
         RK_TRACE(true, kTrCombDone);
         // wave 0 polls: its share of the next layer's tiles goes out only now, after its q and combine polls (a
         // poll returns only after the wave's earlier loads), and lands before its gather poll
-        if constexpr (!LAST) tile_issue<NQ>(p, l + 1, t0, NQ, R.tr);
+        if constexpr (!LAST) tile_issue<NQ>(p, l + 1, qt, NQ, R.tr);
     }
     __syncthreads();
     o_publish(p, l, tag, h, r, R.orr, S);
@@ -1134,7 +1178,7 @@ RK_DEV void latency_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, i
 template <int REP>
 RK_DEV void latency_main(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int j) {
     LatencyRegs<REP> R;
-    tile_issue<LatencyRegs<REP>::NQ>(p, 0, j * LatencyRegs<REP>::NQ, LatencyRegs<REP>::NQ, R.tr);
+    tile_issue<LatencyRegs<REP>::NQ>(p, 0, [&](int u) { return qkv_tile(p, j, u); }, LatencyRegs<REP>::NQ, R.tr);
     for (int l = 0; l + 1 < p.L; ++l) latency_layer<REP, false>(p, S, step, pos, tok, j, l, R);
     latency_layer<REP, true>(p, S, step, pos, tok, j, p.L - 1, R);
     HeadRegs none;
@@ -1159,11 +1203,10 @@ RK_DEV void stream_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, in
     const int w = wave_id();
     const uint32_t tag = tag_of(step, l);
     const int t0 = (int)(n_tiles(p) - (size_t)p.inter / 8) + 2 * sb, nt = 2 * (se - sb);
+    const auto mlp_tiles = [&](int t) { return t0 + t; };
     const XIn in = x_fetch<kStreamXSleep>(p, S, l, step, pos, tok);
     x_norm(p, S, l, in, -1);
-#if RK_SB_SCHED != 1
     down_issue(p, l, sb, se, R.dr);
-#endif
     tile_compute<kMaxTiles>(R.tr, nt, S);
     __syncthreads();
     RK_TRACE(true, kTrTilesDone);
@@ -1172,29 +1215,14 @@ RK_DEV void stream_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, in
     RK_TRACE(true, kTrActReady);
     down_publish(p, l, tag, si, sb, se, R.dr, S);
     RK_TRACE(true, kTrDownPublished);
-#if RK_SB_SCHED == 0
-    if constexpr (!LAST) tile_issue<kMaxTiles>(p, l + 1, t0, nt, R.tr);
+    if constexpr (!LAST) tile_issue<kMaxTiles>(p, l + 1, mlp_tiles, nt, R.tr);
     else head_issue(p, si, R.hr);
-#elif RK_SB_SCHED == 1
-    if constexpr (!LAST) {
-        tile_issue<kMaxTiles, true>(p, l + 1, t0, nt, R.tr);
-        down_issue<true>(p, l + 1, sb, se, R.dr);
-    } else {
-        head_issue(p, si, R.hr);
-    }
-#else
-    if constexpr (!LAST) tile_issue<kMaxTiles, true>(p, l + 1, t0, nt, R.tr);
-    else head_issue(p, si, R.hr);
-#endif
 }
 
 RK_DEV void stream_main(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int si, int sb, int se) {
     StreamRegs R;
     const int t0 = (int)(n_tiles(p) - (size_t)p.inter / 8) + 2 * sb;
-    tile_issue<kMaxTiles>(p, 0, t0, 2 * (se - sb), R.tr);
-#if RK_SB_SCHED == 1
-    down_issue(p, 0, sb, se, R.dr);
-#endif
+    tile_issue<kMaxTiles>(p, 0, [&](int t) { return t0 + t; }, 2 * (se - sb), R.tr);
     for (int l = 0; l + 1 < p.L; ++l) stream_layer<false>(p, S, step, pos, tok, si, sb, se, l, R);
     stream_layer<true>(p, S, step, pos, tok, si, sb, se, p.L - 1, R);
     final_phase(p, S, step, pos, si, R.hr);
@@ -1276,6 +1304,18 @@ extern "C" int rk_decode_step_roles(const rk_decode_roles_params* params, rk_str
         hipLaunchKernelGGL(decode_roles_kernel<2>, dim3(kNB), dim3(kThreads), sizeof(Lds), st, p);
     else
         hipLaunchKernelGGL(decode_roles_kernel<4>, dim3(kNB), dim3(kThreads), sizeof(Lds), st, p);
+    return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
+}
+
+namespace {
+__global__ __launch_bounds__(kThreads) void placement_kernel(int32_t* xcc) {
+    if (threadIdx.x == 0) xcc[blockIdx.x] = (int32_t)__builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11));
+}
+}  // namespace
+
+extern "C" int rk_decode_roles_placement(int32_t* xcc, rk_stream_t stream) {
+    if (!xcc) return RK_ERR_NULL;
+    hipLaunchKernelGGL(placement_kernel, dim3(kNB), dim3(kThreads), 0, (hipStream_t)stream, xcc);
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
 

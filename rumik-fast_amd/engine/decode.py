@@ -448,7 +448,7 @@ class RkDecodeRolesParams(ctypes.Structure):
         (n, ctypes.c_void_p) for n in (
             "tok", "pos", "emb_q", "emb_s", "win_t", "win_sm", "wo_q", "wo_sm", "wd_t", "wd_sm", "ln_w", "norm_w",
             "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "role", "tx", "tq", "tkv", "tpo", "tml",
-            "top", "tdp", "ctr", "status", "hn")]
+            "top", "tdp", "ctr", "status", "hn")] + [("local_xcd", ctypes.c_int)]
 
 
 class RkDecodeRolesLimits(ctypes.Structure):
@@ -468,28 +468,51 @@ def group_scale_min(sm):
     return sm.reshape(sm.shape[0] // 16, 16, -1).permute(0, 2, 1).contiguous()
 
 
+def latency_xcd(cfg):
+    """b % 8 of latency group g's blocks (its 64 / NKV blocks, those of KV head g): 2g for 4 groups, g for 8."""
+    return [g * (8 // cfg.NKV) for g in range(cfg.NKV)]
+
+
 def role_table(cfg, lim=None):
     """Block -> role for the role-split step: int16 [blocks, 4] = (kind, index, slice begin, slice end).
-    Latency blocks (kind 0): the blocks b with (b // 8) % 4 == 0 (8 on each XCD: block b runs on XCD b % 8),
-    numbered in block order. Stream blocks (kind 1): the others, numbered XCD by XCD (the 24 of XCD x get indices
-    24x .. 24x + 23), so stream blocks with neighbouring MLP slices, which share w_down scale rows, sit on one XCD
-    and its L2; stream block i takes slices [i * n / 192, (i + 1) * n / 192) of the n = inter / 16."""
+    A launch deals block b to XCD (b + c) % 8 (the dispatcher's round robin, confirmed by placement_ok), so the
+    blocks with equal b % 8 share an XCD.
+    Latency blocks (kind 0): group g (indices j = g * 64 / NKV .. + 64 / NKV - 1: KV head g's attention splits,
+    combines and q / k / v tiles, which exchange words only inside the group) on one XCD, latency_xcd(cfg)[g],
+    taking that XCD's lowest blocks. Stream blocks (kind 1): the others, numbered XCD by XCD, so stream blocks with
+    neighbouring MLP slices, which share w_down scale rows, sit on one XCD and its L2; stream block i takes slices
+    [i * n / 192, (i + 1) * n / 192) of the n = inter / 16."""
     lim = lim or roles_limits()
     nb, nl = lim.blocks, lim.latency_blocks
     ns = nb - nl
     nsl = cfg.inter // 16
     if -(-nsl // ns) > lim.max_slices:
         raise ValueError("too many MLP slices per stream block")
+    if nl % cfg.NKV or nb % 8 or nl // cfg.NKV > nb // 8:
+        raise ValueError("latency groups do not fit the XCDs")
     table = torch.zeros(nb, 4, dtype=torch.int16)
-    lat = [b for b in range(nb) if (b // 8) % 4 == 0]
-    if len(lat) != nl:
-        raise ValueError("latency block placement does not match the kernel")
+    per = nl // cfg.NKV
+    lat = [x + 8 * k for x in latency_xcd(cfg) for k in range(per)]
     for j, b in enumerate(lat):
         table[b] = torch.tensor([0, j, 0, 0], dtype=torch.int16)
-    stream = sorted((b for b in range(nb) if (b // 8) % 4 != 0), key=lambda b: (b % 8, b))
+    taken = set(lat)
+    stream = sorted((b for b in range(nb) if b not in taken), key=lambda b: (b % 8, b))
     for i, b in enumerate(stream):
         table[b] = torch.tensor([1, i, i * nsl // ns, (i + 1) * nsl // ns], dtype=torch.int16)
     return table
+
+
+def placement_ok(device) -> bool:
+    """Are a launch's blocks dealt to the XCDs round robin on this device (block b on XCD (b + c) % 8, so blocks
+    with equal b % 8 share an XCD: the placement the latency groups' L2-local exchanges rely on)? One tiny launch,
+    synchronized."""
+    d = torch.device(device)
+    xcc = torch.full((roles_limits().blocks,), -1, dtype=torch.int32, device=d)
+    HL.check(HL.lib().rk_decode_roles_placement(xcc.data_ptr(), HL.stream(d)), "decode_roles_placement")
+    got = xcc.cpu()
+    if (got < 0).any() or (got >= 8).any():
+        return False
+    return bool(((got - torch.arange(got.numel(), dtype=torch.int32)) % 8 == (got[0] % 8)).all())
 
 
 class RoleDecode(_OneLaunch):
@@ -499,7 +522,8 @@ class RoleDecode(_OneLaunch):
     PersistentDecode; hidden 2048, head dim 128, 16 query heads with 4 or 8 KV heads, 256 CUs.
     nsp: attention splits per KV head (default min(16, 64 / NKV)); min_chunk: the fewest cache slots per split."""
 
-    def __init__(self, cfg: Config, weights, device="cuda", nsp=None, min_chunk=32, keep_layer_weights=False):
+    def __init__(self, cfg: Config, weights, device="cuda", nsp=None, min_chunk=32, keep_layer_weights=False,
+                 local_xcd=None):
         if cfg.H != 2048 or cfg.HD != 128 or cfg.NH * cfg.HD != 2048 or cfg.NKV not in (4, 8):
             raise ValueError("the role-split step is built for hidden 2048 / head dim 128 / 16 q and 4 or 8 kv heads")
         self.cfg, self.dev = cfg, torch.device(device)
@@ -548,8 +572,12 @@ class RoleDecode(_OneLaunch):
         self.pos = torch.zeros(1, dtype=torch.int64, device=d)
         self.cos, self.sin = rope_tables(c.S, c.HD, c.rope_theta, torch.float16, d)
         sliding = sum(1 << i for i, on in enumerate(c.sliding) if on)
+        if local_xcd is None:
+            local_xcd = placement_ok(d)
+        self.local_xcd = bool(local_xcd)
         P = RkDecodeRolesParams(L=c.L, NH=c.NH, NKV=c.NKV, inter=c.inter, S=c.S, n_audio=c.n_audio, nsp=self.nsp,
-                                min_chunk=int(min_chunk), eps=c.eps, scale=c.HD ** -0.5, sliding=sliding)
+                                min_chunk=int(min_chunk), eps=c.eps, scale=c.HD ** -0.5, sliding=sliding,
+                                local_xcd=int(self.local_xcd))
         for name, t in (("tok", self.tok), ("pos", self.pos), ("emb_q", self.emb[0]), ("emb_s", self.emb[1]),
                         ("win_t", self.win_t), ("win_sm", self.win_sm), ("wo_q", self.wo_q), ("wo_sm", self.wo_sm),
                         ("wd_t", self.wd_t), ("wd_sm", self.wd_sm), ("ln_w", self.ln), ("norm_w", self.norm),

@@ -48,6 +48,7 @@ _SIGS = {
     "rk_decode_get_limits": ([_p], _i),
     "rk_decode_step_roles": ([_p, _p], _i),
     "rk_decode_roles_params_size": ([], _i),
+    "rk_decode_roles_placement": ([_p, _p], _i),
     "rk_decode_roles_get_limits": ([_p], _i),
     "rk_embed_ln_rows": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _f, _p], _i),
     "rk_add_ln_rows": ([_p, _p, _p, _p, _p, _i, _i, _i, _f, _p], _i),

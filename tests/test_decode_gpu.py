@@ -20,14 +20,18 @@ from oracle import int4 as O
 
 pytestmark = pytest.mark.gpu
 
-# the two one-launch engines: every block doing every role (csrc/decode_persistent.hip) and the grid split into
-# latency and stream blocks (csrc/decode_roles.hip)
-ONE_LAUNCH = ["persistent", "roles"]
+# the one-launch engines: every block doing every role (csrc/decode_persistent.hip) and the grid split into
+# latency and stream blocks (csrc/decode_roles.hip), the latter with its latency groups' exchanges kept in their
+# XCD's L2 (local_xcd, the default where the placement probe confirms the round-robin XCD placement) and through memory
+ONE_LAUNCH = ["persistent", "roles", "roles_mem"]
 
 
 def _one_launch(engine, cfg, w, dev):
-    return (decode.PersistentDecode(cfg, w, device=dev) if engine == "persistent"
-            else decode.RoleDecode(cfg, w, device=dev))
+    if engine == "persistent":
+        return decode.PersistentDecode(cfg, w, device=dev)
+    eng = decode.RoleDecode(cfg, w, device=dev, local_xcd=False if engine == "roles_mem" else None)
+    assert eng.local_xcd == (engine == "roles"), "blocks with equal b % 8 did not share an XCD"
+    return eng
 
 
 def _np(t):
@@ -146,6 +150,15 @@ def test_persistent_full_width(use_graph, engine, dev):
     # the one-launch step: hidden 2048, 16 / 4 heads, MLP 11008, 3 layers (one of them NoPE), ctx 300
     cfg = decode.Config(L=3, vocab=64, sliding=[True, False, True])
     reps = _run(cfg, dev, ctx=300, steps=3, use_graph=use_graph, engine=engine)
+    print(reps[-1])
+
+
+@pytest.mark.parametrize("engine", ["roles", "roles_mem"])
+def test_roles_eight_kv_heads(engine, dev):
+    # 16 q / 8 kv heads: latency groups of 8 blocks (4 q/k/v tiles each, 8 splits per KV head of at most 128
+    # slots, so a 1024-slot cache), ctx 300
+    cfg = decode.Config(L=2, NKV=8, S=1024, vocab=64, sliding=[True, False])
+    reps = _run(cfg, dev, ctx=300, steps=2, use_graph=False, engine=engine)
     print(reps[-1])
 
 

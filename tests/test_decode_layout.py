@@ -135,20 +135,25 @@ def test_interleave_gate_up_rows():
 
 
 # ---------------------------------------------------------------------------------------------- role-split step
-@pytest.mark.parametrize("inter", [11008, 2048, 128])
-def test_role_table_partitions_the_work(inter):
-    """64 latency blocks, 8 on each XCD (block b runs on XCD b % 8), numbered 0..63 once each; 192 stream blocks
-    numbered 0..191 once each, XCD by XCD, whose MLP slices form a contiguous partition of inter / 16 with at most
-    max_slices each (stream blocks may hold none when the MLP is narrow)."""
+@pytest.mark.parametrize("inter,nkv", [(11008, 4), (2048, 4), (128, 4), (11008, 8)])
+def test_role_table_partitions_the_work(inter, nkv):
+    """64 latency blocks numbered 0..63 once each, latency group g (indices g * 64 / NKV .. + 64 / NKV - 1, the
+    blocks that exchange KV head g's q / k / v and split partials) with one b % 8 (one XCD: a launch deals block b
+    to XCD (b + c) % 8), no two groups with the same; 192 stream blocks numbered 0..191 once each, XCD by XCD,
+    whose MLP slices form a contiguous partition of inter / 16 with at most max_slices each (stream blocks may hold
+    none when the MLP is narrow)."""
     lim = decode.roles_limits()
-    cfg = decode.Config(inter=inter)
+    cfg = decode.Config(inter=inter, NKV=nkv)
     t = decode.role_table(cfg, lim)
     assert t.shape == (lim.blocks, 4)
     kind, idx, sb, se = (t[:, i].tolist() for i in range(4))
     lat = [b for b in range(lim.blocks) if kind[b] == 0]
     assert len(lat) == lim.latency_blocks
     assert sorted(idx[b] for b in lat) == list(range(lim.latency_blocks))
-    assert all(sum(1 for b in lat if b % 8 == x) == lim.latency_blocks // 8 for x in range(8))
+    per = lim.latency_blocks // nkv
+    xcds = [{b % 8 for b in lat if idx[b] // per == g} for g in range(nkv)]
+    assert all(len(x) == 1 for x in xcds) and len(set.union(*xcds)) == nkv
+    assert [next(iter(x)) for x in xcds] == decode.latency_xcd(cfg)
     stream = sorted((b for b in range(lim.blocks) if kind[b] == 1), key=lambda b: idx[b])
     assert [idx[b] for b in stream] == list(range(lim.blocks - lim.latency_blocks))
     end = 0
@@ -156,9 +161,8 @@ def test_role_table_partitions_the_work(inter):
         assert sb[b] == end and 0 <= se[b] - sb[b] <= lim.max_slices
         end = se[b]
     assert end == inter // 16
-    # consecutive stream indices on one XCD (24 per XCD)
-    per = len(stream) // 8
-    assert all(len({stream[i] % 8 for i in range(x * per, (x + 1) * per)}) == 1 for x in range(8))
+    # stream indices run XCD by XCD
+    assert [b % 8 for b in stream] == sorted(b % 8 for b in stream)
 
 
 def test_role_limits_match_the_kernel_contract():

@@ -178,6 +178,7 @@ __device__ unsigned long long* g_roles_trace;
 struct Lds {
     uint4 hfrag[kH / 8];                      // MFMA A fragments of h (group g: entries 16g .. 16g + 15)
     float hsum[kNG];                          // per-group sums of h
+    float hbias[kNG];                         // per group: 1024 x the sum of its A fragment entries (biased codes)
     alignas(16) uint32_t hnat[kH / 2];        // the final h as natural fp16 pairs (the int8 head's input)
     float2 lnst[kWaves];                      // per wave: sum and squared deviations of its 128 x values
     float tpart[kWaves][kMaxTiles][16];       // K-split partial dots of the block's tiles (per wave = group)
@@ -360,23 +361,36 @@ RK_DEV u4_t layer_norm(const Params& p, Lds& S, int l, const XIn& in) {
 // (x0,x4),(x1,x5),(x2,x6),(x3,x7). The codes' tile layout gives MFMA lane j + 16s of 32-column chunk t4 the columns
 // 32s + 8 t4 .. + 7 (a lane's 16 bytes are the row's bytes [16s, 16s + 16), word t4 feeding chunk t4), so block
 // m = 4s + t4 goes to entry 16g + 4 t4 + s = 16g + 4 (m % 4) + m / 4, where chunk t4's A operand reads it.
+// The tiles' codes stay biased (dequant_frag_biased), so the (x1,x5), (x3,x7) pairs are staged divided by 16 and
+// hbias[g] = 1024 x the sum of the staged values is what the tile dots subtract.
 RK_DEV void stage_h(const u4_t& h, Lds& S) {
     const int L = lane_id(), w = wave_id();
     const int g = 4 * w + (L >> 4), m = L & 15;
     uint32_t hp[4];
     pair_permute(h, hp);
+    const h2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    hp[1] = as_u32(as_h2(hp[1]) * s16);
+    hp[3] = as_u32(as_h2(hp[3]) * s16);
     S.hfrag[16 * g + 4 * (m & 3) + (m >> 2)] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-    float s = 0.f;
+    float s = 0.f, a = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const h2_t v = as_h2(h[e]);
+        const h2_t v = as_h2(h[e]), f = as_h2(hp[e]);
         s += (float)v.x + (float)v.y;
+        a += (float)f.x + (float)f.y;
     }
     s += dpp<0x128>(s);  // row_ror 8
     s += dpp<0x124>(s);  // row_ror 4
     s += dpp<0x122>(s);  // row_ror 2
     s += dpp<0x121>(s);  // row_ror 1: every lane of the 16-lane row holds the group's sum
-    if (m == 0) S.hsum[g] = s;
+    a += dpp<0x128>(a);
+    a += dpp<0x124>(a);
+    a += dpp<0x122>(a);
+    a += dpp<0x121>(a);
+    if (m == 0) {
+        S.hsum[g] = s;
+        S.hbias[g] = 1024.f * a;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------- w_in tiles
@@ -412,7 +426,7 @@ template <int NT>
 RK_DEV void tile_compute(const TileRegs<NT>& r, int nt, Lds& S) {
     const int w = wave_id(), L = lane_id(), s = L >> 4;
     const Int4Masks km = int4_masks();
-    const float hs = S.hsum[w];
+    const float hs = S.hsum[w], hb = S.hbias[w];
 #pragma unroll
     for (int t0 = 0; t0 < NT; t0 += 2) {
         f4_t d[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
@@ -422,7 +436,7 @@ RK_DEV void tile_compute(const TileRegs<NT>& r, int nt, Lds& S) {
 #pragma unroll
             for (int e = 0; e < 2; ++e)
                 if (t0 + e < NT)
-                    d[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag(r.w[t0 + e][t4], km), d[e], 0, 0, 0);
+                    d[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag_biased(r.w[t0 + e][t4], km), d[e], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -430,7 +444,7 @@ RK_DEV void tile_compute(const TileRegs<NT>& r, int nt, Lds& S) {
             const int t = t0 + e;
             if (t < NT && L < 16 && t < nt) {
                 const uint32_t sm = r.sm[t];
-                S.tpart[w][t][L] = __builtin_fmaf(d[e][0], h16((uint16_t)sm), h16((uint16_t)(sm >> 16)) * hs);
+                S.tpart[w][t][L] = __builtin_fmaf(d[e][0] - hb, h16((uint16_t)sm), h16((uint16_t)(sm >> 16)) * hs);
             }
         }
     }

@@ -43,6 +43,21 @@ RK_DEV h8_t dequant_frag(uint32_t w, const Int4Masks& k) {
     return r;
 }
 
+// The MFMA B fragment with the codes left biased: (1024 + c0, 1024 + c4), (1024 + 16 c1, 1024 + 16 c5),
+// (1024 + c2, 1024 + c6), (1024 + 16 c3, 1024 + 16 c7), all exact in fp16: 5 VALU per 8 codes instead of 9. Against
+// A' (the activations in the same order with the (x1,x5), (x3,x7) pairs pre-scaled by 1/16, exact) an MFMA gives
+// sum_k x_k c_k + 1024 sum_k A'_k: the caller subtracts the second term, one fp32 constant per A operand (the
+// products are exact in fp32; the constant adds at most a few fp32 ulps of 1024 sum A' to each dot).
+RK_DEV h8_t dequant_frag_biased(uint32_t w, const Int4Masks& k) {
+    const uint32_t b = w >> 8;
+    const h2_t p0 = as_h2((w & k.lo) | k.magic), p1 = as_h2((w & k.hi) | k.magic);
+    const h2_t p2 = as_h2((b & k.lo) | k.magic), p3 = as_h2((b & k.hi) | k.magic);
+    h8_t r;
+    r[0] = p0.x; r[1] = p0.y; r[2] = p1.x; r[3] = p1.y;
+    r[4] = p2.x; r[5] = p2.y; r[6] = p3.x; r[7] = p3.y;
+    return r;
+}
+
 // 8 consecutive fp16 activations (x0..x7) -> pairs (x0,x4),(x1,x5),(x2,x6),(x3,x7), matching dequant_pairs
 RK_DEV void pair_permute(u4_t d, uint32_t (&h)[4]) {
     h[0] = perm(d.z, d.x, 0x05040100u);

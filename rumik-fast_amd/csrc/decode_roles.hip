@@ -178,7 +178,7 @@ __device__ unsigned long long* g_roles_trace;
 struct Lds {
     uint4 hfrag[kH / 8];                      // MFMA A fragments of h (group g: entries 16g .. 16g + 15)
     float hsum[kNG];                          // per-group sums of h
-    float hbias[kNG];                         // per group: 1024 x the sum of its A fragment entries (biased codes)
+    float hbias[kNG];                         // per group: 64 x the sum of its odd-column h (biased high nibbles)
     alignas(16) uint32_t hnat[kH / 2];        // the final h as natural fp16 pairs (the int8 head's input)
     float2 lnst[kWaves];                      // per wave: sum and squared deviations of its 128 x values
     float tpart[kWaves][kMaxTiles][16];       // K-split partial dots of the block's tiles (per wave = group)
@@ -361,23 +361,20 @@ RK_DEV u4_t layer_norm(const Params& p, Lds& S, int l, const XIn& in) {
 // (x0,x4),(x1,x5),(x2,x6),(x3,x7). The codes' tile layout gives MFMA lane j + 16s of 32-column chunk t4 the columns
 // 32s + 8 t4 .. + 7 (a lane's 16 bytes are the row's bytes [16s, 16s + 16), word t4 feeding chunk t4), so block
 // m = 4s + t4 goes to entry 16g + 4 t4 + s = 16g + 4 (m % 4) + m / 4, where chunk t4's A operand reads it.
-// The tiles' codes stay biased (dequant_frag_biased), so the (x1,x5), (x3,x7) pairs are staged divided by 16 and
-// hbias[g] = 1024 x the sum of the staged values is what the tile dots subtract.
+// The tiles' high-nibble codes stay biased by 64 (dequant_frag_hi64): hbias[g] = 64 x the sum of the group's
+// odd-column h, the pairs (x1,x5), (x3,x7), is what the tile dots subtract.
 RK_DEV void stage_h(const u4_t& h, Lds& S) {
     const int L = lane_id(), w = wave_id();
     const int g = 4 * w + (L >> 4), m = L & 15;
     uint32_t hp[4];
     pair_permute(h, hp);
-    const h2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-    hp[1] = as_u32(as_h2(hp[1]) * s16);
-    hp[3] = as_u32(as_h2(hp[3]) * s16);
     S.hfrag[16 * g + 4 * (m & 3) + (m >> 2)] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
     float s = 0.f, a = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const h2_t v = as_h2(h[e]), f = as_h2(hp[e]);
+        const h2_t v = as_h2(h[e]);
         s += (float)v.x + (float)v.y;
-        a += (float)f.x + (float)f.y;
+        a += (float)v.y;  // natural pairs (x_2e, x_2e+1): the odd column
     }
     s += dpp<0x128>(s);  // row_ror 8
     s += dpp<0x124>(s);  // row_ror 4
@@ -389,7 +386,7 @@ RK_DEV void stage_h(const u4_t& h, Lds& S) {
     a += dpp<0x121>(a);
     if (m == 0) {
         S.hsum[g] = s;
-        S.hbias[g] = 1024.f * a;
+        S.hbias[g] = 64.f * a;
     }
 }
 
@@ -436,7 +433,7 @@ RK_DEV void tile_compute(const TileRegs<NT>& r, int nt, Lds& S) {
 #pragma unroll
             for (int e = 0; e < 2; ++e)
                 if (t0 + e < NT)
-                    d[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag_biased(r.w[t0 + e][t4], km), d[e], 0, 0, 0);
+                    d[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag_hi64(r.w[t0 + e][t4], km), d[e], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll

@@ -13,10 +13,12 @@ RK_DEV uint32_t opaque_vgpr(uint32_t v) {
 }
 
 struct Int4Masks {
-    uint32_t lo, hi, magic;
+    uint32_t lo, hi, magic, magic64;
 };
 
-RK_DEV Int4Masks int4_masks() { return {opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)}; }
+RK_DEV Int4Masks int4_masks() {
+    return {opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u), opaque_vgpr(0x54005400u)};
+}
 
 // One dword of int4 codes (8 columns c0..c7, nibble i = column i) -> exact fp16 codes in the order
 // (c0,c4),(c1,c5),(c2,c6),(c3,c7): (w & 0x000F000F) | 0x64006400 is the fp16 pair (1024 + c0, 1024 + c4) (1024.0
@@ -43,15 +45,18 @@ RK_DEV h8_t dequant_frag(uint32_t w, const Int4Masks& k) {
     return r;
 }
 
-// The MFMA B fragment with the codes left biased: (1024 + c0, 1024 + c4), (1024 + 16 c1, 1024 + 16 c5),
-// (1024 + c2, 1024 + c6), (1024 + 16 c3, 1024 + 16 c7), all exact in fp16: 5 VALU per 8 codes instead of 9. Against
-// A' (the activations in the same order with the (x1,x5), (x3,x7) pairs pre-scaled by 1/16, exact) an MFMA gives
-// sum_k x_k c_k + 1024 sum_k A'_k: the caller subtracts the second term, one fp32 constant per A operand (the
-// products are exact in fp32; the constant adds at most a few fp32 ulps of 1024 sum A' to each dot).
-RK_DEV h8_t dequant_frag_biased(uint32_t w, const Int4Masks& k) {
+// The MFMA B fragment with the high-nibble codes left biased: (c0, c4), (64 + c1, 64 + c5), (c2, c6),
+// (64 + c3, 64 + c7), all exact fp16. A high nibble sits at bits 4..7 of its half, which under the exponent of 64.0
+// (0x5400, mantissa LSB worth 1/16) is worth exactly c: one v_and_or per pair, no fix-up (7 VALU per 8 codes
+// instead of 9). Against A (the activations in the same order, unscaled) an MFMA gives sum_k x_k c_k +
+// 64 sum_{k odd} x_k, the odd columns being those of the high nibbles: the caller subtracts 64 x (the sum of the
+// odd-column activations). The products are exact in fp32; the bias is about 8x the mean code, so it adds a few
+// fp32 ulps of a number of that size to each dot, far below the fp16 rounding of the result.
+RK_DEV h8_t dequant_frag_hi64(uint32_t w, const Int4Masks& k) {
+    const h2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
     const uint32_t b = w >> 8;
-    const h2_t p0 = as_h2((w & k.lo) | k.magic), p1 = as_h2((w & k.hi) | k.magic);
-    const h2_t p2 = as_h2((b & k.lo) | k.magic), p3 = as_h2((b & k.hi) | k.magic);
+    const h2_t p0 = as_h2((w & k.lo) | k.magic) + m1024, p1 = as_h2((w & k.hi) | k.magic64);
+    const h2_t p2 = as_h2((b & k.lo) | k.magic) + m1024, p3 = as_h2((b & k.hi) | k.magic64);
     h8_t r;
     r[0] = p0.x; r[1] = p0.y; r[2] = p1.x; r[3] = p1.y;
     r[4] = p2.x; r[5] = p2.y; r[6] = p3.x; r[7] = p3.y;

@@ -25,7 +25,8 @@ in flight); roofline.read_ceilings: that ceiling at each projection's exact byte
 and a dense bf16 GEMV's read rate.
 parity: the layer launch's outputs on copy 0 (q/k/v rows and down) and the w_in projection against the float64
 oracle (max_rel and max_rel_strict).
-decode_tok_s: the 36-layer step's tokens per second at ctx 256 / 1024 / 2048 (config 4).
+decode_tok_s: the 36-layer step's tokens per second at ctx 256 / 1024 / 2048 (config 4), as the role-split one-launch
+kernel (decode.RoleDecode); decode.persistent_engine times the every-block-every-role kernel on the same weights.
 cpu_baseline: the reference's CPU path for the same step, dequantize then matmul in torch fp32
 (kernels/int4_gemv.py:27-30 as kernels/bench_gemv.py:43 runs it) on CPU tensors with every thread torch is given,
 with a matmul-only time, and the numpy oracle's single-threaded dequantization and configs 2 / 3 / a config-4 layer
@@ -242,24 +243,13 @@ def cpu_baseline(budget_s):
     return res
 
 
-def run_decode(dev, steps):
-    """Config 4: tok/s of the 36-layer step as the one-launch persistent kernel, captured in a hipGraph
-    (random-init int4 weights, int8 head, fp16 KV cache ~N(0,1) filled to ctx - 1 slots; each step writes slot
-    ctx - 1 and attends over ctx slots). pos is reset before every replay (one tiny fill kernel per step, inside
-    the timed loop). Timed with HIP events on the engine's stream."""
+def _time_steps(eng, cfg, steps, ctxs):
+    """us per token of eng's captured step at each context (pos reset before every replay: one tiny fill kernel per
+    step, inside the timed loop), HIP events on the engine's stream"""
     import torch
-    import decode
-    import synth
-    cfg = decode.Config()
-    w = decode.random_weights(cfg, 4, device=dev)
-    w["head"][0][-1].zero_()  # </audio>'s row: its logit 0 is never sampled, so the generate run below is full length
-    eng = decode.PersistentDecode(cfg, w, device=dev, keep_layer_weights=True)  # the prefill reads the int4 layout
-    out = {"engine": "persistent one-launch step (hipGraph)", "weights_bytes_per_token": cfg.weight_bytes(),
-           "layers": cfg.L, "blocks": eng.nblocks}
-    eng.fill_cache(cfg.S, seed=5)
-    eng.set_state(7, 0)
+    res = {}
     eng.capture()
-    for ctx in (256, 1024, 2048):
+    for ctx in ctxs:
         for _ in range(10):
             eng.pos.fill_(ctx - 1)
             eng.replay()
@@ -273,10 +263,40 @@ def run_decode(dev, steps):
         torch.cuda.synchronize()
         dt = e0.elapsed_time(e1) / 1e3
         if eng.status_word() != 0:
-            raise RuntimeError(f"persistent decode step reported status {eng.status_word()}")
+            raise RuntimeError(f"one-launch decode step reported status {eng.status_word()}")
         nbytes = cfg.weight_bytes() + cfg.kv_bytes(ctx)
-        out[f"ctx{ctx}"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1),
+        res[f"ctx{ctx}"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1),
                             "GB_s": round(nbytes * steps / dt / 1e9, 1), "bytes_per_token": nbytes}
+    return res
+
+
+def run_decode(dev, steps):
+    """Config 4: tok/s of the 36-layer step as the role-split one-launch kernel (decode.RoleDecode), captured in a
+    hipGraph (random-init int4 weights, int8 head, fp16 KV cache ~N(0,1) filled to ctx - 1 slots; each step writes
+    slot ctx - 1 and attends over ctx slots); the every-block-every-role one-launch kernel (PersistentDecode) is
+    timed beside it on the same weights."""
+    import torch
+    import decode
+    import synth
+    cfg = decode.Config()
+    w = decode.random_weights(cfg, 4, device=dev)
+    w["head"][0][-1].zero_()  # </audio>'s row: its logit 0 is never sampled, so the generate run below is full length
+    ctxs = (256, 1024, 2048)
+    old = decode.PersistentDecode(cfg, w, device=dev, keep_layer_weights=True)
+    old.fill_cache(cfg.S, seed=5)
+    old.set_state(7, 0)
+    persistent = _time_steps(old, cfg, steps, ctxs)
+    log(f"[bench] decode, every-block-every-role step: {persistent}")
+    del old
+    torch.cuda.empty_cache()
+    eng = decode.RoleDecode(cfg, w, device=dev, keep_layer_weights=True)  # the prefill reads the int4 layout
+    out = {"engine": "role-split one-launch step (hipGraph)", "weights_bytes_per_token": cfg.weight_bytes(),
+           "layers": cfg.L, "blocks": eng.nblocks, "latency_groups_in_l2": eng.local_xcd,
+           "persistent_engine": persistent}
+    eng.fill_cache(cfg.S, seed=5)
+    eng.set_state(7, 0)
+    out.update(_time_steps(eng, cfg, steps, ctxs))
+    for ctx in ctxs:
         log(f"[bench] decode ctx {ctx}: {out[f'ctx{ctx}']}")
     # the same step with the sampling tail inside the graph (a full token: decode, head, stop predictor, top-30,
     # Gumbel-max pick; the sampled token is the next step's input), ctx 256
@@ -303,7 +323,7 @@ def run_decode(dev, steps):
     torch.cuda.synchronize()
     dt = e0.elapsed_time(e1) / 1e3
     if eng.status_word() != 0:
-        raise RuntimeError(f"persistent decode step reported status {eng.status_word()}")
+        raise RuntimeError(f"one-launch decode step reported status {eng.status_word()}")
     out["sampled_ctx256"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1)}
     log(f"[bench] decode + sampling ctx 256: {out['sampled_ctx256']}")
     # the host generate loop (frames of 8 replays, pinned read-back, one frame queued ahead): a 4-token prompt, then

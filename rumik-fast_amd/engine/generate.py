@@ -1,7 +1,8 @@
 """The host side of generation on MI355X: prompt, then captured decode steps read back a frame at a time.
 
-Mirrors RumikInt4.generate / to_codes (reference engine/rumik_int4.py:251-324) over PersistentDecode with the sampling
-tail attached (one hipGraph = decode step + sample; the sampled token is the next replay's input):
+Mirrors RumikInt4.generate / to_codes (reference engine/rumik_int4.py:251-324) over a one-launch decode engine
+(RoleDecode or PersistentDecode) with the sampling tail attached (one hipGraph = decode step + sample; the sampled
+token is the next replay's input):
 - frames of Q tokens (Q = num_quantizers, one Mimi frame): Q graph replays, then an asynchronous copy of the frame's
   tokens to pinned host memory and an event; the next frame is queued before waiting for the current one (double
   buffering: the GPU never idles while the host handles a frame), and waiting on the event waits only for the work
@@ -25,11 +26,12 @@ import torch
 
 
 class DecodeError(RuntimeError):
-    """The persistent decode step reported a nonzero status (see PersistentDecode.status_word)."""
+    """The one-launch decode step reported a nonzero status (see _OneLaunch.status_word in decode.py)."""
 
 
 class Generator:
-    """`eng`: a decode.PersistentDecode with attach_sampler() done. first_unit_id / last_unit_id bound the audio
+    """`eng`: a one-launch decode engine (decode.RoleDecode, the fastest, or decode.PersistentDecode) with
+    attach_sampler() done. first_unit_id / last_unit_id bound the audio
     token ids (config.json first_unit_id / last_unit_id); Q = num_quantizers."""
 
     def __init__(self, eng, Q=8, first_unit_id=None, last_unit_id=None, max_new=None, prefill=None):

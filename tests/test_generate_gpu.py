@@ -16,11 +16,17 @@ pytestmark = pytest.mark.gpu
 FIRST, Q = 100, 8
 
 
-def _engine(dev, b2, seed=3):
+@pytest.fixture(params=["roles", "persistent"])
+def kind(request):
+    """the one-launch engine under the loop: the role-split step (the default) or the every-block-every-role one"""
+    return request.param
+
+
+def _engine(dev, b2, kind, seed=3):
     cfg = decode.Config(L=2, vocab=1024, n_audio=700, S=512)
     w = decode.random_weights(cfg, seed, device=dev)
     w["head"][0][-1].zero_()  # </audio>'s logit is 0: never among the top 30 of 700 (~N(0, 18)) logits by chance
-    eng = decode.PersistentDecode(cfg, w, device=dev)
+    eng = (decode.RoleDecode if kind == "roles" else decode.PersistentDecode)(cfg, w, device=dev)
     g = torch.Generator().manual_seed(seed)
     stop = {"0.weight": torch.ones(cfg.H), "0.bias": torch.zeros(cfg.H),
             "1.weight": (torch.randn(512, cfg.H, generator=g) / cfg.H ** 0.5).bfloat16(),
@@ -43,8 +49,8 @@ def _stepwise(eng, prompt, seed, n):
     return toks
 
 
-def test_frames_match_stepwise_decoding(dev):
-    eng, ids = _engine(dev, b2=-50.0)
+def test_frames_match_stepwise_decoding(dev, kind):
+    eng, ids = _engine(dev, b2=-50.0, kind=kind)
     gen = Generator(eng, Q=Q, first_unit_id=FIRST, last_unit_id=FIRST + 698, max_new=64)
     prompt = [5, 17, 300, 41]
     toks, stats = gen.generate(prompt, seed=11)
@@ -58,20 +64,20 @@ def test_frames_match_stepwise_decoding(dev):
     assert torch.equal(codes, to_codes(toks, FIRST, FIRST + 698, Q))
 
 
-def test_stop_after_min_new(dev):
-    eng, ids = _engine(dev, b2=50.0)  # the stop logit is far above zero: </audio> from step min_new on
+def test_stop_after_min_new(dev, kind):
+    eng, ids = _engine(dev, b2=50.0, kind=kind)  # the stop logit is far above zero: </audio> from step min_new on
     gen = Generator(eng, Q=Q, max_new=64)
     toks, stats = gen.generate([3, 9], seed=2)
     assert len(toks) == eng.min_new and eng.end_id not in toks
     assert int(eng.out[eng.min_new].item()) == eng.end_id
 
 
-def test_nonzero_status_stops_generation(dev):
+def test_nonzero_status_stops_generation(dev, kind):
     """A step whose status word is nonzero ends generation with DecodeError instead of emitting tokens sampled from
     invalid logits. The condition is forced from the host: after the first frame the device position is moved past
     the cache, so the next step's blocks all leave at entry (status bit 2); no wait times out."""
     from generate import DecodeError
-    eng, ids = _engine(dev, b2=-50.0)
+    eng, ids = _engine(dev, b2=-50.0, kind=kind)
     gen = Generator(eng, Q=Q, max_new=64)
     seen = []
 

@@ -99,9 +99,11 @@ def test_prefill_matches_stepwise_oracle(dev, T):
             assert rep["norm_rel"] < 1e-2, (i, t, rep)
 
 
-def test_generate_from_batched_prefill(dev):
+@pytest.mark.parametrize("kind", ["roles", "persistent"])
+def test_generate_from_batched_prefill(dev, kind):
     cfg, wd, md = _model(dev, seed=22)
-    eng = decode.PersistentDecode(cfg, wd, device=dev, keep_layer_weights=True)
+    eng = (decode.RoleDecode if kind == "roles" else decode.PersistentDecode)(cfg, wd, device=dev,
+                                                                              keep_layer_weights=True)
     g = torch.Generator().manual_seed(5)
     stop = {"0.weight": torch.ones(cfg.H), "0.bias": torch.zeros(cfg.H),
             "1.weight": (torch.randn(512, cfg.H, generator=g) / cfg.H ** 0.5).bfloat16(),

@@ -73,6 +73,15 @@ RK_DEV uint32_t pack_h2(float a, float b) {
 // lane / thread indices through an empty asm: every use recomputes its addresses instead of the optimizer hoisting
 // dozens of 64-bit addresses out of the layer loop, where they would stay live (and spill) across the whole step
 RK_DEV int lane_id() { return (int)opaque_vgpr(threadIdx.x & 63); }
+// The launch parameters (the kernel's only argument, at offset 0 of the kernarg segment) through a pointer the
+// optimizer cannot see through: each layer re-reads the fields it uses with scalar loads instead of keeping every
+// field, and every pointer derived from one, live across the whole kernel, which overflows the SGPRs into VGPR lanes
+// (a v_writelane / v_readlane pair around every use).
+RK_DEV const rk_decode_roles_params& fresh() {
+    auto q = __builtin_amdgcn_kernarg_segment_ptr();  // constant address space: scalar loads
+    asm volatile("" : "+s"(q));
+    return *(const rk_decode_roles_params*)q;
+}
 RK_DEV int tid() { return (int)opaque_vgpr(threadIdx.x); }
 RK_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -1118,8 +1127,10 @@ struct LatencyRegs {
 };
 
 template <int REP, bool LAST>
-RK_DEV void latency_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int j, int l,
+RK_DEV void latency_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos, int64_t tok, int j, int l,
                           LatencyRegs<REP>& R) {
+    const Params& p = fresh();
+    (void)p_in;
     constexpr int NQ = LatencyRegs<REP>::NQ;
     const int w = wave_id();
     const uint32_t tag = tag_of(step, l);
@@ -1209,8 +1220,10 @@ struct StreamRegs {
 };
 
 template <bool LAST>
-RK_DEV void stream_layer(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int si, int sb, int se,
+RK_DEV void stream_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos, int64_t tok, int si, int sb, int se,
                          int l, StreamRegs& R) {
+    const Params& p = fresh();
+    (void)p_in;
     const int w = wave_id();
     const uint32_t tag = tag_of(step, l);
     const int t0 = (int)(n_tiles(p) - (size_t)p.inter / 8) + 2 * sb, nt = 2 * (se - sb);

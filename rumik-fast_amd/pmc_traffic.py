@@ -22,10 +22,11 @@ The same two steps for the one-launch layer projections (bench.py's step: w_in +
 launch of rk_gemv_int4_g128_layer): `run-layer` and `summarize-layer` (key gemv_layer_config1 of
 profiles/traffic.json).
 
-The same two steps for the one-launch 36-layer decode step (config 4): `run-decode` launches the copy kernel, then
-DECODE_STEPS eager steps at each of ctx 256, 1024 and 2048 (one dispatch each); `summarize-decode` gives the HBM bytes
-per token against the algorithmic bytes (every weight once plus the K/V slots read) and writes
-profiles/decode_step_traffic.json.
+The same two steps for the one-launch 36-layer decode step (config 4): `run-decode [roles|persistent]` launches the
+copy kernel, then DECODE_STEPS eager steps at each of ctx 256, 1024 and 2048 (one dispatch each) of the role-split
+step (decode.RoleDecode, the default) or the every-block-every-role one (decode.PersistentDecode);
+`summarize-decode DIR DIR [roles|persistent]` gives the HBM bytes per token against the algorithmic bytes (every
+weight once plus the K/V slots read) and writes that engine's entry of profiles/decode_step_traffic.json.
 """
 import csv
 import glob
@@ -192,7 +193,10 @@ DECODE_STEPS = 4
 DECODE_CTX = (256, 1024, 2048)
 
 
-def run_decode():
+DECODE_KERNEL = {"roles": "decode_roles_kernel", "persistent": "decode_step_kernel"}
+
+
+def run_decode(engine="roles"):
     sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "kernels"))
     sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "engine"))
     import torch
@@ -201,7 +205,8 @@ def run_decode():
     src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device=dev)
     dst = torch.empty_like(src)
     cfg = decode.Config()
-    eng = decode.PersistentDecode(cfg, decode.random_weights(cfg, 4, device=dev), device=dev)
+    cls = {"roles": decode.RoleDecode, "persistent": decode.PersistentDecode}[engine]
+    eng = cls(cfg, decode.random_weights(cfg, 4, device=dev), device=dev)
     eng.fill_cache(cfg.S, seed=5)
     eng.set_state(7, 0)
     torch.cuda.synchronize()
@@ -229,12 +234,12 @@ def _per_dispatch_list(rows, counter, pred):
     return [per[k] for k in sorted(per)]
 
 
-def summarize_decode(fetch_dir, write_dir):
+def summarize_decode(fetch_dir, write_dir, engine="roles"):
     sys.path.insert(0, str(ROOT / "rumik-fast_amd" / "engine"))
     import decode
     cfg = decode.Config()
     is_copy = lambda n: "neg" in n.lower()  # noqa: E731
-    is_dec = lambda n: "decode_step_kernel" in n  # noqa: E731
+    is_dec = lambda n: DECODE_KERNEL[engine] in n  # noqa: E731
     fr, wr = _rows(fetch_dir), _rows(write_dir)
     f_copy, _ = _per_dispatch(fr, "FETCH_SIZE", is_copy)
     w_copy, _ = _per_dispatch(wr, "WRITE_SIZE", is_copy)
@@ -243,7 +248,8 @@ def summarize_decode(fetch_dir, write_dir):
     n = DECODE_STEPS
     if len(fd) != n * len(DECODE_CTX) or len(wd) != n * len(DECODE_CTX):
         raise SystemExit(f"expected {n * len(DECODE_CTX)} decode dispatches, got {len(fd)} / {len(wd)}")
-    rec = {"fetch_scale": round(kf, 4), "write_scale": round(kw, 4), "steps_per_ctx": n}
+    rec = {"kernel": DECODE_KERNEL[engine], "fetch_scale": round(kf, 4), "write_scale": round(kw, 4),
+           "steps_per_ctx": n}
     print("| ctx | FETCH_SIZE / step | WRITE_SIZE / step | HBM bytes / token (scaled) | algorithmic bytes / token "
           "| traffic / algorithmic |\n|---|---|---|---|---|---|")
     for i, ctx in enumerate(DECODE_CTX):
@@ -254,7 +260,12 @@ def summarize_decode(fetch_dir, write_dir):
         rec[f"ctx{ctx}"] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "traffic_bytes": round(fb + wb),
                             "algorithmic_bytes": alg, "ratio": round((fb + wb) / alg, 4)}
         print(f"| {ctx} | {f:,.0f} KiB | {w:,.0f} KiB | {fb + wb:,.0f} B | {alg:,} B | {(fb + wb) / alg:.3f} |")
-    (ROOT / "profiles" / "decode_step_traffic.json").write_text(json.dumps(rec, indent=1) + "\n")
+    path = ROOT / "profiles" / "decode_step_traffic.json"
+    allrec = json.loads(path.read_text()) if path.exists() else {}
+    if "ctx256" in allrec:  # the single-engine layout: that record is the every-block-every-role kernel's
+        allrec = {"persistent": allrec}
+    allrec[engine] = rec
+    path.write_text(json.dumps(allrec, indent=1) + "\n")
 
 
 if __name__ == "__main__":
@@ -264,11 +275,11 @@ if __name__ == "__main__":
         run_layer()
     elif len(sys.argv) == 4 and sys.argv[1] == "summarize-layer":
         summarize_layer(sys.argv[2], sys.argv[3])
-    elif len(sys.argv) >= 2 and sys.argv[1] == "run-decode":
-        run_decode()
+    elif len(sys.argv) in (2, 3) and sys.argv[1] == "run-decode":
+        run_decode(*sys.argv[2:])
     elif len(sys.argv) == 4 and sys.argv[1] == "summarize":
         summarize(sys.argv[2], sys.argv[3])
-    elif len(sys.argv) == 4 and sys.argv[1] == "summarize-decode":
-        summarize_decode(sys.argv[2], sys.argv[3])
+    elif len(sys.argv) in (4, 5) and sys.argv[1] == "summarize-decode":
+        summarize_decode(*sys.argv[2:])
     else:
         raise SystemExit(__doc__)

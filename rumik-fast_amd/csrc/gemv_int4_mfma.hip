@@ -5,7 +5,7 @@
 //
 // Why MFMA for a GEMV: at ~7 TB/s a SIMD receives ~1 KB of codes every ~360 cycles. Doing the multiply-adds on
 // the VALU (v_dot2_f32_f16) costs ~13 VALU ops per 8 codes plus a cross-lane reduction (measured: 129 VALU
-// instructions per KB, VALU-bound at ~2.2 TB/s). Here the VALU only unpacks the codes (7 ops per 8 codes) and
+// instructions per KB, VALU-bound at ~2.2 TB/s). Here the VALU only dequantizes (9 ops per 8 codes) and
 // v_mfma_f32_16x16x32_f16 does the products and the reduction over K; only 1/16 of each MFMA is useful, but the
 // matrix pipe has >10x headroom at this arithmetic intensity.
 //
@@ -13,16 +13,12 @@
 // D[i][j] in lane j+16*(i/4) element i%4 — checked on the hardware):
 //   * a wave owns a tile of 16 rows; lane l works on row j = l%16 and on the 16-byte quarter s = l/16 of each
 //     128-column group: one global_load_dwordx4 per (row, group), so a wave instruction reads 16 rows x 64 B;
-//   * the 4 dwords of that quarter are the B fragments of 4 MFMAs (K-slice s) in the order
-//     (c0,c4),(c1,c5),(c2,c6),(c3,c7): low nibbles by the 1024 magic, (w & 0x000F000F) | 0x64006400 = fp16
-//     (1024 + c0, 1024 + c4), minus 1024 in packed fp16; high nibbles left biased, (w & 0x00F000F0) | 0x54005400 =
-//     fp16 (64 + c1, 64 + c5) (bits 4..7 under the exponent of 64.0 are worth c), all exact;
-//   * A holds x in the same permuted order, staged once per block in LDS as 16-byte fragments; every A row is the
-//     same x, so every lane's D element 0 is its row's sum_k x_k c_k + 64 sum_{k odd} x_k over the group (no
-//     cross-lane reduction);
-//   * per group: acc += scale * (dot - xbias_g) + min * xsum_g, fp32, with xsum_g = sum of x and
-//     xbias_g = 64 x the sum of its odd-column x, both from LDS (the products are exact in fp32; the bias, ~8x the
-//     mean code, adds a few fp32 ulps of a number of that size to each group's dot);
+//   * the 4 dwords of that quarter are the B fragments of 4 MFMAs (K-slice s): the 1024-magic dequant,
+//     (w & 0x000F000F) | 0x64006400 = fp16 (1024 + c0, 1024 + c4), minus 1024 in packed fp16, gives exact codes
+//     in the order (c0,c4),(c1,c5),(c2,c6),(c3,c7) (high nibbles: 1024 + 16c, times 1/16 minus 64);
+//   * A holds x in the same permuted order, staged once per block in LDS as 16-byte fragments; every A row is
+//     the same x, so every lane's D element 0 is its row's dot over the group (no cross-lane reduction);
+//   * per group: acc += scale * dot + min * xsum_g, fp32; xsum_g comes from LDS;
 //   * KS waves of a block split the groups of the same tile (fills the chip for N = 2048); partial sums are added
 //     through LDS, lanes 0..15 of the first wave store.
 #include "internal.h"
@@ -44,17 +40,19 @@ RK_DEV uint32_t opaque_vgpr(uint32_t v) {
 }
 
 struct Consts {
-    uint32_t lo_mask, hi_mask, magic, magic64;
+    uint32_t lo_mask, hi_mask, magic;
 };
 
-// one dword of codes (8 columns) -> B fragment (c0, c4, 64 + c1, 64 + c5, c2, c6, 64 + c3, 64 + c7), exact fp16
+// one dword of codes (8 columns) -> B fragment (c0,c4,c1,c5,c2,c6,c3,c7) as exact fp16
 RK_DEV h8_t dequant8(uint32_t w, const Consts& k) {
     const h2_t m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    const h2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const h2_t m64 = {(_Float16)-64.f, (_Float16)-64.f};
     const uint32_t b = w >> 8;
     const h2_t p0 = as_h2(and_or(w, k.lo_mask, k.magic)) + m1024;
-    const h2_t p1 = as_h2(and_or(w, k.hi_mask, k.magic64));
+    const h2_t p1 = as_h2(and_or(w, k.hi_mask, k.magic)) * s16 + m64;
     const h2_t p2 = as_h2(and_or(b, k.lo_mask, k.magic)) + m1024;
-    const h2_t p3 = as_h2(and_or(b, k.hi_mask, k.magic64));
+    const h2_t p3 = as_h2(and_or(b, k.hi_mask, k.magic)) * s16 + m64;
     h8_t r;
     r[0] = p0.x; r[1] = p0.y; r[2] = p1.x; r[3] = p1.y;
     r[4] = p2.x; r[5] = p2.y; r[6] = p3.x; r[7] = p3.y;
@@ -62,8 +60,7 @@ RK_DEV h8_t dequant8(uint32_t w, const Consts& k) {
 }
 
 // Stage x in LDS: fragment f = g*16 + t*4 + s holds the 8 values of columns 128g + 32s + 8t + (0,4,1,5,2,6,3,7)
-// as fp16; xs[g] = (fp32 sum of the group's 128 values, 64 x the fp32 sum of its odd-column values). Every thread
-// of the block takes part.
+// as fp16; xsum[g] = fp32 sum of the group's 128 values. Every thread of the block takes part.
 // kXPre 8-column blocks per thread are loaded into registers before the weights (x_issue), so that staging them
 // (stage_x) waits for x only: vector-memory results return in issue order. Longer x (more than kXPre blocks per
 // thread) is loaded in the staging loop itself.
@@ -82,7 +79,7 @@ RK_DEV void x_issue(const void* __restrict__ x, int K, XRegs& xr) {
 
 // one 8-column block: fp16 pairs in dequant order (or bf16 converted) + its fp32 sum -> LDS fragment; the
 // 16 threads of a group then sum their parts inside a 16-lane DPP row
-RK_DEV void stage_block(int i, int nb, int xdt, u4_t d, uint4* __restrict__ frag, float2* __restrict__ xs) {
+RK_DEV void stage_block(int i, int nb, int xdt, u4_t d, uint4* __restrict__ frag, float* __restrict__ xsum) {
     // the conversion runs unconditionally (only the LDS writes are guarded): a value used only under i < nb would let
     // the compiler sink its load behind the weight loads, and the staging would then wait for all of them
     const bool ok = i < nb;
@@ -113,28 +110,22 @@ RK_DEV void stage_block(int i, int nb, int xdt, u4_t d, uint4* __restrict__ frag
 #pragma unroll
         for (int e = 0; e < 4; ++e) sum = dot2(as_h2(d[e]), one, sum);
     }
-    const float a = dot2(as_h2(h[3]), one, dot2(as_h2(h[1]), one, 0.f));  // (x1,x5) + (x3,x7): the odd columns
     const int g = i >> 4, r = i & 15;  // column offset in the group: 8r = 32s + 8t
     const int s = r >> 2, t = r & 3;
     if (ok) frag[g * 16 + t * 4 + s] = make_uint4(h[0], h[1], h[2], h[3]);
     sum = ok ? sum : 0.f;
-    float ab = ok ? a : 0.f;
     sum += dpp<0x128>(sum);  // 16 consecutive threads hold one group: sum inside their 16-lane DPP row (row_ror:8)
     sum += dpp<0x124>(sum);  // row_ror:4
     sum += dpp<0x122>(sum);  // row_ror:2
     sum += dpp<0x121>(sum);  // row_ror:1
-    ab += dpp<0x128>(ab);
-    ab += dpp<0x124>(ab);
-    ab += dpp<0x122>(ab);
-    ab += dpp<0x121>(ab);
-    if (ok && (i & 15) == 0) xs[i >> 4] = make_float2(sum, 64.f * ab);
+    if (ok && (i & 15) == 0) xsum[i >> 4] = sum;
 }
 
 // XREG (K / 8 <= kXPre * blockDim, chosen on the host): every block of x is in registers already. It is a template
 // parameter so that the x loads are not sunk into a branch behind the weight loads.
 template <bool XREG>
 RK_DEV void stage_x(const void* __restrict__ x, int xdt, int K, const XRegs& xr, uint4* __restrict__ frag,
-                    float2* __restrict__ xsum) {
+                    float* __restrict__ xsum) {
     const int nb = K >> 3;  // 8-column blocks
     if constexpr (XREG) {
         stage_block(threadIdx.x, nb, xdt, xr.d[0], frag, xsum);  // unguarded: its x load stays ahead of the weights
@@ -195,10 +186,10 @@ RK_DEV void load_batch(Batch& b, const uint8_t* qrow, const uint16_t* srow, cons
 
 // dequant + 4 MFMAs per group (each group waits only for its own codes; the next group's x fragments are read from
 // LDS while the current group's MFMAs run), then the group affines into acc once the batch's scales / mins are in
-// (whatever order the compiler issued them in): acc += scale * (dot - xbias_g) + min * xsum_g. FULL batches have
-// no per-group checks.
+// (whatever order the compiler issued them in): acc += scale * dot + min * xsum_g. FULL batches have no per-group
+// checks.
 template <bool FULL>
-RK_DEV void compute_batch(const Batch& b, const uint4* frag, const float2* xsum, int s, int gb, int g1,
+RK_DEV void compute_batch(const Batch& b, const uint4* frag, const float* xsum, int s, int gb, int g1,
                           const Consts& kc, float& acc) {
     float dg[kGB];
     h8_t A[4];
@@ -229,8 +220,7 @@ RK_DEV void compute_batch(const Batch& b, const uint4* frag, const float2* xsum,
     for (int e = 0; e < kGB; ++e) {
         const int g = gb + e;
         if (FULL || g < g1) {
-            const float2 xg = xsum[g];
-            acc = __builtin_fmaf(dg[e] - xg.y, f16_bits_to_f32(b.sv[e]), __builtin_fmaf(f16_bits_to_f32(b.mv[e]), xg.x, acc));
+            acc = __builtin_fmaf(dg[e], f16_bits_to_f32(b.sv[e]), __builtin_fmaf(f16_bits_to_f32(b.mv[e]), xsum[g], acc));
         }
     }
 }
@@ -258,8 +248,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
     extern __shared__ __align__(16) uint8_t smem[];
     const int NG = K >> 7;
     uint4* frag = reinterpret_cast<uint4*>(smem);
-    float2* xsum = reinterpret_cast<float2*>(smem + (size_t)K * 2);
-    float* red = reinterpret_cast<float*>(xsum + NG);  // [waves][16]
+    float* xsum = reinterpret_cast<float*>(smem + (size_t)K * 2);
+    float* red = xsum + NG;  // [waves][16]
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int team = wave / KS, kw = wave - team * KS;
@@ -287,8 +277,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
     stage_x<XREG>(x, xdt, K, xr, frag, xsum);
     __syncthreads();
 
-    const Consts kc = {opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u),
-                       opaque_vgpr(0x54005400u)};
+    const Consts kc = {opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
     float acc = 0.f;
     if (g1 - g0 == kGB) {  // wave-uniform: one full batch, nothing more to load (straight-line waits)
         compute_batch<true>(cur, frag, xsum, s, g0, g1, kc, acc);
@@ -333,7 +322,7 @@ hipError_t launch_mfma(const void* x, int xdt, const uint8_t* q, const uint16_t*
     const int tiles = (plain + 15) / 16 + (inter + 7) / 8;
     const int blocks = (tiles + teams - 1) / teams;
     const int threads = 64 * KS * teams;
-    const size_t lds = (size_t)K * 2 + (size_t)(K / 128) * 8 + (size_t)teams * KS * 16 * 4;
+    const size_t lds = (size_t)K * 2 + (size_t)(K / 128) * 4 + (size_t)teams * KS * 16 * 4;
 #define RK_LAUNCH(XR, PR)                                                                                          \
     hipLaunchKernelGGL((gemv_int4_mfma_kernel<KS, VEC, XR, PR>), dim3(blocks), dim3(threads), lds, st, x, xdt, q, s, \
                        m, y, ydt, plain, inter, act, K)
@@ -373,7 +362,7 @@ static int gemv_mfma_run(const void* x, int x_dtype, const uint8_t* q, const uin
     if (((uintptr_t)x & 15) || ((uintptr_t)q & 15)) return RK_ERR_ALIGN;
     if (waves && !(waves == 1 || waves == 2 || waves == 4 || waves == 8 || waves == 16)) return RK_ERR_BLOCK;
     if (waves > 4) waves = 4;  // blocks hold at most 4 waves here (each may use up to 168 VGPRs)
-    if ((size_t)K * 2 + (size_t)(K / 128) * 8 + 16 * 16 * 4 > 160 * 1024) return RK_ERR_SHAPE;  // x must fit in LDS
+    if ((size_t)K * 2 + (size_t)(K / 128) * 4 + 16 * 16 * 4 > 160 * 1024) return RK_ERR_SHAPE;  // x must fit in LDS
     int ks, teams;
     plan_mfma((plain + 15) / 16 + (inter + 7) / 8, K, waves, &ks, &teams);
     const int NG = K / 128;

@@ -1,8 +1,9 @@
 #!/usr/bin/env python3
-"""HBM traffic per launch of the fused w_in int4 GEMV + SiLU*up (rows [qkv 3072 | gate 11008 | up 11008], K=2048;
-the dominant kernel of bench.py's step), from rocprofv3 hardware counters.
+"""HBM traffic per launch from rocprofv3 hardware counters: the one-launch layer projections (rk_gemv_int4_g128_layer,
+the dominant kernel of bench.py's step and the source of its roofline.traffic), the fused w_in int4 GEMV + SiLU*up
+(rows [qkv 3072 | gate 11008 | up 11008], K=2048) and the one-launch 36-layer decode step.
 
-Two steps:
+Two steps for the fused w_in GEMV:
 
     run        launches a plain elementwise copy of known size (torch.neg over 256 MiB fp16: reads and writes
                268,435,456 B each) and then the fused w_in GEMV over 16 rotated weight copies, eagerly, one dispatch

@@ -82,9 +82,10 @@ def test_ragged(M, N, K, dev):
 @pytest.mark.parametrize("M,N,K", [(34, 2048, 11008), (34, 3072, 4096), (5, 200, 4096), (128, 2048, 11008),
                                    (64, 2048, 11008)])
 def test_split_k_matches_single_pass(M, N, K, dev):
-    """The split-K plans (fp32 partials + ordered sum: the stream kernel's K chunks for M <= 48, the 64 x 64 tile
-    kernel's K splits above) against the single-pass kernel of rk_mm_int4_g128 and the oracle; both calls go through
-    the C ABI, the second twice into one workspace."""
+    """The workspace entry's split-K plans (fp32 partials + ordered sum over K splits of the tile kernels; the stream
+    kernel, which serves M <= 48 only for K <= 2048 and has no K split, takes none of these shapes) against the
+    single-pass kernel of rk_mm_int4_g128 and the oracle; both calls go through the C ABI, the second twice into one
+    workspace."""
     L = H.lib()
     nws = L.rk_mm_int4_workspace_bytes(M, N, K)
     assert nws > 0

@@ -349,28 +349,36 @@ struct KVChunks {
 };
 
 // loads of key block j0 (slots past `last` re-read slot `last`: every load valid and unconditional, so the compiler
-// waits for exactly the chunks it stores; those keys are masked out of S and get P = 0)
+// waits for exactly the chunks it stores; those keys are masked out of S and get P = 0). Chunk e of K is key
+// e / 16, dims 8 (e % 16) .. + 8 (16 consecutive lanes: one 256-byte row); chunk e of V is key e % 32, dims
+// 8 (e / 32) .. + 8, so that the 32 lanes writing one transposed row of Vt write 32 consecutive keys (64 bytes)
+// instead of 16 lanes hitting one bank 512 bytes apart.
+constexpr int kKsPad = 8;  // K rows padded by 16 bytes: the QK fragment reads of 16 rows then spread over the banks
+
 template <int CH>
 RK_DEV void kv_load(const uint16_t* kg, const uint16_t* vg, int j0, int last, KVChunks<CH>& c) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-        const int e = threadIdx.x + u * blockDim.x, kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
-        const size_t row = (size_t)min(j0 + kj, last) * kHD + d8;
-        c.k[u] = *reinterpret_cast<const u4_t*>(kg + row);
-        c.v[u] = *reinterpret_cast<const u4_t*>(vg + row);
+        const int e = threadIdx.x + u * blockDim.x;
+        const int kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
+        c.k[u] = *reinterpret_cast<const u4_t*>(kg + (size_t)min(j0 + kj, last) * kHD + d8);
+        const int vj = e % kKB, v8 = (e / kKB) * 8;
+        c.v[u] = *reinterpret_cast<const u4_t*>(vg + (size_t)min(j0 + vj, last) * kHD + v8);
     }
 }
 
 template <int CH>
-RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kHD], uint16_t (*Vt)[kKB]) {
+RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kHD + kKsPad], uint16_t (*Vt)[kKB]) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-        const int e = threadIdx.x + u * blockDim.x, kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
+        const int e = threadIdx.x + u * blockDim.x;
+        const int kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
         *reinterpret_cast<u4_t*>(&Ks[kj][d8]) = c.k[u];
+        const int vj = e % kKB, v8 = (e / kKB) * 8;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            Vt[d8 + 2 * w][kj] = (uint16_t)c.v[u][w];
-            Vt[d8 + 2 * w + 1][kj] = (uint16_t)(c.v[u][w] >> 16);
+            Vt[v8 + 2 * w][vj] = (uint16_t)c.v[u][w];
+            Vt[v8 + 2 * w + 1][vj] = (uint16_t)(c.v[u][w] >> 16);
         }
     }
 }
@@ -380,7 +388,7 @@ __global__ __launch_bounds__(64 * REP) void prefill_attn_kernel(const uint16_t* 
                                                                  const uint16_t* vc, uint16_t* o, int T, int p0,
                                                                  int NH, int NKV, int S, float scale) {
     constexpr int CH = kKB * kHD / 8 / (64 * REP);
-    __shared__ __align__(16) uint16_t Ks[kKB][kHD];     // K rows of the key block
+    __shared__ __align__(16) uint16_t Ks[kKB][kHD + kKsPad];  // K rows of the key block (padded)
     __shared__ __align__(16) uint16_t Vt[kHD][kKB];     // V transposed: Vt[dim][key]
     extern __shared__ __align__(16) uint16_t Ps[];      // per wave: P [16 queries][32 keys]
     const int g = blockIdx.x, q0 = blockIdx.y * kQT;

@@ -25,6 +25,10 @@ constexpr int kMaxPer = 32;  // H <= 8192
 constexpr int kHD = 128;
 constexpr int kKB = 32;      // keys per block step
 constexpr int kQT = 16;      // queries per tile
+#ifndef RK_ATTN_KS
+#define RK_ATTN_KS 2
+#endif
+constexpr int kAttnKS = RK_ATTN_KS;  // key groups per attention block (query heads per KV head <= 4)
 
 RK_DEV float block_sum(float v, float* red) {
     v = wave_sum(v);
@@ -340,63 +344,82 @@ RK_DEV float row16_sum(float v) {
     return v;
 }
 
-// grid (NKV, ceil(T / 16)), 64 * REP threads. q: [T, NH * 128] fp16 (RoPE applied); kc / vc: the layer's cache
+// grid (NKV, ceil(T / 16)), 64 * REP * KS threads. q: [T, NH * 128] fp16 (RoPE applied); kc / vc: the layer's cache
 // [NKV, S, 128] fp16 holding slots 0 .. p0 + T - 1; o: [T, NH * 128] fp16. Query t attends slots 0 .. p0 + t.
-// the K / V chunks (8 dims of one key) of a key block that thread tid stages: CH = 512 / blockDim per thread
+// Wave w = REP ks + r computes query head g REP + r over the key blocks ks, ks + KS, ks + 2 KS, ... of the tile's
+// range (KS wave groups walk the keys side by side, each with its own online softmax), and the KS partial results
+// of a head are merged through LDS at the end. One step stages KS key blocks (one per group) in LDS.
 template <int CH>
 struct KVChunks {
     u4_t k[CH], v[CH];  // native vectors (HIP's uint4 is a struct with a union, which stays in scratch memory)
 };
 
-// loads of key block j0 (slots past `last` re-read slot `last`: every load valid and unconditional, so the compiler
-// waits for exactly the chunks it stores; those keys are masked out of S and get P = 0). Chunk e of K is key
-// e / 16, dims 8 (e % 16) .. + 8 (16 consecutive lanes: one 256-byte row); chunk e of V is key e % 32, dims
-// 8 (e / 32) .. + 8, so that the 32 lanes writing one transposed row of Vt write 32 consecutive keys (64 bytes)
-// instead of 16 lanes hitting one bank 512 bytes apart.
+// Chunk e of a step (e < KS * 512): key block e / 512 of the step; within it, chunk e' = e % 512 of K and of V is
+// key e' / 16, dims 8 (e' % 16) .. + 8 (16 consecutive lanes: one 256-byte row, coalesced). V goes to LDS
+// transposed, Vt[dim][key], each dim row rotated by 8 ((dim / 8) % 4) keys (vt_col): the 16 lanes that write one
+// key's dims into rows 8 apart (64 bytes each) then spread over four bank groups instead of one, and a 16-byte
+// fragment read (8 keys of one row) stays contiguous. Slots past `last` re-read slot `last`: every load valid and
+// unconditional, so the compiler waits for exactly the chunks it stores; those keys are masked out of S (P = 0).
 constexpr int kKsPad = 8;  // K rows padded by 16 bytes: the QK fragment reads of 16 rows then spread over the banks
+constexpr int kChunksPerKB = kKB * kHD / 8;  // 512
+
+// column of key j in transposed row d of Vt
+RK_DEV int vt_col(int d, int j) { return (j + 8 * ((d >> 3) & 3)) & (kKB - 1); }
 
 template <int CH>
-RK_DEV void kv_load(const uint16_t* kg, const uint16_t* vg, int j0, int last, KVChunks<CH>& c) {
+RK_DEV void kv_load(const uint16_t* kg, const uint16_t* vg, int s0, int KS, int last, KVChunks<CH>& c) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-        const int e = threadIdx.x + u * blockDim.x;
-        const int kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
+        const int e = threadIdx.x + u * blockDim.x, kb = e / kChunksPerKB, ep = e % kChunksPerKB;
+        const int j0 = (s0 + kb) * kKB;  // s0: the step's first key block
+        const int kj = ep / (kHD / 8), d8 = (ep % (kHD / 8)) * 8;
         c.k[u] = *reinterpret_cast<const u4_t*>(kg + (size_t)min(j0 + kj, last) * kHD + d8);
-        const int vj = e % kKB, v8 = (e / kKB) * 8;
-        c.v[u] = *reinterpret_cast<const u4_t*>(vg + (size_t)min(j0 + vj, last) * kHD + v8);
+        c.v[u] = *reinterpret_cast<const u4_t*>(vg + (size_t)min(j0 + kj, last) * kHD + d8);
     }
+    (void)KS;
 }
 
 template <int CH>
-RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kHD + kKsPad], uint16_t (*Vt)[kKB]) {
+RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kKB][kHD + kKsPad], uint16_t (*Vt)[kHD][kKB]) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-        const int e = threadIdx.x + u * blockDim.x;
-        const int kj = e / (kHD / 8), d8 = (e % (kHD / 8)) * 8;
-        *reinterpret_cast<u4_t*>(&Ks[kj][d8]) = c.k[u];
-        const int vj = e % kKB, v8 = (e / kKB) * 8;
+        const int e = threadIdx.x + u * blockDim.x, kb = e / kChunksPerKB, ep = e % kChunksPerKB;
+        const int kj = ep / (kHD / 8), d8 = (ep % (kHD / 8)) * 8;
+        *reinterpret_cast<u4_t*>(&Ks[kb][kj][d8]) = c.k[u];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            Vt[v8 + 2 * w][vj] = (uint16_t)c.v[u][w];
-            Vt[v8 + 2 * w + 1][vj] = (uint16_t)(c.v[u][w] >> 16);
+            Vt[kb][d8 + 2 * w][vt_col(d8 + 2 * w, kj)] = (uint16_t)c.v[u][w];
+            Vt[kb][d8 + 2 * w + 1][vt_col(d8 + 2 * w + 1, kj)] = (uint16_t)(c.v[u][w] >> 16);
         }
     }
 }
 
-template <int REP>
-__global__ __launch_bounds__(64 * REP) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc,
-                                                                 const uint16_t* vc, uint16_t* o, int T, int p0,
-                                                                 int NH, int NKV, int S, float scale) {
-    constexpr int CH = kKB * kHD / 8 / (64 * REP);
-    __shared__ __align__(16) uint16_t Ks[kKB][kHD + kKsPad];  // K rows of the key block (padded)
-    __shared__ __align__(16) uint16_t Vt[kHD][kKB];     // V transposed: Vt[dim][key]
-    extern __shared__ __align__(16) uint16_t Ps[];      // per wave: P [16 queries][32 keys]
+// dynamic LDS of prefill_attn_kernel<REP, KS>: the staging (KS key blocks of K and transposed V, one P tile per
+// wave), reused after the key loop for the merge (REP partial results of 16 x 128 fp32 plus m / l per row)
+constexpr size_t attn_stage_bytes(int REP, int KS) {
+    return (size_t)KS * kKB * (kHD + kKsPad) * 2 + (size_t)KS * kHD * kKB * 2 + (size_t)REP * KS * kQT * kKB * 2;
+}
+constexpr size_t attn_merge_bytes(int REP) { return (size_t)REP * (64 * 32 + 2 * kQT) * 4; }
+constexpr size_t attn_lds_bytes(int REP, int KS) {
+    return attn_stage_bytes(REP, KS) > attn_merge_bytes(REP) ? attn_stage_bytes(REP, KS) : attn_merge_bytes(REP);
+}
+
+template <int REP, int KS>
+__global__ __launch_bounds__(64 * REP * KS) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc,
+                                                                      const uint16_t* vc, uint16_t* o, int T, int p0,
+                                                                      int NH, int NKV, int S, float scale) {
+    constexpr int CH = KS * kChunksPerKB / (64 * REP * KS);
+    extern __shared__ __align__(16) uint8_t lds[];
+    auto Ks = reinterpret_cast<uint16_t(*)[kKB][kHD + kKsPad]>(lds);
+    auto Vt = reinterpret_cast<uint16_t(*)[kHD][kKB]>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2);
+    uint16_t* Ps = reinterpret_cast<uint16_t*>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2 + (size_t)KS * kHD * kKB * 2);
     const int g = blockIdx.x, q0 = blockIdx.y * kQT;
-    const int lane = threadIdx.x & 63, r = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int r = w % REP, ks = w / REP;
     const int h = g * REP + r;
     const int li = lane & 15, lq = lane >> 4;  // A / B fragment: row or column li, k-group lq
     const int ldq = NH * kHD;
-    uint16_t* P = Ps + r * kQT * kKB;
+    uint16_t* P = Ps + w * kQT * kKB;
     // Q fragments of this wave's head: query q0 + li, dims 32c + 8 lq .. + 8
     h8_t Qf[4];
     {
@@ -417,70 +440,110 @@ __global__ __launch_bounds__(64 * REP) void prefill_attn_kernel(const uint16_t* 
     const uint16_t* kg = kc + (size_t)g * S * kHD;
     const uint16_t* vg = vc + (size_t)g * S * kHD;
     const int last = p0 + min(q0 + kQT, T) - 1;  // the last slot any query of the tile sees
-    // K / V of the next two key blocks are in flight in registers while a block is computed: set A holds the even
-    // steps, set B the odd ones (the loop is unrolled by two so that neither is copied)
+    const int kb0 = 0, kb1 = last / kKB + 1;      // the tile's key blocks
+    const int nsteps = (kb1 - kb0 + KS - 1) / KS;  // steps of KS key blocks
+    // K / V of the next two steps are in flight in registers while a step is computed: set A holds the even steps,
+    // set B the odd ones (the loop is unrolled by two so that neither is copied)
     KVChunks<CH> ka, kb;
-    kv_load<CH>(kg, vg, 0, last, ka);
-    kv_load<CH>(kg, vg, kKB, last, kb);
-    // one key block step (a macro, not a lambda: the register sets must stay promotable to registers)
-#define RK_ATTN_STEP(j0, cur) \
-    __syncthreads();  /* the previous block step's K / V are no longer read */ \
+    kv_load<CH>(kg, vg, kb0, KS, last, ka);
+    kv_load<CH>(kg, vg, kb0 + KS, KS, last, kb);
+    // one step (a macro, not a lambda: the register sets must stay promotable to registers)
+#define RK_ATTN_STEP(st, cur) \
+    __syncthreads();  /* the previous step's K / V are no longer read */ \
     kv_store<CH>(cur, Ks, Vt); \
     __syncthreads(); \
-    kv_load<CH>(kg, vg, j0 + 2 * kKB, last, cur);  /* two steps ahead (clamped: past the end it re-reads `last`) */ \
-    /* S = Q K^T for keys j0 + 16 hf + li (D layout: row 4 lq + e, key li) */ \
-    f4_t Sd[2]; \
+    kv_load<CH>(kg, vg, kb0 + ((st) + 2) * KS, KS, last, cur);  /* two steps ahead (clamped past the end) */ \
+    if (kb0 + (st) * KS + ks < kb1) {  /* wave-uniform: this group's key block of the step exists */ \
+        const int j0 = (kb0 + (st) * KS + ks) * kKB; \
+        /* S = Q K^T for keys j0 + 16 hf + li (D layout: row 4 lq + e, key li) */ \
+        f4_t Sd[2]; \
 _Pragma("unroll") \
-    for (int hf = 0; hf < 2; ++hf) { \
-        f4_t d = {0.f, 0.f, 0.f, 0.f}; \
+        for (int hf = 0; hf < 2; ++hf) { \
+            f4_t d = {0.f, 0.f, 0.f, 0.f}; \
 _Pragma("unroll") \
-        for (int c = 0; c < 4; ++c) { \
-            const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Ks[16 * hf + li][32 * c + 8 * lq])); \
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Qf[c], B, d, 0, 0, 0); \
+            for (int c = 0; c < 4; ++c) { \
+                const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Ks[ks][16 * hf + li][32 * c + 8 * lq])); \
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Qf[c], B, d, 0, 0, 0); \
+            } \
+            Sd[hf] = d; \
         } \
-        Sd[hf] = d; \
+        float alpha[4]; \
+_Pragma("unroll") \
+        for (int e = 0; e < 4; ++e) { \
+            const int qpos = p0 + q0 + 4 * lq + e; \
+            float s0 = Sd[0][e] * scale, s1 = Sd[1][e] * scale; \
+            if (j0 + li > qpos) s0 = -INFINITY; \
+            if (j0 + 16 + li > qpos) s1 = -INFINITY; \
+            const float mb = row16_max(fmaxf(s0, s1)); \
+            const float mn = fmaxf(m[e], mb); \
+            const float p0v = mn == -INFINITY ? 0.f : __expf(s0 - mn); \
+            const float p1v = mn == -INFINITY ? 0.f : __expf(s1 - mn); \
+            const _Float16 h0 = (_Float16)p0v, h1 = (_Float16)p1v; \
+            alpha[e] = mn == -INFINITY ? 1.f : __expf(m[e] - mn); \
+            l[e] = l[e] * alpha[e] + row16_sum((float)h0 + (float)h1); \
+            m[e] = mn; \
+            P[(4 * lq + e) * kKB + li] = __builtin_bit_cast(uint16_t, h0); \
+            P[(4 * lq + e) * kKB + 16 + li] = __builtin_bit_cast(uint16_t, h1); \
+        } \
+_Pragma("unroll") \
+        for (int c = 0; c < 8; ++c) \
+_Pragma("unroll") \
+            for (int e = 0; e < 4; ++e) O[c][e] *= alpha[e]; \
+        __builtin_amdgcn_wave_barrier(); \
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); \
+        /* O += P V: A = P[query li][keys 8 lq .. + 8], B = Vt[dim 16 c + li][keys 8 lq .. + 8] */ \
+        const h8_t A = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&P[li * kKB + 8 * lq])); \
+_Pragma("unroll") \
+        for (int c = 0; c < 8; ++c) { \
+            const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Vt[ks][16 * c + li][vt_col(16 * c + li, 8 * lq)])); \
+            O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, O[c], 0, 0, 0); \
+        } \
+        __builtin_amdgcn_wave_barrier();  /* P is rewritten in the next step only after these reads */ \
     } \
-    float alpha[4]; \
-_Pragma("unroll") \
-    for (int e = 0; e < 4; ++e) { \
-        const int qpos = p0 + q0 + 4 * lq + e; \
-        float s0 = Sd[0][e] * scale, s1 = Sd[1][e] * scale; \
-        if (j0 + li > qpos) s0 = -INFINITY; \
-        if (j0 + 16 + li > qpos) s1 = -INFINITY; \
-        const float mb = row16_max(fmaxf(s0, s1)); \
-        const float mn = fmaxf(m[e], mb); \
-        const float p0v = mn == -INFINITY ? 0.f : __expf(s0 - mn); \
-        const float p1v = mn == -INFINITY ? 0.f : __expf(s1 - mn); \
-        const _Float16 h0 = (_Float16)p0v, h1 = (_Float16)p1v; \
-        alpha[e] = mn == -INFINITY ? 1.f : __expf(m[e] - mn); \
-        l[e] = l[e] * alpha[e] + row16_sum((float)h0 + (float)h1); \
-        m[e] = mn; \
-        P[(4 * lq + e) * kKB + li] = __builtin_bit_cast(uint16_t, h0); \
-        P[(4 * lq + e) * kKB + 16 + li] = __builtin_bit_cast(uint16_t, h1); \
-    } \
-_Pragma("unroll") \
-    for (int c = 0; c < 8; ++c) \
-_Pragma("unroll") \
-        for (int e = 0; e < 4; ++e) O[c][e] *= alpha[e]; \
-    __builtin_amdgcn_wave_barrier(); \
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); \
-    /* O += P V: A = P[query li][keys 8 lq .. + 8], B = Vt[dim 16 c + li][keys 8 lq .. + 8] */ \
-    const h8_t A = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&P[li * kKB + 8 * lq])); \
-_Pragma("unroll") \
-    for (int c = 0; c < 8; ++c) { \
-        const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Vt[16 * c + li][8 * lq])); \
-        O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, O[c], 0, 0, 0); \
-    } \
-    __builtin_amdgcn_wave_barrier();  /* P is rewritten in the next step only after these reads */ \
-     \
     do {} while (0)
-    for (int j0 = 0; j0 <= last; j0 += 2 * kKB) {
-        RK_ATTN_STEP(j0, ka);
-        if (j0 + kKB <= last) {
-            RK_ATTN_STEP(j0 + kKB, kb);
+    for (int st = 0; st < nsteps; st += 2) {
+        RK_ATTN_STEP(st, ka);
+        if (st + 1 < nsteps) {  // block-uniform
+            RK_ATTN_STEP(st + 1, kb);
         }
     }
 #undef RK_ATTN_STEP
+    // merge the KS partials of each head into group 0, one group at a time, in group order: (m, l, O) of group k
+    // through LDS (lane-major O, m / l per row), then m' = max, l' = l a + l_k b, O' = O a + O_k b
+    if constexpr (KS > 1) {
+        float* mo = reinterpret_cast<float*>(lds) + (size_t)r * (64 * 32 + 2 * kQT);
+        for (int k = 1; k < KS; ++k) {
+            __syncthreads();  // the staging (or the previous round's values) is no longer read
+            if (ks == k) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mo[(c * 4 + e) * 64 + lane] = O[c][e];
+                if (li == 0) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        mo[64 * 32 + 4 * lq + e] = m[e];
+                        mo[64 * 32 + kQT + 4 * lq + e] = l[e];
+                    }
+                }
+            }
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float mk = mo[64 * 32 + 4 * lq + e], lk = mo[64 * 32 + kQT + 4 * lq + e];
+                    const float mn = fmaxf(m[e], mk);
+                    const float a = mn == -INFINITY ? 0.f : __expf(m[e] - mn);
+                    const float b = mn == -INFINITY ? 0.f : __expf(mk - mn);
+                    l[e] = l[e] * a + lk * b;
+                    m[e] = mn;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) O[c][e] = O[c][e] * a + mo[(c * 4 + e) * 64 + lane] * b;
+                }
+            }
+        }
+    }
+    if (ks != 0) return;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int t = q0 + 4 * lq + e;
@@ -583,22 +646,19 @@ extern "C" int rk_prefill_attn(const void* q, const void* kc, const void* vc, vo
     if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return RK_ERR_SHAPE;
     if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return RK_ERR_ALIGN;
     const dim3 grid(NKV, (T + kQT - 1) / kQT);
-    const size_t lds = (size_t)rep * kQT * kKB * 2;
     const hipStream_t st = (hipStream_t)stream;
+    // key groups per block (KS): 16 waves at most
+#define RK_ATTN(R, K)                                                                                              \
+    hipLaunchKernelGGL((prefill_attn_kernel<R, K>), grid, dim3(64 * R * K), attn_lds_bytes(R, K), st,               \
+                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S, \
+                       scale)
     switch (rep) {
-        case 1: hipLaunchKernelGGL(prefill_attn_kernel<1>, grid, dim3(64), lds, st,
-                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
-                       scale); break;
-        case 2: hipLaunchKernelGGL(prefill_attn_kernel<2>, grid, dim3(128), lds, st,
-                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
-                       scale); break;
-        case 4: hipLaunchKernelGGL(prefill_attn_kernel<4>, grid, dim3(256), lds, st,
-                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
-                       scale); break;
-        case 8: hipLaunchKernelGGL(prefill_attn_kernel<8>, grid, dim3(512), lds, st,
-                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S,
-                       scale); break;
+        case 1: RK_ATTN(1, kAttnKS); break;
+        case 2: RK_ATTN(2, kAttnKS); break;
+        case 4: RK_ATTN(4, kAttnKS); break;
+        case 8: RK_ATTN(8, 2); break;
         default: return RK_ERR_SHAPE;
     }
+#undef RK_ATTN
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }

@@ -37,10 +37,12 @@ def _rows_close(got, ref, tol=1e-2):
     assert (nr < tol).all() and (cos > 0.9999).all(), (int(t), int(h), float(nr[t, h]), float(cos[t, h]))
 
 
-@pytest.mark.parametrize("T,p0", [(1, 0), (16, 0), (37, 0), (130, 0), (20, 50), (512, 0), (512, 50)])
-def test_prefill_attention_matches_oracle(dev, T, p0):
-    """T = 512 is the benchmarked prompt (16 key blocks of 32 per query tile at the last tile)."""
-    NH, NKV, HD = 16, 4, 128
+@pytest.mark.parametrize("T,p0,NKV", [(1, 0, 4), (16, 0, 4), (37, 0, 4), (130, 0, 4), (20, 50, 4), (512, 0, 4),
+                                      (512, 50, 4), (130, 0, 8), (130, 0, 2)])
+def test_prefill_attention_matches_oracle(dev, T, p0, NKV):
+    """T = 512 is the benchmarked prompt (16 key blocks of 32 per query tile at the last tile); NKV 8 / 2 give 2 / 8
+    query heads per KV head (other wave layouts of the block)."""
+    NH, HD = 16, 128
     S = 256 if p0 + T <= 256 else 640
     g = torch.Generator().manual_seed(T + 7 * p0)
     q = torch.randn(T, NH * HD, generator=g).half()

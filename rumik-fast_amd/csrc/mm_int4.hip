@@ -638,7 +638,7 @@ constexpr int kStreamTab = 4;         // scale / min table entries copied per th
 
 // A build option (RK_STREAM_TRACE; off in the product library, where RK_STR is empty): wall-clock stamps per (block,
 // wave, event) in scalar registers, stored at the end of the launch to the buffer rk_stream_trace_set names
-// ([block][8 waves][16 events] uint64, 100 MHz ticks); rumik-fast_amd/mm_stream_trace.py builds and reads it.
+// ([block][8 waves][16 events] uint64, 100 MHz ticks), which the host reads after the launch.
 // Events: 0 start, 1 prologue loads issued, 2 X fragments and row sums done, 3 tables in LDS (barrier passed),
 // 4 / 5 tile 0 computed / reduced (its barrier passed), 6 / 7 tile 1, 8 / 9 the block's last tile, 10 loop done,
 // 11 stores issued, 12 stores complete.

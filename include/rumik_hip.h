@@ -333,12 +333,17 @@ int rk_decode_get_limits(rk_decode_limits* out);
  * rk_decode_step_persistent: RumikFused._step, engine/rumik_fused.py:97-121, with _logits :84-89). 256 blocks of
  * 1024 threads (one per CU, co-residency checked). Latency blocks (64, role kind 0, index j): residual rows
  * [32j, 32j + 32), attention split j % (64 / NKV) of KV head g = j / (64 / NKV), the combine of head j / 4 and its
- * o slice for rows [512 (j % 4), + 512), and nq = (NH + 2 NKV) * 8 / 64 q/k/v tiles of latency group g (the blocks
- * of KV head g): entries [nq i, nq i + nq), i = j % (64 / NKV), of the group's list [q tiles of heads g REP ..
- * g REP + REP - 1 | k tiles of KV head g | v tiles of KV head g] (REP = NH / NKV, 8 tiles per head). Stream blocks (192,
- * kind 1, index i): MLP slices [sb, se) of 16 channels (their gate / up tiles and w_down columns; a contiguous
- * partition of the inter / 16 slices, at most 4 per block) and int8 head rows i + 192 (w + 16 k). role[b] =
- * {kind, index, sb, se} for block b (sb = se = 0 for latency blocks); every index exactly once.
+ * o slice for rows [512 (j % 4), + 512). Stream blocks (192, kind 1, index i): MLP slices [sb, se) of 16 channels
+ * (their gate / up tiles and w_down columns; a contiguous partition of the inter / 16 slices, at most 4 per block)
+ * and int8 head rows i + 192 (w + 16 k). role[b] = {kind, index, sb, se} for block b (sb = se = 0 for latency
+ * blocks); every index exactly once. The q/k/v tiles (the first NQT = (NH + 2 NKV) * 8 w_in tiles) are computed
+ * where stream_qkv_from says, per step (pos is the same in every block): pos < stream_qkv_from: by the latency
+ * blocks, nq = NQT / 64 tiles of latency group g (the blocks of KV head g): entries [nq i, nq i + nq), i = j % (64
+ * / NKV), of the group's list [q tiles of heads g REP .. g REP + REP - 1 | k tiles of KV head g | v tiles of KV head
+ * g] (REP = NH / NKV, 8 tiles per head), each latency block polling x and running the LayerNorm for them;
+ * pos >= stream_qkv_from: by the stream blocks, tiles [i NQT / 192, (i + 1) NQT / 192) after their LayerNorm, the
+ * latency blocks then starting each layer at the q poll. Both give bit-identical results (the same tiles and
+ * K-split sums); the second is faster at long contexts (RoleDecode switches at pos 384).
  * Shapes: NH * 128 == 2048, NKV 4 or 8, inter a multiple of 128 with at most 4 slices per stream block,
  * 1 <= n_audio <= 192 * 16 * 64; nsp (splits per KV head) <= min(16, 64 / NKV) and S <= nsp * 128; min_chunk (the
  * fewest slots per split) a positive multiple of 8 (RK_ERR_SHAPE / RK_ERR_BLOCK otherwise).
@@ -350,9 +355,9 @@ int rk_decode_get_limits(rk_decode_limits* out);
  * All of them, ctr [256] and status start at zero; after a nonzero status, re-zero them. Status bits as for
  * rk_decode_step_persistent (1 wait timed out, 2 pos outside [0, S), 3 residual beyond the fp16 range).
  * local_xcd = 1: every latency group's blocks share one XCD (the role table gives them equal b % 8, and a launch
- * deals block b to XCD (b + c) % 8, which rk_decode_roles_placement lets the host confirm), so the group's q / k / v
- * and split-partial words stay in that XCD's L2 (faster hops); with local_xcd = 0 they are written through to
- * memory like the other exchanges. */
+ * deals block b to XCD (b + c) % 8, which rk_decode_roles_placement lets the host confirm), so the group's split
+ * partials and (latency q/k/v) q / k / v words stay in that XCD's L2 (faster hops); with local_xcd = 0 they are
+ * written through to memory like the other exchanges (stream q/k/v words always are). */
 typedef struct rk_decode_roles_params {
     int L, NH, NKV, inter, S, n_audio, nsp, min_chunk;
     float eps, scale;
@@ -388,6 +393,7 @@ typedef struct rk_decode_roles_params {
     unsigned* status;
     uint16_t* hn;           /* [2048] fp16 final LayerNorm output, or NULL */
     int local_xcd;          /* 1: latency-group exchanges through the group's XCD L2 (see above) */
+    long long stream_qkv_from; /* steps with pos >= this compute q/k/v on the stream blocks, 0: always (see above) */
 } rk_decode_roles_params;
 
 int rk_decode_step_roles(const rk_decode_roles_params* params, rk_stream_t stream);

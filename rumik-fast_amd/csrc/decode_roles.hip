@@ -9,11 +9,13 @@
 // o -> residual sum -> x) runs on blocks that carry little weight traffic, and the bulk of the bytes is streamed
 // by blocks that poll once per layer and have slack:
 //   latency blocks (kNL = 64, 8 per XCD): latency block j owns residual rows [32j, 32j + 32) (it gathers their
-//     o and down partials and publishes them), q/k/v tiles [nq j, nq j + nq) (nq = 3 at 16 q / 4 kv heads),
-//     attention split j % (64 / NKV) of KV head j / (64 / NKV), and the combine of head j / 4 with the o
-//     projection of that head for rows [512 (j % 4), + 512);
+//     o and down partials and publishes them), attention split j % (64 / NKV) of KV head j / (64 / NKV), and the
+//     combine of head j / 4 with the o projection of that head for rows [512 (j % 4), + 512);
 //   stream blocks (192): a run of 3-4 MLP slices (16 channels: their 16 gate and 16 up rows, and the w_down
 //     columns) each; x -> LayerNorm -> gate / up -> act -> down partials for all 2048 rows.
+// The q/k/v projection sits on either side, chosen per step from pos (see "the roles" below): at short contexts
+// the latency blocks poll x, run the LayerNorm and compute their group's q/k/v tiles; at long ones the stream
+// blocks compute them after their LayerNorm and the latency blocks start each layer at the q poll.
 // Inside a block all 16 waves go through the same phases and meet at block barriers (every wave reaches every
 // barrier, an aborted wait included, so no barrier can hang); wave w owns column group w (columns
 // [128w, 128w + 128)) of every 2048-vector: its part of x, its LayerNorm statistics and its h fragments, and the
@@ -23,8 +25,9 @@
 // (fp16 value | tag << 16, the tag names the step and the layer) written with an agent-scope atomic store and
 // polled by the consumer with agent-scope loads (coherent across the XCDs' L2s). Every exchange buffer has two
 // halves, used by even and odd layers: a block writes a half again only two layers later, and by then every
-// block has finished reading it (a block at layer l + 2 has polled x of layer l + 2, which every latency block
-// published after its layer-(l + 1) gather, which needed every stream block's layer-(l + 1) partials).
+// block has finished reading it (a block at layer l + 2 has polled x of layer l + 2, or with stream q/k/v the q/k/v
+// that the stream blocks computed from it; every latency block published that x after its layer-(l + 1) gather,
+// which needed every block's layer-(l + 1) partials).
 //
 // Every wait is bounded by wall-clock time (200 ms): on expiry the kernel sets an abort bit in `status`, every
 // later wait returns at once and the grid drains with garbage results. A residual sum that leaves the fp16 range
@@ -46,6 +49,7 @@ constexpr int kLPairs = kLRows / 2;           // 16
 constexpr int kOQ = 4;                        // o row quarters per head (16 heads x 4 = 64 latency blocks)
 constexpr int kOItems = kH / kOQ * 4;         // 2048 items of 16 bytes per (head, quarter): 2 per thread
 constexpr int kMaxTiles = 8;                  // gate / up tiles per stream block
+constexpr int kMaxQkv = 2;                    // q / k / v tiles per stream block
 constexpr int kMaxSlices = 4;                 // w_down 16-column slices per stream block
 constexpr int kSlotsPerWave = 8;
 constexpr int kMaxRep = 4;
@@ -190,7 +194,8 @@ struct Lds {
     float hbias[kNG];                         // per group: 64 x the sum of its odd-column h (biased high nibbles)
     alignas(16) uint32_t hnat[kH / 2];        // the final h as natural fp16 pairs (the int8 head's input)
     float2 lnst[kWaves];                      // per wave: sum and squared deviations of its 128 x values
-    float tpart[kWaves][kMaxTiles][16];       // K-split partial dots of the block's tiles (per wave = group)
+    float tpart[kWaves][kMaxTiles + kMaxQkv][16];  // K-split partial dots of the block's tiles (per wave = group):
+                                              //   gate / up tiles in slots [0, 8), q / k / v tiles in [8, 10)
     float act[kMaxSlices * 16];               // stream: act of the block's MLP channels
     alignas(16) uint32_t qst[kMaxRep + 2][64];  // latency: q of the group's heads, then k and v at pos (pairs)
     float s_m[kWaves][kMaxRep], s_l[kWaves][kMaxRep];
@@ -427,22 +432,24 @@ RK_DEV void tile_issue(const Params& p, int l, TileOf tile, int nt, TileRegs<NT>
     }
 }
 
-// the wave's group of tiles [0, nt) -> S.tpart[w][t][row]; per 32-column chunk two tiles' MFMAs are in flight
+// the wave's group of tiles [0, nt) -> S.tpart[w][slot0 + t][row]; per 32-column chunk two tiles' MFMAs are in
+// flight (the register entries past nt are not computed: the branches are wave-uniform and hold no memory access)
 template <int NT>
-RK_DEV void tile_compute(const TileRegs<NT>& r, int nt, Lds& S) {
+RK_DEV void tile_compute(const TileRegs<NT>& r, int nt, Lds& S, int slot0) {
     const int w = wave_id(), L = lane_id(), s = L >> 4;
     const Int4Masks km = int4_masks();
     const float hs = S.hsum[w], hb = S.hbias[w];
 #pragma unroll
     for (int t0 = 0; t0 < NT; t0 += 2) {
+        if (t0 >= nt) break;
+        const bool two = t0 + 1 < nt;
         f4_t d[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) {
             const h8_t A = __builtin_bit_cast(h8_t, S.hfrag[16 * w + 4 * t4 + s]);
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-                if (t0 + e < NT)
-                    d[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag_hi64(r.w[t0 + e][t4], km), d[e], 0, 0, 0);
+            d[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag_hi64(r.w[t0][t4], km), d[0], 0, 0, 0);
+            if (t0 + 1 < NT && two)
+                d[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, dequant_frag_hi64(r.w[t0 + 1][t4], km), d[1], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -450,7 +457,7 @@ RK_DEV void tile_compute(const TileRegs<NT>& r, int nt, Lds& S) {
             const int t = t0 + e;
             if (t < NT && L < 16 && t < nt) {
                 const uint32_t sm = r.sm[t];
-                S.tpart[w][t][L] = __builtin_fmaf(d[e][0] - hb, h16((uint16_t)sm), h16((uint16_t)(sm >> 16)) * hs);
+                S.tpart[w][slot0 + t][L] = __builtin_fmaf(d[e][0] - hb, h16((uint16_t)sm), h16((uint16_t)(sm >> 16)) * hs);
             }
         }
     }
@@ -647,10 +654,10 @@ RK_DEV void split_publish(const Params& p, int l, const Split& s, int nsg, uint3
     }
 }
 
-// Wave 0: head h's combine out = sum_i w_i o_i / sum_i w_i, w_i = exp(m_i - max m) l_i over the splits holding at
+// Wave 0: head h's combine out = sum_i w_i o_i / sum_i w_i, w_i = exp(m_i - max m) l_i over the cnt splits holding at
 // least one slot (<= 16: one poll batch per iteration, lane L = dim pair, lane j % 16 also split j's (m, l)); the
 // sums run in split order. The output, rounded to fp16, goes to S.attn as natural pairs, its sum to S.asum.
-RK_DEV bool combine(const Params& p, Lds& S, int l, int h, int64_t pos, uint32_t tag) {
+RK_DEV bool combine(const Params& p, Lds& S, int l, int h, int cnt, uint32_t tag) {
     const int L = lane_id();
     RK_TRACE(true, kTrCombStart);
 #ifdef RK_ROLES_TRACE
@@ -658,7 +665,6 @@ RK_DEV bool combine(const Params& p, Lds& S, int l, int h, int64_t pos, uint32_t
     RK_TRACE(true, kTrCombDrained);
 #endif
     int rounds = 0;
-    const int cnt = comb_splits(p, pos);
     const size_t hb = ((size_t)(l & 1) * p.NH + h) * p.nsp;
     const uint32_t z = opaque_vgpr(0u);
     const uint64_t* po = reinterpret_cast<const uint64_t*>(p.tpo + hb * kHD) + L + z;
@@ -997,8 +1003,8 @@ RK_DEV void head_compute(const Params& p, int si, const HeadRegs& hr, const Lds&
     if (L < nrows) p.logits[head_row(si, L)] = res;
 }
 
-// after the last layer, every block: the final LayerNorm -> h as natural pairs (and, block 0, the exported final
-// hidden state); stream blocks (si >= 0) then compute their head rows
+// after the last layer, every stream block: the final LayerNorm -> h as natural pairs (and, stream block 0, the
+// exported final hidden state), then the block's head rows
 RK_DEV void final_phase(const Params& p, Lds& S, uint32_t step, int64_t pos, int si, const HeadRegs& hr) {
     XIn in;
     in.x = u4_t{0u, 0u, 0u, 0u};
@@ -1006,23 +1012,24 @@ RK_DEV void final_phase(const Params& p, Lds& S, uint32_t step, int64_t pos, int
     if (x_wave()) {
         in.w = ln_w_issue(p.norm_w);
         x_poll<1>(p, S, p.L, step, in.x);
-        if (p.L == 1 && blockIdx.x == 0 && threadIdx.x == 0) p.pos[0] = pos + 1;  // every block has read pos
+        if (p.L == 1 && si == 0 && threadIdx.x == 0) p.pos[0] = pos + 1;  // every block has read pos
     }
     const u4_t h = layer_norm(p, S, p.L, in);
     if (x_wave()) {
         const int c = 64 * wave_id() + lane_id();  // the lane's 8-column block: natural pairs 4c .. 4c + 3
         *reinterpret_cast<uint4*>(&S.hnat[4 * c]) = make_uint4(h[0], h[1], h[2], h[3]);
-        if (p.hn && blockIdx.x == 0) reinterpret_cast<uint4*>(p.hn)[c] = make_uint4(h[0], h[1], h[2], h[3]);
+        if (p.hn && si == 0) reinterpret_cast<uint4*>(p.hn)[c] = make_uint4(h[0], h[1], h[2], h[3]);
     }
     __syncthreads();
-    if (si >= 0) head_compute(p, si, hr, S);
+    head_compute(p, si, hr, S);
 }
 
-// the start of layer l in every block: x (the embedding at layer 0, else polled) and the LayerNorm weights, in the
-// x-waves (the other waves return at once)
-// XSLEEP: the x poll's pause between rounds (stream blocks wait long with slack: ~0.5 us; latency blocks 64 clocks)
+// the start of layer l in a stream block: x (the embedding at layer 0, else polled) and the LayerNorm weights, in
+// the x-waves (the other waves return at once). Stream block 0 advances pos once x of layer 1 is in: that x needed
+// every latency block's gather of layer 0, which needed every block's partials, so every block has read pos.
+// XSLEEP: the x poll's pause between rounds, in units of 64 clocks.
 template <int XSLEEP>
-RK_DEV XIn x_fetch(const Params& p, Lds& S, int l, uint32_t step, int64_t pos, int64_t tok) {
+RK_DEV XIn x_fetch(const Params& p, Lds& S, int l, uint32_t step, int64_t pos, int64_t tok, int si) {
     XIn in;
     in.x = u4_t{0u, 0u, 0u, 0u};
     in.w = in.x;
@@ -1032,26 +1039,15 @@ RK_DEV XIn x_fetch(const Params& p, Lds& S, int l, uint32_t step, int64_t pos, i
         in.x = x_embed(p, tok);
     } else {
         x_poll<XSLEEP>(p, S, l, step, in.x);
-        if (l == 1 && blockIdx.x == 0 && threadIdx.x == 0) p.pos[0] = pos + 1;  // every block has read pos
+        if (l == 1 && si == 0 && threadIdx.x == 0) p.pos[0] = pos + 1;
     }
     RK_TRACE(true, kTrXPolled);
     RK_TRACE_MAX(kTrXPolledAll);
     return in;
 }
 
-// -> LayerNorm -> h staged; latency block j keeps its own 32 rows of x (x-wave j / 16, lanes 4 (j % 16) .. + 3)
-RK_DEV void x_norm(const Params& p, Lds& S, int l, const XIn& in, int lb) {
-    if (lb >= 0 && wave_id() == lb / 16) {
-        const int L = lane_id(), l0 = 4 * (lb % 16);
-        if (L >= l0 && L < l0 + 4) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const h2_t xh = as_h2(in.x[e]);
-                S.xrow[8 * (L - l0) + 2 * e] = (float)xh.x;
-                S.xrow[8 * (L - l0) + 2 * e + 1] = (float)xh.y;
-            }
-        }
-    }
+// -> LayerNorm -> h staged
+RK_DEV void x_norm(const Params& p, Lds& S, int l, const XIn& in) {
     const u4_t h = layer_norm(p, S, l, in);
     if (x_wave()) stage_h(h, S);
     __syncthreads();
@@ -1059,10 +1055,18 @@ RK_DEV void x_norm(const Params& p, Lds& S, int l, const XIn& in, int lb) {
 }
 
 // ---------------------------------------------------------------------------------------------- the roles
-// Latency block j's u-th q/k/v tile (u < nq = (REP + 2) * 8 / (64 / NKV)): latency group g = j / (64 / NKV)
-// computes exactly the rows its attention splits poll, the q rows of heads g REP .. g REP + REP - 1 and the k and v
-// rows of KV head g (REP * 8 + 8 + 8 tiles), member i = j % (64 / NKV) taking entries [i nq, i nq + nq) of that
-// list, so the group's q / k / v exchange never leaves the group.
+// Two placements of the q / k / v projection, chosen per step from pos (the same in every block):
+//   latency q/k/v (pos < p.stream_qkv_from): every latency block polls x, runs the LayerNorm and computes nq =
+//     (NH + 2 NKV) * 8 / 64 q/k/v tiles of its own group's list, [q tiles of heads g REP .. g REP + REP - 1 | k
+//     tiles of KV head g | v tiles of KV head g], member i = j % (64 / NKV) taking entries [i nq, i nq + nq), so the
+//     group's q/k/v exchange stays in the group's XCD;
+//   stream q/k/v (pos >= p.stream_qkv_from): stream block si computes w_in tiles [qkv_first(si), qkv_first(si + 1))
+//     of the first NQT = (NH + 2 NKV) * 8 ([q of every head | k | v]) right after its LayerNorm and publishes them
+//     written through; the latency blocks skip x, the LayerNorm and the tiles, and start each layer at the q poll.
+// Measured (36 layers, us per token at ctx 256 / 512 / 1024 / 2048): latency q/k/v 500 / 520 / 539 / 585, stream
+// q/k/v 510 / 499 / 500 / 522. The second takes ~4 us of x / LayerNorm / tiles per layer off the latency chain; at
+// short contexts that gain is spent in the stream blocks, whose MLP then ends later and whose next-layer weight
+// burst lands on the gather's polls.
 RK_DEV int qkv_tile(const Params& p, int j, int u) {
     constexpr int kTH = kHD / 16;  // tiles per head
     const int per = kNL / p.NKV, rep = p.NH / p.NKV, nq = (rep + 2) * kTH / per;
@@ -1072,18 +1076,24 @@ RK_DEV int qkv_tile(const Params& p, int j, int u) {
     return (p.NH + p.NKV) * kTH + g * kTH + (t - qt - kTH);
 }
 
-// q/k/v tile epilogue, wave 0 lane (tile t = L / 16, row j = L % 16): RoPE on q / k rows (pairs 2i, 2i + 1 sit in
-// adjacent lanes), published tagged; k and v also written into the cache at pos
-RK_DEV void qkv_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, int lb, int nq, const Lds& S) {
+RK_DEV int qkv_first(const Params& p, int si) {
+    return (int)((long)si * ((p.NH + 2 * p.NKV) * (kHD / 16)) / kNS);
+}
+
+// q/k/v tile epilogue, wave 0 lane (tile t = L / 16, row j = L % 16; the tile's partials in S.tpart slot slot0 + t,
+// its w_in tile index tile(t)): RoPE on q / k rows (pairs 2i, 2i + 1 sit in adjacent lanes), published tagged (into
+// the group's L2 when local, else written through); k and v also written into the cache at pos
+template <class TileOf>
+RK_DEV void qkv_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, TileOf tile, int nq, int slot0,
+                         bool local, const Lds& S) {
     const int L = lane_id();
     const int t = L >> 4, j = L & 15;
-    const float y = t < nq ? tile_out(S, t, j) : 0.f;
+    const float y = t < nq ? tile_out(S, slot0 + t, j) : 0.f;
     const float partner = dpp<0xB1>(y);  // row j ^ 1 (quad_perm [1,0,3,2])
     if (t >= nq) return;
     const int NH = p.NH, NKV = p.NKV;
-    const int row = qkv_tile(p, lb, t) * 16 + j;
+    const int row = tile(t) * 16 + j;
     const int qk_rows = (NH + NKV) * kHD;
-    const bool local = p.local_xcd != 0;
     uint32_t* tq = p.tq + (size_t)(l & 1) * NH * kHD;
     uint32_t* tkv = p.tkv + (size_t)(l & 1) * 2 * NKV * kHD;
     if (row < qk_rows) {
@@ -1108,59 +1118,66 @@ RK_DEV void qkv_epilogue(const Params& p, int l, int64_t pos, uint32_t tag, int 
     }
 }
 
-// Latency block j, one layer: x -> LayerNorm -> its q/k/v tiles (published); the split's q poll -> attention ->
-// split partials; the head's combine -> o slice -> o partials; the rows' gather -> x rows.
-// Load placement: vector-memory results return in issue order per wave, so a wave's poll waits for every load the
-// wave issued before it; each load is therefore issued right after a poll and needed before (or long after) that
-// wave's next one. This layer's K / V slots and o items are issued right after the x poll (needed ~2 and ~4 us
-// later), the next layer's tiles once this layer's are computed, by wave 0 (which polls q and the combine) only
-// after its combine poll, so nothing is outstanding at the q, combine and gather polls. (Every load sequence is
-// unconditional and in the same place for all layers: a load skipped or moved on some path makes the compiler's
-// counter waits on that path's merge conservative, e.g. the LayerNorm then waiting for every load in flight.) LAST: the last layer, which issues no next-layer loads (the loop is
-// peeled so that every load sequence is straight-line code: see tile_issue).
+// Latency block j, one layer: [latency q/k/v: x -> LayerNorm -> its q/k/v tiles, published] the split's q poll ->
+// attention -> split partials; the head's combine -> o slice -> o partials; the rows' gather -> x rows. The block's
+// residual rows live in S.xrow (the gather updates them).
+// Load placement: vector-memory results return in issue order per wave, and a CU's loads share one queue, so a
+// poll waits for the loads issued before it; each load is therefore issued right after a poll and needed before
+// (or long after) the next one. Stream q/k/v: this layer's K / V slots and o items are issued by every wave at the
+// layer's start and drain while the stream blocks compute q/k/v. Latency q/k/v: they are issued right after the x
+// poll (by the x-waves after the LayerNorm: issued before it, they queue ahead of the statistics), the next layer's
+// tiles once this layer's are computed, by wave 0 (which polls q and the combine) only after its combine poll.
+// (Every load sequence is unconditional and in the same place for all layers: a load skipped or moved on some path
+// makes the compiler's counter waits on that path's merge conservative.) LAST: the last layer, which issues no
+// next-layer loads (the loop is peeled so that every load sequence is straight-line code: see tile_issue).
 template <int REP>
 struct LatencyRegs {
-    static constexpr int NQ = REP == 4 ? 3 : 4;  // q/k/v tiles per latency block (16 q heads, 64 / REP kv heads)
+    static constexpr int NQ = REP == 4 ? 3 : 4;  // latency q/k/v tiles per block (16 q heads, 64 / REP kv heads)
     TileRegs<NQ> tr;
     KVRegs kv;
     ORegs orr;
 };
 
-template <int REP, bool LAST>
+template <int REP, bool SQ, bool LAST>
 RK_DEV void latency_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos, int64_t tok, int j, int l,
-                          LatencyRegs<REP>& R) {
+                          const Split& s, int cnt, LatencyRegs<REP>& R) {
     const Params& p = fresh();
     (void)p_in;
     constexpr int NQ = LatencyRegs<REP>::NQ;
     const int w = wave_id();
     const uint32_t tag = tag_of(step, l);
     const int h = j / kOQ, r = j % kOQ;
-    const auto qt = [&](int u) { return qkv_tile(p, j, u); };
-    const Split s = split_of(p, j, pos);
     const AttnPlan ap = attn_plan<REP>(s);
-    // this layer's K / V slots and o items: the x-waves issue theirs after the LayerNorm (issued before it, they
-    // queue in the CU's memory pipeline behind the other waves' and hold up the statistics), the others at once
-    const XIn in = x_fetch<1>(p, S, l, step, pos, tok);
-    if (!x_wave()) {
+    if constexpr (SQ) {
         kv_issue(p, l, s, ap, R.kv);
         o_issue(p, l, h, r, R.orr);
-    }
-    x_norm(p, S, l, in, j);
-    if (x_wave()) {
-        kv_issue(p, l, s, ap, R.kv);
-        o_issue(p, l, h, r, R.orr);
-    }
-    RK_TRACE_MAX(kTrLoadsIssued);
-    tile_compute<NQ>(R.tr, NQ, S);
-    __syncthreads();
-    RK_TRACE(true, kTrTilesDone);
-    if (w == 0) {
-        qkv_epilogue(p, l, pos, tag, j, NQ, S);
-        RK_TRACE(true, kTrQkvPublished);
-        if (s.att) q_poll<REP>(p, S, l, s, pos, tag);
+        RK_TRACE_MAX(kTrLoadsIssued);
+        if (w == 0 && s.att) q_poll<REP>(p, S, l, s, pos, tag);
         RK_TRACE(true, kTrQPolled);
-    } else if constexpr (!LAST) {
-        tile_issue<NQ>(p, l + 1, qt, NQ, R.tr);
+    } else {
+        const auto qt = [&](int u) { return qkv_tile(p, j, u); };
+        const XIn in = x_fetch<1>(p, S, l, step, pos, tok, -1);
+        if (!x_wave()) {
+            kv_issue(p, l, s, ap, R.kv);
+            o_issue(p, l, h, r, R.orr);
+        }
+        x_norm(p, S, l, in);
+        if (x_wave()) {
+            kv_issue(p, l, s, ap, R.kv);
+            o_issue(p, l, h, r, R.orr);
+        }
+        RK_TRACE_MAX(kTrLoadsIssued);
+        tile_compute<NQ>(R.tr, NQ, S, 0);
+        __syncthreads();
+        RK_TRACE(true, kTrTilesDone);
+        if (w == 0) {
+            qkv_epilogue(p, l, pos, tag, qt, NQ, 0, p.local_xcd != 0, S);
+            RK_TRACE(true, kTrQkvPublished);
+            if (s.att) q_poll<REP>(p, S, l, s, pos, tag);
+            RK_TRACE(true, kTrQPolled);
+        } else if constexpr (!LAST) {
+            tile_issue<NQ>(p, l + 1, qt, NQ, R.tr);
+        }
     }
     __syncthreads();
     RK_TRACE(true, kTrAttnStart);
@@ -1184,11 +1201,11 @@ RK_DEV void latency_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos
         RK_TRACE(true, kTrSplitPublished);
     }
     if (w == 0) {
-        combine(p, S, l, h, pos, tag);
+        combine(p, S, l, h, cnt, tag);
         RK_TRACE(true, kTrCombDone);
-        // wave 0 polls: its share of the next layer's tiles goes out only now, after its q and combine polls (a
-        // poll returns only after the wave's earlier loads), and lands before its gather poll
-        if constexpr (!LAST) tile_issue<NQ>(p, l + 1, qt, NQ, R.tr);
+        // latency q/k/v: wave 0 polls, so its share of the next layer's tiles goes out only now, after its q and
+        // combine polls (a poll returns only after the wave's earlier loads), and lands before its gather poll
+        if constexpr (!SQ && !LAST) tile_issue<NQ>(p, l + 1, [&](int u) { return qkv_tile(p, j, u); }, NQ, R.tr);
     }
     __syncthreads();
     o_publish(p, l, tag, h, r, R.orr, S);
@@ -1197,29 +1214,42 @@ RK_DEV void latency_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos
     __syncthreads();
 }
 
-template <int REP>
-RK_DEV void latency_main(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int j) {
-    LatencyRegs<REP> R;
-    tile_issue<LatencyRegs<REP>::NQ>(p, 0, [&](int u) { return qkv_tile(p, j, u); }, LatencyRegs<REP>::NQ, R.tr);
-    for (int l = 0; l + 1 < p.L; ++l) latency_layer<REP, false>(p, S, step, pos, tok, j, l, R);
-    latency_layer<REP, true>(p, S, step, pos, tok, j, p.L - 1, R);
-    HeadRegs none;
-    final_phase(p, S, step, pos, -1, none);
+// layer 0's residual rows of latency block j: the embedding rows 32j .. 32j + 31, rounded to fp16 as x_embed does
+RK_DEV void x_rows_init(const Params& p, Lds& S, int64_t tok, int j) {
+    const int t = threadIdx.x;
+    if (t < kLRows) {
+        const float es = h16(p.emb_s[tok]);
+        S.xrow[t] = rnd16((float)p.emb_q[(size_t)tok * kH + kLRows * j + t] * es);
+    }
 }
 
-// Stream block si (slices [sb, se)), one layer: x -> LayerNorm -> this layer's down columns issued -> gate / up tiles
-// -> act -> down partials for all 2048 rows -> the next layer's tiles issued (the last layer issues the block's
-// head rows instead). The block's ~190 KB per layer thus goes out in two halves a few microseconds apart rather
-// than as one chip-wide burst that saturates HBM while the latency blocks' exchanges are in flight; the tiles,
-// issued last, also hold back the block's next x poll until they have landed (results return in issue order), so
-// waiting blocks do not re-poll x while the chip streams.
+template <int REP, bool SQ>
+RK_DEV void latency_run(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int j) {
+    LatencyRegs<REP> R;
+    x_rows_init(p, S, tok, j);  // read by the first gather, several barriers later
+    const Split s = split_of(p, j, pos);  // the same for every layer of the step
+    const int cnt = comb_splits(p, pos);
+    if constexpr (!SQ)
+        tile_issue<LatencyRegs<REP>::NQ>(p, 0, [&](int u) { return qkv_tile(p, j, u); }, LatencyRegs<REP>::NQ, R.tr);
+    for (int l = 0; l + 1 < p.L; ++l) latency_layer<REP, SQ, false>(p, S, step, pos, tok, j, l, s, cnt, R);
+    latency_layer<REP, SQ, true>(p, S, step, pos, tok, j, p.L - 1, s, cnt, R);
+}
+
+// Stream block si (slices [sb, se)), one layer: x -> LayerNorm -> [stream q/k/v: its q / k / v tiles, published]
+// -> gate / up tiles -> act -> down partials for all 2048 rows -> the next layer's tiles issued (the last layer
+// issues the block's head rows instead). Stream q/k/v: wave 0's q / k / v stores go out before any wave issues this
+// layer's down columns (a barrier between them), so they do not queue behind them; the down columns then load
+// under the gate / up tiles. Latency q/k/v: the down columns are issued right after the LayerNorm. Either way the
+// block's ~200 KB per layer goes out in two parts a few microseconds apart, and the tiles, issued last, land before
+// the block's next x poll (results return in issue order), which therefore does not re-poll while the chip streams.
 struct StreamRegs {
     TileRegs<kMaxTiles> tr;
+    TileRegs<kMaxQkv> qr;
     DownRegs dr;
     HeadRegs hr;
 };
 
-template <bool LAST>
+template <bool SQ, bool LAST>
 RK_DEV void stream_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos, int64_t tok, int si, int sb, int se,
                          int l, StreamRegs& R) {
     const Params& p = fresh();
@@ -1227,11 +1257,20 @@ RK_DEV void stream_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos,
     const int w = wave_id();
     const uint32_t tag = tag_of(step, l);
     const int t0 = (int)(n_tiles(p) - (size_t)p.inter / 8) + 2 * sb, nt = 2 * (se - sb);
+    const int q0 = qkv_first(p, si), nq = qkv_first(p, si + 1) - q0;
     const auto mlp_tiles = [&](int t) { return t0 + t; };
-    const XIn in = x_fetch<kStreamXSleep>(p, S, l, step, pos, tok);
-    x_norm(p, S, l, in, -1);
+    const auto qkv_tiles = [&](int t) { return q0 + t; };
+    const XIn in = x_fetch<kStreamXSleep>(p, S, l, step, pos, tok, si);
+    x_norm(p, S, l, in);
+    if constexpr (SQ) {
+        tile_compute<kMaxQkv>(R.qr, nq, S, kMaxTiles);
+        __syncthreads();
+        if (w == 0) qkv_epilogue(p, l, pos, tag, qkv_tiles, nq, kMaxTiles, false, S);
+        RK_TRACE(true, kTrQkvPublished);
+        __syncthreads();  // wave 0's q / k / v stores are in the queue before this layer's down columns
+    }
     down_issue(p, l, sb, se, R.dr);
-    tile_compute<kMaxTiles>(R.tr, nt, S);
+    tile_compute<kMaxTiles>(R.tr, nt, S, 0);
     __syncthreads();
     RK_TRACE(true, kTrTilesDone);
     if (w == 0) act_epilogue(nt, S);
@@ -1239,16 +1278,23 @@ RK_DEV void stream_layer(const Params& p_in, Lds& S, uint32_t step, int64_t pos,
     RK_TRACE(true, kTrActReady);
     down_publish(p, l, tag, si, sb, se, R.dr, S);
     RK_TRACE(true, kTrDownPublished);
-    if constexpr (!LAST) tile_issue<kMaxTiles>(p, l + 1, mlp_tiles, nt, R.tr);
-    else head_issue(p, si, R.hr);
+    if constexpr (!LAST) {
+        if constexpr (SQ) tile_issue<kMaxQkv>(p, l + 1, qkv_tiles, nq, R.qr);
+        tile_issue<kMaxTiles>(p, l + 1, mlp_tiles, nt, R.tr);
+    } else {
+        head_issue(p, si, R.hr);
+    }
 }
 
-RK_DEV void stream_main(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int si, int sb, int se) {
+template <bool SQ>
+RK_DEV void stream_run(const Params& p, Lds& S, uint32_t step, int64_t pos, int64_t tok, int si, int sb, int se) {
     StreamRegs R;
     const int t0 = (int)(n_tiles(p) - (size_t)p.inter / 8) + 2 * sb;
+    const int q0 = qkv_first(p, si);
+    if constexpr (SQ) tile_issue<kMaxQkv>(p, 0, [&](int t) { return q0 + t; }, qkv_first(p, si + 1) - q0, R.qr);
     tile_issue<kMaxTiles>(p, 0, [&](int t) { return t0 + t; }, 2 * (se - sb), R.tr);
-    for (int l = 0; l + 1 < p.L; ++l) stream_layer<false>(p, S, step, pos, tok, si, sb, se, l, R);
-    stream_layer<true>(p, S, step, pos, tok, si, sb, se, p.L - 1, R);
+    for (int l = 0; l + 1 < p.L; ++l) stream_layer<SQ, false>(p, S, step, pos, tok, si, sb, se, l, R);
+    stream_layer<SQ, true>(p, S, step, pos, tok, si, sb, se, p.L - 1, R);
     final_phase(p, S, step, pos, si, R.hr);
 }
 
@@ -1275,10 +1321,18 @@ __global__ __launch_bounds__(kThreads) void decode_roles_kernel(Params p) {
 #endif
     if (t == 0) S.abort = 0u;
     __syncthreads();
-    if (kind == 0)
-        latency_main<REP>(p, S, step, pos, tok, idx);
-    else
-        stream_main(p, S, step, pos, tok, idx, sb, se);
+    const bool sq = pos >= p.stream_qkv_from;  // the same in every block: the step's q/k/v placement
+    if (kind == 0) {
+        if (sq)
+            latency_run<REP, true>(p, S, step, pos, tok, idx);
+        else
+            latency_run<REP, false>(p, S, step, pos, tok, idx);
+    } else {
+        if (sq)
+            stream_run<true>(p, S, step, pos, tok, idx, sb, se);
+        else
+            stream_run<false>(p, S, step, pos, tok, idx, sb, se);
+    }
 #ifdef RK_ROLES_TRACE
     __syncthreads();
     if (g_roles_trace)
@@ -1312,7 +1366,8 @@ extern "C" int rk_decode_step_roles(const rk_decode_roles_params* params, rk_str
     const int rep = p.NH / p.NKV;
     if (!(rep == 2 || rep == 4)) return RK_ERR_SHAPE;  // NKV 8 or 4: 64 / NKV latency blocks per KV head
     if (p.inter <= 0 || p.inter % 128 || (p.inter / 16 + kNS - 1) / kNS > kMaxSlices) return RK_ERR_SHAPE;
-    if (((p.NH + 2 * p.NKV) * kHD / 16) % kNL) return RK_ERR_SHAPE;  // q/k/v tiles spread evenly
+    if (((p.NH + 2 * p.NKV) * kHD / 16) % kNL) return RK_ERR_SHAPE;                // latency q/k/v: spread evenly
+    if ((p.NH + 2 * p.NKV) * (kHD / 16) > kMaxQkv * kNS) return RK_ERR_SHAPE;  // stream q/k/v tiles per block
     if (p.n_audio <= 0 || p.n_audio > kNS * kWaves * 64) return RK_ERR_SHAPE;  // <= 64 head rows per wave
     if (p.nsp <= 0 || p.nsp > kNL / p.NKV || p.nsp > kMaxSplits || p.min_chunk <= 0 || p.min_chunk % 8 ||
         (p.S + p.nsp - 1) / p.nsp > kWaves * kSlotsPerWave)  // every slot of a split is in some wave's registers

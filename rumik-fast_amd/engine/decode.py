@@ -448,7 +448,7 @@ class RkDecodeRolesParams(ctypes.Structure):
         (n, ctypes.c_void_p) for n in (
             "tok", "pos", "emb_q", "emb_s", "win_t", "win_sm", "wo_q", "wo_sm", "wd_t", "wd_sm", "ln_w", "norm_w",
             "cos_t", "sin_t", "kc", "vc", "head_q", "head_s", "logits", "role", "tx", "tq", "tkv", "tpo", "tml",
-            "top", "tdp", "ctr", "status", "hn")] + [("local_xcd", ctypes.c_int)]
+            "top", "tdp", "ctr", "status", "hn")] + [("local_xcd", ctypes.c_int), ("stream_qkv_from", ctypes.c_longlong)]
 
 
 class RkDecodeRolesLimits(ctypes.Structure):
@@ -517,13 +517,18 @@ def placement_ok(device) -> bool:
 
 class RoleDecode(_OneLaunch):
     """The decode step as one persistent launch with the grid split by role (csrc/decode_roles.hip): 64 latency
-    blocks run the step's chain (x, LayerNorm, q/k/v, attention, combine, o, the residual rows), 192 stream blocks
-    the MLP (gate / up, SiLU, down) and the int8 head. Same weights, state and outputs as DecodeStep and
+    blocks run the step's chain (attention, combine, o, the residual rows; at short contexts also x, LayerNorm and
+    q/k/v), 192 stream blocks the MLP (gate / up, SiLU, down), the int8 head and, at long contexts, q/k/v. Same weights, state and outputs as DecodeStep and
     PersistentDecode; hidden 2048, head dim 128, 16 query heads with 4 or 8 KV heads, 256 CUs.
-    nsp: attention splits per KV head (default min(16, 64 / NKV)); min_chunk: the fewest cache slots per split."""
+    nsp: attention splits per KV head (default min(16, 64 / NKV)); min_chunk: the fewest cache slots per split.
+    stream_qkv_from: steps at pos >= this compute q/k/v on the stream blocks (the latency blocks then skip x, the
+    LayerNorm and the q/k/v tiles), earlier ones on the latency blocks; both give the same results, and the default
+    switches where the second became faster in the step's timing (0: always the stream blocks)."""
+
+    STREAM_QKV_FROM = 384
 
     def __init__(self, cfg: Config, weights, device="cuda", nsp=None, min_chunk=32, keep_layer_weights=False,
-                 local_xcd=None):
+                 local_xcd=None, stream_qkv_from=None):
         if cfg.H != 2048 or cfg.HD != 128 or cfg.NH * cfg.HD != 2048 or cfg.NKV not in (4, 8):
             raise ValueError("the role-split step is built for hidden 2048 / head dim 128 / 16 q and 4 or 8 kv heads")
         self.cfg, self.dev = cfg, torch.device(device)
@@ -577,7 +582,9 @@ class RoleDecode(_OneLaunch):
         self.local_xcd = bool(local_xcd)
         P = RkDecodeRolesParams(L=c.L, NH=c.NH, NKV=c.NKV, inter=c.inter, S=c.S, n_audio=c.n_audio, nsp=self.nsp,
                                 min_chunk=int(min_chunk), eps=c.eps, scale=c.HD ** -0.5, sliding=sliding,
-                                local_xcd=int(self.local_xcd))
+                                local_xcd=int(self.local_xcd),
+                                stream_qkv_from=int(self.STREAM_QKV_FROM if stream_qkv_from is None
+                                                    else stream_qkv_from))
         for name, t in (("tok", self.tok), ("pos", self.pos), ("emb_q", self.emb[0]), ("emb_s", self.emb[1]),
                         ("win_t", self.win_t), ("win_sm", self.win_sm), ("wo_q", self.wo_q), ("wo_sm", self.wo_sm),
                         ("wd_t", self.wd_t), ("wd_sm", self.wd_sm), ("ln_w", self.ln), ("norm_w", self.norm),

@@ -22,15 +22,19 @@ pytestmark = pytest.mark.gpu
 
 # the one-launch engines: every block doing every role (csrc/decode_persistent.hip) and the grid split into
 # latency and stream blocks (csrc/decode_roles.hip), the latter with its latency groups' exchanges kept in their
-# XCD's L2 (local_xcd, the default where the placement probe confirms the round-robin XCD placement) and through memory
-ONE_LAUNCH = ["persistent", "roles", "roles_mem"]
+# XCD's L2 (local_xcd, the default where the placement probe confirms the round-robin XCD placement) and through
+# memory, and with q/k/v computed where its default picks by position (latency blocks below pos 384), always on the
+# stream blocks ("roles_sq") or always on the latency blocks ("roles_lq")
+ONE_LAUNCH = ["persistent", "roles", "roles_mem", "roles_sq", "roles_lq"]
 
 
 def _one_launch(engine, cfg, w, dev):
     if engine == "persistent":
         return decode.PersistentDecode(cfg, w, device=dev)
-    eng = decode.RoleDecode(cfg, w, device=dev, local_xcd=False if engine == "roles_mem" else None)
-    assert eng.local_xcd == (engine == "roles"), "blocks with equal b % 8 did not share an XCD"
+    sqf = {"roles_sq": 0, "roles_lq": 1 << 40}.get(engine)
+    eng = decode.RoleDecode(cfg, w, device=dev, local_xcd=False if engine == "roles_mem" else None,
+                            stream_qkv_from=sqf)
+    assert eng.local_xcd == (engine != "roles_mem"), "blocks with equal b % 8 did not share an XCD"
     return eng
 
 
@@ -153,13 +157,42 @@ def test_persistent_full_width(use_graph, engine, dev):
     print(reps[-1])
 
 
-@pytest.mark.parametrize("engine", ["roles", "roles_mem"])
+@pytest.mark.parametrize("engine", ["roles", "roles_mem", "roles_sq"])
 def test_roles_eight_kv_heads(engine, dev):
     # 16 q / 8 kv heads: latency groups of 8 blocks (4 q/k/v tiles each, 8 splits per KV head of at most 128
     # slots, so a 1024-slot cache), ctx 300
     cfg = decode.Config(L=2, NKV=8, S=1024, vocab=64, sliding=[True, False])
     reps = _run(cfg, dev, ctx=300, steps=2, use_graph=False, engine=engine)
     print(reps[-1])
+
+
+def test_roles_qkv_placements_identical(dev):
+    """q/k/v on the latency blocks and on the stream blocks compute the same tiles with the same K-split sums, so two
+    steps of each, from the same state (ctx 383: the default engine switches placement at pos 384, on its second
+    step), give bit-identical logits, final hidden state, residual stream and new K / V cache slots."""
+    cfg = decode.Config(L=3, vocab=64, S=1024, sliding=[True, False, True])
+    w = decode.random_weights(cfg, 9, device=dev, gen_device="cuda")
+    g = torch.Generator(device=dev).manual_seed(3)
+    kc = torch.randn(cfg.L, cfg.NKV, cfg.S, cfg.HD, device=dev, generator=g).half()
+    vc = torch.randn(cfg.L, cfg.NKV, cfg.S, cfg.HD, device=dev, generator=g).half()
+    outs = []
+    for sqf in (1 << 40, 0, None):
+        eng = decode.RoleDecode(cfg, w, device=dev, stream_qkv_from=sqf, keep_layer_weights=True)
+        eng.kc.copy_(kc)
+        eng.vc.copy_(vc)
+        eng.set_state(7, 383)
+        res = []
+        for _ in range(2):
+            eng.step()
+            torch.cuda.synchronize()
+            assert eng.status_word() == 0
+            res.append((eng.logits.clone(), eng.hn.clone(), eng.x.clone()))
+        outs.append((res, eng.kc[:, :, 383:385].clone(), eng.vc[:, :, 383:385].clone()))
+        del eng
+    for other in outs[1:]:
+        for (la, ha, xa), (lb, hb, xb) in zip(outs[0][0], other[0]):
+            assert torch.equal(la, lb) and torch.equal(ha, hb) and torch.equal(xa, xb)
+        assert torch.equal(outs[0][1], other[1]) and torch.equal(outs[0][2], other[2])
 
 
 @pytest.mark.parametrize("engine", ONE_LAUNCH)

@@ -200,6 +200,7 @@ struct Lds {
     alignas(16) uint32_t qst[kMaxRep + 2][64];  // latency: q of the group's heads, then k and v at pos (pairs)
     float s_m[kWaves][kMaxRep], s_l[kWaves][kMaxRep];
     float2 s_acc[kWaves][kMaxRep][64];        // per-wave attention partials
+    alignas(16) float s_p[kWaves][kMaxRep][kSlotsPerWave];  // per wave: exp(score - max) of its slots, per head
     uint32_t attn[kHD / 2];                   // the head's attention output, natural fp16 pairs
     float asum;                               //   and the sum of its 128 values (the o projection's min term)
     float2 gpart[kWaves][kLPairs];            // gather: per wave, down-partial sums of the row pairs
@@ -566,7 +567,7 @@ RK_DEV bool q_poll(const Params& p, Lds& S, int l, const Split& s, int64_t pos, 
 // Attention wave (sg, hg): heads hg HPW .. + HPW - 1 over slot group sg (m = -inf, l = 0 where no slot is
 // valid). Each lane dots its 16 key dims with the same 16 dims of the query heads (v_dot2, fp32 sums) and the eight
 // chunk lanes of a slot reduce with three DPP steps; per head the max and the sum of exp over the slots reduce over
-// lane bits 3..5; PV takes each p through readlane. Slots past the split's end are selected away (never multiplied
+// lane bits 3..5; PV reads the slots' p back from LDS (one broadcast read per 4 slots). Slots past the split's end are selected away (never multiplied
 // by p = 0), so a NaN left in a slot beyond pos cannot reach the result (the reference's masked loads, other = 0).
 // Results per (slot group, head) in S.s_m / s_l / s_acc.
 template <int HPW>
@@ -580,7 +581,6 @@ RK_DEV void attention(const Params& p, const Split& s, int64_t pos, const KVRegs
         kk[0] = *reinterpret_cast<const u4_t*>(&S.qst[kMaxRep][8 * c]);
         kk[1] = *reinterpret_cast<const u4_t*>(&S.qst[kMaxRep][8 * c + 4]);
     }
-    float pe[HPW];
 #pragma unroll
     for (int r = 0; r < HPW; ++r) {
         const int hd = hg * HPW + r;
@@ -603,15 +603,26 @@ RK_DEV void attention(const Params& p, const Split& s, int64_t pos, const KVRegs
         float ls = e + dpp<0x128>(e);
         ls = sum_xor<16>(ls);
         ls = sum_xor<32>(ls);
-        pe[r] = e;
+        if (c == 0) S.s_p[sg][hd][u] = e;  // the slot's weight, read back by every lane below
         if (L == 0) {
             S.s_m[sg][hd] = m;
             S.s_l[sg][hd] = ls;
         }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the wave's weights in LDS before its lanes read them
     float2 acc[HPW];
+    float pw[HPW][kSlotsPerWave];
 #pragma unroll
-    for (int r = 0; r < HPW; ++r) acc[r] = make_float2(0.f, 0.f);
+    for (int r = 0; r < HPW; ++r) {
+        acc[r] = make_float2(0.f, 0.f);
+        const f4_t* src = reinterpret_cast<const f4_t*>(S.s_p[sg][hg * HPW + r]);  // one broadcast read per 4 slots
+#pragma unroll
+        for (int q = 0; q < kSlotsPerWave / 4; ++q) {
+            const f4_t v = src[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pw[r][4 * q + e] = v[e];
+        }
+    }
 #pragma unroll
     for (int uu = 0; uu < kSlotsPerWave; ++uu) {
         const int su = s0 + uu;
@@ -619,9 +630,8 @@ RK_DEV void attention(const Params& p, const Split& s, int64_t pos, const KVRegs
         const float v0 = (float)vp.x, v1 = (float)vp.y;
 #pragma unroll
         for (int r = 0; r < HPW; ++r) {
-            const float pr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pe[r]), 8 * uu));
-            acc[r].x = __builtin_fmaf(pr, v0, acc[r].x);
-            acc[r].y = __builtin_fmaf(pr, v1, acc[r].y);
+            acc[r].x = __builtin_fmaf(pw[r][uu], v0, acc[r].x);
+            acc[r].y = __builtin_fmaf(pw[r][uu], v1, acc[r].y);
         }
     }
 #pragma unroll

@@ -10,8 +10,8 @@
 //
 // prefill_attn on the matrix cores (v_mfma_f32_16x16x32_f16; operand layouts: A[i][k] in lane i + 16 (k / 8),
 // element k % 8; B[k][j] in lane j + 16 (k / 8); D[i][j] in lane j + 16 (i / 4), element i % 4). Block = (KV head
-// g, tile of 16 queries); wave r = query head g * REP + r. Per key block of 32 slots the block stages K [32 x 128]
-// and V transposed [128 x 32] in LDS once for all REP heads; each wave computes S = Q K^T (2 x 4 MFMAs), the causal
+// g, a share of its query heads, tile of 16 queries); wave r = the share's head r. Per key block of 32 slots the
+// block stages K [32 x 128] and V transposed [128 x 32] in LDS once for its heads; each wave computes S = Q K^T (2 x 4 MFMAs), the causal
 // mask and an online softmax (row statistics reduced over the 16 lanes of a DPP row), stores P (fp16, the
 // reference's tensor-core PV in 16-bit) to its LDS tile in the A layout and accumulates O += P V (8 MFMAs, fp32).
 #include "common.h"
@@ -344,9 +344,10 @@ RK_DEV float row16_sum(float v) {
     return v;
 }
 
-// grid (NKV, ceil(T / 16)), 64 * REP * KS threads. q: [T, NH * 128] fp16 (RoPE applied); kc / vc: the layer's cache
+// grid (NKV * (NH / NKV) / REP, ceil(T / 16)), 64 * REP * KS threads: block x = (KV head g, share z) computes query
+// heads g (NH / NKV) + z REP .. + REP - 1. q: [T, NH * 128] fp16 (RoPE applied); kc / vc: the layer's cache
 // [NKV, S, 128] fp16 holding slots 0 .. p0 + T - 1; o: [T, NH * 128] fp16. Query t attends slots 0 .. p0 + t.
-// Wave w = REP ks + r computes query head g REP + r over the key blocks ks, ks + KS, ks + 2 KS, ... of the tile's
+// Wave w = REP ks + r computes the share's query head r over the key blocks ks, ks + KS, ks + 2 KS, ... of the tile's
 // range (KS wave groups walk the keys side by side, each with its own online softmax), and the KS partial results
 // of a head are merged through LDS at the end. One step stages KS key blocks (one per group) in LDS.
 template <int CH>
@@ -408,15 +409,18 @@ template <int REP, int KS>
 __global__ __launch_bounds__(64 * REP * KS) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc,
                                                                       const uint16_t* vc, uint16_t* o, int T, int p0,
                                                                       int NH, int NKV, int S, float scale) {
+    // REP: the query heads of one KV head this block computes (all NH / NKV of them, or a share: blockIdx.x then
+    // names the KV head and the share)
     constexpr int CH = KS * kChunksPerKB / (64 * REP * KS);
     extern __shared__ __align__(16) uint8_t lds[];
     auto Ks = reinterpret_cast<uint16_t(*)[kKB][kHD + kKsPad]>(lds);
     auto Vt = reinterpret_cast<uint16_t(*)[kHD][kKB]>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2);
     uint16_t* Ps = reinterpret_cast<uint16_t*>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2 + (size_t)KS * kHD * kKB * 2);
-    const int g = blockIdx.x, q0 = blockIdx.y * kQT;
+    const int shares = NH / NKV / REP;
+    const int g = blockIdx.x / shares, q0 = blockIdx.y * kQT;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r = w % REP, ks = w / REP;
-    const int h = g * REP + r;
+    const int h = g * (NH / NKV) + (blockIdx.x % shares) * REP + r;
     const int li = lane & 15, lq = lane >> 4;  // A / B fragment: row or column li, k-group lq
     const int ldq = NH * kHD;
     uint16_t* P = Ps + w * kQT * kKB;
@@ -645,17 +649,19 @@ extern "C" int rk_prefill_attn(const void* q, const void* kc, const void* vc, vo
     const int rep = NH / NKV;  // query heads per KV head: 1, 2, 4 or 8 (the staging splits a key block evenly)
     if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return RK_ERR_SHAPE;
     if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return RK_ERR_ALIGN;
-    const dim3 grid(NKV, (T + kQT - 1) / kQT);
     const hipStream_t st = (hipStream_t)stream;
-    // key groups per block (KS): 16 waves at most
-#define RK_ATTN(R, K)                                                                                              \
-    hipLaunchKernelGGL((prefill_attn_kernel<R, K>), grid, dim3(64 * R * K), attn_lds_bytes(R, K), st,               \
-                       (const uint16_t*)q, (const uint16_t*)kc, (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S, \
-                       scale)
+    // HPB query heads per block (a share of the KV head's rep), KS key groups per block (16 waves at most). With 4
+    // heads per KV head each block takes 2 of them, so a 512-token prompt runs 256 blocks (one per CU) instead of
+    // 128, each staging its K / V for two heads: T = 512 19.2 -> 17.2 us per layer (one head per block: 26 us, the
+    // staging then dominates; 2 heads and 4 key groups 16.7 but 8.4 against 7.5 us at T = 69)
+#define RK_ATTN(HPB, K)                                                                                             \
+    hipLaunchKernelGGL((prefill_attn_kernel<HPB, K>), dim3(NKV * (rep / (HPB)), (T + kQT - 1) / kQT),                \
+                       dim3(64 * (HPB) * (K)), attn_lds_bytes(HPB, K), st, (const uint16_t*)q, (const uint16_t*)kc,   \
+                       (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S, scale)
     switch (rep) {
         case 1: RK_ATTN(1, kAttnKS); break;
         case 2: RK_ATTN(2, kAttnKS); break;
-        case 4: RK_ATTN(4, kAttnKS); break;
+        case 4: RK_ATTN(2, kAttnKS); break;
         case 8: RK_ATTN(8, 2); break;
         default: return RK_ERR_SHAPE;
     }

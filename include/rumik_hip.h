@@ -156,7 +156,9 @@ int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const
  * workspace only, RK_MM_PREP128 / RK_MM_PREP64 / RK_MM_PREP48 (X prepared once into the workspace in matrix-core
  * fragment order, then blocks of 128 / 64 / 48 rows x 128 columns fed by direct memory-to-LDS copies; chosen when
  * the shape has enough column blocks to fill the chip, K is short enough for a block's scale and min rows to sit
- * in LDS, and N * K / 128 is a multiple of 8), or, for M <= 48 and K <= 2048 (with or without a workspace),
+ * in LDS, and N * K / 128 is a multiple of 8; RK_MM_WIDE128 is the same for M > 64 and K in 512 .. 2048 with
+ * K / 128 even: 128 x 128 blocks of four waves, each owning 64 x 64 of the block, two blocks per CU), or, for
+ * M <= 48 and K <= 2048 (with or without a workspace),
  * RK_MM_STREAM (X held in registers as matrix-core fragments for the whole launch while 16-column tiles of codes
  * stream past, one block per CU, no workspace);
  * *splits = the number of K splits (1 = none; > 1 only with a workspace). Host-only query, no GPU needed; RK_ERR_SHAPE for sizes rk_mm_int4_g128 rejects. Part of the
@@ -169,12 +171,13 @@ int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const
 #define RK_MM_PREP64 4
 #define RK_MM_PREP48 5
 #define RK_MM_STREAM 6
+#define RK_MM_WIDE128 7
 int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits);
 
 /* Bytes of workspace rk_mm_int4_g128_ws uses for this shape (0: it needs none). Shapes whose output tiles alone
  * leave CUs idle (few rows and columns, long K) are split over K into fp32 partial sums that a second kernel adds
  * in a fixed order; shapes on the RK_MM_PREP* kernels hold X prepared in fragment order (ceil(M / 16) * 16 * K
- * fp16) and its per-group row sums (K / 128 * ceil(M / 16) * 16 fp32). Part of the same drop-in for mm_int4
+ * fp16) and its per-group row sums (K / 128 * ceil(M / 16) * 16 fp32); so do those on RK_MM_WIDE128. Part of the same drop-in for mm_int4
  * (reference kernels/mm_int4.py:59-73), which allocates its output per call; the Python wrapper allocates this
  * workspace the same way. */
 size_t rk_mm_int4_workspace_bytes(int M, int N, int K);

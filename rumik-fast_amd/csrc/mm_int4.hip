@@ -13,6 +13,7 @@
 //     per block in LDS; a lane's 4 D rows are 4 consecutive m, one ds_read_b128).
 // Codes never leave int4 in HBM; every product is exact, sums are fp32.
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -617,6 +618,249 @@ RK_PREP_INST(4)
 RK_PREP_INST(8)
 #undef RK_PREP_INST
 
+// ------------------------------------------------------------------------------- prepared-X kernel, wide waves
+// mm_int4_wide_kernel: the prepared X of mm_xprep_kernel, blocks of 128 rows x 128 columns with four waves in a
+// 2 x 2 layout, wave (wm, wn) owning rows 64 wm .. + 63 and columns 64 wn .. + 63 (4 x 4 MFMA tiles), two blocks
+// per CU:
+//   * each X fragment read from LDS feeds four MFMAs (the fragment reads set the pace of the one-column-tile
+//     layout); each code column is dequantised by the two waves that share it;
+//   * codes go straight into registers, two steps ahead; X copies go into a two-slot LDS ring with
+//     global_load_lds, one barrier per step;
+//   * the min term sum_g xs[m][g] min[n][g] is each accumulator's starting value, computed on the matrix cores in
+//     fp32 (v_mfma_f32_16x16x4f32, four groups per instruction) while the first copies land, from row sums copied
+//     into the ring slot that step 0 leaves free; the per-step affine is one FMA per output (scale);
+//   * the two blocks of a CU pass their barriers independently, so one block's affine, waits and barrier overlap
+//     the other block's MFMAs.
+// The ring slot of step g + 1 is filled after the barrier of step g, which every wave passes only once it has
+// left step g - 1 (the slot's previous step).
+constexpr int kWideRing = 2;
+constexpr int kWideSlot = 8 * 4 * 64 * 16;              // one step's X fragments: 8 m tiles x 4 MFMA steps
+constexpr int kWideOut = 4 * 64 * 65 * 4;               // epilogue transpose, per wave [64][65] fp32
+constexpr int kWideArea = kWideOut > kWideRing * kWideSlot ? kWideOut : kWideRing * kWideSlot;
+
+size_t mm_wide_lds_bytes(int ng) { return (size_t)kWideArea + (size_t)2 * 128 * ng * 2; }
+
+// The ring's barrier: this wave's copies older than its newest `vm` loads are done and its LDS reads are done
+// (lgkmcnt(0): the copies issued after the barrier refill the slot the last reads came from); the asm statements
+// keep the compiler from moving LDS accesses across it (s_barrier itself is no memory operation).
+template <int VM>
+RK_DEV void wide_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (0 << 8) | ((VM >> 4) << 14));  // vmcnt(VM) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Requires K / 128 even, >= 4 and <= 16 (the row sums fit in one ring slot), (N * K / 128) % 8 == 0 and 16-byte aligned
+// scale / min arrays; the host checks all of them.
+__global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __restrict__ Xp,
+                                                              const float* __restrict__ xsg, int Mp,
+                                                              const uint8_t* __restrict__ q,
+                                                              const uint16_t* __restrict__ sc,
+                                                              const uint16_t* __restrict__ mn, void* __restrict__ Y,
+                                                              int ydt, int ldy, int M, int N, int K) {
+    constexpr int BM = 128;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    // 1-D grid, XCD-grouped: the row blocks of one column block run on one L2
+    const int G = gridDim.x, L = blockIdx.x, GY = (Mp + BM - 1) / BM;
+    const int Lv = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
+    const int mb = (Lv % GY) * BM, nb = (Lv / GY) * 128;
+    const int NG = K >> 7;
+    const int mts = min(8, (Mp - mb) >> 4);  // m tiles of this block present in Xp
+    uint16_t* tsc = reinterpret_cast<uint16_t*>(smem + kWideArea);  // [128][NG]
+    uint16_t* tmn = tsc + 128 * NG;
+    float* xsl = reinterpret_cast<float*>(smem + kWideSlot);  // row sums [g][128] in ring slot 1 until step 0
+    const int jn = lane & 15, sq = lane >> 4;
+
+    // the block's scale and min rows ([n][g], contiguous; 16-byte copies clamped inside the arrays) and row sums
+    {
+        const int nch = 16 * NG;
+        const int lastc = (int)(((size_t)N * NG * 2) / 16) - 1;
+        const size_t c0 = (size_t)nb * NG / 8;
+        for (int b0 = wave * 64; b0 < nch; b0 += 256) {
+            const int ci = min((int)(c0 + b0 + lane), lastc);
+            if (b0 + lane < nch) {
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(sc) + ci,
+                                                 reinterpret_cast<uint4*>(tsc) + b0, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(mn) + ci,
+                                                 reinterpret_cast<uint4*>(tmn) + b0, 16, 0, 0);
+            }
+        }
+        // xs[g][mb .. mb + 127] (rows past Mp repeat its last 4: their sums are never stored), 32 chunks a group
+        for (int b0 = wave * 64; b0 < 32 * NG; b0 += 256) {
+            const int c = b0 + lane, g = c >> 5, r4 = min(c & 31, 4 * mts - 1);
+            if (c < 32 * NG)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(xsg + (size_t)g * Mp + mb) + r4,
+                                                 reinterpret_cast<uint4*>(xsl) + b0, 16, 0, 0);
+        }
+    }
+    // step g's X fragments i = wave + 4 k (m tile i / 4, MFMA step t = i % 4) into ring slot `sl`
+    auto issue_x = [&](int g, int sl) {
+        uint4* slot = reinterpret_cast<uint4*>(smem + (size_t)sl * kWideSlot);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = wave + 4 * k, mt = i >> 2, t = i & 3;
+            __builtin_amdgcn_global_load_lds(Xp + (((size_t)(mb / 16 + min(mt, mts - 1)) * NG + g) * 4 + t) * 64 + lane,
+                                             slot + (mt * 4 + t) * 64, 16, 0, 0);
+        }
+    };
+    // this lane's code bytes: column nb + 64 wn + 16 nt + jn (clamped), bytes 16 sq .. + 15 of each group. The
+    // addresses pass through a volatile asm statement, which stays behind the X copies issued before it, so the
+    // code loads follow those copies (the wait counts rely on that order; plain loads of read-only memory would
+    // otherwise be free to move ahead of them).
+    const uint8_t* wsrc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) wsrc[nt] = q + (size_t)min(nb + 64 * wn + 16 * nt + jn, N - 1) * (size_t)(K >> 1) + 16 * sq;
+    using gu4 = const __attribute__((address_space(1))) u4_t;
+    auto load_w = [&](int g, u4_t (&w)[4]) {
+        uint64_t a[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) a[nt] = (uint64_t)(wsrc[nt] + 64 * g);
+        asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) w[nt] = *(gu4*)a[nt];
+    };
+
+    issue_x(0, 0);
+    u4_t wa[4], wb[4];  // codes of the even / odd steps
+    load_w(0, wa);
+    load_w(1, wb);
+    // the epilogue's arguments come in before the loop (a scalar load in flight would turn the loop's LDS waits
+    // into lgkmcnt(0))
+    asm volatile("" ::: "memory");
+    asm volatile("" ::"s"(Y), "s"(ydt), "s"(ldy), "s"(M), "s"(N));
+
+    // the min term as the accumulators' start: tables and row sums landed (older than the 16 loads above)
+    wide_barrier<16>();
+    f4_t acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int qq = 0; qq < NG; qq += 4) {
+        const int gl = qq + sq;
+        float mv[4], xa[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) mv[nt] = gl < NG ? f16_bits_to_f32(tmn[(64 * wn + 16 * nt + jn) * NG + gl]) : 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) xa[mt] = gl < NG ? xsl[gl * 128 + 64 * wm + 16 * mt + jn] : 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[mt], mv[nt], acc[mt][nt], 0, 0, 0);
+    }
+
+    const DqConsts kc = {opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u)};
+    // one K step (slot sl = g % 2): this wave's codes of step g are in w; on return they hold step g + 2's. Every
+    // step issues the same loads in the same order (the last steps repeat the last group's, into the free slot and
+    // the consumed registers), so one wait count fits every step: when step g starts, the loads newer than its X
+    // copies and codes are step g + 1's codes (4 loads).
+    auto step = [&](int g, int sl, u4_t (&w)[4], auto last) {
+        wide_barrier<4>();
+        if constexpr (!decltype(last)::value) issue_x(min(g + 1, NG - 1), sl ^ 1);  // into step g - 1's slot
+        const uint4* slot = reinterpret_cast<const uint4*>(smem + (size_t)sl * kWideSlot);
+        h8_t A[4][4];  // the wave's 4 m tiles x 4 MFMA steps
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) A[mt][t] = __builtin_bit_cast(h8_t, slot[((4 * wm + mt) * 4 + t) * 64 + lane]);
+        float sv[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) sv[nt] = f16_bits_to_f32(tsc[(64 * wn + 16 * nt + jn) * NG + g]);
+        // column tiles in pairs: dequantise the pair's codes, then per m tile pair the 4 MFMA steps on 2 x 2 tiles
+        // (four independent chains) and their affine
+#pragma unroll
+        for (int np = 0; np < 4; np += 2) {
+            h8_t B[2][4];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) B[j][t] = dequant8(w[np + j][t], kc);
+            if constexpr (!decltype(last)::value)
+                if (np == 2) load_w(min(g + 2, NG - 1), w);
+#pragma unroll
+            for (int mp = 0; mp < 4; mp += 2) {
+                f4_t c[2][2];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            c[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mp + i][t], B[j][t],
+                                                                            t == 0 ? f4_t{0.f, 0.f, 0.f, 0.f} : c[i][j],
+                                                                            0, 0, 0);
+                // D[i][j]: row 4 (lane / 16) + e of the m tile, column lane % 16 of the tile: scale in fp32
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[mp + i][np + j][e] = __builtin_fmaf(c[i][j][e], sv[np + j], acc[mp + i][np + j][e]);
+            }
+        }
+    };
+    // NG is even. Step 0 runs before the loop: the code loads above may be issued in any order, and a code register
+    // possibly in flight at the loop's first wait would make the compiler's waits in every iteration vmcnt(0); from
+    // step 1 on the load order is the loop's own. The last step, after the loop, issues no loads.
+    using more = std::integral_constant<bool, false>;
+    __builtin_assume(NG >= 4);  // the loop runs at least once (the host checks)
+    step(0, 0, wa, more{});
+    for (int g = 1; g + 1 < NG; g += 2) {
+        step(g, 1, wb, more{});
+        step(g + 1, 0, wa, more{});
+    }
+    step(NG - 1, 1, wb, std::integral_constant<bool, true>{});
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8));  // vmcnt(0) lgkmcnt(0): copies landed, ring reads done
+    __builtin_amdgcn_s_barrier();                           // every wave has left the ring
+    asm volatile("" ::: "memory");
+
+    // the wave's 64 x 64 tile through LDS ([64][65] fp32), then 16-byte row pieces: lane -> row 8 i + lane / 8,
+    // columns 8 (lane % 8) .. + 7
+    float* tb = reinterpret_cast<float*>(smem) + wave * (64 * 65);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tb[(mt * 16 + 4 * sq + e) * 65 + 16 * nt + jn] = acc[mt][nt][e];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave reads back only its own tile
+    const int m0 = mb + 64 * wm, n0 = nb + 64 * wn;
+    const bool vec_ok = (((uintptr_t)Y | (size_t)ldy * (ydt == RK_F32 ? 4 : 2)) & (ydt == RK_F32 ? 15 : 7)) == 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 8 * i + (lane >> 3), cc = 8 * (lane & 7);
+        const int m = m0 + r, n = n0 + cc;
+        if (m >= M || n >= N) continue;
+        const float* p = tb + r * 65 + cc;
+        const size_t o = (size_t)m * ldy + n;
+        if (n + 7 < N && vec_ok) {
+            if (ydt == RK_F32) {
+                *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(Y) + o) = f4_t{p[0], p[1], p[2], p[3]};
+                *reinterpret_cast<f4_t*>(reinterpret_cast<float*>(Y) + o + 4) = f4_t{p[4], p[5], p[6], p[7]};
+            } else if (ydt == RK_F16) {
+                const h8_t h = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
+                                (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
+                *reinterpret_cast<h8_t*>(reinterpret_cast<uint16_t*>(Y) + o) = h;
+            } else {
+                u4_t b;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    b[e] = (uint32_t)f32_to_bf16_bits(p[2 * e]) | ((uint32_t)f32_to_bf16_bits(p[2 * e + 1]) << 16);
+                *reinterpret_cast<u4_t*>(reinterpret_cast<uint16_t*>(Y) + o) = b;
+            }
+        } else {
+            for (int e = 0; e < 8 && n + e < N; ++e) store_act(Y, ydt, o + e, p[e]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------- small-M stream
 // For M <= 16 MT rows (MT <= 3) and K <= 2048 X is small enough to stay in registers: a block of eight waves holds X
 // as MFMA A fragments for the whole launch, wave w owning <= 2 of the <= 16 groups, and
@@ -906,6 +1150,25 @@ hipError_t launch_mm_prep(const void* X, int xdt, int ldx, const uint8_t* q, con
     return hipGetLastError();
 }
 
+template <int MT>
+hipError_t launch_mm_wide(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s, const uint16_t* m,
+                          void* Y, int ydt, int ldy, int M, int N, int K, void* ws, hipStream_t st) {
+    constexpr int BM = 16 * MT;
+    const int NG = K / 128, Mp = (M + 15) / 16 * 16;
+    uint4* Xp = static_cast<uint4*>(ws);
+    float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (size_t)Mp * K * 2);
+    const size_t chunks = (size_t)Mp * NG * 16;
+    const dim3 pg((unsigned)((chunks + 255) / 256));
+    if (xdt == RK_BF16)
+        hipLaunchKernelGGL((mm_xprep_kernel<true>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
+    else
+        hipLaunchKernelGGL((mm_xprep_kernel<false>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
+    const dim3 grid(((N + 127) / 128) * ((Mp + BM - 1) / BM));
+    hipLaunchKernelGGL(mm_int4_wide_kernel, grid, dim3(256), mm_wide_lds_bytes(NG), st, Xp, xs, Mp, q, s, m,
+                       Y, ydt, ldy, M, N, K);
+    return hipGetLastError();
+}
+
 // Y[m, n] = sum over splits of part[split][m][n] (fixed order), in Y's dtype
 __global__ __launch_bounds__(256) void mm_splitk_reduce(const float* __restrict__ part, int splits,
                                                         void* __restrict__ Y, int ydt, int ldy, int M, int N) {
@@ -995,7 +1258,7 @@ constexpr size_t kLdsMax = 160 * 1024;
 
 // Kernel choice for one shape. With a caller's workspace (rk_mm_int4_g128_ws) and enough 128-column blocks to give
 // most CUs one (cfg 3 / 4 / 5: the prepared-X kernel with 128 / 64 / 48-row blocks; its workspace holds the prepared
-// X). Otherwise 128 x 128 tiles (cfg 1) when that still gives every CU a block, else 64 x 64 tiles (cfg 2), split
+// X; cfg 7 in place of cfg 3 when K / 128 is even and 4 .. 16: the wide-wave kernel, two blocks per CU). Otherwise 128 x 128 tiles (cfg 1) when that still gives every CU a block, else 64 x 64 tiles (cfg 2), split
 // over K when a workspace or the fixed scratch is allowed and the tiles alone leave CUs idle (each split keeps >= 4
 // groups); cfg 0 is the register-staged kernel, for K too long to stage one block's scales in LDS.
 struct MmPlan {
@@ -1027,6 +1290,9 @@ MmPlan mm_plan(int M, int N, int K, int mode) {
         const long Mp = (M + 15) / 16 * 16;
         const long blocks = (long)((N + 127) / 128) * ((Mp + 16 * mt - 1) / (16 * mt));
         const size_t lds = mt == 3 ? mm_prep_lds_bytes<3>(NG) : mt == 4 ? mm_prep_lds_bytes<4>(NG) : mm_prep_lds_bytes<8>(NG);
+        if (mt == 8 && NG % 2 == 0 && NG >= 4 && NG <= 16 && blocks >= kPrepMinBlocks &&
+            mm_wide_lds_bytes(NG) <= kLdsMax / 2)
+            return {7, 1, mm_prep_ws_bytes(M, K)};
         if (blocks >= kPrepMinBlocks && lds <= kLdsMax) return {mt == 8 ? 3 : mt == 4 ? 4 : 5, 1, mm_prep_ws_bytes(M, K)};
     }
     const bool allow_ws = mode != kMmPlain;
@@ -1066,6 +1332,8 @@ int mm_run(const MmPlan& p, const void* X, int x_dtype, int ldx, const uint8_t* 
         e = launch_mm_prep<3>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
     else if (p.cfg == 6)
         e = launch_mm_stream(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
+    else if (p.cfg == 7)
+        e = launch_mm_wide<8>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
     else
         e = launch_mm<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
@@ -1113,8 +1381,8 @@ extern "C" int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_
 extern "C" int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* splits) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return RK_ERR_SHAPE;
     const MmPlan p = mm_plan(M, N, K, use_workspace != 0 ? kMmWorkspace : kMmPlain);
-    static const int kCode[7] = {RK_MM_REGS,    RK_MM_TILE128, RK_MM_TILE64, RK_MM_PREP128,
-                                 RK_MM_PREP64, RK_MM_PREP48,  RK_MM_STREAM};
+    static const int kCode[8] = {RK_MM_REGS,   RK_MM_TILE128, RK_MM_TILE64, RK_MM_PREP128,
+                                 RK_MM_PREP64, RK_MM_PREP48,  RK_MM_STREAM, RK_MM_WIDE128};
     if (kernel) *kernel = kCode[p.cfg];
     if (splits) *splits = p.splits;
     return RK_OK;
@@ -1131,9 +1399,10 @@ extern "C" int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uin
     const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
     if (st != RK_OK) return st;
     MmPlan p = mm_plan(M, N, K, kMmWorkspace);
-    // the prepared-X kernel copies the scale / min rows in 16-byte pieces; other arrays take the tile plan, which
+    // the prepared-X kernels copy the scale / min rows in 16-byte pieces; other arrays take the tile plan, which
     // needs no more workspace (shapes with that many column blocks are not split over K)
-    if (p.cfg >= 3 && p.cfg <= 5 && (((uintptr_t)scale | (uintptr_t)min) & 15)) p = mm_plan(M, N, K, kMmScratch);
+    if ((p.cfg == 3 || p.cfg == 4 || p.cfg == 5 || p.cfg == 7) && (((uintptr_t)scale | (uintptr_t)min) & 15))
+        p = mm_plan(M, N, K, kMmScratch);
     if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) return RK_ERR_SHAPE;
     if (p.ws > 0 && ((uintptr_t)workspace & 15)) return RK_ERR_ALIGN;
     return mm_run(p, X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, workspace,

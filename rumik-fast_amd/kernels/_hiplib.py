@@ -81,8 +81,8 @@ def lib():
     return _lib
 
 
-MM_REGS, MM_TILE128, MM_TILE64, MM_PREP128, MM_PREP64, MM_PREP48, MM_STREAM = 0, 1, 2, 3, 4, 5, 6
-MM_PREP = (MM_PREP128, MM_PREP64, MM_PREP48)
+MM_REGS, MM_TILE128, MM_TILE64, MM_PREP128, MM_PREP64, MM_PREP48, MM_STREAM, MM_WIDE128 = 0, 1, 2, 3, 4, 5, 6, 7
+MM_PREP = (MM_PREP128, MM_PREP64, MM_PREP48, MM_WIDE128)  # the plans that prepare X into the workspace
 MM_SCRATCH_BYTES = 8 << 20  # RK_MM_SCRATCH_BYTES: the fixed split-K scratch of rk_mm_int4_g128_noalloc
 # status codes (RK_OK and RK_ERR_* of the header)
 OK, ERR_SHAPE, ERR_BLOCK, ERR_DTYPE, ERR_NULL, ERR_ALIGN, ERR_LAUNCH, ERR_SCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
@@ -90,7 +90,7 @@ OK, ERR_SHAPE, ERR_BLOCK, ERR_DTYPE, ERR_NULL, ERR_ALIGN, ERR_LAUNCH, ERR_SCRATC
 
 def mm_plan(M: int, N: int, K: int, use_workspace: bool = True):
     """(kernel, splits) that rk_mm_int4_g128[_ws] runs for this shape (kernel: MM_REGS / MM_TILE128 / MM_TILE64, or
-    with a workspace MM_PREP128 / MM_PREP64 / MM_PREP48)."""
+    with a workspace MM_PREP128 / MM_PREP64 / MM_PREP48 / MM_WIDE128)."""
     k, sp = _i(), _i()
     check(lib().rk_mm_int4_plan(M, N, K, int(use_workspace), ctypes.byref(k), ctypes.byref(sp)), "mm_int4_plan")
     return k.value, sp.value

@@ -171,9 +171,11 @@ def test_sampler_entry_points_validate_before_any_device_work():
                               16384, 8, 30, P, P, 2048, P, None, S) == -4
 
 
-@pytest.mark.parametrize("M,N,K,kernel", [(512, 22016, 2048, HL.MM_PREP128), (201, 25088, 2048, HL.MM_PREP128),
-                                          (69, 25088, 2048, HL.MM_PREP128), (34, 22016, 2048, HL.MM_STREAM),
-                                          (64, 22016, 4096, HL.MM_PREP64), (128, 22016, 2048, HL.MM_PREP128),
+@pytest.mark.parametrize("M,N,K,kernel", [(512, 22016, 2048, HL.MM_WIDE128), (201, 25088, 2048, HL.MM_WIDE128),
+                                          (69, 25088, 2048, HL.MM_WIDE128), (34, 22016, 2048, HL.MM_STREAM),
+                                          (64, 22016, 4096, HL.MM_PREP64), (128, 22016, 2048, HL.MM_WIDE128),
+                                          (512, 20480, 1152, HL.MM_PREP128), (130, 20480, 256, HL.MM_PREP128),
+                                          (512, 22016, 4096, HL.MM_PREP128), (200, 20600, 512, HL.MM_WIDE128),
                                           (512, 3072, 2048, HL.MM_TILE64), (512, 2048, 11008, HL.MM_TILE64),
                                           (34, 3072, 2048, HL.MM_STREAM), (34, 22017, 128, HL.MM_STREAM),
                                           (34, 2048, 11008, HL.MM_TILE64), (48, 20480, 2048, HL.MM_STREAM),
@@ -182,8 +184,8 @@ def test_sampler_entry_points_validate_before_any_device_work():
 def test_mm_int4_workspace_plan(M, N, K, kernel):
     """With a workspace, M <= 48 at K <= 2048 takes the stream kernel unless a block's scale / min tables would
     exceed 2048 entries (very wide N); otherwise shapes with >= 160 column blocks of 128 take the prepared-X kernel
-    (48 / 64 / 128-row blocks by M); too few blocks, K too long for the block's scale tables, or N * K / 128 not a
-    multiple of 8 keep the tile plan."""
+    (48 / 64 / 128-row blocks by M; for M > 64 the wide-wave kernel when K / 128 is even and 4 .. 16); too few
+    blocks, K too long for the block's scale tables, or N * K / 128 not a multiple of 8 keep the tile plan."""
     assert HL.mm_plan(M, N, K, use_workspace=True)[0] == kernel
 
 
@@ -202,7 +204,10 @@ def test_mm_int4_plan_query(M, N, K, kernel):
     if k2 in HL.MM_PREP:  # prepared X (fp16, rows padded to 16) and its per-group row sums (fp32)
         Mp = (M + 15) // 16 * 16
         assert sp2 == 1 and nbytes == Mp * K * 2 + (K // 128) * Mp * 4
-        assert k2 == (HL.MM_PREP48 if M <= 48 else HL.MM_PREP64 if M <= 64 else HL.MM_PREP128)
+        ng = K // 128
+        wide = ng % 2 == 0 and 4 <= ng <= 16
+        assert k2 == (HL.MM_PREP48 if M <= 48 else HL.MM_PREP64 if M <= 64 else
+                      HL.MM_WIDE128 if wide else HL.MM_PREP128)
     else:
         assert (sp2 > 1) == (nbytes > 0) and nbytes == (sp2 * M * N * 4 if sp2 > 1 else 0)
     with pytest.raises(RuntimeError):

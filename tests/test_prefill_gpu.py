@@ -39,12 +39,12 @@ def test_config3_shapes(M, N, K, dev):
     print(f"M={M} N={N} K={K}: {rep}")
 
 
-@pytest.mark.parametrize("N,K,kernel", [(3072, 2048, H.MM_TILE64), (22016, 2048, H.MM_PREP128),
+@pytest.mark.parametrize("N,K,kernel", [(3072, 2048, H.MM_TILE64), (22016, 2048, H.MM_WIDE128),
                                          (2048, 11008, H.MM_TILE64)])
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 def test_config3_m512(N, K, kernel, xdt, dev):
     """M = 512 on every config-3 shape through the drop-in (workspace entry); gate+up 22016 x 2048 runs the
-    prepared-X kernel (asserted; its tile-kernel run is test_prepared_x_against_tile_kernels)."""
+    wide-wave prepared-X kernel (asserted; its tile-kernel run is test_prepared_x_against_tile_kernels)."""
     assert H.mm_plan(512, N, K)[0] == kernel
     X, q, s, m = synth.prefill_case(512, N, K, 3)
     X = X.to(xdt)
@@ -53,7 +53,7 @@ def test_config3_m512(N, K, kernel, xdt, dev):
     print(f"M=512 N={N} K={K} {xdt}: {rep}")
 
 
-@pytest.mark.parametrize("T,kernel", [(34, H.MM_STREAM), (69, H.MM_PREP128), (201, H.MM_PREP128)])
+@pytest.mark.parametrize("T,kernel", [(34, H.MM_STREAM), (69, H.MM_WIDE128), (201, H.MM_WIDE128)])
 def test_reference_w_in_prompts(T, kernel, dev):
     """The reference's own check (kernels/mm_int4.py:92-106): w_in 25088 x 2048 at T in {34, 69, 201}, bf16 X as
     the engine passes it, through the drop-in (the kernels the plan picks, asserted); T = 69 / 201 on the tile
@@ -197,12 +197,13 @@ def _ws(M, N, K, dev):
     return torch.full((max(n, 16),), 0xFF, device=dev, dtype=torch.uint8)  # stale contents must not matter
 
 
-@pytest.mark.parametrize("M,N,K,prep,tile", [(512, 22016, 2048, H.MM_PREP128, H.MM_TILE128),
-                                             (201, 25088, 2048, H.MM_PREP128, H.MM_TILE128),
-                                             (69, 25088, 2048, H.MM_PREP128, H.MM_TILE64),
+@pytest.mark.parametrize("M,N,K,prep,tile", [(512, 22016, 2048, H.MM_WIDE128, H.MM_TILE128),
+                                             (201, 25088, 2048, H.MM_WIDE128, H.MM_TILE128),
+                                             (69, 25088, 2048, H.MM_WIDE128, H.MM_TILE64),
                                              (40, 65536, 2048, H.MM_PREP48, H.MM_TILE64),
-                                             (128, 22016, 2048, H.MM_PREP128, H.MM_TILE64),
-                                             (64, 22016, 4096, H.MM_PREP64, H.MM_TILE64)])
+                                             (128, 22016, 2048, H.MM_WIDE128, H.MM_TILE64),
+                                             (64, 22016, 4096, H.MM_PREP64, H.MM_TILE64),
+                                             (512, 20480, 1152, H.MM_PREP128, H.MM_TILE128)])
 def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
     """Each benchmarked / reference prompt shape on both plans: both within the oracle bar, and equal to each other up
     to fp32 summation order."""
@@ -227,7 +228,9 @@ def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
                                            (63, 20480, 384, torch.bfloat16, torch.float32),
                                            (61, 20360, 1152, torch.float16, torch.bfloat16),
                                            (130, 20480, 256, torch.bfloat16, torch.bfloat16),
-                                           (200, 20600, 512, torch.float16, torch.float32)])
+                                           (200, 20600, 512, torch.float16, torch.float32),
+                                           (96, 20488, 1024, torch.bfloat16, torch.bfloat16),
+                                           (77, 20520, 1536, torch.float16, torch.float16)])
 def test_prepared_x_ragged_and_dtypes(M, N, K, xdt, ydt, dev):
     """Ragged rows (the last block's missing m tiles, rows past M), ragged columns (N not a multiple of 128 or 8),
     odd group counts, every input / output dtype; nothing is written outside [M, N]."""
@@ -244,10 +247,12 @@ def test_prepared_x_ragged_and_dtypes(M, N, K, xdt, ydt, dev):
     assert torch.all(Yw[M] == 7.0) and torch.all(Yw[:, N:] == 7.0)
 
 
-def test_prepared_x_strided_rows_and_scale_fallback(dev):
+@pytest.mark.parametrize("M,kernel", [(50, H.MM_PREP64), (100, H.MM_WIDE128)])
+def test_prepared_x_strided_rows_and_scale_fallback(M, kernel, dev):
     """X rows with a stride beyond K; scale / min arrays that are not 16-byte aligned take the tile plan instead
     (same workspace size suffices) — both within the bar."""
-    M, N, K = 50, 20480, 512
+    N, K = 20480, 512
+    assert H.mm_plan(M, N, K, use_workspace=True) == (kernel, 1)
     X, q, s, m = synth.prefill_case(M, N, K, 23)
     Xw = torch.zeros(M, K + 64, dtype=torch.float16)
     Xw[:, :K] = X

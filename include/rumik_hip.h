@@ -156,8 +156,9 @@ int rk_mm_int4_g128(const void* X, int x_dtype, int ldx, const uint8_t* q, const
  * workspace only, RK_MM_PREP128 / RK_MM_PREP64 / RK_MM_PREP48 (X prepared once into the workspace in matrix-core
  * fragment order, then blocks of 128 / 64 / 48 rows x 128 columns fed by direct memory-to-LDS copies; chosen when
  * the shape has enough column blocks to fill the chip, K is short enough for a block's scale and min rows to sit
- * in LDS, and N * K / 128 is a multiple of 8; RK_MM_WIDE128 is the same for M > 64 and K in 512 .. 2048 with
- * K / 128 even: 128 x 128 blocks of four waves, each owning 64 x 64 of the block, two blocks per CU), or, for
+ * in LDS, and N * K / 128 is a multiple of 8; RK_MM_WIDE128 is the same for M > 64 with K / 128 even and >= 4:
+ * 128 x 128 blocks of four waves, each owning 64 x 64 of the block, two blocks per CU, split over K (*splits > 1)
+ * for M >= 256 with K / 128 > 16 when the tiles are few), or, for
  * M <= 48 and K <= 2048 (with or without a workspace),
  * RK_MM_STREAM (X held in registers as matrix-core fragments for the whole launch while 16-column tiles of codes
  * stream past, one block per CU, no workspace);
@@ -177,7 +178,8 @@ int rk_mm_int4_plan(int M, int N, int K, int use_workspace, int* kernel, int* sp
 /* Bytes of workspace rk_mm_int4_g128_ws uses for this shape (0: it needs none). Shapes whose output tiles alone
  * leave CUs idle (few rows and columns, long K) are split over K into fp32 partial sums that a second kernel adds
  * in a fixed order; shapes on the RK_MM_PREP* kernels hold X prepared in fragment order (ceil(M / 16) * 16 * K
- * fp16) and its per-group row sums (K / 128 * ceil(M / 16) * 16 fp32); so do those on RK_MM_WIDE128. Part of the same drop-in for mm_int4
+ * fp16) and its per-group row sums (K / 128 * ceil(M / 16) * 16 fp32); so do those on RK_MM_WIDE128, plus
+ * splits * M * N fp32 partial sums when split. Part of the same drop-in for mm_int4
  * (reference kernels/mm_int4.py:59-73), which allocates its output per call; the Python wrapper allocates this
  * workspace the same way. */
 size_t rk_mm_int4_workspace_bytes(int M, int N, int K);

@@ -638,7 +638,15 @@ constexpr int kWideSlot = 8 * 4 * 64 * 16;              // one step's X fragment
 constexpr int kWideOut = 4 * 64 * 65 * 4;               // epilogue transpose, per wave [64][65] fp32
 constexpr int kWideArea = kWideOut > kWideRing * kWideSlot ? kWideOut : kWideRing * kWideSlot;
 
-size_t mm_wide_lds_bytes(int ng) { return (size_t)kWideArea + (size_t)2 * 128 * ng * 2; }
+// ngs: the most groups one block takes (its split of K)
+size_t mm_wide_lds_bytes(int ngs) { return (size_t)kWideArea + (size_t)2 * 128 * ngs * 2; }
+
+// split sp of `splits` over the K / 128 groups, in whole pairs of groups: first group and count
+__host__ __device__ inline void wide_split(int NG, int splits, int sp, int& g_lo, int& ngs) {
+    const int P = NG >> 1, p_lo = sp * P / splits, p_hi = (sp + 1) * P / splits;
+    g_lo = 2 * p_lo;
+    ngs = 2 * (p_hi - p_lo);
+}
 
 // The ring's barrier: this wave's copies older than its newest `vm` loads are done and its LDS reads are done
 // (lgkmcnt(0): the copies issued after the barrier refill the slot the last reads came from); the asm statements
@@ -651,50 +659,58 @@ RK_DEV void wide_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Requires K / 128 even, >= 4 and <= 16 (the row sums fit in one ring slot), (N * K / 128) % 8 == 0 and 16-byte aligned
-// scale / min arrays; the host checks all of them.
+// Block = (tile, split): with splits > 1 each block takes an even range of >= 4 groups (wide_split) and writes
+// its fp32 partial sums to part[split][M][N] (mm_splitk_reduce adds them in split order); with splits = 1 it takes
+// all groups and writes Y. Requires K / 128 even, every split's group count >= 4 and <= kWideMaxGroups, and 4-byte
+// aligned scale / min arrays; the host checks all of them.
+constexpr int kWideMaxGroups = 26;  // LDS: 2 x 128 x 26 fp16 of tables beside the 66.5 KiB area stays <= 80 KiB
+
 __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __restrict__ Xp,
                                                               const float* __restrict__ xsg, int Mp,
                                                               const uint8_t* __restrict__ q,
                                                               const uint16_t* __restrict__ sc,
                                                               const uint16_t* __restrict__ mn, void* __restrict__ Y,
-                                                              int ydt, int ldy, int M, int N, int K) {
+                                                              int ydt, int ldy, int M, int N, int K, int splits) {
     constexpr int BM = 128;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
-    // 1-D grid, XCD-grouped: the row blocks of one column block run on one L2
+    // 1-D grid, XCD-grouped: the row blocks of one column block (and split) run on one L2
     const int G = gridDim.x, L = blockIdx.x, GY = (Mp + BM - 1) / BM;
     const int Lv = (G % 8 == 0) ? (L % 8) * (G / 8) + L / 8 : L;
-    const int mb = (Lv % GY) * BM, nb = (Lv / GY) * 128;
+    const int T = G / splits, sp = Lv / T, tl = Lv - sp * T;
+    const int mb = (tl % GY) * BM, nb = (tl / GY) * 128;
     const int NG = K >> 7;
+    int g_lo, ngs;  // this block's groups g_lo .. g_lo + ngs - 1
+    wide_split(NG, splits, sp, g_lo, ngs);
     const int mts = min(8, (Mp - mb) >> 4);  // m tiles of this block present in Xp
-    uint16_t* tsc = reinterpret_cast<uint16_t*>(smem + kWideArea);  // [128][NG]
-    uint16_t* tmn = tsc + 128 * NG;
+    uint16_t* tsc = reinterpret_cast<uint16_t*>(smem + kWideArea);  // [128][ngs]
+    uint16_t* tmn = tsc + 128 * ngs;
     float* xsl = reinterpret_cast<float*>(smem + kWideSlot);  // row sums [g][128] in ring slot 1 until step 0
     const int jn = lane & 15, sq = lane >> 4;
 
-    // the block's scale and min rows ([n][g], contiguous; 16-byte copies clamped inside the arrays) and row sums
+    // the block's scale and min entries ([n][g] for its groups: 4-byte copies, as g_lo and NG are even; columns
+    // past N repeat the last) and row sums
     {
-        const int nch = 16 * NG;
-        const int lastc = (int)(((size_t)N * NG * 2) / 16) - 1;
-        const size_t c0 = (size_t)nb * NG / 8;
-        for (int b0 = wave * 64; b0 < nch; b0 += 256) {
-            const int ci = min((int)(c0 + b0 + lane), lastc);
-            if (b0 + lane < nch) {
-                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(sc) + ci,
-                                                 reinterpret_cast<uint4*>(tsc) + b0, 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(mn) + ci,
-                                                 reinterpret_cast<uint4*>(tmn) + b0, 16, 0, 0);
+        const int hw = ngs >> 1, nd = 128 * hw;  // dwords per column, per table
+        for (int b0 = wave * 64; b0 < nd; b0 += 256) {
+            const int i = b0 + lane, c = i / hw, d = i - c * hw;
+            const size_t src = ((size_t)min(nb + c, N - 1) * NG + g_lo) / 2 + d;
+            if (i < nd) {
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(sc) + src,
+                                                 reinterpret_cast<uint32_t*>(tsc) + b0, 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(mn) + src,
+                                                 reinterpret_cast<uint32_t*>(tmn) + b0, 4, 0, 0);
             }
         }
         // xs[g][mb .. mb + 127] (rows past Mp repeat its last 4: their sums are never stored), 32 chunks a group
-        for (int b0 = wave * 64; b0 < 32 * NG; b0 += 256) {
+        for (int b0 = wave * 64; b0 < 32 * ngs; b0 += 256) {
             const int c = b0 + lane, g = c >> 5, r4 = min(c & 31, 4 * mts - 1);
-            if (c < 32 * NG)
-                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(xsg + (size_t)g * Mp + mb) + r4,
-                                                 reinterpret_cast<uint4*>(xsl) + b0, 16, 0, 0);
+            if (c < 32 * ngs)
+                __builtin_amdgcn_global_load_lds(
+                    reinterpret_cast<const uint4*>(xsg + (size_t)(g_lo + g) * Mp + mb) + r4,
+                    reinterpret_cast<uint4*>(xsl) + b0, 16, 0, 0);
         }
     }
     // step g's X fragments i = wave + 4 k (m tile i / 4, MFMA step t = i % 4) into ring slot `sl`
@@ -703,8 +719,9 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int i = wave + 4 * k, mt = i >> 2, t = i & 3;
-            __builtin_amdgcn_global_load_lds(Xp + (((size_t)(mb / 16 + min(mt, mts - 1)) * NG + g) * 4 + t) * 64 + lane,
-                                             slot + (mt * 4 + t) * 64, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(
+                Xp + (((size_t)(mb / 16 + min(mt, mts - 1)) * NG + g_lo + g) * 4 + t) * 64 + lane,
+                slot + (mt * 4 + t) * 64, 16, 0, 0);
         }
     };
     // this lane's code bytes: column nb + 64 wn + 16 nt + jn (clamped), bytes 16 sq .. + 15 of each group. The
@@ -718,7 +735,7 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
     auto load_w = [&](int g, u4_t (&w)[4]) {
         uint64_t a[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) a[nt] = (uint64_t)(wsrc[nt] + 64 * g);
+        for (int nt = 0; nt < 4; ++nt) a[nt] = (uint64_t)(wsrc[nt] + 64 * (g_lo + g));
         asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) w[nt] = *(gu4*)a[nt];
@@ -740,13 +757,13 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
-    for (int qq = 0; qq < NG; qq += 4) {
+    for (int qq = 0; qq < ngs; qq += 4) {
         const int gl = qq + sq;
         float mv[4], xa[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) mv[nt] = gl < NG ? f16_bits_to_f32(tmn[(64 * wn + 16 * nt + jn) * NG + gl]) : 0.f;
+        for (int nt = 0; nt < 4; ++nt) mv[nt] = gl < ngs ? f16_bits_to_f32(tmn[(64 * wn + 16 * nt + jn) * ngs + gl]) : 0.f;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) xa[mt] = gl < NG ? xsl[gl * 128 + 64 * wm + 16 * mt + jn] : 0.f;
+        for (int mt = 0; mt < 4; ++mt) xa[mt] = gl < ngs ? xsl[gl * 128 + 64 * wm + 16 * mt + jn] : 0.f;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -761,7 +778,7 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
     // copies and codes are step g + 1's codes (4 loads).
     auto step = [&](int g, int sl, u4_t (&w)[4], auto last) {
         wide_barrier<4>();
-        if constexpr (!decltype(last)::value) issue_x(min(g + 1, NG - 1), sl ^ 1);  // into step g - 1's slot
+        if constexpr (!decltype(last)::value) issue_x(min(g + 1, ngs - 1), sl ^ 1);  // into step g - 1's slot
         const uint4* slot = reinterpret_cast<const uint4*>(smem + (size_t)sl * kWideSlot);
         h8_t A[4][4];  // the wave's 4 m tiles x 4 MFMA steps
 #pragma unroll
@@ -770,7 +787,7 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
             for (int t = 0; t < 4; ++t) A[mt][t] = __builtin_bit_cast(h8_t, slot[((4 * wm + mt) * 4 + t) * 64 + lane]);
         float sv[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) sv[nt] = f16_bits_to_f32(tsc[(64 * wn + 16 * nt + jn) * NG + g]);
+        for (int nt = 0; nt < 4; ++nt) sv[nt] = f16_bits_to_f32(tsc[(64 * wn + 16 * nt + jn) * ngs + g]);
         // column tiles in pairs: dequantise the pair's codes, then per m tile pair the 4 MFMA steps on 2 x 2 tiles
         // (four independent chains) and their affine
 #pragma unroll
@@ -781,7 +798,7 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
 #pragma unroll
                 for (int t = 0; t < 4; ++t) B[j][t] = dequant8(w[np + j][t], kc);
             if constexpr (!decltype(last)::value)
-                if (np == 2) load_w(min(g + 2, NG - 1), w);
+                if (np == 2) load_w(min(g + 2, ngs - 1), w);
 #pragma unroll
             for (int mp = 0; mp < 4; mp += 2) {
                 f4_t c[2][2];
@@ -809,13 +826,13 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
     // possibly in flight at the loop's first wait would make the compiler's waits in every iteration vmcnt(0); from
     // step 1 on the load order is the loop's own. The last step, after the loop, issues no loads.
     using more = std::integral_constant<bool, false>;
-    __builtin_assume(NG >= 4);  // the loop runs at least once (the host checks)
+    __builtin_assume(ngs >= 4);  // the loop runs at least once (the host checks)
     step(0, 0, wa, more{});
-    for (int g = 1; g + 1 < NG; g += 2) {
+    for (int g = 1; g + 1 < ngs; g += 2) {
         step(g, 1, wb, more{});
         step(g + 1, 0, wa, more{});
     }
-    step(NG - 1, 1, wb, std::integral_constant<bool, true>{});
+    step(ngs - 1, 1, wb, std::integral_constant<bool, true>{});
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8));  // vmcnt(0) lgkmcnt(0): copies landed, ring reads done
     __builtin_amdgcn_s_barrier();                           // every wave has left the ring
@@ -832,6 +849,7 @@ __global__ __launch_bounds__(256, 2) void mm_int4_wide_kernel(const uint4* __res
             for (int e = 0; e < 4; ++e) tb[(mt * 16 + 4 * sq + e) * 65 + 16 * nt + jn] = acc[mt][nt][e];
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave reads back only its own tile
     const int m0 = mb + 64 * wm, n0 = nb + 64 * wn;
+    if (splits > 1) Y = reinterpret_cast<float*>(Y) + (size_t)sp * M * ldy;  // this split's partial sums
     const bool vec_ok = (((uintptr_t)Y | (size_t)ldy * (ydt == RK_F32 ? 4 : 2)) & (ydt == RK_F32 ? 15 : 7)) == 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -1150,10 +1168,22 @@ hipError_t launch_mm_prep(const void* X, int xdt, int ldx, const uint8_t* q, con
     return hipGetLastError();
 }
 
-template <int MT>
+// Y[m, n] = sum over splits of part[split][m][n] (fixed order), in Y's dtype
+__global__ __launch_bounds__(256) void mm_splitk_reduce(const float* __restrict__ part, int splits,
+                                                        void* __restrict__ Y, int ydt, int ldy, int M, int N) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, MN = (size_t)M * N;
+    if (i >= MN) return;
+    float v = 0.f;
+    for (int k = 0; k < splits; ++k) v += part[k * MN + i];
+    store_act(Y, ydt, (i / N) * ldy + i % N, v);
+}
+
+// The wide-wave plan: X prepared into the workspace, then (tile, split) blocks; with splits > 1 the fp32 partial
+// sums follow the prepared X in the workspace and mm_splitk_reduce adds them in split order.
+size_t mm_wide_part_offset(int M, int K) { return (mm_prep_ws_bytes(M, K) + 255) / 256 * 256; }
+
 hipError_t launch_mm_wide(const void* X, int xdt, int ldx, const uint8_t* q, const uint16_t* s, const uint16_t* m,
-                          void* Y, int ydt, int ldy, int M, int N, int K, void* ws, hipStream_t st) {
-    constexpr int BM = 16 * MT;
+                          void* Y, int ydt, int ldy, int M, int N, int K, int splits, void* ws, hipStream_t st) {
     const int NG = K / 128, Mp = (M + 15) / 16 * 16;
     uint4* Xp = static_cast<uint4*>(ws);
     float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (size_t)Mp * K * 2);
@@ -1163,20 +1193,22 @@ hipError_t launch_mm_wide(const void* X, int xdt, int ldx, const uint8_t* q, con
         hipLaunchKernelGGL((mm_xprep_kernel<true>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
     else
         hipLaunchKernelGGL((mm_xprep_kernel<false>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
-    const dim3 grid(((N + 127) / 128) * ((Mp + BM - 1) / BM));
-    hipLaunchKernelGGL(mm_int4_wide_kernel, grid, dim3(256), mm_wide_lds_bytes(NG), st, Xp, xs, Mp, q, s, m,
-                       Y, ydt, ldy, M, N, K);
+    const int tiles = ((N + 127) / 128) * ((Mp + 127) / 128);
+    int g_lo, ngs;
+    wide_split(NG, splits, splits - 1, g_lo, ngs);  // the last split has the most groups
+    const size_t lds = mm_wide_lds_bytes(ngs);
+    if (splits == 1) {
+        hipLaunchKernelGGL(mm_int4_wide_kernel, dim3(tiles), dim3(256), lds, st, Xp, xs, Mp, q, s, m, Y, ydt, ldy,
+                           M, N, K, 1);
+    } else {
+        float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + mm_wide_part_offset(M, K));
+        hipLaunchKernelGGL(mm_int4_wide_kernel, dim3(tiles * splits), dim3(256), lds, st, Xp, xs, Mp, q, s, m,
+                           (void*)part, (int)RK_F32, N, M, N, K, splits);
+        const size_t mn = (size_t)M * N;
+        hipLaunchKernelGGL(mm_splitk_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, splits, Y,
+                           ydt, ldy, M, N);
+    }
     return hipGetLastError();
-}
-
-// Y[m, n] = sum over splits of part[split][m][n] (fixed order), in Y's dtype
-__global__ __launch_bounds__(256) void mm_splitk_reduce(const float* __restrict__ part, int splits,
-                                                        void* __restrict__ Y, int ydt, int ldy, int M, int N) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, MN = (size_t)M * N;
-    if (i >= MN) return;
-    float v = 0.f;
-    for (int k = 0; k < splits; ++k) v += part[k * MN + i];
-    store_act(Y, ydt, (i / N) * ldy + i % N, v);
 }
 
 template <int MT, int D>
@@ -1258,7 +1290,8 @@ constexpr size_t kLdsMax = 160 * 1024;
 
 // Kernel choice for one shape. With a caller's workspace (rk_mm_int4_g128_ws) and enough 128-column blocks to give
 // most CUs one (cfg 3 / 4 / 5: the prepared-X kernel with 128 / 64 / 48-row blocks; its workspace holds the prepared
-// X; cfg 7 in place of cfg 3 when K / 128 is even and 4 .. 16: the wide-wave kernel, two blocks per CU). Otherwise 128 x 128 tiles (cfg 1) when that still gives every CU a block, else 64 x 64 tiles (cfg 2), split
+// X; cfg 7 ahead of them for M > 64 when K / 128 is even and >= 4: the wide-wave kernel, two blocks per CU, split
+// over K when its tiles are few). Otherwise 128 x 128 tiles (cfg 1) when that still gives every CU a block, else 64 x 64 tiles (cfg 2), split
 // over K when a workspace or the fixed scratch is allowed and the tiles alone leave CUs idle (each split keeps >= 4
 // groups); cfg 0 is the register-staged kernel, for K too long to stage one block's scales in LDS.
 struct MmPlan {
@@ -1281,18 +1314,44 @@ MmPlan mm_stream_plan(int M, int N, int K, int mode) {
     return {6, 1, 0};
 }
 
+MmPlan mm_plan(int M, int N, int K, int mode);
+
+// The wide-wave plan (cfg 7) for M > 64 and an even group count >= 4: splits over K (whole pairs of groups, >= 4
+// groups and <= kWideMaxGroups each) only when the 128 x 128 tiles alone leave the chip's two-blocks-per-CU slots
+// mostly idle, M >= 256 and K / 128 > 16; used when tiles x splits reaches kPrepMinBlocks. The workspace holds the prepared X, the partial
+// sums when split, and at least what the tile plan that unaligned scale / min arrays fall back to needs.
+constexpr long kWideSlots = 512;  // two blocks per CU on 256 CUs
+MmPlan mm_wide_plan(int M, int N, int K) {
+    const int NG = K / 128, P = NG / 2;
+    const long Mp = (M + 15) / 16 * 16;
+    const long tiles = (long)((N + 127) / 128) * ((Mp + 127) / 128);
+    const int smin = (P + kWideMaxGroups / 2 - 1) / (kWideMaxGroups / 2);
+    if (tiles >= kPrepMinBlocks && smin > 1) return {-1, 0, 0};  // enough tiles: no split just to fit the tables
+    // few tiles: the split's fp32 partial sums (S x M x N) and the reduce launch paid off only for long K at large M
+    // (measured: 512 x 2048 x 11008 58 us against 75 on the tile plan; 512 x 3072 x 2048 34 against 24,
+    // 128 x 2048 x 11008 32 against 26)
+    if (tiles < kPrepMinBlocks && (M < 256 || NG <= 16)) return {-1, 0, 0};
+    int S = smin;
+    if (tiles < kPrepMinBlocks) S = std::max<long>(smin, std::min<long>((kWideSlots + tiles / 2) / tiles, P / 2));
+    if (S > P / 2 || tiles * S < kPrepMinBlocks) return {-1, 0, 0};
+    size_t ws = S > 1 ? mm_wide_part_offset(M, K) + (size_t)S * M * N * sizeof(float) : mm_prep_ws_bytes(M, K);
+    ws = std::max(ws, mm_plan(M, N, K, kMmScratch).ws);
+    return {7, S, ws};
+}
+
 MmPlan mm_plan(int M, int N, int K, int mode) {
     const int NG = K / 128;
     const MmPlan sp = mm_stream_plan(M, N, K, mode);
     if (sp.cfg == 6) return sp;
+    if (mode == kMmWorkspace && M > 64 && NG % 2 == 0 && NG >= 4) {
+        const MmPlan w = mm_wide_plan(M, N, K);
+        if (w.cfg == 7) return w;
+    }
     if (mode == kMmWorkspace && ((long)N * NG) % 8 == 0) {
         const int mt = M <= 48 ? 3 : M <= 64 ? 4 : 8;
         const long Mp = (M + 15) / 16 * 16;
         const long blocks = (long)((N + 127) / 128) * ((Mp + 16 * mt - 1) / (16 * mt));
         const size_t lds = mt == 3 ? mm_prep_lds_bytes<3>(NG) : mt == 4 ? mm_prep_lds_bytes<4>(NG) : mm_prep_lds_bytes<8>(NG);
-        if (mt == 8 && NG % 2 == 0 && NG >= 4 && NG <= 16 && blocks >= kPrepMinBlocks &&
-            mm_wide_lds_bytes(NG) <= kLdsMax / 2)
-            return {7, 1, mm_prep_ws_bytes(M, K)};
         if (blocks >= kPrepMinBlocks && lds <= kLdsMax) return {mt == 8 ? 3 : mt == 4 ? 4 : 5, 1, mm_prep_ws_bytes(M, K)};
     }
     const bool allow_ws = mode != kMmPlain;
@@ -1333,7 +1392,7 @@ int mm_run(const MmPlan& p, const void* X, int x_dtype, int ldx, const uint8_t* 
     else if (p.cfg == 6)
         e = launch_mm_stream(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     else if (p.cfg == 7)
-        e = launch_mm_wide<8>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, ws, s);
+        e = launch_mm_wide(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, p.splits, ws, s);
     else
         e = launch_mm<2, 2>(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K, s);
     return e == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
@@ -1399,9 +1458,10 @@ extern "C" int rk_mm_int4_g128_ws(const void* X, int x_dtype, int ldx, const uin
     const int st = mm_check(X, x_dtype, ldx, q, scale, min, Y, y_dtype, ldy, M, N, K);
     if (st != RK_OK) return st;
     MmPlan p = mm_plan(M, N, K, kMmWorkspace);
-    // the prepared-X kernels copy the scale / min rows in 16-byte pieces; other arrays take the tile plan, which
-    // needs no more workspace (shapes with that many column blocks are not split over K)
-    if ((p.cfg == 3 || p.cfg == 4 || p.cfg == 5 || p.cfg == 7) && (((uintptr_t)scale | (uintptr_t)min) & 15))
+    // the prepared-X kernels copy the scale / min rows in 16-byte pieces (the wide-wave kernel in 4-byte pieces);
+    // other arrays take the tile plan, whose workspace the plan's size covers
+    if (((p.cfg == 3 || p.cfg == 4 || p.cfg == 5) && (((uintptr_t)scale | (uintptr_t)min) & 15)) ||
+        (p.cfg == 7 && (((uintptr_t)scale | (uintptr_t)min) & 3)))
         p = mm_plan(M, N, K, kMmScratch);
     if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) return RK_ERR_SHAPE;
     if (p.ws > 0 && ((uintptr_t)workspace & 15)) return RK_ERR_ALIGN;

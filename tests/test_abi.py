@@ -52,17 +52,24 @@ def test_version_and_status_strings():
 
 
 @pytest.mark.parametrize("M,N,K,splits", [(34, 2048, 11008, 8), (34, 3072, 2048, 1), (128, 2048, 11008, 4),
-                                          (200, 33, 11008, 21), (34, 22016, 2048, 1), (512, 2048, 11008, 1),
+                                          (200, 33, 11008, 21), (34, 22016, 2048, 1), (512, 2048, 11008, 8),
                                           (512, 22016, 2048, 1), (4, 32, 256, 1), (64, 2048, 11008, 8),
                                           (5, 200, 4096, 8)])
 def test_mm_int4_split_k_plan(M, N, K, splits):
     """fp32 partials only where 64 x 64 output tiles leave CUs idle: splits = min(ceil(256 / tiles), groups / 4);
-    shapes on the prepared-X kernel hold the prepared X instead, and the stream kernel (M <= 48, K <= 2048) none"""
+    shapes on the prepared-X kernels hold the prepared X instead (the wide-wave kernel split over K, for M >= 256
+    with long K and few 128 x 128 tiles, also its partials: splits = min(round(512 / tiles), groups / 4)), and the
+    stream kernel (M <= 48, K <= 2048) none"""
     nbytes = HL.lib().rk_mm_int4_workspace_bytes(M, N, K)
-    assert HL.mm_plan(M, N, K)[1] == (splits if HL.mm_plan(M, N, K)[0] not in HL.MM_PREP else 1)
-    if HL.mm_plan(M, N, K)[0] in HL.MM_PREP:
+    kernel, sp = HL.mm_plan(M, N, K)
+    assert sp == splits
+    if kernel in HL.MM_PREP:
         Mp = (M + 15) // 16 * 16
-        assert splits == 1 and nbytes == Mp * K * 2 + (K // 128) * Mp * 4
+        prep = Mp * K * 2 + (K // 128) * Mp * 4
+        if sp == 1:
+            assert nbytes == prep
+        else:
+            assert kernel == HL.MM_WIDE128 and nbytes >= (prep + 255) // 256 * 256 + sp * M * N * 4
     else:
         assert nbytes == (splits * M * N * 4 if splits > 1 else 0)
 
@@ -176,7 +183,8 @@ def test_sampler_entry_points_validate_before_any_device_work():
                                           (64, 22016, 4096, HL.MM_PREP64), (128, 22016, 2048, HL.MM_WIDE128),
                                           (512, 20480, 1152, HL.MM_PREP128), (130, 20480, 256, HL.MM_PREP128),
                                           (512, 22016, 4096, HL.MM_PREP128), (200, 20600, 512, HL.MM_WIDE128),
-                                          (512, 3072, 2048, HL.MM_TILE64), (512, 2048, 11008, HL.MM_TILE64),
+                                          (512, 3072, 2048, HL.MM_TILE64), (512, 2048, 11008, HL.MM_WIDE128),
+                                          (256, 2048, 11008, HL.MM_WIDE128), (128, 2048, 11008, HL.MM_TILE64),
                                           (34, 3072, 2048, HL.MM_STREAM), (34, 22017, 128, HL.MM_STREAM),
                                           (34, 2048, 11008, HL.MM_TILE64), (48, 20480, 2048, HL.MM_STREAM),
                                           (49, 20480, 2048, HL.MM_PREP64), (40, 65536, 2048, HL.MM_PREP48),
@@ -184,8 +192,9 @@ def test_sampler_entry_points_validate_before_any_device_work():
 def test_mm_int4_workspace_plan(M, N, K, kernel):
     """With a workspace, M <= 48 at K <= 2048 takes the stream kernel unless a block's scale / min tables would
     exceed 2048 entries (very wide N); otherwise shapes with >= 160 column blocks of 128 take the prepared-X kernel
-    (48 / 64 / 128-row blocks by M; for M > 64 the wide-wave kernel when K / 128 is even and 4 .. 16); too few
-    blocks, K too long for the block's scale tables, or N * K / 128 not a multiple of 8 keep the tile plan."""
+    (48 / 64 / 128-row blocks by M; for M > 64 the wide-wave kernel when K / 128 is even and >= 4, split over K
+    for M >= 256 with long K and few tiles); too few blocks, K too long for the block's scale tables, or N * K / 128
+    not a multiple of 8 keep the tile plan."""
     assert HL.mm_plan(M, N, K, use_workspace=True)[0] == kernel
 
 
@@ -203,11 +212,12 @@ def test_mm_int4_plan_query(M, N, K, kernel):
     nbytes = HL.lib().rk_mm_int4_workspace_bytes(M, N, K)
     if k2 in HL.MM_PREP:  # prepared X (fp16, rows padded to 16) and its per-group row sums (fp32)
         Mp = (M + 15) // 16 * 16
-        assert sp2 == 1 and nbytes == Mp * K * 2 + (K // 128) * Mp * 4
-        ng = K // 128
-        wide = ng % 2 == 0 and 4 <= ng <= 16
-        assert k2 == (HL.MM_PREP48 if M <= 48 else HL.MM_PREP64 if M <= 64 else
-                      HL.MM_WIDE128 if wide else HL.MM_PREP128)
+        prep = Mp * K * 2 + (K // 128) * Mp * 4
+        if sp2 == 1:
+            assert nbytes == prep
+        else:  # the wide-wave kernel split over K: fp32 partial sums after the prepared X
+            assert k2 == HL.MM_WIDE128 and nbytes >= (prep + 255) // 256 * 256 + sp2 * M * N * 4
+        assert k2 == (HL.MM_PREP48 if M <= 48 else HL.MM_PREP64 if M <= 64 else k2)
     else:
         assert (sp2 > 1) == (nbytes > 0) and nbytes == (sp2 * M * N * 4 if sp2 > 1 else 0)
     with pytest.raises(RuntimeError):

@@ -40,11 +40,12 @@ def test_config3_shapes(M, N, K, dev):
 
 
 @pytest.mark.parametrize("N,K,kernel", [(3072, 2048, H.MM_TILE64), (22016, 2048, H.MM_WIDE128),
-                                         (2048, 11008, H.MM_TILE64)])
+                                         (2048, 11008, H.MM_WIDE128)])
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 def test_config3_m512(N, K, kernel, xdt, dev):
     """M = 512 on every config-3 shape through the drop-in (workspace entry); gate+up 22016 x 2048 runs the
-    wide-wave prepared-X kernel (asserted; its tile-kernel run is test_prepared_x_against_tile_kernels)."""
+    wide-wave prepared-X kernel and down 2048 x 11008 the same kernel split over K (asserted; their tile-kernel
+    runs are in test_prepared_x_against_tile_kernels)."""
     assert H.mm_plan(512, N, K)[0] == kernel
     X, q, s, m = synth.prefill_case(512, N, K, 3)
     X = X.to(xdt)
@@ -203,11 +204,12 @@ def _ws(M, N, K, dev):
                                              (40, 65536, 2048, H.MM_PREP48, H.MM_TILE64),
                                              (128, 22016, 2048, H.MM_WIDE128, H.MM_TILE64),
                                              (64, 22016, 4096, H.MM_PREP64, H.MM_TILE64),
-                                             (512, 20480, 1152, H.MM_PREP128, H.MM_TILE128)])
+                                             (512, 20480, 1152, H.MM_PREP128, H.MM_TILE128),
+                                             (512, 2048, 11008, H.MM_WIDE128, H.MM_TILE64)])
 def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
     """Each benchmarked / reference prompt shape on both plans: both within the oracle bar, and equal to each other up
     to fp32 summation order."""
-    assert H.mm_plan(M, N, K, use_workspace=True) == (prep, 1)
+    assert H.mm_plan(M, N, K, use_workspace=True)[0] == prep
     assert H.mm_plan(M, N, K, use_workspace=False) == (tile, 1)
     X, q, s, m = synth.prefill_case(M, N, K, 21)
     X = X.bfloat16() if M in (40, 69, 201) else X  # the engine passes bf16 on the w_in prompts
@@ -230,7 +232,9 @@ def test_prepared_x_against_tile_kernels(M, N, K, prep, tile, dev):
                                            (130, 20480, 256, torch.bfloat16, torch.bfloat16),
                                            (200, 20600, 512, torch.float16, torch.float32),
                                            (96, 20488, 1024, torch.bfloat16, torch.bfloat16),
-                                           (77, 20520, 1536, torch.float16, torch.float16)])
+                                           (77, 20520, 1536, torch.float16, torch.float16),
+                                           (300, 1000, 4352, torch.bfloat16, torch.float32),
+                                           (260, 1544, 3328, torch.float16, torch.bfloat16)])
 def test_prepared_x_ragged_and_dtypes(M, N, K, xdt, ydt, dev):
     """Ragged rows (the last block's missing m tiles, rows past M), ragged columns (N not a multiple of 128 or 8),
     odd group counts, every input / output dtype; nothing is written outside [M, N]."""

@@ -412,16 +412,14 @@ __global__ __launch_bounds__(512) void mm_int4_lds_kernel(const void* __restrict
 #define RK_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
 // Xp[mt][g][t][lane] (16 bytes): afrag of X[16 mt + j][128 g + 32 s + 8 t .. + 7], lane = j + 16 s (rows past M are
-// zero); xs[g][m] = fp32 sum of X[m][128 g .. 128 g + 127]. One thread per 16-byte chunk (m, g, c = 4 s + t).
+// zero); xs[g][m] = fp32 sum of X[m][128 g .. 128 g + 127]. One thread per 16-byte chunk (m, g, c = 4 s + t); block
+// b = (m tile, group) covers the 16 rows' 16 chunks of one group, so it writes one whole 4 KiB fragment block.
 template <bool BF16>
 __global__ __launch_bounds__(256) void mm_xprep_kernel(const void* __restrict__ X, int ldx, int M, int Mp, int K,
                                                        uint4* __restrict__ Xp, float* __restrict__ xs) {
     const int NG = K >> 7;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)Mp * NG * 16) return;  // whole 16-lane rows leave together (the total is a multiple of 16)
-    const int c = (int)(idx & 15);
-    const size_t rg = idx >> 4;
-    const int g = (int)(rg % NG), m = (int)(rg / NG);
+    const int c = threadIdx.x & 15;                               // chunk within the row's group
+    const int g = blockIdx.x % NG, m = (blockIdx.x / NG) * 16 + (threadIdx.x >> 4);  // grid: Mp / 16 * NG blocks
     u4_t d = {0u, 0u, 0u, 0u};
     if (m < M)
         d = *reinterpret_cast<const u4_t*>(reinterpret_cast<const uint16_t*>(X) + (size_t)m * ldx + 128 * g + 8 * c);
@@ -1156,8 +1154,7 @@ hipError_t launch_mm_prep(const void* X, int xdt, int ldx, const uint8_t* q, con
     const int NG = K / 128, Mp = (M + 15) / 16 * 16;
     uint4* Xp = static_cast<uint4*>(ws);
     float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (size_t)Mp * K * 2);
-    const size_t chunks = (size_t)Mp * NG * 16;
-    const dim3 pg((unsigned)((chunks + 255) / 256));
+    const dim3 pg((unsigned)(Mp / 16 * NG));  // one block per (m tile, group)
     if (xdt == RK_BF16)
         hipLaunchKernelGGL((mm_xprep_kernel<true>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
     else
@@ -1178,6 +1175,22 @@ __global__ __launch_bounds__(256) void mm_splitk_reduce(const float* __restrict_
     store_act(Y, ydt, (i / N) * ldy + i % N, v);
 }
 
+// the same four outputs per thread (16-byte loads of each split), for N % 4 == 0 and a 16-byte aligned part
+__global__ __launch_bounds__(256) void mm_splitk_reduce4(const float* __restrict__ part, int splits,
+                                                         void* __restrict__ Y, int ydt, int ldy, int M, int N) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4, MN = (size_t)M * N;
+    if (i >= MN) return;
+    f4_t v = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < splits; ++k) {
+        const f4_t p = *reinterpret_cast<const f4_t*>(part + k * MN + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += p[e];
+    }
+    const size_t o = (i / N) * ldy + i % N;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_act(Y, ydt, o + e, v[e]);
+}
+
 // The wide-wave plan: X prepared into the workspace, then (tile, split) blocks; with splits > 1 the fp32 partial
 // sums follow the prepared X in the workspace and mm_splitk_reduce adds them in split order.
 size_t mm_wide_part_offset(int M, int K) { return (mm_prep_ws_bytes(M, K) + 255) / 256 * 256; }
@@ -1187,8 +1200,7 @@ hipError_t launch_mm_wide(const void* X, int xdt, int ldx, const uint8_t* q, con
     const int NG = K / 128, Mp = (M + 15) / 16 * 16;
     uint4* Xp = static_cast<uint4*>(ws);
     float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (size_t)Mp * K * 2);
-    const size_t chunks = (size_t)Mp * NG * 16;
-    const dim3 pg((unsigned)((chunks + 255) / 256));
+    const dim3 pg((unsigned)(Mp / 16 * NG));  // one block per (m tile, group)
     if (xdt == RK_BF16)
         hipLaunchKernelGGL((mm_xprep_kernel<true>), pg, dim3(256), 0, st, X, ldx, M, Mp, K, Xp, xs);
     else
@@ -1205,8 +1217,12 @@ hipError_t launch_mm_wide(const void* X, int xdt, int ldx, const uint8_t* q, con
         hipLaunchKernelGGL(mm_int4_wide_kernel, dim3(tiles * splits), dim3(256), lds, st, Xp, xs, Mp, q, s, m,
                            (void*)part, (int)RK_F32, N, M, N, K, splits);
         const size_t mn = (size_t)M * N;
-        hipLaunchKernelGGL(mm_splitk_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, splits, Y,
-                           ydt, ldy, M, N);
+        if (N % 4 == 0)
+            hipLaunchKernelGGL(mm_splitk_reduce4, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0, st, part,
+                               splits, Y, ydt, ldy, M, N);
+        else
+            hipLaunchKernelGGL(mm_splitk_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, splits,
+                               Y, ydt, ldy, M, N);
     }
     return hipGetLastError();
 }

@@ -26,7 +26,9 @@ and a dense bf16 GEMV's read rate.
 parity: the layer launch's outputs on copy 0 (q/k/v rows and down) and the w_in projection against the float64
 oracle (max_rel and max_rel_strict).
 decode_tok_s: the 36-layer step's tokens per second at ctx 256 / 1024 / 2048 (config 4), as the role-split one-launch
-kernel (decode.RoleDecode); decode.persistent_engine times the every-block-every-role kernel on the same weights.
+kernel (decode.RoleDecode) replayed as the generate loop replays it: graphs of 8 consecutive steps (one Mimi frame)
+ending at slot ctx - 1; the one-step replay figure is beside it (`single_step_replays`);
+decode.persistent_engine times the every-block-every-role kernel on the same weights.
 cpu_baseline: the reference's CPU path for the same step, dequantize then matmul in torch fp32
 (kernels/int4_gemv.py:27-30 as kernels/bench_gemv.py:43 runs it) on CPU tensors with every thread torch is given,
 with a matmul-only time, and the numpy oracle's single-threaded dequantization and configs 2 / 3 / a config-4 layer
@@ -243,30 +245,52 @@ def cpu_baseline(budget_s):
     return res
 
 
+FRAME = 8  # tokens per generate-loop frame (num_quantizers: one Mimi frame), one hipGraph replay
+
+
 def _time_steps(eng, cfg, steps, ctxs):
-    """us per token of eng's captured step at each context (pos reset before every replay: one tiny fill kernel per
-    step, inside the timed loop), HIP events on the engine's stream"""
+    """us per token of eng's step at each context, HIP events on the engine's stream, two ways:
+    - frames (the reported figure): graphs of FRAME consecutive steps (capture_frame, as the generate loop replays
+      them), each frame started at pos = ctx - FRAME so its steps write slots ctx - 8 .. ctx - 1 (attention over
+      ctx - 7 .. ctx slots); one tiny fill kernel per frame resets pos;
+    - single: one-step graph replays with pos reset to ctx - 1 before every replay (one fill kernel per step)."""
     import torch
     res = {}
     eng.capture()
-    for ctx in ctxs:
-        for _ in range(10):
-            eng.pos.fill_(ctx - 1)
-            eng.replay()
+    eng.capture_frame(FRAME)
+    nfr = max(1, steps // FRAME)
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(steps):
-            eng.pos.fill_(ctx - 1)
-            eng.replay()
+        for _ in range(n):
+            fn()
         e1.record()
         torch.cuda.synchronize()
-        dt = e0.elapsed_time(e1) / 1e3
+        return e0.elapsed_time(e1) / 1e3
+
+    for ctx in ctxs:
+        def one():
+            eng.pos.fill_(ctx - 1)
+            eng.replay()
+
+        def frame():
+            eng.pos.fill_(ctx - FRAME)
+            eng.replay_frame(FRAME)
+        dt1 = timed(one, steps)
+        dt = timed(frame, nfr)
         if eng.status_word() != 0:
             raise RuntimeError(f"one-launch decode step reported status {eng.status_word()}")
+        n = nfr * FRAME
         nbytes = cfg.weight_bytes() + cfg.kv_bytes(ctx)
-        res[f"ctx{ctx}"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1),
-                            "GB_s": round(nbytes * steps / dt / 1e9, 1), "bytes_per_token": nbytes}
+        res[f"ctx{ctx}"] = {"us_per_token": round(dt * 1e6 / n, 1), "tok_s": round(n / dt, 1),
+                            "GB_s": round(nbytes * n / dt / 1e9, 1), "bytes_per_token": nbytes,
+                            "timing": f"graphs of {FRAME} steps (slots ctx-{FRAME}..ctx-1), {n} tokens",
+                            "single_step_replays": {"us_per_token": round(dt1 * 1e6 / steps, 1),
+                                                    "tok_s": round(steps / dt1, 1)}}
     return res
 
 
@@ -312,19 +336,23 @@ def run_decode(dev, steps):
     ctx = 256
     eng.pos.fill_(ctx - 1)  # the capture's warm-up step needs a cache slot (the last loop left pos at S)
     eng.capture()
-    for _ in range(10):
-        eng.pos.fill_(ctx - 1); eng.step_i.fill_(9); eng.replay()
+    eng.capture_frame(FRAME)
+    nfr = max(1, steps // FRAME)
+    for _ in range(3):
+        eng.pos.fill_(ctx - FRAME); eng.step_i.fill_(9); eng.replay_frame(FRAME)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(steps):
-        eng.pos.fill_(ctx - 1); eng.step_i.fill_(9); eng.replay()
+    for _ in range(nfr):
+        eng.pos.fill_(ctx - FRAME); eng.step_i.fill_(9); eng.replay_frame(FRAME)
     e1.record()
     torch.cuda.synchronize()
     dt = e0.elapsed_time(e1) / 1e3
     if eng.status_word() != 0:
         raise RuntimeError(f"one-launch decode step reported status {eng.status_word()}")
-    out["sampled_ctx256"] = {"us_per_token": round(dt * 1e6 / steps, 1), "tok_s": round(steps / dt, 1)}
+    n = nfr * FRAME
+    out["sampled_ctx256"] = {"us_per_token": round(dt * 1e6 / n, 1), "tok_s": round(n / dt, 1),
+                             "timing": f"graphs of {FRAME} steps with the sampling tail (slots 248..255)"}
     log(f"[bench] decode + sampling ctx 256: {out['sampled_ctx256']}")
     # the host generate loop (frames of 8 replays, pinned read-back, one frame queued ahead): a 4-token prompt, then
     # 256 generated tokens from position 4

@@ -3,8 +3,9 @@
 Mirrors RumikInt4.generate / to_codes (reference engine/rumik_int4.py:251-324) over a one-launch decode engine
 (RoleDecode or PersistentDecode) with the sampling tail attached (one hipGraph = decode step + sample; the sampled
 token is the next replay's input):
-- frames of Q tokens (Q = num_quantizers, one Mimi frame): Q graph replays, then an asynchronous copy of the frame's
-  tokens to pinned host memory and an event; the next frame is queued before waiting for the current one (double
+- frames of Q tokens (Q = num_quantizers, one Mimi frame): one replay of a graph holding Q consecutive steps (no
+  launch gap between them; the same tokens as Q one-step replays), then an asynchronous copy of the frame's tokens to
+  pinned host memory and an event; the next frame is queued before waiting for the current one (double
   buffering: the GPU never idles while the host handles a frame), and waiting on the event waits only for the work
   before it;
 - generation stops at </audio> (tokens after it in the same frame are dropped, a frame queued after it is ignored),
@@ -47,6 +48,7 @@ class Generator:
         self.host_status = torch.zeros(eng.out.shape[0], dtype=torch.int32, pin_memory=True)
         if eng.graph is None:
             eng.capture()
+        eng.capture_frame(self.Q)  # a frame's Q steps as one graph: no launch gap between its tokens
 
     def _fail(self, status, where):
         self.eng.reset()
@@ -97,9 +99,8 @@ class Generator:
 
         def launch():
             nonlocal pos, n
-            for _ in range(self.Q):
-                e.replay()
-                pos += 1
+            e.replay_frame(self.Q)
+            pos += self.Q
             host[n:n + self.Q].copy_(e.out[n:n + self.Q], non_blocking=True)
             self.host_status[n:n + 1].copy_(e.status, non_blocking=True)
             ev = torch.cuda.Event()

@@ -195,6 +195,52 @@ def test_roles_qkv_placements_identical(dev):
         assert torch.equal(outs[0][1], other[1]) and torch.equal(outs[0][2], other[2])
 
 
+@pytest.mark.parametrize("engine", ["roles", "persistent"])
+def test_frame_graph_equals_single_replays(engine, dev):
+    """capture_frame(n): n consecutive steps (decode + sampling tail) in ONE graph, as the generate loop and the
+    bench replay them, do exactly what n replays of the one-step graph do: from the same state and seed the sampled
+    tokens, the new K / V slots, logits, hidden state, pos and step counter are bit-identical (ctx 377 .. 381
+    crosses the role-split step's q/k/v placement switch at pos 384 on the second frame)."""
+    cfg = decode.Config(L=2, vocab=64, n_audio=700, S=512)
+    w = decode.random_weights(cfg, 12, device=dev, gen_device="cuda")
+    eng = _one_launch(engine, cfg, w, dev)
+    g = torch.Generator().manual_seed(13)
+    stop = {"0.weight": torch.ones(cfg.H), "0.bias": torch.zeros(cfg.H),
+            "1.weight": (torch.randn(512, cfg.H, generator=g) / cfg.H ** 0.5).bfloat16(),
+            "1.bias": torch.zeros(512), "3.weight": torch.randn(1, 512, generator=g) / 512 ** 0.5,
+            "3.bias": torch.tensor([-5.0])}
+    ids = torch.arange(cfg.n_audio, dtype=torch.int64) % (cfg.vocab - 1)
+    ids[-1] = cfg.vocab - 1
+    eng.attach_sampler(stop, ids, end_id=cfg.vocab - 1)
+    gk = torch.Generator(device=dev).manual_seed(14)
+    eng.kc.normal_(generator=gk)
+    eng.vc.normal_(generator=gk)
+    kc0, vc0 = eng.kc.clone(), eng.vc.clone()
+    n, pos0 = 5, 377
+    eng.set_state(3, pos0)
+    eng.capture()
+    eng.capture_frame(n)
+    res = []
+    for use_frame in (False, True):
+        eng.kc.copy_(kc0); eng.vc.copy_(vc0); eng.set_state(3, pos0)
+        eng.step_i.zero_(); eng.out.zero_()
+        torch.manual_seed(21)
+        for _ in range(2):  # two frames: the second starts from the state the first left
+            if use_frame:
+                eng.replay_frame(n)
+            else:
+                for _ in range(n):
+                    eng.replay()
+        torch.cuda.synchronize()
+        assert eng.status_word() == 0
+        res.append((eng.out[:2 * n].clone(), eng.kc[:, :, pos0:pos0 + 2 * n].clone(),
+                    eng.vc[:, :, pos0:pos0 + 2 * n].clone(), eng.logits.clone(), eng.hn.clone(), eng.pos.clone(),
+                    eng.step_i.clone(), eng.tok.clone()))
+    assert int(res[0][5].item()) == pos0 + 2 * n and int(res[0][6].item()) == 2 * n
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("engine", ONE_LAUNCH)
 def test_persistent_small_mlp_and_ctx_edges(engine, dev):
     # inter 2048, contexts at the edges: first slot and the last slot of the cache (the role-split step: 128 MLP

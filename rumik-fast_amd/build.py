@@ -31,12 +31,17 @@ FLAGS = [
 ]
 
 
+# per-source additions: the prefill attention keeps its MFMA accumulators in VGPRs (its online-softmax rescale
+# multiplies them between MFMAs; in AGPRs every multiply costs a copy out and back)
+EXTRA = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: Path, obj: Path):
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass does not know the packed-fp32 feature and says so; that warning is expected
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)

@@ -11,9 +11,13 @@
 // prefill_attn on the matrix cores (v_mfma_f32_16x16x32_f16; operand layouts: A[i][k] in lane i + 16 (k / 8),
 // element k % 8; B[k][j] in lane j + 16 (k / 8); D[i][j] in lane j + 16 (i / 4), element i % 4). Block = (KV head
 // g, a share of its query heads, tile of 16 queries); wave r = the share's head r. Per key block of 32 slots the
-// block stages K [32 x 128] and V transposed [128 x 32] in LDS once for its heads; each wave computes S = Q K^T (2 x 4 MFMAs), the causal
-// mask and an online softmax (row statistics reduced over the 16 lanes of a DPP row), stores P (fp16, the
-// reference's tensor-core PV in 16-bit) to its LDS tile in the A layout and accumulates O += P V (8 MFMAs, fp32).
+// block stages K [32 x 128] and V transposed [128 x 32] in LDS once for its heads; each wave computes S = Q K^T (2 x 4
+// MFMAs), the causal mask and an online softmax in log2 units (lazy running max, see the key loop), stores P (fp16,
+// the reference's tensor-core PV in 16-bit) to its LDS tile in the A layout and accumulates O += P V (8 MFMAs, fp32).
+// The launch time is the longest query tile's key loop, whose steps are bound by the waves' VALU work (one or two
+// waves per SIMD), so the loop keeps the per-score instruction count down: the row max is reduced across lanes only
+// when a ballot says some score passed the running max by more than 2^8, O is rescaled only then, the row sums stay
+// per lane until the loop ends, and the causal mask is applied only on blocks that reach past the tile's first query.
 #include "common.h"
 
 #include <initializer_list>
@@ -355,42 +359,84 @@ struct KVChunks {
     u4_t k[CH], v[CH];  // native vectors (HIP's uint4 is a struct with a union, which stays in scratch memory)
 };
 
-// Chunk e of a step (e < KS * 512): key block e / 512 of the step; within it, chunk e' = e % 512 of K and of V is
-// key e' / 16, dims 8 (e' % 16) .. + 8 (16 consecutive lanes: one 256-byte row, coalesced). V goes to LDS
-// transposed, Vt[dim][key], each dim row rotated by 8 ((dim / 8) % 4) keys (vt_col): the 16 lanes that write one
-// key's dims into rows 8 apart (64 bytes each) then spread over four bank groups instead of one, and a 16-byte
-// fragment read (8 keys of one row) stays contiguous. Slots past `last` re-read slot `last`: every load valid and
+// Staging of one step's KS key blocks (K rows to Ks, V transposed to Vt[dim][key] so that a 16-byte MFMA fragment
+// read holds 8 consecutive keys of one dim; each dim row rotated by 8 ((dim / 8) % 4) keys, vt_col, so the stores
+// of one instruction spread over more banks). Slots past `last` re-read slot `last`: every load valid and
 // unconditional, so the compiler waits for exactly the chunks it stores; those keys are masked out of S (P = 0).
+// Two forms, by the 16-byte chunks (8 dims of one key) a thread holds per step:
+// - QUAD (at least 4 chunks): a thread's chunks come as quads, 4 consecutive keys at the same 8 dims (quad qq of key
+//   block kb = qd / 128: dims 8 (qq % 16), keys 4 (qq / 16) .. + 3; each of the quad's 4 loads is one 256-byte row
+//   per 16 lanes, coalesced), and V goes to Vt as 8-byte words of 4 keys per dim: 8 stores per quad instead of 32
+//   2-byte ones (those measured ~0.5 us per step of two key blocks, a third of the step). Vt rows of 80 bytes.
+//   (Measured and not kept: lanes along the keys, 16 quads of one dim row per store instruction into unrotated rows,
+//   which spreads the stores over all banks but splits every load over 16 half-lines: 15.6 against 14.8 us.)
+// - CHUNK (fewer): chunk e (< KS * 512) is key block e / 512, key (e % 512) / 16, dims 8 (e % 16) (16 consecutive
+//   lanes: one 256-byte row); V is stored 2 bytes at a time into rows of kKB keys.
+constexpr float kLazyMax = 8.f;  // log2 units: a row's running max moves only when exceeded by more than this
 constexpr int kKsPad = 8;  // K rows padded by 16 bytes: the QK fragment reads of 16 rows then spread over the banks
 constexpr int kChunksPerKB = kKB * kHD / 8;  // 512
+constexpr int kVtRow = kKB + 8;     // QUAD: halves per Vt row (80 bytes)
+constexpr int kVtBlk = kHD * kVtRow;  // QUAD: halves per key block of Vt (the CHUNK form uses kHD * kKB of them)
 
-// column of key j in transposed row d of Vt
+// column of key j in transposed row d
 RK_DEV int vt_col(int d, int j) { return (j + 8 * ((d >> 3) & 3)) & (kKB - 1); }
-
-template <int CH>
-RK_DEV void kv_load(const uint16_t* kg, const uint16_t* vg, int s0, int KS, int last, KVChunks<CH>& c) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-        const int e = threadIdx.x + u * blockDim.x, kb = e / kChunksPerKB, ep = e % kChunksPerKB;
-        const int j0 = (s0 + kb) * kKB;  // s0: the step's first key block
-        const int kj = ep / (kHD / 8), d8 = (ep % (kHD / 8)) * 8;
-        c.k[u] = *reinterpret_cast<const u4_t*>(kg + (size_t)min(j0 + kj, last) * kHD + d8);
-        c.v[u] = *reinterpret_cast<const u4_t*>(vg + (size_t)min(j0 + kj, last) * kHD + d8);
-    }
-    (void)KS;
+// offset in halves of key j of dim row d of Vt key block b (j a multiple of 4 for QUAD, of 8 for CHUNK)
+template <bool QUAD>
+RK_DEV int vt_off(int b, int d, int j) {
+    if constexpr (QUAD)
+        return b * kVtBlk + d * kVtRow + vt_col(d, j);
+    else
+        return (b * kHD + d) * kKB + vt_col(d, j);
 }
 
 template <int CH>
-RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kKB][kHD + kKsPad], uint16_t (*Vt)[kHD][kKB]) {
+RK_DEV void kv_load(const uint16_t* kg, const uint16_t* vg, int s0, int last, KVChunks<CH>& c) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-        const int e = threadIdx.x + u * blockDim.x, kb = e / kChunksPerKB, ep = e % kChunksPerKB;
-        const int kj = ep / (kHD / 8), d8 = (ep % (kHD / 8)) * 8;
-        *reinterpret_cast<u4_t*>(&Ks[kb][kj][d8]) = c.k[u];
+        int j, d8;
+        if constexpr (CH % 4 == 0) {
+            const int qd = threadIdx.x + (u / 4) * blockDim.x, qq = qd % (kChunksPerKB / 4);
+            j = (s0 + qd / (kChunksPerKB / 4)) * kKB + 4 * (qq / (kHD / 8)) + u % 4;
+            d8 = (qq % (kHD / 8)) * 8;
+        } else {
+            const int e = threadIdx.x + u * blockDim.x;
+            j = (s0 + e / kChunksPerKB) * kKB + (e % kChunksPerKB) / (kHD / 8);
+            d8 = (e % (kHD / 8)) * 8;
+        }
+        c.k[u] = *reinterpret_cast<const u4_t*>(kg + (size_t)min(j, last) * kHD + d8);
+        c.v[u] = *reinterpret_cast<const u4_t*>(vg + (size_t)min(j, last) * kHD + d8);
+    }
+}
+
+template <int CH>
+RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kKB][kHD + kKsPad], uint16_t* Vt) {
+    if constexpr (CH % 4 == 0) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            Vt[kb][d8 + 2 * w][vt_col(d8 + 2 * w, kj)] = (uint16_t)c.v[u][w];
-            Vt[kb][d8 + 2 * w + 1][vt_col(d8 + 2 * w + 1, kj)] = (uint16_t)(c.v[u][w] >> 16);
+        for (int g = 0; g < CH / 4; ++g) {
+            const int qd = threadIdx.x + g * blockDim.x, kb = qd / (kChunksPerKB / 4), qq = qd % (kChunksPerKB / 4);
+            const int k4 = 4 * (qq / (kHD / 8)), d8 = (qq % (kHD / 8)) * 8;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) *reinterpret_cast<u4_t*>(&Ks[kb][k4 + u][d8]) = c.k[4 * g + u];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {  // dims d8 + 2w (low halves) and d8 + 2w + 1 (high halves) of the 4 keys
+                const uint32_t v0 = c.v[4 * g][w], v1 = c.v[4 * g + 1][w], v2 = c.v[4 * g + 2][w], v3 = c.v[4 * g + 3][w];
+                const u2_t lo = {(v0 & 0xFFFFu) | (v1 << 16), (v2 & 0xFFFFu) | (v3 << 16)};
+                const u2_t hi = {(v0 >> 16) | (v1 & 0xFFFF0000u), (v2 >> 16) | (v3 & 0xFFFF0000u)};
+                *reinterpret_cast<u2_t*>(Vt + vt_off<true>(kb, d8 + 2 * w, k4)) = lo;
+                *reinterpret_cast<u2_t*>(Vt + vt_off<true>(kb, d8 + 2 * w + 1, k4)) = hi;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int e = threadIdx.x + u * blockDim.x, kb = e / kChunksPerKB, ep = e % kChunksPerKB;
+            const int kj = ep / (kHD / 8), d8 = (ep % (kHD / 8)) * 8;
+            *reinterpret_cast<u4_t*>(&Ks[kb][kj][d8]) = c.k[u];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                Vt[vt_off<false>(kb, d8 + 2 * w, kj)] = (uint16_t)c.v[u][w];
+                Vt[vt_off<false>(kb, d8 + 2 * w + 1, kj)] = (uint16_t)(c.v[u][w] >> 16);
+            }
         }
     }
 }
@@ -398,7 +444,7 @@ RK_DEV void kv_store(const KVChunks<CH>& c, uint16_t (*Ks)[kKB][kHD + kKsPad], u
 // dynamic LDS of prefill_attn_kernel<REP, KS>: the staging (KS key blocks of K and transposed V, one P tile per
 // wave), reused after the key loop for the merge (REP partial results of 16 x 128 fp32 plus m / l per row)
 constexpr size_t attn_stage_bytes(int REP, int KS) {
-    return (size_t)KS * kKB * (kHD + kKsPad) * 2 + (size_t)KS * kHD * kKB * 2 + (size_t)REP * KS * kQT * kKB * 2;
+    return (size_t)KS * kKB * (kHD + kKsPad) * 2 + (size_t)KS * kVtBlk * 2 + (size_t)REP * KS * kQT * kKB * 2;
 }
 constexpr size_t attn_merge_bytes(int REP) { return (size_t)REP * (64 * 32 + 2 * kQT) * 4; }
 constexpr size_t attn_lds_bytes(int REP, int KS) {
@@ -406,7 +452,7 @@ constexpr size_t attn_lds_bytes(int REP, int KS) {
 }
 
 template <int REP, int KS>
-__global__ __launch_bounds__(64 * REP * KS) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc,
+__global__ __launch_bounds__(64 * REP * KS) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_attn_kernel(const uint16_t* q, const uint16_t* kc,
                                                                       const uint16_t* vc, uint16_t* o, int T, int p0,
                                                                       int NH, int NKV, int S, float scale) {
     // REP: the query heads of one KV head this block computes (all NH / NKV of them, or a share: blockIdx.x then
@@ -414,14 +460,16 @@ __global__ __launch_bounds__(64 * REP * KS) void prefill_attn_kernel(const uint1
     constexpr int CH = KS * kChunksPerKB / (64 * REP * KS);
     extern __shared__ __align__(16) uint8_t lds[];
     auto Ks = reinterpret_cast<uint16_t(*)[kKB][kHD + kKsPad]>(lds);
-    auto Vt = reinterpret_cast<uint16_t(*)[kHD][kKB]>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2);
-    uint16_t* Ps = reinterpret_cast<uint16_t*>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2 + (size_t)KS * kHD * kKB * 2);
+    constexpr bool QUAD = CH % 4 == 0;
+    uint16_t* Vt = reinterpret_cast<uint16_t*>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2);
+    uint16_t* Ps = reinterpret_cast<uint16_t*>(lds + (size_t)KS * kKB * (kHD + kKsPad) * 2 + (size_t)KS * kVtBlk * 2);
     const int shares = NH / NKV / REP;
     const int g = blockIdx.x / shares, q0 = blockIdx.y * kQT;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r = w % REP, ks = w / REP;
     const int h = g * (NH / NKV) + (blockIdx.x % shares) * REP + r;
     const int li = lane & 15, lq = lane >> 4;  // A / B fragment: row or column li, k-group lq
+    const float sl2 = scale * 1.44269504088896341f;  // scores in log2 units: P = 2^(s sl2 - m)
     const int ldq = NH * kHD;
     uint16_t* P = Ps + w * kQT * kKB;
     // Q fragments of this wave's head: query q0 + li, dims 32c + 8 lq .. + 8
@@ -432,6 +480,9 @@ __global__ __launch_bounds__(64 * REP * KS) void prefill_attn_kernel(const uint1
         for (int c = 0; c < 4; ++c)
             Qf[c] = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(q + (size_t)qi * ldq + h * kHD + 32 * c + 8 * lq));
     }
+    // the Q loads go out before the K / V prefetch: results return in issue order, so the first step's S = Q K^T then
+    // waits only for its own K / V block, not for the second set behind it
+    __builtin_amdgcn_sched_barrier(0);
     f4_t O[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) O[c] = f4_t{0.f, 0.f, 0.f, 0.f};
@@ -449,69 +500,108 @@ __global__ __launch_bounds__(64 * REP * KS) void prefill_attn_kernel(const uint1
     // K / V of the next two steps are in flight in registers while a step is computed: set A holds the even steps,
     // set B the odd ones (the loop is unrolled by two so that neither is copied)
     KVChunks<CH> ka, kb;
-    kv_load<CH>(kg, vg, kb0, KS, last, ka);
-    kv_load<CH>(kg, vg, kb0 + KS, KS, last, kb);
-    // one step (a macro, not a lambda: the register sets must stay promotable to registers)
+    kv_load<CH>(kg, vg, kb0, last, ka);
+    __builtin_amdgcn_sched_barrier(0);  // set A issued before set B (the order the steps consume them in)
+    kv_load<CH>(kg, vg, kb0 + KS, last, kb);
+    // one step (a macro, not a lambda: the register sets must stay promotable to registers). (Measured and not kept: a
+    // double-buffered staging with one barrier per step, each wave storing step st + 1 while computing step st: no
+    // faster, 15.1 against 14.8 us; the step is bound by the waves' own LDS traffic, not by the barrier.)
 #define RK_ATTN_STEP(st, cur) \
     __syncthreads();  /* the previous step's K / V are no longer read */ \
     kv_store<CH>(cur, Ks, Vt); \
     __syncthreads(); \
-    kv_load<CH>(kg, vg, kb0 + ((st) + 2) * KS, KS, last, cur);  /* two steps ahead (clamped past the end) */ \
+    kv_load<CH>(kg, vg, kb0 + ((st) + 2) * KS, last, cur);  /* two steps ahead (clamped past the end) */ \
     if (kb0 + (st) * KS + ks < kb1) {  /* wave-uniform: this group's key block of the step exists */ \
         const int j0 = (kb0 + (st) * KS + ks) * kKB; \
         /* S = Q K^T for keys j0 + 16 hf + li (D layout: row 4 lq + e, key li) */ \
+        /* all 8 K fragments are read before the first MFMA (the reads' latencies overlap instead of adding up) */ \
+        h8_t Bk[2][4]; \
+_Pragma("unroll") \
+        for (int hf = 0; hf < 2; ++hf) \
+_Pragma("unroll") \
+            for (int c = 0; c < 4; ++c) \
+                Bk[hf][c] = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Ks[ks][16 * hf + li][32 * c + 8 * lq])); \
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0); \
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0); \
         f4_t Sd[2]; \
 _Pragma("unroll") \
         for (int hf = 0; hf < 2; ++hf) { \
             f4_t d = {0.f, 0.f, 0.f, 0.f}; \
 _Pragma("unroll") \
-            for (int c = 0; c < 4; ++c) { \
-                const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Ks[ks][16 * hf + li][32 * c + 8 * lq])); \
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Qf[c], B, d, 0, 0, 0); \
-            } \
+            for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(Qf[c], Bk[hf][c], d, 0, 0, 0); \
             Sd[hf] = d; \
         } \
-        float alpha[4]; \
+        /* scores in log2 units (scale * log2 e folded in); the causal mask only on blocks that reach past the */ \
+        /* tile's first query (wave-uniform). Lazy running max: a row's m moves only when one of the block's */ \
+        /* scores exceeds it by more than kLazyMax, so P = 2^(s - m) <= 2^kLazyMax (fp16 holds it at the same */ \
+        /* relative precision); a lane-local compare and one ballot decide, and only then are the row maxima */ \
+        /* reduced and O rescaled. l holds per-lane partial sums (reduced across the row after the key loop). */ \
+        const bool diag = j0 + kKB - 1 > p0 + q0; \
+        float sc0[4], sc1[4]; \
+        bool big = false; \
 _Pragma("unroll") \
         for (int e = 0; e < 4; ++e) { \
-            const int qpos = p0 + q0 + 4 * lq + e; \
-            float s0 = Sd[0][e] * scale, s1 = Sd[1][e] * scale; \
-            if (j0 + li > qpos) s0 = -INFINITY; \
-            if (j0 + 16 + li > qpos) s1 = -INFINITY; \
-            const float mb = row16_max(fmaxf(s0, s1)); \
-            const float mn = fmaxf(m[e], mb); \
-            const float p0v = mn == -INFINITY ? 0.f : __expf(s0 - mn); \
-            const float p1v = mn == -INFINITY ? 0.f : __expf(s1 - mn); \
+            sc0[e] = Sd[0][e] * sl2; \
+            sc1[e] = Sd[1][e] * sl2; \
+            if (diag) { \
+                const int qpos = p0 + q0 + 4 * lq + e; \
+                if (j0 + li > qpos) sc0[e] = -INFINITY; \
+                if (j0 + 16 + li > qpos) sc1[e] = -INFINITY; \
+            } \
+            big = big || fmaxf(sc0[e], sc1[e]) > m[e] + kLazyMax; /* never for a masked score */ \
+        } \
+        float alpha[4] = {1.f, 1.f, 1.f, 1.f}; \
+        const bool moved = __any(big); \
+        if (moved) { \
+_Pragma("unroll") \
+            for (int e = 0; e < 4; ++e) { \
+                const float mb = row16_max(fmaxf(sc0[e], sc1[e])); \
+                if (mb > m[e] + kLazyMax) { \
+                    alpha[e] = __builtin_amdgcn_exp2f(m[e] - mb);  /* m = -inf: 0 (O and l are still 0) */ \
+                    m[e] = mb; \
+                } \
+            } \
+        } \
+_Pragma("unroll") \
+        for (int e = 0; e < 4; ++e) { \
+            const float p0v = m[e] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc0[e] - m[e]); \
+            const float p1v = m[e] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc1[e] - m[e]); \
             const _Float16 h0 = (_Float16)p0v, h1 = (_Float16)p1v; \
-            alpha[e] = mn == -INFINITY ? 1.f : __expf(m[e] - mn); \
-            l[e] = l[e] * alpha[e] + row16_sum((float)h0 + (float)h1); \
-            m[e] = mn; \
+            l[e] = l[e] * alpha[e] + ((float)h0 + (float)h1); \
             P[(4 * lq + e) * kKB + li] = __builtin_bit_cast(uint16_t, h0); \
             P[(4 * lq + e) * kKB + 16 + li] = __builtin_bit_cast(uint16_t, h1); \
         } \
+        if (moved) { \
 _Pragma("unroll") \
-        for (int c = 0; c < 8; ++c) \
+            for (int c = 0; c < 8; ++c) \
 _Pragma("unroll") \
-            for (int e = 0; e < 4; ++e) O[c][e] *= alpha[e]; \
+                for (int e = 0; e < 4; ++e) O[c][e] *= alpha[e]; \
+        } \
         __builtin_amdgcn_wave_barrier(); \
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); \
         /* O += P V: A = P[query li][keys 8 lq .. + 8], B = Vt[dim 16 c + li][keys 8 lq .. + 8] */ \
         const h8_t A = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&P[li * kKB + 8 * lq])); \
+        h8_t Bv[8]; \
 _Pragma("unroll") \
-        for (int c = 0; c < 8; ++c) { \
-            const h8_t B = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(&Vt[ks][16 * c + li][vt_col(16 * c + li, 8 * lq)])); \
-            O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, O[c], 0, 0, 0); \
-        } \
+        for (int c = 0; c < 8; ++c) \
+            Bv[c] = __builtin_bit_cast(h8_t, *reinterpret_cast<const uint4*>(Vt + vt_off<QUAD>(ks, 16 * c + li, 8 * lq))); \
+        __builtin_amdgcn_sched_group_barrier(0x100, 9, 0); \
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0); \
+_Pragma("unroll") \
+        for (int c = 0; c < 8; ++c) O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bv[c], O[c], 0, 0, 0); \
         __builtin_amdgcn_wave_barrier();  /* P is rewritten in the next step only after these reads */ \
     } \
     do {} while (0)
+    // both steps of an iteration run unconditionally (a step past the tile's last key block stages clamped slots and
+    // computes nothing): with the second step conditional, the compiler's counter waits at the loop head cannot tell
+    // which loads are outstanding and wait for all of them, the set prefetched for the next step included
     for (int st = 0; st < nsteps; st += 2) {
         RK_ATTN_STEP(st, ka);
-        if (st + 1 < nsteps) {  // block-uniform
-            RK_ATTN_STEP(st + 1, kb);
-        }
+        RK_ATTN_STEP(st + 1, kb);
     }
 #undef RK_ATTN_STEP
+#pragma unroll
+    for (int e = 0; e < 4; ++e) l[e] = row16_sum(l[e]);  // the row's partial sums across its 16 lanes
     // merge the KS partials of each head into group 0, one group at a time, in group order: (m, l, O) of group k
     // through LDS (lane-major O, m / l per row), then m' = max, l' = l a + l_k b, O' = O a + O_k b
     if constexpr (KS > 1) {
@@ -537,8 +627,8 @@ _Pragma("unroll") \
                 for (int e = 0; e < 4; ++e) {
                     const float mk = mo[64 * 32 + 4 * lq + e], lk = mo[64 * 32 + kQT + 4 * lq + e];
                     const float mn = fmaxf(m[e], mk);
-                    const float a = mn == -INFINITY ? 0.f : __expf(m[e] - mn);
-                    const float b = mn == -INFINITY ? 0.f : __expf(mk - mn);
+                    const float a = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[e] - mn);  // m in log2 units
+                    const float b = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk - mn);
                     l[e] = l[e] * a + lk * b;
                     m[e] = mn;
 #pragma unroll
@@ -652,16 +742,23 @@ extern "C" int rk_prefill_attn(const void* q, const void* kc, const void* vc, vo
     const hipStream_t st = (hipStream_t)stream;
     // HPB query heads per block (a share of the KV head's rep), KS key groups per block (16 waves at most). With 4
     // heads per KV head each block takes 2 of them, so a 512-token prompt runs 256 blocks (one per CU) instead of
-    // 128, each staging its K / V for two heads: T = 512 19.2 -> 17.2 us per layer (one head per block: 26 us, the
-    // staging then dominates; 2 heads and 4 key groups 16.7 but 8.4 against 7.5 us at T = 69)
+    // 128, each staging its K / V for two heads (one head per block: the staging then dominates)
 #define RK_ATTN(HPB, K)                                                                                             \
     hipLaunchKernelGGL((prefill_attn_kernel<HPB, K>), dim3(NKV * (rep / (HPB)), (T + kQT - 1) / kQT),                \
                        dim3(64 * (HPB) * (K)), attn_lds_bytes(HPB, K), st, (const uint16_t*)q, (const uint16_t*)kc,   \
                        (const uint16_t*)vc, (uint16_t*)o, T, p0, NH, NKV, S, scale)
+    // the launch time is the longest query tile's key loop (p0 + T keys): past 384 keys four key groups per block
+    // (two waves per SIMD) beat two (T = 512: 13.9 against 14.5 us; at T = 16 .. 256 two are faster)
+    const bool long_keys = p0 + T > 384;
     switch (rep) {
         case 1: RK_ATTN(1, kAttnKS); break;
         case 2: RK_ATTN(2, kAttnKS); break;
-        case 4: RK_ATTN(2, kAttnKS); break;
+        case 4:
+            if (long_keys)
+                RK_ATTN(2, 4);
+            else
+                RK_ATTN(2, kAttnKS);
+            break;
         case 8: RK_ATTN(8, 2); break;
         default: return RK_ERR_SHAPE;
     }

@@ -37,18 +37,28 @@ def _rows_close(got, ref, tol=1e-2):
     assert (nr < tol).all() and (cos > 0.9999).all(), (int(t), int(h), float(nr[t, h]), float(cos[t, h]))
 
 
-@pytest.mark.parametrize("T,p0,NKV", [(1, 0, 4), (16, 0, 4), (37, 0, 4), (130, 0, 4), (20, 50, 4), (512, 0, 4),
-                                      (512, 50, 4), (130, 0, 8), (130, 0, 2)])
-def test_prefill_attention_matches_oracle(dev, T, p0, NKV):
+@pytest.mark.parametrize("T,p0,NKV,qs,ramp", [(1, 0, 4, 1, 0), (16, 0, 4, 1, 0), (37, 0, 4, 1, 0), (130, 0, 4, 1, 0),
+                                              (20, 50, 4, 1, 0), (512, 0, 4, 1, 0), (512, 50, 4, 1, 0),
+                                              (130, 0, 8, 1, 0), (130, 0, 2, 1, 0), (384, 0, 4, 1, 0),
+                                              (385, 0, 4, 1, 0), (300, 100, 4, 1, 0), (512, 0, 4, 6, 1),
+                                              (200, 0, 4, 6, 1), (96, 0, 4, 4, 2)])
+def test_prefill_attention_matches_oracle(dev, T, p0, NKV, qs, ramp):
     """T = 512 is the benchmarked prompt (16 key blocks of 32 per query tile at the last tile); NKV 8 / 2 give 2 / 8
-    query heads per KV head (other wave layouts of the block)."""
+    query heads per KV head (other wave layouts of the block); p0 + T = 384 / 385 sit on either side of the switch
+    to four key groups per block. qs scales q (score ranges of tens), and ramp grows the keys' norm along the
+    sequence (1: slot 0 x0.2 .. last slot x3, so a row's running max keeps moving in later key blocks and the lazy
+    rescale fires mid-loop; 2: the reverse, the max set by the first blocks)."""
     NH, HD = 16, 128
     S = 256 if p0 + T <= 256 else 640
-    g = torch.Generator().manual_seed(T + 7 * p0)
-    q = torch.randn(T, NH * HD, generator=g).half()
+    g = torch.Generator().manual_seed(T + 7 * p0 + 13 * ramp)
+    q = (torch.randn(T, NH * HD, generator=g) * qs).half()
     kc = torch.zeros(NKV, S, HD, dtype=torch.float16)
     vc = torch.zeros_like(kc)
-    kc[:, :p0 + T] = torch.randn(NKV, p0 + T, HD, generator=g).half()
+    kr = torch.randn(NKV, p0 + T, HD, generator=g)
+    if ramp:
+        gain = torch.linspace(0.2, 3.0, p0 + T) if ramp == 1 else torch.linspace(3.0, 0.2, p0 + T)
+        kr = kr * gain[None, :, None]
+    kc[:, :p0 + T] = kr.half()
     vc[:, :p0 + T] = torch.randn(NKV, p0 + T, HD, generator=g).half()
     o = torch.empty(T, NH * HD, dtype=torch.float16, device=dev)
     PF.prefill_attn(q.to(dev), kc.to(dev), vc.to(dev), o, T, p0, NH, NKV, HD, S, HD ** -0.5)

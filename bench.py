@@ -362,21 +362,28 @@ def run_decode(dev, steps):
     toks, st = gen.generate([1, 2, 3, 4], seed=0)
     out["generate"] = {k: st[k] for k in ("prompt_tokens", "tokens", "prefill_ms", "first_frame_ms", "decode_tok_s")}
     log(f"[bench] generate: {out['generate']}")
-    # batched prompt prefill (36 layers: mm_int4, the matrix-core causal attention, row glue), eager, best of 3
+    # batched prompt prefill (36 layers: mm_int4, the matrix-core causal attention, row glue), best of 3: eager
+    # launches from the host (`ms`) and, as a serving loop would replay it, the hipGraph of the prompt's 16-row
+    # length bucket (`graph_ms`; T = 34 and 69 run as 48 and 80 rows)
     import prefill as PF
     pf = PF.Prefill(cfg, w, eng.kc, eng.vc, eng.cos, eng.sin, max_T=512)
+    pfg = PF.Prefill(cfg, w, eng.kc, eng.vc, eng.cos, eng.sin, max_T=512, graphs=True)
     res = {}
-    for T in (69, 512):
+    for T in (34, 69, 512):
         ids = [(7 * i) % cfg.vocab for i in range(T)]
-        pf.run(ids)
-        best = math.inf
-        for _ in range(3):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            pf.run(ids)
-            torch.cuda.synchronize()
-            best = min(best, time.perf_counter() - t0)
-        res[f"T{T}"] = {"ms": round(best * 1e3, 2), "tok_s": round(T / best, 1)}
+        row = {}
+        for key, p in (("ms", pf), ("graph_ms", pfg)):
+            p.run(ids)
+            best = math.inf
+            for _ in range(3):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                p.run(ids)
+                torch.cuda.synchronize()
+                best = min(best, time.perf_counter() - t0)
+            row[key] = round(best * 1e3, 2)
+        row["tok_s"] = round(T / row["ms"] * 1e3, 1)
+        res[f"T{T}"] = row
     g = graph_of([lambda: PF.prefill_attn(pf.q, eng.kc[0], eng.vc[0], pf.o, 512, 0, cfg.NH, cfg.NKV, cfg.HD, cfg.S,
                                           cfg.HD ** -0.5)] * 10)
     us = time_graph_us(g, 10)

@@ -56,8 +56,14 @@ class Prefill:
     decode.random_weights / weights.load return; keep it: PersistentDecode re-lays out its own copy), `kc` / `vc`:
     the engine's cache [L, NKV, S, HD], `cos` / `sin`: its RoPE tables."""
 
-    def __init__(self, cfg, w, kc, vc, cos, sin, max_T=512):
+    def __init__(self, cfg, w, kc, vc, cos, sin, max_T=512, graphs=False, bucket=16):
+        """graphs: run each prompt as a replay of a hipGraph holding all of its ~220 launches, one graph per prompt
+        length rounded up to a multiple of `bucket` (captured on the first prompt of that bucket). The rows past the
+        prompt run on token id 0: they change none of the prompt's rows (every kernel is row-wise or causal), and
+        their K / V go to cache slots the decode step overwrites (slot pos) before any step attends to them."""
         self.cfg, self.w, self.kc, self.vc, self.cos, self.sin = cfg, w, kc, vc, cos, sin
+        self.graphs = {} if graphs else None
+        self.bucket = int(bucket)
         c, d, dt = cfg, kc.device, kc.dtype
         if dt != torch.float16:
             raise RuntimeError("the prefill attention runs on fp16 K / V")
@@ -81,7 +87,26 @@ class Prefill:
         T = len(ids)
         if not 1 <= T <= self.max_T:
             raise ValueError(f"prompt of {T} tokens (1..{self.max_T})")
-        self.ids[:T].copy_(torch.as_tensor(list(ids), dtype=torch.int64))
+        if self.graphs is None:
+            self.ids[:T].copy_(torch.as_tensor(list(ids), dtype=torch.int64))
+            self._enqueue(T)
+        else:
+            Tb = min(self.max_T, -(-T // self.bucket) * self.bucket)
+            self.ids[:Tb].copy_(torch.as_tensor(list(ids) + [0] * (Tb - T), dtype=torch.int64))
+            g = self.graphs.get(Tb)
+            if g is None:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self._enqueue(Tb)
+                self.graphs[Tb] = g
+            g.replay()
+        if hn is not None:
+            hn.copy_(self.h[T - 1])
+        return self.h[T - 1]
+
+    def _enqueue(self, T):
+        """Every kernel of the prefill of rows 0..T-1 (the prompt ids already in self.ids), on the current stream."""
+        c, w = self.cfg, self.w
         embed_ln_rows(self.ids[:T], w["emb"][0], w["emb"][1], w["ln"][0], self.x, self.h, c.eps)
         scale = c.HD ** -0.5
         for i in range(c.L):
@@ -92,6 +117,3 @@ class Prefill:
             MM.mm_int4(self.o[:T], *w["w_o"][i], out=self.a[:T])
             MM.mm_int4(self.act[:T], *w["w_down"][i], out=self.d[:T])
             add_ln_rows(self.x, self.a, self.d, w["norm"] if i == c.L - 1 else w["ln"][i + 1], self.h, T, c.eps)
-        if hn is not None:
-            hn.copy_(self.h[T - 1])
-        return self.h[T - 1]

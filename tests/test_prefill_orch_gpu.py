@@ -111,6 +111,30 @@ def test_prefill_matches_stepwise_oracle(dev, T):
             assert rep["norm_rel"] < 1e-2, (i, t, rep)
 
 
+def test_prefill_graph_buckets_match_eager(dev):
+    """Prefill(graphs=True): each prompt replays the hipGraph of its length rounded up to 16 (the rows past the
+    prompt run on token 0). Against the eager prefill of the same prompt: the final hidden state and cache slots
+    0..T-1 of every layer (the padded rows change none of the prompt's rows; the products' plans may differ with the
+    padded row count, so the bar is the parity tolerance, not bit equality). Prompts of 37 and 45 tokens share the
+    48-row graph (captured once, replayed with new ids), 69 tokens takes the 80-row one."""
+    cfg, wd, md = _model(dev, S=256)
+    eng = decode.PersistentDecode(cfg, wd, device=dev, keep_layer_weights=True)
+    eager = PF.Prefill(cfg, wd, eng.kc, eng.vc, eng.cos, eng.sin, max_T=128)
+    graph = PF.Prefill(cfg, wd, eng.kc, eng.vc, eng.cos, eng.sin, max_T=128, graphs=True)
+    g = torch.Generator().manual_seed(8)
+    for T in (37, 45, 69):
+        ids = [int(v) for v in torch.randint(0, cfg.vocab, (T,), generator=g)]
+        h_e = eager.run(ids).clone()
+        kc_e, vc_e = eng.kc[:, :, :T].clone(), eng.vc[:, :, :T].clone()
+        eng.kc.zero_(); eng.vc.zero_()
+        h_g = graph.run(ids).clone()
+        torch.cuda.synchronize()
+        for name, got, ref in (("hn", h_g, h_e), ("k", eng.kc[:, :, :T], kc_e), ("v", eng.vc[:, :, :T], vc_e)):
+            rep = O.parity_report(_np(got).reshape(-1), _np(ref).reshape(-1))
+            assert rep["norm_rel"] < 1e-3 and rep["cosine"] > 0.99999, (T, name, rep)
+    assert sorted(graph.graphs) == [48, 80]
+
+
 @pytest.mark.parametrize("kind", ["roles", "persistent"])
 def test_generate_from_batched_prefill(dev, kind):
     cfg, wd, md = _model(dev, seed=22)

@@ -324,6 +324,7 @@ class _OneLaunch:
         self.step_i = torch.zeros(1, dtype=torch.int64, device=self.dev)
         self.out = torch.zeros(max_new + 8, dtype=torch.int64, device=self.dev)
         self.sampler = sample.FusedSampler(self, lambda: self.logits)
+        self.graph, self.frames = None, {}  # graphs captured before hold the step without the tail
         return self.sampler
 
     def step(self):

@@ -9,9 +9,9 @@
 // Top-k ordering (the reference's, sample.py:7-11): each logit and its index are one int64 key,
 //   key = sortable(bits(x)) << 32 | index,  sortable(b) = b ^ ((b >> 31) & 0x7FFFFFFF)
 // so key order is value order (monotonic also for -inf) with ties broken by the larger index; keys are unique.
-// Stage 1: one wave per chunk of 512 logits sorts the chunk with a bitonic network held in registers (8 keys per
-// lane, element lane * 8 + e): the 24 stages with partner distance < 8 stay inside a lane, the 21 others exchange
-// all 8 keys of a lane with one partner lane (16 independent 32-bit shuffles per stage). Stage 2: the chunks' top-32
+// Stage 1: four waves per chunk of 512 logits sort the chunk with a bitonic network held in registers (2 keys per
+// lane, element 2 t + i): partners at distance 1 stay inside a lane, at 2 .. 64 are one 64-bit shuffle away, and
+// the three stages at distance 128 / 256 exchange through LDS between the waves. Stage 2: the chunks' top-32
 // lists are merged pairwise in a tree, one wave per merge (a 32-key list and the other reversed form a bitonic
 // sequence of 64, one key per lane; 6 shuffle stages keep the top 32 in order), 16 waves per level. An LDS bitonic
 // sort of the whole chunk / candidate list (what the Triton code's tl.sort does) measured ~1 us per network stage
@@ -40,7 +40,6 @@ constexpr int kMaxNC = 4096;   // candidate slots of the pick (at most 128 chunk
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kStopRows = kWaves;  // stop-predictor rows per block (one per wave)
-constexpr int kChunksPerBlock = 1;  // stage 1: wave 0 of a block per chunk (one sort per SIMD: the network is VALU-bound)
 
 RK_DEV int32_t sortable(float x) {
     const int32_t b = __builtin_bit_cast(int32_t, x);
@@ -77,48 +76,62 @@ RK_DEV int64_t shfl_xor64(int64_t v, int m) {
     return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
 }
 
-// one wave sorts the 512 keys of chunk c (element lane * 8 + e) descending and stores them to out[0 .. 512)
-RK_DEV void chunk_sort(const void* logits, int ldt, bool early, int nv, int end_idx, int c, int64_t* out) {
-    const int lane = threadIdx.x & 63;
-    int64_t v[8];
+// Waves 0..3 of the block (one per SIMD) sort the 512 keys of chunk c descending and store them to out[0 .. 512):
+// element e = 2 t + i of thread t < 256 (two keys per lane). Partners at distance 1 sit in the same lane, at 2 .. 64
+// in another lane of the same wave (one 64-bit shuffle per key), at 128 and 256 in another wave (through xs, 512
+// keys of LDS). Every thread of the block runs the loop and reaches its barriers (the other waves and a block
+// without a chunk, `active` false, only pass them), so the block's barriers always pair up. (One wave with eight keys
+// per lane measured ~7 us per chunk: the network's dependent compare / select / shuffle chain on one SIMD.)
+RK_DEV void chunk_sort(const void* logits, int ldt, bool early, int nv, int end_idx, int c, bool active, int64_t* out,
+                       int64_t* xs) {
+    const int t = threadIdx.x;
+    const bool on = active && t < 256;
+    int64_t v[2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const int i = c * kCH + lane * 8 + e;
-        float x = i < nv ? load_act(logits, ldt, (size_t)i) : -INFINITY;
-        if (early && i == end_idx) x = -INFINITY;  // no </audio> during the first min_new tokens
-        v[e] = make_key(x, i);
+    for (int i = 0; i < 2; ++i) {
+        const int e = c * kCH + 2 * t + i;
+        float x = on && e < nv ? load_act(logits, ldt, (size_t)e) : -INFINITY;
+        if (early && e == end_idx) x = -INFINITY;  // no </audio> during the first min_new tokens
+        v[i] = make_key(x, e);
     }
 #pragma unroll
     for (int k = 2; k <= kCH; k <<= 1) {
+        const bool desc = ((2 * t) & k) == 0;  // the direction of both of the lane's elements (k >= 2)
 #pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            if (j < 8) {  // partners inside the lane
+            if (j == 1) {
+                const bool sw = desc ? v[0] < v[1] : v[0] > v[1];
+                const int64_t a = v[0], b = v[1];
+                v[0] = sw ? b : a;
+                v[1] = sw ? a : b;
+            } else if (j < 128) {  // partner lane t ^ (j / 2), same wave, same slot
+                const int m = j >> 1;
+                const bool keep_max = ((t & m) == 0) == desc;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int pe = e ^ j;
-                    if (pe > e) {
-                        const bool desc = ((lane * 8 + e) & k) == 0;
-                        const int64_t a = v[e], b = v[pe];
-                        const bool sw = desc ? a < b : a > b;
-                        v[e] = sw ? b : a;
-                        v[pe] = sw ? a : b;
-                    }
+                for (int i = 0; i < 2; ++i) {
+                    const int64_t o = shfl_xor64(v[i], m);
+                    v[i] = keep_max ? (o > v[i] ? o : v[i]) : (o < v[i] ? o : v[i]);
                 }
-            } else {  // partner lane: lane ^ (j / 8), same slot
-                const int m = j >> 3;
-                const bool lower = (lane & m) == 0;  // this lane holds the lower element of each pair
-                const bool desc = ((lane * 8) & k) == 0;  // the same for all 8 slots (k >= 16)
-                const bool keep_max = lower == desc;
-                int64_t o[8];
+            } else {  // partner in another wave
+                __syncthreads();  // the previous exchange's reads are done
+                if (on) {
+                    xs[2 * t] = v[0];
+                    xs[2 * t + 1] = v[1];
+                }
+                __syncthreads();
+                const bool keep_max = (((2 * t) & j) == 0) == desc;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = shfl_xor64(v[e], m);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = keep_max ? (o[e] > v[e] ? o[e] : v[e]) : (o[e] < v[e] ? o[e] : v[e]);
+                for (int i = 0; i < 2; ++i) {
+                    const int64_t o = on ? xs[(2 * t + i) ^ j] : v[i];
+                    v[i] = keep_max ? (o > v[i] ? o : v[i]) : (o < v[i] ? o : v[i]);
+                }
             }
         }
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) st_agent(out + lane * 8 + e, v[e]);
+    if (on) {
+        st_agent(out + 2 * t, v[0]);
+        st_agent(out + 2 * t + 1, v[1]);
+    }
 }
 
 // one wave: the top 32 of two descending 32-key lists a, b (LDS) into dst[0 .. 32) in order (dst may alias a)
@@ -200,13 +213,14 @@ RK_DEV void stop_rows(const void* h, int hdt, const float* lnw, const float* lnb
     if (lane == 0) st_agent(z1 + r, 0.5f * acc * (1.0f + erff(acc * 0.7071067811865476f)));  // exact GELU (F.gelu)
 }
 
-// ---- stage 1 (reference topk_partial, sample.py:53-61): wave 0 of block blk sorts chunk blk
+// ---- stage 1 (reference topk_partial, sample.py:53-61): block blk sorts chunk blk (waves 0..3; every thread of
+// the block calls in, for the barriers)
 RK_DEV void topk_chunks(const void* logits, int ldt, const int64_t* step, int64_t* keys, int nv, int end_idx,
                         int min_new, int blk) {
-    const int c = blk * kChunksPerBlock + (threadIdx.x >> 6);
-    if ((threadIdx.x >> 6) >= kChunksPerBlock || c * kCH >= nv) return;
+    __shared__ int64_t xs[kCH];
+    const int c = blk;
     const bool early = step[0] < (int64_t)min_new;
-    chunk_sort(logits, ldt, early, nv, end_idx, c, keys + (size_t)c * kCH);
+    chunk_sort(logits, ldt, early, nv, end_idx, c, c * kCH < nv, keys + (size_t)c * kCH, xs);
 }
 
 // ---- stage 2 (reference pick, sample.py:65-93): the top 32 of the chunks' lists, sample, stop rule, counters.
@@ -349,7 +363,7 @@ extern "C" int rk_topk_partial(const void* logits, int logits_dtype, const int64
     if (logits_dtype != RK_F16 && logits_dtype != RK_BF16 && logits_dtype != RK_F32) return RK_ERR_DTYPE;
     if (nv <= 0) return RK_ERR_SHAPE;
     const int nch = (nv + kCH - 1) / kCH;
-    hipLaunchKernelGGL(topk_partial_kernel, dim3((nch + kChunksPerBlock - 1) / kChunksPerBlock), dim3(kThreads), 0,
+    hipLaunchKernelGGL(topk_partial_kernel, dim3(nch), dim3(kThreads), 0,
                        (hipStream_t)stream, logits, logits_dtype, step, keys, nv, end_idx, min_new);
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }
@@ -388,7 +402,7 @@ extern "C" int rk_sample_tail(const void* h, int h_dtype, const float* lnw, cons
     a.hdt = h_dtype; a.wdt = w1_dtype; a.ldt = logits_dtype; a.H = H; a.nz = nz; a.nv = nv; a.end_idx = end_idx;
     a.min_new = min_new; a.nch = nch; a.topk = topk; a.nzb = (nz + kStopRows - 1) / kStopRows;
     const size_t lds = std::max((size_t)H * sizeof(float), (size_t)nch * kKeep * sizeof(int64_t));
-    const int chunk_blocks = (nch + kChunksPerBlock - 1) / kChunksPerBlock;
+    const int chunk_blocks = nch;  // one block per chunk
     hipLaunchKernelGGL(sample_tail_kernel, dim3(a.nzb + chunk_blocks), dim3(kThreads), lds, (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_LAUNCH;
 }

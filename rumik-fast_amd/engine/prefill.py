@@ -56,7 +56,7 @@ class Prefill:
     decode.random_weights / weights.load return; keep it: PersistentDecode re-lays out its own copy), `kc` / `vc`:
     the engine's cache [L, NKV, S, HD], `cos` / `sin`: its RoPE tables."""
 
-    def __init__(self, cfg, w, kc, vc, cos, sin, max_T=512, graphs=False, bucket=16):
+    def __init__(self, cfg, w, kc, vc, cos, sin, max_T=512, graphs=False, bucket=16, overlap=None):
         """graphs: run each prompt as a replay of a hipGraph holding all of its ~220 launches, one graph per prompt
         length rounded up to a multiple of `bucket` (captured on the first prompt of that bucket). The rows past the
         prompt run on token id 0: they change none of the prompt's rows (every kernel is row-wise or causal), and
@@ -64,6 +64,15 @@ class Prefill:
         self.cfg, self.w, self.kc, self.vc, self.cos, self.sin = cfg, w, kc, vc, cos, sin
         self.graphs = {} if graphs else None
         self.bucket = int(bucket)
+        # overlap: the down product's branch (its X pre-pass, product and split-K sum) runs on a second stream,
+        # beside the attention and the o product (both read only what post_rows wrote and meet again at
+        # add_ln_rows); default priority, like every stream here. None: on for graph replays and for prompts of at
+        # least 256 rows (eagerly, the two extra stream switches per layer cost more host time than a short prompt's
+        # kernels take).
+        self.overlap = overlap
+        self.side = torch.cuda.Stream(device=kc.device)
+        self.ev_fork = [torch.cuda.Event() for _ in range(cfg.L)]
+        self.ev_join = [torch.cuda.Event() for _ in range(cfg.L)]
         c, d, dt = cfg, kc.device, kc.dtype
         if dt != torch.float16:
             raise RuntimeError("the prefill attention runs on fp16 K / V")
@@ -109,11 +118,22 @@ class Prefill:
         c, w = self.cfg, self.w
         embed_ln_rows(self.ids[:T], w["emb"][0], w["emb"][1], w["ln"][0], self.x, self.h, c.eps)
         scale = c.HD ** -0.5
+        main = torch.cuda.current_stream(self.kc.device)
+        ov = self.overlap if self.overlap is not None else (self.graphs is not None or T >= 256)
         for i in range(c.L):
             MM.mm_int4(self.h[:T], *w["w_in"][i], out=self.y[:T])
             post_rows(self.y, 0, self.cos, self.sin, self.kc[i], self.vc[i], self.q, self.act, T, c.NH, c.NKV, c.HD,
                       c.S, c.inter, c.sliding[i])
+            if ov:
+                self.ev_fork[i].record(main)  # act is written
+                self.side.wait_event(self.ev_fork[i])
+                with torch.cuda.stream(self.side):
+                    MM.mm_int4(self.act[:T], *w["w_down"][i], out=self.d[:T])
+                self.ev_join[i].record(self.side)
             prefill_attn(self.q, self.kc[i], self.vc[i], self.o, T, 0, c.NH, c.NKV, c.HD, c.S, scale)
             MM.mm_int4(self.o[:T], *w["w_o"][i], out=self.a[:T])
-            MM.mm_int4(self.act[:T], *w["w_down"][i], out=self.d[:T])
+            if ov:
+                main.wait_event(self.ev_join[i])  # d is written (and act may be rewritten by the next layer)
+            else:
+                MM.mm_int4(self.act[:T], *w["w_down"][i], out=self.d[:T])
             add_ln_rows(self.x, self.a, self.d, w["norm"] if i == c.L - 1 else w["ln"][i + 1], self.h, T, c.eps)

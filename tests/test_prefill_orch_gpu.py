@@ -135,6 +135,28 @@ def test_prefill_graph_buckets_match_eager(dev):
     assert sorted(graph.graphs) == [48, 80]
 
 
+@pytest.mark.parametrize("T", [37, 300])
+def test_prefill_overlap_is_bit_identical(dev, T):
+    """The down product's branch on a second stream (overlap=True) runs the same kernels on the same inputs as the
+    serial order, so the final hidden state and every K / V slot written are bit-identical; both eagerly and, for
+    T = 37, as a graph replay (graphs=True; 48 rows)."""
+    cfg, wd, md = _model(dev, S=512)
+    eng = decode.PersistentDecode(cfg, wd, device=dev, keep_layer_weights=True)
+    ids = [int(v) for v in torch.randint(0, cfg.vocab, (T,), generator=torch.Generator().manual_seed(T))]
+    outs = []
+    for kw in (dict(overlap=False), dict(overlap=True), dict(overlap=True, graphs=True)):
+        if kw.get("graphs") and T > 64:
+            continue
+        eng.kc.zero_(); eng.vc.zero_()
+        pf = PF.Prefill(cfg, wd, eng.kc, eng.vc, eng.cos, eng.sin, max_T=max(64, T), **kw)
+        h = pf.run(ids).clone()
+        torch.cuda.synchronize()
+        outs.append((h, eng.kc[:, :, :T].clone(), eng.vc[:, :, :T].clone()))
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("kind", ["roles", "persistent"])
 def test_generate_from_batched_prefill(dev, kind):
     cfg, wd, md = _model(dev, seed=22)

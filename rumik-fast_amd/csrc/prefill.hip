@@ -283,20 +283,30 @@ __global__ __launch_bounds__(64) void post_rows_kernel(const void* y, int ldy, i
     }
 }
 
-// post_rows, one block of 256 threads per row t: the q / k heads as 32-bit pairs (RoPE), v and silu(gate) * up as
-// 8-column chunks (shapes with HD % 8 == 0, inter % 8 == 0 and 16-byte aligned rows)
+// post_rows on a 2-D grid (row t, part): one item per thread, so a short prompt still spreads over the chip (one
+// block per row left 34 of 256 CUs busy at T = 34, each walking 25k values: 8.5 us). Parts [0, nqk): the q / k heads
+// as 32-bit pairs (RoPE), 256 pairs per part; part nqk: v as 8-column chunks; parts after it: silu(gate) * up as
+// 8-column chunks, 256 per part. Shapes with HD % 8 == 0, inter % 8 == 0 and 16-byte aligned rows.
+constexpr int kPostPart = 256;
+
+__host__ __device__ inline int post_qk_parts(int NH, int NKV, int HD) { return ((NH + NKV) * (HD / 2) + kPostPart - 1) / kPostPart; }
+__host__ __device__ inline int post_act_parts(int inter) { return (inter / 8 + kPostPart - 1) / kPostPart; }
+
 template <bool BF16>
-__global__ __launch_bounds__(256) void post_rows_vec_kernel(const uint16_t* __restrict__ y, int ldy, int p0,
-                                                            const uint16_t* __restrict__ cos_t,
-                                                            const uint16_t* __restrict__ sin_t,
-                                                            uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                                                            uint16_t* __restrict__ qo, uint16_t* __restrict__ act,
-                                                            int NH, int NKV, int HD, int S, int inter, int rope) {
-    const int t = blockIdx.x, tid = threadIdx.x, pos = p0 + t;
+__global__ __launch_bounds__(kPostPart) void post_rows_vec_kernel(const uint16_t* __restrict__ y, int ldy, int p0,
+                                                                  const uint16_t* __restrict__ cos_t,
+                                                                  const uint16_t* __restrict__ sin_t,
+                                                                  uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                                  uint16_t* __restrict__ qo, uint16_t* __restrict__ act,
+                                                                  int NH, int NKV, int HD, int S, int inter, int rope) {
+    const int t = blockIdx.x, part = blockIdx.y, tid = threadIdx.x, pos = p0 + t;
     const uint16_t* yr = y + (size_t)t * ldy;
     const int dt = BF16 ? RK_BF16 : RK_F16;
-    const int hp = HD / 2;
-    for (int pi = tid; pi < (NH + NKV) * hp; pi += 256) {
+    const int hp = HD / 2, nqk = post_qk_parts(NH, NKV, HD);
+    const u4_t* y4 = reinterpret_cast<const u4_t*>(yr);
+    if (part < nqk) {
+        const int pi = part * kPostPart + tid;
+        if (pi >= (NH + NKV) * hp) return;
         const int hd = pi / hp, j = pi - hd * hp;
         const uint32_t v = *reinterpret_cast<const uint32_t*>(yr + (size_t)hd * HD + 2 * j);
         const float xe = load_act(&v, dt, 0), xo = load_act(&v, dt, 1);
@@ -313,22 +323,22 @@ __global__ __launch_bounds__(256) void post_rows_vec_kernel(const uint16_t* __re
         uint16_t* dst = hd < NH ? qo + (size_t)t * NH * HD + (size_t)hd * HD + 2 * j
                                 : kc + ((size_t)(hd - NH) * S + pos) * HD + 2 * j;
         *reinterpret_cast<uint32_t*>(dst) = o;
-    }
-    const u4_t* y4 = reinterpret_cast<const u4_t*>(yr);
-    const int vb = (NH + NKV) * HD / 8, nv = NKV * HD / 8;
-    for (int c = tid; c < nv; c += 256) {
-        const int hv = (8 * c) / HD, off = 8 * c - hv * HD;
-        *reinterpret_cast<u4_t*>(vc + ((size_t)hv * S + pos) * HD + off) = y4[vb + c];
-    }
-    const int gb = (NH + 2 * NKV) * HD / 8, ni = inter / 8;
-    u4_t* a4 = reinterpret_cast<u4_t*>(act + (size_t)t * inter);
-    for (int c = tid; c < ni; c += 256) {
+    } else if (part == nqk) {
+        const int vb = (NH + NKV) * HD / 8, nv = NKV * HD / 8;
+        for (int c = tid; c < nv; c += kPostPart) {
+            const int hv = (8 * c) / HD, off = 8 * c - hv * HD;
+            *reinterpret_cast<u4_t*>(vc + ((size_t)hv * S + pos) * HD + off) = y4[vb + c];
+        }
+    } else {
+        const int gb = (NH + 2 * NKV) * HD / 8, ni = inter / 8;
+        const int c = (part - nqk - 1) * kPostPart + tid;
+        if (c >= ni) return;
         float g[8], u[8], o[8];
         unpack8<BF16>(y4[gb + c], g);
         unpack8<BF16>(y4[gb + ni + c], u);
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
-        a4[c] = pack8<BF16>(o);
+        reinterpret_cast<u4_t*>(act + (size_t)t * inter)[c] = pack8<BF16>(o);
     }
 }
 
@@ -713,14 +723,15 @@ extern "C" int rk_post_rows(const void* y, int ldy, int p0, const void* cos_t, c
                      !((uintptr_t)act & 15) && !((uintptr_t)kc & 3) && !((uintptr_t)q_out & 3);
     if (vec) {
         const auto* y16 = static_cast<const uint16_t*>(y);
+        const dim3 pgrid(T, post_qk_parts(NH, NKV, HD) + 1 + post_act_parts(inter));
         const auto* c16 = static_cast<const uint16_t*>(cos_t);
         const auto* s16 = static_cast<const uint16_t*>(sin_t);
         if (dt == RK_BF16)
-            hipLaunchKernelGGL(post_rows_vec_kernel<true>, dim3(T), dim3(256), 0, st, y16, ldy, p0, c16, s16,
+            hipLaunchKernelGGL(post_rows_vec_kernel<true>, pgrid, dim3(kPostPart), 0, st, y16, ldy, p0, c16, s16,
                                (uint16_t*)kc, (uint16_t*)vc, (uint16_t*)q_out, (uint16_t*)act, NH, NKV, HD, S, inter,
                                rope);
         else
-            hipLaunchKernelGGL(post_rows_vec_kernel<false>, dim3(T), dim3(256), 0, st, y16, ldy, p0, c16, s16,
+            hipLaunchKernelGGL(post_rows_vec_kernel<false>, pgrid, dim3(kPostPart), 0, st, y16, ldy, p0, c16, s16,
                                (uint16_t*)kc, (uint16_t*)vc, (uint16_t*)q_out, (uint16_t*)act, NH, NKV, HD, S, inter,
                                rope);
     } else {

@@ -190,11 +190,12 @@ def test_generate_from_batched_prefill(dev, kind):
 # ---- the row kernels on their own (vector path: H % 8 == 0 and 16-byte aligned rows; scalar path otherwise)
 @pytest.mark.parametrize("dtype,H,T,offset", [(torch.float16, 2048, 37, 0), (torch.bfloat16, 2048, 5, 0),
                                               (torch.float16, 200, 9, 0), (torch.float16, 196, 9, 0),
-                                              (torch.float16, 2048, 3, 1)])
+                                              (torch.float16, 2048, 3, 1), (torch.float16, 4096, 6, 0),
+                                              (torch.bfloat16, 8192, 3, 0)])
 def test_add_ln_rows(dev, dtype, H, T, offset):
     """x[t] = dt(x[t] + a[t] + b[t]) exactly; h[t] = LayerNorm(x[t]) * w against the oracle's fp32 LayerNorm.
-    H = 200 takes the vector kernel with a partial last pass, H = 196 (rows not 16-byte aligned) and offset = 1
-    (every buffer shifted by one element) the scalar one."""
+    H = 200 takes the vector kernel with a partial last pass, H = 4096 / 8192 with two / four passes, H = 196 (rows
+    not 16-byte aligned) and offset = 1 (every buffer shifted by one element) the scalar one."""
     g = torch.Generator().manual_seed(H + T)
     x, a, b = (torch.randn(T * H + offset, generator=g).to(dtype) for _ in range(3))
     w = (torch.rand(H + offset, generator=g) + 0.5).to(dtype)

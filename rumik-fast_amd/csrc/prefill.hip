@@ -16,8 +16,9 @@
 // the reference's tensor-core PV in 16-bit) to its LDS tile in the A layout and accumulates O += P V (8 MFMAs, fp32).
 // The launch time is the longest query tile's key loop, whose steps are bound by the waves' VALU work (one or two
 // waves per SIMD), so the loop keeps the per-score instruction count down: the row max is reduced across lanes only
-// when a ballot says some score passed the running max by more than 2^8, O is rescaled only then, the row sums stay
-// per lane until the loop ends, and the causal mask is applied only on blocks that reach past the tile's first query.
+// when a ballot says some score exceeds its row's running max by more than 8 (log2 units, a factor of 256), O is
+// rescaled only then, the row sums stay per lane until the loop ends, and the causal mask is applied only on blocks
+// that reach past the tile's first query.
 #include "common.h"
 
 #include <initializer_list>
@@ -32,7 +33,7 @@ constexpr int kQT = 16;      // queries per tile
 #ifndef RK_ATTN_KS
 #define RK_ATTN_KS 2
 #endif
-constexpr int kAttnKS = RK_ATTN_KS;  // key groups per attention block (query heads per KV head <= 4)
+constexpr int kAttnKS = RK_ATTN_KS;  // key groups per attention block up to 384 keys (four past it; <= 4 heads per KV head)
 
 RK_DEV float block_sum(float v, float* red) {
     v = wave_sum(v);

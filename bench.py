@@ -362,10 +362,21 @@ def run_decode(dev, steps):
     toks, st = gen.generate([1, 2, 3, 4], seed=0)
     out["generate"] = {k: st[k] for k in ("prompt_tokens", "tokens", "prefill_ms", "first_frame_ms", "decode_tok_s")}
     log(f"[bench] generate: {out['generate']}")
+    # time to first frame with the batched prefill: a 34-token prompt (the reference's README quotes 50 ms for its
+    # whole 34-token prefill) through Prefill's graph replay, the head and the sampling tail, then 64 tokens
+    import prefill as PF
+    pfq = PF.Prefill(cfg, w, eng.kc, eng.vc, eng.cos, eng.sin, max_T=64, graphs=True)
+    genp = generate.Generator(eng, Q=8, max_new=64, prefill=pfq)
+    prompt = [(5 * i + 3) % cfg.vocab for i in range(34)]
+    genp.generate(prompt, seed=0)  # warm (captures the 48-row prefill graph)
+    toks, st = genp.generate(prompt, seed=0)
+    out["generate_prefilled"] = {k: st[k] for k in ("prompt_tokens", "tokens", "prefill_ms", "first_frame_ms",
+                                                    "decode_tok_s")}
+    log(f"[bench] generate with the batched prefill: {out['generate_prefilled']}")
+    del genp, pfq
     # batched prompt prefill (36 layers: mm_int4, the matrix-core causal attention, row glue), best of 3: eager
     # launches from the host (`ms`) and, as a serving loop would replay it, the hipGraph of the prompt's 16-row
     # length bucket (`graph_ms`; T = 34 and 69 run as 48 and 80 rows)
-    import prefill as PF
     pf = PF.Prefill(cfg, w, eng.kc, eng.vc, eng.cos, eng.sin, max_T=512)
     pfg = PF.Prefill(cfg, w, eng.kc, eng.vc, eng.cos, eng.sin, max_T=512, graphs=True)
     res = {}

@@ -77,6 +77,30 @@ RK_DEV void swap_halves(float v, float& a, float& b) {
     a = __builtin_bit_cast(float, x);
     b = __builtin_bit_cast(float, y);
 }
+// v of lane i ^ M for M = 1, 2, 4, 8, 16, 32 from VALU lane moves only (no LDS round trip): DPP quad permutes for
+// 1 and 2, row_half_mirror (i -> 7 - i in each 8 lanes) followed by the quad reversal (i -> 3 - i in each 4) for 4,
+// row_ror:8 inside the 16-lane rows for 8, and the lane swaps above for 16 and 32 (lane i keeps the half it lacks).
+template <int M>
+RK_DEV uint32_t xor_lanes(uint32_t v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane distance");
+    const int x = (int)v;
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);
+    if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);
+    if constexpr (M == 4)
+        return (uint32_t)__builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF,
+                                                  true);
+    if constexpr (M == 8) return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);
+    if constexpr (M >= 16) {
+        int a = x, b = x;
+        if constexpr (M == 32)
+            asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+        else
+            asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+        return (uint32_t)((__lane_id() & M) ? a : b);  // a: the lower half's values, b: the upper half's
+    }
+    return v;
+}
+
 template <int M>
 RK_DEV float sum_xor(float v) {  // v[i] + v[i ^ M], M = 16 or 32
     float a, b;

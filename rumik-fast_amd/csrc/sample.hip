@@ -71,9 +71,22 @@ RK_DEV float ld_agent(const float* p) {
                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
+// v of lane i ^ m (m a power of two below 64, a constant once the callers' loops are unrolled), both halves by
+// VALU lane moves (no LDS round trip)
+template <int M>
+RK_DEV int64_t xor64(int64_t v) {
+    const uint32_t lo = xor_lanes<M>((uint32_t)v), hi = xor_lanes<M>((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 RK_DEV int64_t shfl_xor64(int64_t v, int m) {
-    const int lo = __shfl_xor((int)(uint32_t)v, m), hi = __shfl_xor((int)(v >> 32), m);
-    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+    switch (m) {
+        case 1: return xor64<1>(v);
+        case 2: return xor64<2>(v);
+        case 4: return xor64<4>(v);
+        case 8: return xor64<8>(v);
+        case 16: return xor64<16>(v);
+        default: return xor64<32>(v);
+    }
 }
 
 // Waves 0..3 of the block (one per SIMD) sort the 512 keys of chunk c descending and store them to out[0 .. 512):

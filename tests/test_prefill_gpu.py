@@ -280,7 +280,7 @@ def test_prepared_x_strided_rows_and_scale_fallback(M, kernel, dev):
     _check(Y2, ref, "unaligned scales")
 
 
-# ---- the small-M stream kernel (M <= 48: X held in registers, code tiles streamed, K chunks of 16 groups)
+# ---- the small-M stream kernel (M <= 48 and K <= 2048: X held in registers, code tiles streamed, no K split)
 F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
 
 
